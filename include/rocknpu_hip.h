@@ -1,0 +1,72 @@
+/*
+ * rocknpu_hip.h — device-pointer launch layer of the MI355X build.
+ *
+ * These entry points replace the NPU executor layer the reference's C ABI
+ * drives (crates/rocknpu-matmul) and the llama.cpp CPU decode kernels the
+ * reference plugin leaves M=1 to. Every pointer is a DEVICE pointer; `stream`
+ * is a hipStream_t (NULL = the null stream). Calls validate their arguments on
+ * the host, enqueue kernels and return without synchronising; status codes
+ * are those of rocknpu.h (0 ok, -1 invalid argument, -3 launch failure).
+ *
+ * Device layouts: W8 is [n, k_pad] int8 row-major with k_pad a multiple of 64
+ * and columns k..k_pad zero; A8 is [m, k_pad] likewise; scales are f32; Q8_K
+ * rows are k/256 blocks of 292 bytes (f32 d, int8 qs[256], int16 bsums[16]).
+ */
+#ifndef ROCKNPU_HIP_H
+#define ROCKNPU_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Kernel (a): GGUF K-quant -> W8 repack. Replaces the host repack
+ * prepare_q4_k_w8a8 / prepare_q5_k_w8a8 / prepare_q6_k_w8a8
+ * (crates/rocknpu-capi/src/lib.rs:711-757, :759-806, :974-994) and the
+ * resident weight placement of Int8DecodePool::prepare_weights_mtile_direct_with_split
+ * (crates/rocknpu-matmul/src/int8_decode_pool.rs:606-615).
+ * kind 4/5 need `blocks` 16-byte aligned, kind 6 2-byte aligned; w8 16-byte
+ * aligned. A row whose dequantised values are not all finite gets scale NaN
+ * (the reference rejects such a weight). */
+int rocknpu_hip_repack_w8(uint32_t kind, const uint8_t * blocks, size_t blocks_bytes, size_t k,
+                          size_t n, size_t k_pad, int8_t * w8, float * scales, void * stream);
+
+/* Kernel (b): per-token symmetric int8 quantisation of A [m, lda] f32 (first k
+ * columns) into A8 [m, k_pad]. Replaces the per-row quantize_symmetric_into
+ * loop of crates/rocknpu-capi/src/lib.rs:1776-1791 (definition :614-654).
+ * A row holding a non-finite value gets scale NaN and a zero int8 row. */
+int rocknpu_hip_quantize_a8(const float * a, size_t m, size_t k, size_t lda, size_t k_pad,
+                            int8_t * a8, float * scales, void * stream);
+
+/* Kernel (c): out[m, ldo] = (f32(A8 W8^T) * a_scales[m]) * w_scales[n] on int8
+ * MFMA; if out_i32 is non-NULL the exact int32 accumulators are also written
+ * there as [m, n]. Replaces Int8DecodePool::execute_prepared_mtile_direct
+ * (crates/rocknpu-matmul/src/int8_decode_pool.rs:625-686) plus the
+ * rescale_i32_row sink (crates/rocknpu-capi/src/lib.rs:692-709, :1868-1884).
+ * a8 and w8 16-byte aligned, k_pad a multiple of 64. */
+int rocknpu_hip_gemm_w8a8(const int8_t * a8, const float * a_scales, const int8_t * w8,
+                          const float * w_scales, size_t m, size_t n, size_t k_pad, float * out,
+                          size_t ldo, int32_t * out_i32, void * stream);
+
+/* Q8_K activation quantisation of x [m, ldx] f32 (k a multiple of 256) into
+ * m rows of k/256 Q8_K blocks. Replaces ggml quantize_row_q8_K
+ * (llama.cpp, ggml-quants.c quantize_row_q8_K_ref). q8k 4-byte aligned. */
+int rocknpu_hip_quantize_q8_k(const float * x, size_t m, size_t k, size_t ldx, uint8_t * q8k,
+                              void * stream);
+
+/* Kernel (d): decode GEMV out[mi * ldo + ni] = vec_dot(W row ni, Q8_K row mi)
+ * for Q4_K (kind 4, `w` 16-byte aligned) or Q6_K (kind 6, 2-byte aligned)
+ * weights. Replaces ggml_vec_dot_q4_K_q8_K / ggml_vec_dot_q6_K_q8_K (llama.cpp
+ * ggml-cpu). If isum/msum are non-NULL the exact per-(mi, ni, block) integer
+ * sums are written there as [m][n][k/256] (msum is 0 for Q6_K). */
+int rocknpu_hip_gemv_q8_k(uint32_t kind, const uint8_t * w, size_t w_bytes, size_t k, size_t n,
+                          const uint8_t * q8k, size_t m, float * out, size_t ldo, int32_t * isum,
+                          int32_t * msum, void * stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif

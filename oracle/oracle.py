@@ -1,0 +1,172 @@
+"""ctypes wrapper of the C oracle (liboracle.so) — TEST INFRASTRUCTURE ONLY.
+
+Used by tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg as
+the checker; nothing in the product imports it. The C functions and the
+reference lines they restate are listed in oracle.h.
+"""
+from __future__ import annotations
+
+import ctypes
+import subprocess
+from pathlib import Path
+
+import numpy as np
+
+HERE = Path(__file__).resolve().parent
+LIB_PATH = HERE / "liboracle.so"
+
+QK = 256
+BLOCK_BYTES = {4: 144, 5: 176, 6: 210}
+Q8K_BYTES = 292
+
+_lib = None
+
+_u8p = ctypes.POINTER(ctypes.c_uint8)
+_i8p = ctypes.POINTER(ctypes.c_int8)
+_i32p = ctypes.POINTER(ctypes.c_int32)
+_f32p = ctypes.POINTER(ctypes.c_float)
+_f64p = ctypes.POINTER(ctypes.c_double)
+_sz = ctypes.c_size_t
+
+
+class OracleError(RuntimeError):
+    """The oracle returned a non-zero status (the reference's -1)."""
+
+
+def build() -> Path:
+    subprocess.run(["make", "-s", "-C", str(HERE)], check=True)
+    return LIB_PATH
+
+
+def lib() -> ctypes.CDLL:
+    global _lib
+    if _lib is None:
+        if not LIB_PATH.exists():
+            build()
+        L = ctypes.CDLL(str(LIB_PATH))
+        L.or_fp16_to_f32.argtypes = [ctypes.c_uint16]
+        L.or_fp16_to_f32.restype = ctypes.c_float
+        L.or_dequant_rows.argtypes = [ctypes.c_uint32, _u8p, _sz, _sz, _f32p]
+        L.or_quantize_symmetric_row.argtypes = [_f32p, _sz, _i8p, _f32p]
+        L.or_repack_w8.argtypes = [ctypes.c_uint32, _u8p, _sz, _sz, _sz, _i8p, _f32p]
+        L.or_quantize_a8.argtypes = [_f32p, _sz, _sz, _sz, _i8p, _f32p]
+        L.or_gemm_i32.argtypes = [_i8p, _i8p, _sz, _sz, _sz, _i32p, ctypes.c_int]
+        L.or_gemm_i32.restype = None
+        L.or_rescale.argtypes = [_i32p, _f32p, _f32p, _sz, _sz, _f32p]
+        L.or_rescale.restype = None
+        L.or_matmul_q_w8a8.argtypes = [ctypes.c_uint32, _u8p, _sz, _f32p, _sz, _sz, _sz, _f32p, ctypes.c_int]
+        L.or_quantize_row_q8_k.argtypes = [_f32p, _sz, _u8p]
+        L.or_quantize_row_q8_k.restype = None
+        L.or_vec_dot_q4_k_q8_k.argtypes = [_sz, _u8p, _u8p]
+        L.or_vec_dot_q4_k_q8_k.restype = ctypes.c_float
+        L.or_vec_dot_q6_k_q8_k.argtypes = [_sz, _u8p, _u8p]
+        L.or_vec_dot_q6_k_q8_k.restype = ctypes.c_float
+        L.or_gemv_q8_k.argtypes = [ctypes.c_uint32, _u8p, _sz, _sz, _u8p, _sz, _f32p, ctypes.c_int]
+        L.or_gemv_block_sums.argtypes = [ctypes.c_uint32, _u8p, _sz, _sz, _u8p, _i32p, _i32p, _f64p]
+        _lib = L
+    return _lib
+
+
+def _p(a: np.ndarray, t):
+    assert a.flags["C_CONTIGUOUS"], "oracle inputs must be C-contiguous"
+    return a.ctypes.data_as(t)
+
+
+def fp16_to_f32(bits: int) -> float:
+    return lib().or_fp16_to_f32(bits)
+
+
+def dequant_rows(kind: int, blocks: np.ndarray, k: int, n: int) -> np.ndarray:
+    out = np.empty((n, k), np.float32)
+    if lib().or_dequant_rows(kind, _p(blocks, _u8p), k, n, _p(out, _f32p)) != 0:
+        raise OracleError("dequant_rows")
+    return out
+
+
+def quantize_symmetric_row(x: np.ndarray):
+    x = np.ascontiguousarray(x, np.float32)
+    q = np.empty(x.size, np.int8)
+    s = ctypes.c_float()
+    if lib().or_quantize_symmetric_row(_p(x, _f32p), x.size, _p(q, _i8p), ctypes.byref(s)) != 0:
+        raise OracleError("non-finite row")
+    return q, np.float32(s.value)
+
+
+def repack_w8(kind: int, blocks: np.ndarray, k: int, n: int):
+    w8 = np.empty((n, k), np.int8)
+    sc = np.empty(n, np.float32)
+    if lib().or_repack_w8(kind, _p(blocks, _u8p), blocks.nbytes, k, n, _p(w8, _i8p), _p(sc, _f32p)) != 0:
+        raise OracleError("repack_w8")
+    return w8, sc
+
+
+def quantize_a8(a: np.ndarray, k_pad: int | None = None):
+    a = np.ascontiguousarray(a, np.float32)
+    m, k = a.shape
+    k_pad = k if k_pad is None else k_pad
+    a8 = np.empty((m, k_pad), np.int8)
+    sc = np.empty(m, np.float32)
+    if lib().or_quantize_a8(_p(a, _f32p), m, k, k_pad, _p(a8, _i8p), _p(sc, _f32p)) != 0:
+        raise OracleError("quantize_a8")
+    return a8, sc
+
+
+def gemm_i32(a8: np.ndarray, w8: np.ndarray, threads: int = 1) -> np.ndarray:
+    a8 = np.ascontiguousarray(a8)
+    w8 = np.ascontiguousarray(w8)
+    m, k = a8.shape
+    n = w8.shape[0]
+    assert w8.shape[1] == k
+    c = np.empty((m, n), np.int32)
+    lib().or_gemm_i32(_p(a8, _i8p), _p(w8, _i8p), m, n, k, _p(c, _i32p), threads)
+    return c
+
+
+def rescale(c: np.ndarray, a_scales: np.ndarray, w_scales: np.ndarray) -> np.ndarray:
+    m, n = c.shape
+    out = np.empty((m, n), np.float32)
+    lib().or_rescale(_p(np.ascontiguousarray(c), _i32p), _p(np.ascontiguousarray(a_scales, np.float32), _f32p),
+                     _p(np.ascontiguousarray(w_scales, np.float32), _f32p), m, n, _p(out, _f32p))
+    return out
+
+
+def matmul_q_w8a8(kind: int, blocks: np.ndarray, a: np.ndarray, n: int, threads: int = 1) -> np.ndarray:
+    a = np.ascontiguousarray(a, np.float32)
+    m, k = a.shape
+    out = np.empty((m, n), np.float32)
+    if lib().or_matmul_q_w8a8(kind, _p(blocks, _u8p), blocks.nbytes, _p(a, _f32p), m, k, n, _p(out, _f32p),
+                              threads) != 0:
+        raise OracleError("matmul_q_w8a8")
+    return out
+
+
+def quantize_q8_k(x: np.ndarray) -> np.ndarray:
+    x = np.ascontiguousarray(x, np.float32)
+    if x.ndim == 1:
+        x = x[None, :]
+    m, k = x.shape
+    out = np.empty((m, (k // QK) * Q8K_BYTES), np.uint8)
+    for r in range(m):
+        lib().or_quantize_row_q8_k(_p(x[r], _f32p), k, _p(out[r], _u8p))
+    return out
+
+
+def gemv_q8_k(kind: int, w: np.ndarray, k: int, n: int, q8k: np.ndarray, threads: int = 1) -> np.ndarray:
+    q8k = np.ascontiguousarray(q8k)
+    m = q8k.shape[0]
+    out = np.empty((m, n), np.float32)
+    if lib().or_gemv_q8_k(kind, _p(w, _u8p), k, n, _p(q8k, _u8p), m, _p(out, _f32p), threads) != 0:
+        raise OracleError("gemv_q8_k")
+    return out
+
+
+def gemv_block_sums(kind: int, w: np.ndarray, k: int, n: int, q8k_row: np.ndarray):
+    nb = k // QK
+    isum = np.empty((n, nb), np.int32)
+    msum = np.empty((n, nb), np.int32)
+    mag = np.empty(n, np.float64)
+    q8k_row = np.ascontiguousarray(q8k_row)
+    if lib().or_gemv_block_sums(kind, _p(w, _u8p), k, n, _p(q8k_row, _u8p), _p(isum, _i32p), _p(msum, _i32p),
+                                _p(mag, _f64p)) != 0:
+        raise OracleError("gemv_block_sums")
+    return isum, msum, mag

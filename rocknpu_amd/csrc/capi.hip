@@ -1,0 +1,726 @@
+// Host side of the C ABI in include/rocknpu.h (and the decode extension in
+// include/rocknpu_ggml.h): argument validation with the reference's status
+// codes, a device-resident W8 cache keyed like the reference's
+// DecodeWeightKey, and the W8A8 pipeline (upload -> A8 quant -> int8-MFMA GEMM
+// with fused rescale -> download) on one HIP stream per context.
+//
+// Reference: crates/rocknpu-capi/src/lib.rs. Routing differences, by design:
+// the NPU tile constraints (M in {4..128}, K % 512, N <= 8192, K-split,
+// 128-row chunking, N chunking, K zero-padding) are numerically invisible in
+// the reference and have no GPU counterpart, so every M > 1 shape runs as one
+// GEMM; M = 1 runs the same W8A8 formula (lib.rs:1567-1701).
+#include <hip/hip_runtime.h>
+
+#include <chrono>
+#include <cmath>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <map>
+#include <memory>
+#include <unordered_map>
+#include <vector>
+
+#include "rocknpu.h"
+#include "rocknpu_ggml.h"
+#include "rocknpu_hip.h"
+
+namespace {
+
+constexpr int kOk = ROCKNPU_STATUS_OK;
+constexpr int kInvalid = ROCKNPU_STATUS_INVALID_ARGUMENT;
+constexpr int kExec = ROCKNPU_STATUS_EXECUTION_ERROR;
+constexpr size_t kQK = 256;
+
+size_t block_bytes(uint32_t kind) { return kind == 4 ? 144 : kind == 5 ? 176 : kind == 6 ? 210 : 0; }
+size_t round_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
+
+bool env_enabled(const char* name) {
+    const char* v = std::getenv(name);
+    return v && v[0] != '\0' && std::strcmp(v, "0") != 0;
+}
+
+bool mul_ok(size_t a, size_t b, size_t* out) { return !__builtin_mul_overflow(a, b, out); }
+
+uint64_t now_ns() {
+    return static_cast<uint64_t>(std::chrono::duration_cast<std::chrono::nanoseconds>(
+                                     std::chrono::steady_clock::now().time_since_epoch())
+                                     .count());
+}
+
+// (address, bytes, k, n, kind): lib.rs:33-39. Kind 8 marks caller-supplied
+// int8 weights (the reference files those under Q4K with bytes = k*n).
+struct WeightKey {
+    uintptr_t address;
+    size_t bytes, k, n;
+    uint32_t kind;
+    bool operator==(const WeightKey& o) const {
+        return address == o.address && bytes == o.bytes && k == o.k && n == o.n && kind == o.kind;
+    }
+    bool operator<(const WeightKey& o) const {
+        if (address != o.address) return address < o.address;
+        if (bytes != o.bytes) return bytes < o.bytes;
+        if (k != o.k) return k < o.k;
+        if (n != o.n) return n < o.n;
+        return kind < o.kind;
+    }
+};
+struct KeyHash {
+    size_t operator()(const WeightKey& w) const {
+        size_t h = w.address * 0x9E3779B97F4A7C15ull;
+        h ^= w.bytes + 0x632BE59BD9B4E019ull + (h << 6) + (h >> 2);
+        h ^= w.k + (w.n << 20) + (static_cast<size_t>(w.kind) << 56) + (h << 6) + (h >> 2);
+        return h;
+    }
+};
+
+// Device-resident W8 matrix [n, k_pad] + scales[n]; freed with the entry.
+struct DeviceW8 {
+    int8_t* w8 = nullptr;
+    float* scales = nullptr;
+    size_t n = 0, k = 0, k_pad = 0;
+    DeviceW8() = default;
+    DeviceW8(const DeviceW8&) = delete;
+    DeviceW8& operator=(const DeviceW8&) = delete;
+    ~DeviceW8() {
+        if (w8) (void)hipFree(w8);
+        if (scales) (void)hipFree(scales);
+    }
+    size_t resident_bytes() const { return n * k_pad + n * sizeof(float); }
+};
+using W8Ptr = std::shared_ptr<DeviceW8>;
+
+struct DevBuf {
+    void* p = nullptr;
+    size_t cap = 0;
+    ~DevBuf() {
+        if (p) (void)hipFree(p);
+    }
+    bool ensure(size_t bytes) {
+        if (bytes <= cap) return true;
+        if (p) (void)hipFree(p);
+        p = nullptr;
+        cap = 0;
+        const size_t want = round_up(bytes, size_t(1) << 20);
+        if (hipMalloc(&p, want) != hipSuccess) return false;
+        cap = want;
+        return true;
+    }
+    template <class T>
+    T* as() const { return static_cast<T*>(p); }
+};
+
+struct PinnedBuf {
+    void* p = nullptr;
+    size_t cap = 0;
+    ~PinnedBuf() {
+        if (p) (void)hipHostFree(p);
+    }
+    bool ensure(size_t bytes) {
+        if (bytes <= cap) return true;
+        if (p) (void)hipHostFree(p);
+        p = nullptr;
+        cap = 0;
+        const size_t want = round_up(bytes, size_t(1) << 20);
+        if (hipHostMalloc(&p, want, hipHostMallocDefault) != hipSuccess) return false;
+        cap = want;
+        return true;
+    }
+    template <class T>
+    T* as() const { return static_cast<T*>(p); }
+};
+
+struct Profile {
+    size_t calls = 0, cache_hits = 0, cache_misses = 0;
+    uint64_t prepare_ns = 0, execute_ns = 0;
+};
+
+}  // namespace
+
+struct RockNpuContext {
+    int device = 0;
+    hipStream_t stream = nullptr;
+    // prompt (M > 1) caches, dropped by rocknpu_mtile_release
+    std::unordered_map<WeightKey, W8Ptr, KeyHash> mtile;
+    std::map<std::vector<WeightKey>, W8Ptr> mtile_groups;
+    // decode (M = 1) caches, kept across releases
+    std::unordered_map<WeightKey, W8Ptr, KeyHash> m1;
+    std::map<std::vector<WeightKey>, W8Ptr> m1_groups;
+    // raw K-quant blocks resident for the Q8_K decode GEMV
+    std::unordered_map<WeightKey, std::shared_ptr<DevBuf>, KeyHash> raw;
+    DevBuf d_raw, d_act, d_a8, d_as, d_out, d_q8k;
+    PinnedBuf h_out, h_as;
+    size_t hits = 0, misses = 0, m1_calls = 0;
+    uint64_t hit_ns = 0, miss_ns = 0;
+    Profile mtile_profile, m1_profile;
+    bool profile_mtile = false, profile_m1 = false, trace = false;
+    rocknpu_overlap_fn overlap = nullptr;
+    void* overlap_user = nullptr;
+};
+
+namespace {
+
+bool hip_ok(hipError_t e, RockNpuContext* ctx, const char* what) {
+    if (e == hipSuccess) return true;
+    if (ctx && ctx->trace) std::fprintf(stderr, "ROCKNPU MTILE ERROR %s: %s\n", what, hipGetErrorString(e));
+    return false;
+}
+
+void run_overlap(RockNpuContext* ctx) {
+    rocknpu_overlap_fn fn = ctx->overlap;
+    void* user = ctx->overlap_user;
+    ctx->overlap = nullptr;
+    ctx->overlap_user = nullptr;
+    if (fn) fn(user);
+}
+
+// Look a cached W8 up in `primary`, else reuse the same weight's entry from
+// the other cache (both hold identical W8 for a key).
+W8Ptr find_w8(std::unordered_map<WeightKey, W8Ptr, KeyHash>& primary,
+              std::unordered_map<WeightKey, W8Ptr, KeyHash>& other, const WeightKey& key) {
+    auto it = primary.find(key);
+    if (it != primary.end()) return it->second;
+    auto jt = other.find(key);
+    if (jt != other.end()) {
+        primary.emplace(key, jt->second);
+        return jt->second;
+    }
+    return nullptr;
+}
+
+W8Ptr alloc_w8(size_t n, size_t k) {
+    auto w = std::make_shared<DeviceW8>();
+    w->n = n;
+    w->k = k;
+    w->k_pad = round_up(k, 64);
+    if (hipMalloc(reinterpret_cast<void**>(&w->w8), w->n * w->k_pad) != hipSuccess ||
+        hipMalloc(reinterpret_cast<void**>(&w->scales), w->n * sizeof(float)) != hipSuccess)
+        return nullptr;
+    return w;
+}
+
+// Repack raw K-quant rows into rows [row0, row0 + n) of `dst`; returns
+// kInvalid when a dequantised row is non-finite (prepare_* returns None).
+int repack_into(RockNpuContext* ctx, uint32_t kind, const uint8_t* host, size_t bytes, size_t k, size_t n,
+                DeviceW8& dst, size_t row0) {
+    if (!ctx->d_raw.ensure(bytes) || !ctx->h_as.ensure(n * sizeof(float))) return kExec;
+    if (!hip_ok(hipMemcpyAsync(ctx->d_raw.p, host, bytes, hipMemcpyHostToDevice, ctx->stream), ctx, "upload"))
+        return kExec;
+    int st = rocknpu_hip_repack_w8(kind, ctx->d_raw.as<uint8_t>(), bytes, k, n, dst.k_pad,
+                                   dst.w8 + row0 * dst.k_pad, dst.scales + row0, ctx->stream);
+    if (st != kOk) return st;
+    if (!hip_ok(hipMemcpyAsync(ctx->h_as.p, dst.scales + row0, n * sizeof(float), hipMemcpyDeviceToHost,
+                               ctx->stream),
+                ctx, "scales") ||
+        !hip_ok(hipStreamSynchronize(ctx->stream), ctx, "repack"))
+        return kExec;
+    const float* s = ctx->h_as.as<float>();
+    for (size_t i = 0; i < n; ++i)
+        if (!std::isfinite(s[i])) return kInvalid;
+    return kOk;
+}
+
+// Copy caller int8 [n, k] + scales into rows [row0, row0 + n) of `dst`.
+int upload_w8_into(RockNpuContext* ctx, const int8_t* w, const float* scales, size_t k, size_t n, DeviceW8& dst,
+                   size_t row0) {
+    int8_t* d = dst.w8 + row0 * dst.k_pad;
+    if (dst.k_pad != k) {
+        if (!hip_ok(hipMemsetAsync(d, 0, n * dst.k_pad, ctx->stream), ctx, "pad")) return kExec;
+        if (!hip_ok(hipMemcpy2DAsync(d, dst.k_pad, w, k, k, n, hipMemcpyHostToDevice, ctx->stream), ctx, "w8"))
+            return kExec;
+    } else if (!hip_ok(hipMemcpyAsync(d, w, n * k, hipMemcpyHostToDevice, ctx->stream), ctx, "w8")) {
+        return kExec;
+    }
+    if (!hip_ok(hipMemcpyAsync(dst.scales + row0, scales, n * sizeof(float), hipMemcpyHostToDevice, ctx->stream),
+                ctx, "scales") ||
+        !hip_ok(hipStreamSynchronize(ctx->stream), ctx, "upload"))
+        return kExec;
+    return kOk;
+}
+
+// One projection source for a (possibly concatenated) W8 matrix.
+struct Source {
+    WeightKey key;
+    const uint8_t* blocks;   // raw K-quant rows (kind 4/5/6), or
+    const int8_t* w8;        // caller int8 rows (kind 8)
+    const float* scales;
+};
+
+int build_w8(RockNpuContext* ctx, const std::vector<Source>& srcs, size_t k, W8Ptr* out) {
+    size_t total_n = 0;
+    for (const auto& s : srcs) total_n += s.key.n;
+    W8Ptr w = alloc_w8(total_n, k);
+    if (!w) return kExec;
+    size_t row = 0;
+    for (const auto& s : srcs) {
+        const int st = s.key.kind == 8 ? upload_w8_into(ctx, s.w8, s.scales, k, s.key.n, *w, row)
+                                       : repack_into(ctx, s.key.kind, s.blocks, s.key.bytes, k, s.key.n, *w, row);
+        if (st != kOk) return st;
+        row += s.key.n;
+    }
+    *out = w;
+    return kOk;
+}
+
+// Quantise host activations [m, k], run the GEMM against `w`, download and
+// scatter the columns into outs[i] ([m, ns[i]] each, ns summing to w->n).
+int run_w8a8(RockNpuContext* ctx, const DeviceW8& w, const float* act, size_t m, size_t k,
+             const std::vector<float*>& outs, const std::vector<size_t>& ns, bool decode) {
+    size_t a_bytes, o_elems;
+    if (!mul_ok(m, k, &a_bytes) || !mul_ok(a_bytes, sizeof(float), &a_bytes) || !mul_ok(m, w.n, &o_elems))
+        return kInvalid;
+    if (!ctx->d_act.ensure(a_bytes) || !ctx->d_a8.ensure(m * w.k_pad) || !ctx->d_as.ensure(m * sizeof(float)) ||
+        !ctx->d_out.ensure(o_elems * sizeof(float)) || !ctx->h_out.ensure(o_elems * sizeof(float)) ||
+        !ctx->h_as.ensure(m * sizeof(float)))
+        return kExec;
+    if (!hip_ok(hipMemcpyAsync(ctx->d_act.p, act, a_bytes, hipMemcpyHostToDevice, ctx->stream), ctx, "act"))
+        return kExec;
+    int st = rocknpu_hip_quantize_a8(ctx->d_act.as<float>(), m, k, k, w.k_pad, ctx->d_a8.as<int8_t>(),
+                                     ctx->d_as.as<float>(), ctx->stream);
+    if (st != kOk) return st;
+    st = rocknpu_hip_gemm_w8a8(ctx->d_a8.as<int8_t>(), ctx->d_as.as<float>(), w.w8, w.scales, m, w.n, w.k_pad,
+                               ctx->d_out.as<float>(), w.n, nullptr, ctx->stream);
+    if (st != kOk) return st;
+    if (!hip_ok(hipMemcpyAsync(ctx->h_out.p, ctx->d_out.p, o_elems * sizeof(float), hipMemcpyDeviceToHost,
+                               ctx->stream),
+                ctx, "download") ||
+        !hip_ok(hipMemcpyAsync(ctx->h_as.p, ctx->d_as.p, m * sizeof(float), hipMemcpyDeviceToHost, ctx->stream),
+                ctx, "download"))
+        return kExec;
+    if (decode) run_overlap(ctx);
+    if (!hip_ok(hipStreamSynchronize(ctx->stream), ctx, "execute")) return kExec;
+    const float* as = ctx->h_as.as<float>();
+    for (size_t r = 0; r < m; ++r)
+        if (!std::isfinite(as[r])) return kInvalid;  // non-finite activation row
+    const float* h = ctx->h_out.as<float>();
+    size_t col = 0;
+    for (size_t i = 0; i < outs.size(); ++i) {
+        for (size_t r = 0; r < m; ++r) std::memcpy(outs[i] + r * ns[i], h + r * w.n + col, ns[i] * sizeof(float));
+        col += ns[i];
+    }
+    return kOk;
+}
+
+// Cached single-projection W8A8 (M > 1 -> prompt cache, M = 1 -> decode cache).
+int exec_single(RockNpuContext* ctx, const Source& src, const float* act, float* out, size_t m) {
+    const bool decode = m == 1;
+    const uint64_t t0 = now_ns();
+    auto& primary = decode ? ctx->m1 : ctx->mtile;
+    auto& other = decode ? ctx->mtile : ctx->m1;
+    W8Ptr w = find_w8(primary, other, src.key);
+    const bool hit = w != nullptr;
+    if (!w) {
+        const int st = build_w8(ctx, {src}, src.key.k, &w);
+        if (st != kOk) return st;
+        primary.emplace(src.key, w);
+    }
+    const uint64_t t1 = now_ns();
+    const int st = run_w8a8(ctx, *w, act, m, src.key.k, {out}, {src.key.n}, decode);
+    const uint64_t t2 = now_ns();
+    Profile& p = decode ? ctx->m1_profile : ctx->mtile_profile;
+    p.calls++;
+    (hit ? p.cache_hits : p.cache_misses)++;
+    p.prepare_ns += t1 - t0;
+    p.execute_ns += t2 - t1;
+    if (decode) {
+        ctx->m1_calls++;
+        if (hit) {
+            ctx->hits++;
+            ctx->hit_ns += t2 - t0;
+        } else {
+            ctx->misses++;
+            ctx->miss_ns += t2 - t0;
+        }
+    }
+    return st;
+}
+
+// Cached concatenated-N group: one GEMM, activations quantised once.
+int exec_group(RockNpuContext* ctx, const std::vector<Source>& srcs, const float* act, size_t m,
+               const std::vector<float*>& outs) {
+    const bool decode = m == 1;
+    std::vector<WeightKey> keys;
+    std::vector<size_t> ns;
+    for (const auto& s : srcs) {
+        keys.push_back(s.key);
+        ns.push_back(s.key.n);
+    }
+    auto& cache = decode ? ctx->m1_groups : ctx->mtile_groups;
+    const uint64_t t0 = now_ns();
+    W8Ptr w;
+    auto it = cache.find(keys);
+    const bool hit = it != cache.end();
+    if (hit) {
+        w = it->second;
+    } else {
+        const int st = build_w8(ctx, srcs, srcs[0].key.k, &w);
+        if (st != kOk) return st;
+        cache.emplace(keys, w);
+    }
+    const int st = run_w8a8(ctx, *w, act, m, srcs[0].key.k, outs, ns, decode);
+    const uint64_t t1 = now_ns();
+    if (decode) {
+        ctx->m1_calls++;
+        if (hit) {
+            ctx->hits++;
+            ctx->hit_ns += t1 - t0;
+        } else {
+            ctx->misses++;
+            ctx->miss_ns += t1 - t0;
+        }
+    }
+    return st;
+}
+
+bool kquant_kind(uint32_t kind) { return kind == 4 || kind == 6; }
+
+// Validate a raw K-quant projection: lib.rs:4944-4975.
+bool kquant_shape_ok(uint32_t kind, size_t bytes, size_t k, size_t n) {
+    const size_t bb = block_bytes(kind);
+    size_t expected;
+    return bb != 0 && k != 0 && n != 0 && k % kQK == 0 && mul_ok(n, k / kQK, &expected) &&
+           mul_ok(expected, bb, &expected) && expected == bytes;
+}
+
+bool scales_ok(const float* s, size_t n) {
+    for (size_t i = 0; i < n; ++i)
+        if (!std::isfinite(s[i]) || s[i] <= 0.0f) return false;
+    return true;
+}
+
+Source kquant_source(const uint8_t* w, size_t bytes, uint32_t kind, size_t k, size_t n) {
+    return Source{WeightKey{reinterpret_cast<uintptr_t>(w), bytes, k, n, kind}, w, nullptr, nullptr};
+}
+
+Source w8_source(const int8_t* w, const float* scales, size_t k, size_t n) {
+    return Source{WeightKey{reinterpret_cast<uintptr_t>(w), k * n, k, n, 8}, nullptr, w, scales};
+}
+
+int matmul_kquant(rocknpu_context* ctx, uint32_t kind, const uint8_t* w, size_t bytes, const float* act,
+                  float* out, size_t m, size_t k, size_t n) {
+    if (!ctx || !w || !act || !out || m == 0 || k == 0 || n == 0 || k % kQK != 0) return kInvalid;
+    size_t tmp;
+    if (!mul_ok(m, k, &tmp) || !mul_ok(n, k, &tmp) || !mul_ok(m, n, &tmp)) return kInvalid;
+    if (!kquant_shape_ok(kind, bytes, k, n)) return kInvalid;
+    if (kind == 5 && m == 1) return kInvalid;  // Q5_K is a prompt-path format (lib.rs:5300)
+    return exec_single(ctx, kquant_source(w, bytes, kind, k, n), act, out, m);
+}
+
+// Minimal FP16 bridge kernel: activations rounded to f16 (RNE), f16 weights,
+// f32 accumulation; one thread per output.
+__global__ void f16_matmul_kernel(const _Float16* __restrict__ w, const float* __restrict__ a, float* __restrict__ out,
+                                  int64_t m, int64_t k, int64_t n) {
+    const int64_t idx = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (idx >= m * n) return;
+    const int64_t r = idx / n, c = idx % n;
+    float acc = 0.0f;
+    for (int64_t t = 0; t < k; ++t) {
+        const float x = static_cast<float>(static_cast<_Float16>(a[r * k + t]));
+        acc += x * static_cast<float>(w[c * k + t]);
+    }
+    out[idx] = acc;
+}
+
+}  // namespace
+
+extern "C" {
+
+size_t rocknpu_device_count(void) {
+    int count = 0;
+    if (hipGetDeviceCount(&count) != hipSuccess) return 0;
+    return count > 0 ? 1 : 0;
+}
+
+rocknpu_context* rocknpu_context_create(void) {
+    if (rocknpu_device_count() == 0) return nullptr;
+    auto* ctx = new (std::nothrow) RockNpuContext();
+    if (!ctx) return nullptr;
+    if (hipGetDevice(&ctx->device) != hipSuccess || hipStreamCreate(&ctx->stream) != hipSuccess) {
+        delete ctx;
+        return nullptr;
+    }
+    ctx->profile_mtile = env_enabled("ROCKNPU_MTILE_PROFILE");
+    ctx->profile_m1 = env_enabled("ROCKNPU_M1_PROFILE");
+    ctx->trace = env_enabled("ROCKNPU_MTILE_TRACE");
+    return ctx;
+}
+
+int rocknpu_context_decode_cache_stats(const rocknpu_context* ctx, rocknpu_decode_cache_stats* out) {
+    if (!ctx || !out) return kInvalid;
+    size_t resident = 0;
+    for (const auto& e : ctx->m1) resident += e.second->resident_bytes();
+    for (const auto& e : ctx->m1_groups) resident += e.second->resident_bytes();
+    rocknpu_decode_cache_stats s{};
+    s.hits = ctx->hits;
+    s.misses = ctx->misses;
+    s.entries = ctx->m1.size() + ctx->m1_groups.size();
+    s.resident_bytes = resident;
+    s.hit_ns = ctx->hit_ns;
+    s.miss_ns = ctx->miss_ns;
+    s.tuned_shapes = 0;          // no per-shape worker tuning on the GPU
+    s.worker1_calls = ctx->m1_calls;  // one GPU is one worker
+    s.worker2_calls = 0;
+    s.worker3_calls = 0;
+    s.ksplit_calls = 0;
+    *out = s;
+    return kOk;
+}
+
+void rocknpu_context_destroy(rocknpu_context* ctx) {
+    if (!ctx) return;
+    if (ctx->stream) (void)hipStreamSynchronize(ctx->stream);
+    if (ctx->profile_mtile && ctx->mtile_profile.calls)
+        std::fprintf(stderr, "ROCKNPU MTILE PROFILE calls=%zu hits=%zu misses=%zu prepare_ms=%.3f execute_ms=%.3f\n",
+                     ctx->mtile_profile.calls, ctx->mtile_profile.cache_hits, ctx->mtile_profile.cache_misses,
+                     ctx->mtile_profile.prepare_ns / 1e6, ctx->mtile_profile.execute_ns / 1e6);
+    if (ctx->profile_m1 && ctx->m1_profile.calls)
+        std::fprintf(stderr, "ROCKNPU M1 PROFILE calls=%zu hits=%zu misses=%zu prepare_ms=%.3f execute_ms=%.3f\n",
+                     ctx->m1_profile.calls, ctx->m1_profile.cache_hits, ctx->m1_profile.cache_misses,
+                     ctx->m1_profile.prepare_ns / 1e6, ctx->m1_profile.execute_ns / 1e6);
+    hipStream_t s = ctx->stream;
+    delete ctx;  // frees every cached device buffer
+    if (s) (void)hipStreamDestroy(s);
+}
+
+int rocknpu_context_set_overlap(rocknpu_context* ctx, rocknpu_overlap_fn callback, void* user_data) {
+    if (!ctx) return kInvalid;
+    ctx->overlap = callback;
+    ctx->overlap_user = callback ? user_data : nullptr;
+    return kOk;
+}
+
+int rocknpu_matmul_q_concat_f32_f32_mtile(rocknpu_context* ctx, size_t count, const uint8_t* const* weights,
+                                          const size_t* bytes, const uint32_t* kinds, const size_t* ns,
+                                          const float* act, float* const* outputs, size_t m, size_t k) {
+    if (!ctx || count < 1 || count > 4 || !weights || !bytes || !kinds || !ns || !act || !outputs || m == 0 ||
+        k == 0)
+        return kInvalid;
+    std::vector<Source> srcs;
+    std::vector<float*> outs;
+    for (size_t i = 0; i < count; ++i) {
+        if (!weights[i] || !outputs[i] || ns[i] == 0 || !kquant_kind(kinds[i])) return kInvalid;
+        if (!kquant_shape_ok(kinds[i], bytes[i], k, ns[i])) return kInvalid;
+        srcs.push_back(kquant_source(weights[i], bytes[i], kinds[i], k, ns[i]));
+        outs.push_back(outputs[i]);
+    }
+    return exec_group(ctx, srcs, act, m, outs);
+}
+
+int rocknpu_mtile_release(rocknpu_context* ctx, size_t count, const uint8_t* const* weights) {
+    if (!ctx || !weights || count < 1 || count > 4) return kInvalid;
+    std::vector<uintptr_t> addrs(count);
+    for (size_t i = 0; i < count; ++i) addrs[i] = reinterpret_cast<uintptr_t>(weights[i]);
+    auto involved = [&](const WeightKey& key) {
+        for (uintptr_t a : addrs)
+            if (a == key.address) return true;
+        return false;
+    };
+    for (auto it = ctx->mtile.begin(); it != ctx->mtile.end();)
+        it = involved(it->first) ? ctx->mtile.erase(it) : std::next(it);
+    for (auto it = ctx->mtile_groups.begin(); it != ctx->mtile_groups.end();) {
+        const auto& keys = it->first;
+        bool exact = keys.size() == addrs.size();
+        for (size_t i = 0; exact && i < keys.size(); ++i) exact = keys[i].address == addrs[i];
+        bool any = false;
+        for (const auto& key : keys) any = any || involved(key);
+        it = (!exact && any) ? ctx->mtile_groups.erase(it) : std::next(it);
+    }
+    return kOk;
+}
+
+int rocknpu_prewarm_quantized_m16(rocknpu_context* ctx, const uint8_t* w, size_t bytes, uint32_t kind, size_t k,
+                                  size_t n) {
+    if (!ctx || !w || k == 0 || n == 0 || !kquant_kind(kind) || k % kQK != 0) return kInvalid;
+    if (!kquant_shape_ok(kind, bytes, k, n)) return kInvalid;
+    const Source src = kquant_source(w, bytes, kind, k, n);
+    if (find_w8(ctx->mtile, ctx->m1, src.key)) return kOk;
+    W8Ptr wp;
+    const int st = build_w8(ctx, {src}, k, &wp);
+    if (st == kOk) ctx->mtile.emplace(src.key, wp);
+    return st;
+}
+
+int rocknpu_matmul_f16_f32_f32(rocknpu_context* ctx, const uint16_t* w, const float* act, float* out, size_t m,
+                               size_t k, size_t n) {
+    if (!ctx || !w || !act || !out || m == 0 || k == 0 || n == 0) return kInvalid;
+    size_t a_elems, w_elems, o_elems;
+    if (!mul_ok(m, k, &a_elems) || !mul_ok(n, k, &w_elems) || !mul_ok(m, n, &o_elems)) return kInvalid;
+    if (!ctx->d_act.ensure(a_elems * 4) || !ctx->d_raw.ensure(w_elems * 2) || !ctx->d_out.ensure(o_elems * 4))
+        return kExec;
+    if (!hip_ok(hipMemcpyAsync(ctx->d_act.p, act, a_elems * 4, hipMemcpyHostToDevice, ctx->stream), ctx, "act") ||
+        !hip_ok(hipMemcpyAsync(ctx->d_raw.p, w, w_elems * 2, hipMemcpyHostToDevice, ctx->stream), ctx, "w"))
+        return kExec;
+    const unsigned threads = 256;
+    const size_t blocks = (o_elems + threads - 1) / threads;
+    if (blocks > 0x7fffffff) return kInvalid;
+    f16_matmul_kernel<<<dim3(static_cast<unsigned>(blocks)), dim3(threads), 0, ctx->stream>>>(
+        ctx->d_raw.as<_Float16>(), ctx->d_act.as<float>(), ctx->d_out.as<float>(), static_cast<int64_t>(m),
+        static_cast<int64_t>(k), static_cast<int64_t>(n));
+    if (!hip_ok(hipGetLastError(), ctx, "f16") ||
+        !hip_ok(hipMemcpyAsync(out, ctx->d_out.p, o_elems * 4, hipMemcpyDeviceToHost, ctx->stream), ctx, "out") ||
+        !hip_ok(hipStreamSynchronize(ctx->stream), ctx, "f16"))
+        return kExec;
+    return kOk;
+}
+
+int rocknpu_matmul_w8a8_f32_f32_m1(rocknpu_context* ctx, const int8_t* w, const float* scales, const float* act,
+                                   float* out, size_t k, size_t n) {
+    if (!ctx || !w || !scales || !act || !out || k == 0 || n == 0) return kInvalid;
+    size_t tmp;
+    if (!mul_ok(k, n, &tmp) || !scales_ok(scales, n)) return kInvalid;
+    return exec_single(ctx, w8_source(w, scales, k, n), act, out, 1);
+}
+
+int rocknpu_matmul_w8a8_f32_f32_m16(rocknpu_context* ctx, const int8_t* w, const float* scales, const float* act,
+                                    float* out, size_t k, size_t n) {
+    if (!ctx || !w || !scales || !act || !out || k == 0 || n == 0) return kInvalid;
+    size_t tmp;
+    if (!mul_ok(k, n, &tmp) || !mul_ok(16, k, &tmp) || !mul_ok(16, n, &tmp) || !scales_ok(scales, n))
+        return kInvalid;
+    return exec_single(ctx, w8_source(w, scales, k, n), act, out, 16);
+}
+
+int rocknpu_matmul_w8a8_f32_f32_m1_nsplit(rocknpu_context* ctx, const int8_t* w, const float* scales,
+                                          const float* act, float* out, size_t k, size_t n, size_t chunk_n) {
+    if (!ctx || !w || !scales || !act || !out || k == 0 || n == 0 || chunk_n == 0 || chunk_n % 32 != 0 ||
+        n % 32 != 0)
+        return kInvalid;
+    for (size_t off = 0; off < n; off += chunk_n) {
+        const size_t cur = chunk_n < n - off ? chunk_n : n - off;
+        const int st = rocknpu_matmul_w8a8_f32_f32_m1(ctx, w + off * k, scales + off, act, out + off, k, cur);
+        if (st != kOk) return st;
+    }
+    return kOk;
+}
+
+int rocknpu_matmul_w8a8_pair_f32_f32_m1(rocknpu_context* ctx, const int8_t* w1, const float* s1, size_t n1,
+                                        const int8_t* w2, const float* s2, size_t n2, const float* act, float* o1,
+                                        float* o2, size_t k) {
+    if (!ctx || !w1 || !s1 || !w2 || !s2 || !act || !o1 || !o2 || k == 0 || n1 == 0 || n2 == 0) return kInvalid;
+    size_t tmp;
+    if (!mul_ok(k, n1, &tmp) || !mul_ok(k, n2, &tmp) || !scales_ok(s1, n1) || !scales_ok(s2, n2)) return kInvalid;
+    return exec_group(ctx, {w8_source(w1, s1, k, n1), w8_source(w2, s2, k, n2)}, act, 1, {o1, o2});
+}
+
+int rocknpu_matmul_w8a8_triple_f32_f32_m1(rocknpu_context* ctx, const int8_t* w1, const float* s1, size_t n1,
+                                          const int8_t* w2, const float* s2, size_t n2, const int8_t* w3,
+                                          const float* s3, size_t n3, const float* act, float* o1, float* o2,
+                                          float* o3, size_t k) {
+    if (!ctx || !w1 || !s1 || !w2 || !s2 || !w3 || !s3 || !act || !o1 || !o2 || !o3 || k == 0 || n1 == 0 ||
+        n2 == 0 || n3 == 0)
+        return kInvalid;
+    size_t tmp;
+    if (!mul_ok(k, n1, &tmp) || !mul_ok(k, n2, &tmp) || !mul_ok(k, n3, &tmp) || !scales_ok(s1, n1) ||
+        !scales_ok(s2, n2) || !scales_ok(s3, n3))
+        return kInvalid;
+    return exec_group(ctx, {w8_source(w1, s1, k, n1), w8_source(w2, s2, k, n2), w8_source(w3, s3, k, n3)}, act, 1,
+                      {o1, o2, o3});
+}
+
+int rocknpu_matmul_w8a8_swiglu_down_f32(rocknpu_context* ctx, const int8_t* gw, const float* gs, const int8_t* uw,
+                                        const float* us, const int8_t* dw, const float* ds, const float* act,
+                                        float* out, size_t projection_k, size_t ffn_n, size_t output_n) {
+    if (!ctx || !gw || !gs || !uw || !us || !dw || !ds || !act || !out || projection_k == 0 || ffn_n == 0 ||
+        output_n == 0)
+        return kInvalid;
+    size_t tmp;
+    if (!mul_ok(projection_k, ffn_n, &tmp) || !mul_ok(ffn_n, output_n, &tmp)) return kInvalid;
+    std::vector<float> gate(ffn_n), up(ffn_n);
+    int st = rocknpu_matmul_w8a8_pair_f32_f32_m1(ctx, gw, gs, ffn_n, uw, us, ffn_n, act, gate.data(), up.data(),
+                                                 projection_k);
+    if (st != kOk) return st;
+    for (size_t i = 0; i < ffn_n; ++i) {
+        const float g = gate[i], u = up[i];
+        const float sig = 1.0f / (1.0f + std::exp(-g));  // lib.rs:4378-4383
+        gate[i] = g * sig * u;
+    }
+    return rocknpu_matmul_w8a8_f32_f32_m1(ctx, dw, ds, gate.data(), out, ffn_n, output_n);
+}
+
+int rocknpu_matmul_q_pair_f32_f32_mtile(rocknpu_context* ctx, const uint8_t* w1, size_t b1, uint32_t k1, size_t n1,
+                                        const uint8_t* w2, size_t b2, uint32_t k2, size_t n2, const float* act,
+                                        float* o1, float* o2, size_t m, size_t k) {
+    if (!ctx || !w1 || !w2 || !act || !o1 || !o2 || m == 0 || k == 0 || n1 == 0 || n2 == 0) return kInvalid;
+    if (!kquant_kind(k1) || !kquant_kind(k2)) return kInvalid;
+    if (!kquant_shape_ok(k1, b1, k, n1) || !kquant_shape_ok(k2, b2, k, n2)) return kInvalid;
+    return exec_group(ctx, {kquant_source(w1, b1, k1, k, n1), kquant_source(w2, b2, k2, k, n2)}, act, m, {o1, o2});
+}
+
+int rocknpu_matmul_q_pair_f32_f32_m1(rocknpu_context* ctx, const uint8_t* w1, size_t b1, uint32_t k1, size_t n1,
+                                     const uint8_t* w2, size_t b2, uint32_t k2, size_t n2, const float* act,
+                                     float* o1, float* o2, size_t k) {
+    if (!ctx || !w1 || !w2 || !act || !o1 || !o2 || k == 0 || n1 == 0 || n2 == 0) return kInvalid;
+    if (!kquant_kind(k1) || !kquant_kind(k2)) return kInvalid;
+    if (!kquant_shape_ok(k1, b1, k, n1) || !kquant_shape_ok(k2, b2, k, n2)) return kInvalid;
+    return exec_group(ctx, {kquant_source(w1, b1, k1, k, n1), kquant_source(w2, b2, k2, k, n2)}, act, 1, {o1, o2});
+}
+
+int rocknpu_matmul_q_triple_f32_f32_m1(rocknpu_context* ctx, const uint8_t* w1, size_t b1, uint32_t k1, size_t n1,
+                                       const uint8_t* w2, size_t b2, uint32_t k2, size_t n2, const uint8_t* w3,
+                                       size_t b3, uint32_t k3, size_t n3, const float* act, float* o1, float* o2,
+                                       float* o3, size_t k) {
+    if (!ctx || !w1 || !w2 || !w3 || !act || !o1 || !o2 || !o3 || k == 0 || n1 == 0 || n2 == 0 || n3 == 0)
+        return kInvalid;
+    if (!kquant_kind(k1) || !kquant_kind(k2) || !kquant_kind(k3)) return kInvalid;
+    if (!kquant_shape_ok(k1, b1, k, n1) || !kquant_shape_ok(k2, b2, k, n2) || !kquant_shape_ok(k3, b3, k, n3))
+        return kInvalid;
+    return exec_group(ctx,
+                      {kquant_source(w1, b1, k1, k, n1), kquant_source(w2, b2, k2, k, n2),
+                       kquant_source(w3, b3, k3, k, n3)},
+                      act, 1, {o1, o2, o3});
+}
+
+int rocknpu_matmul_q4_k_f32_f32(rocknpu_context* ctx, const uint8_t* w, size_t bytes, const float* act, float* out,
+                                size_t m, size_t k, size_t n) {
+    return matmul_kquant(ctx, 4, w, bytes, act, out, m, k, n);
+}
+
+int rocknpu_matmul_q5_k_f32_f32(rocknpu_context* ctx, const uint8_t* w, size_t bytes, const float* act, float* out,
+                                size_t m, size_t k, size_t n) {
+    return matmul_kquant(ctx, 5, w, bytes, act, out, m, k, n);
+}
+
+int rocknpu_matmul_q6_k_f32_f32(rocknpu_context* ctx, const uint8_t* w, size_t bytes, const float* act, float* out,
+                                size_t m, size_t k, size_t n) {
+    return matmul_kquant(ctx, 6, w, bytes, act, out, m, k, n);
+}
+
+// llama.cpp CPU decode semantics on the GPU: Q8_K quantisation of the f32
+// activations, then the Q4_K/Q6_K x Q8_K GEMV over device-resident raw blocks.
+int rocknpu_matmul_q_q8k_f32_f32(rocknpu_context* ctx, uint32_t kind, const uint8_t* w, size_t bytes,
+                                 const float* act, float* out, size_t m, size_t k, size_t n) {
+    if (!ctx || !w || !act || !out || m == 0 || k == 0 || n == 0 || !kquant_kind(kind)) return kInvalid;
+    if (!kquant_shape_ok(kind, bytes, k, n)) return kInvalid;
+    size_t a_elems, o_elems;
+    if (!mul_ok(m, k, &a_elems) || !mul_ok(m, n, &o_elems)) return kInvalid;
+    for (size_t i = 0; i < a_elems; ++i)
+        if (!std::isfinite(act[i])) return kInvalid;
+    const WeightKey key{reinterpret_cast<uintptr_t>(w), bytes, k, n, kind};
+    auto it = ctx->raw.find(key);
+    std::shared_ptr<DevBuf> dw;
+    if (it != ctx->raw.end()) {
+        dw = it->second;
+    } else {
+        dw = std::make_shared<DevBuf>();
+        if (!dw->ensure(bytes) ||
+            !hip_ok(hipMemcpyAsync(dw->p, w, bytes, hipMemcpyHostToDevice, ctx->stream), ctx, "raw"))
+            return kExec;
+        ctx->raw.emplace(key, dw);
+    }
+    const size_t q8_bytes = m * (k / kQK) * 292;
+    if (!ctx->d_act.ensure(a_elems * 4) || !ctx->d_q8k.ensure(q8_bytes) || !ctx->d_out.ensure(o_elems * 4))
+        return kExec;
+    if (!hip_ok(hipMemcpyAsync(ctx->d_act.p, act, a_elems * 4, hipMemcpyHostToDevice, ctx->stream), ctx, "act"))
+        return kExec;
+    int st = rocknpu_hip_quantize_q8_k(ctx->d_act.as<float>(), m, k, k, ctx->d_q8k.as<uint8_t>(), ctx->stream);
+    if (st != kOk) return st;
+    st = rocknpu_hip_gemv_q8_k(kind, dw->as<uint8_t>(), bytes, k, n, ctx->d_q8k.as<uint8_t>(), m,
+                               ctx->d_out.as<float>(), n, nullptr, nullptr, ctx->stream);
+    if (st != kOk) return st;
+    if (!hip_ok(hipMemcpyAsync(out, ctx->d_out.p, o_elems * 4, hipMemcpyDeviceToHost, ctx->stream), ctx, "out") ||
+        !hip_ok(hipStreamSynchronize(ctx->stream), ctx, "gemv"))
+        return kExec;
+    return kOk;
+}
+
+}  // extern "C"

@@ -1,0 +1,81 @@
+// Shared definitions for the gfx950 kernels of the MUL_MAT offload path.
+//
+// GGUF K-quant super-blocks hold 256 values. Byte layouts (public ggml ABI;
+// block sizes 144 and 210 are pinned by crates/rocknpu-capi/src/lib.rs:5729-5736):
+//   Q4_K 144 B: f16 d | f16 dmin | u8 scales[12] | u8 qs[128]
+//   Q5_K 176 B: f16 d | f16 dmin | u8 scales[12] | u8 qh[32] | u8 qs[128]
+//   Q6_K 210 B: u8 ql[128] | u8 qh[64] | i8 scales[16] | f16 d
+//   Q8_K 292 B: f32 d | i8 qs[256] | i16 bsums[16]
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+namespace rk {
+
+constexpr int kQK = 256;
+constexpr int kQ4KBytes = 144;
+constexpr int kQ5KBytes = 176;
+constexpr int kQ6KBytes = 210;
+constexpr int kQ8KBytes = 292;
+
+constexpr int kStatusOk = 0;
+constexpr int kStatusInvalid = -1;
+constexpr int kStatusDevice = -2;
+constexpr int kStatusExec = -3;
+
+__host__ __device__ constexpr int block_bytes(int kind) {
+    return kind == 4 ? kQ4KBytes : kind == 5 ? kQ5KBytes : kind == 6 ? kQ6KBytes : 0;
+}
+
+__device__ __forceinline__ float f16_bits_to_f32(uint16_t bits) {
+    _Float16 h;
+    __builtin_memcpy(&h, &bits, 2);
+    return static_cast<float>(h);  // exact widening
+}
+
+__device__ __forceinline__ uint16_t ld_u16(const uint8_t* p) {
+    return *reinterpret_cast<const uint16_t*>(p);
+}
+
+__device__ __forceinline__ uint32_t ld_u32(const uint8_t* p) {
+    return *reinterpret_cast<const uint32_t*>(p);
+}
+
+// 6-bit scale and min of sub-block j (0..7) of a Q4_K/Q5_K block from its
+// packed 12-byte field, given as three little-endian words s0 s1 s2.
+__device__ __forceinline__ void scale_min_k4(int j, uint32_t s0, uint32_t s1, uint32_t s2,
+                                             int& sc, int& mn) {
+    const int b = (j & 3) * 8;
+    if (j < 4) {
+        sc = (s0 >> b) & 63;
+        mn = (s1 >> b) & 63;
+    } else {
+        sc = ((s2 >> b) & 0xF) | (((s0 >> b) >> 6 & 3) << 4);
+        mn = ((s2 >> b) >> 4 & 0xF) | (((s1 >> b) >> 6 & 3) << 4);
+    }
+}
+
+// Rust's `(v / s).round().clamp(-127.0, 127.0) as i8` with IEEE division:
+// round half away from zero, NaN -> 0.
+__device__ __forceinline__ int quant_sym(float v, float s) {
+    float r = roundf(v / s);
+    if (r != r) return 0;
+    r = fminf(fmaxf(r, -127.0f), 127.0f);
+    return static_cast<int>(r);
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+    return v;
+}
+
+__device__ __forceinline__ int wave_or(int v) {
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) v |= __shfl_xor(v, o, 64);
+    return v;
+}
+
+}  // namespace rk

@@ -1,0 +1,107 @@
+// Device-pointer launch layer (include/rocknpu_hip.h): host-side argument
+// checks, then one enqueue per kernel. Every shape and alignment the kernels
+// assume is checked here, before anything reaches the GPU.
+#include <algorithm>
+#include <climits>
+
+#include "common.h"
+#include "rocknpu_hip.h"
+
+namespace rk {
+int launch_repack_w8(int kind, const uint8_t* blocks, int64_t n, int nb, int64_t k_pad, int8_t* w8,
+                     float* scales, hipStream_t stream);
+int launch_quantize_a8(const float* a, int64_t m, int64_t k, int64_t lda, int64_t k_pad, int8_t* a8,
+                       float* scales, hipStream_t stream);
+int launch_quantize_q8_k(const float* x, int64_t m, int64_t k, int64_t ldx, uint8_t* y,
+                         hipStream_t stream);
+int launch_gemm_w8a8(const int8_t* a8, int64_t lda, const int8_t* w8, int64_t ldw, const float* as,
+                     const float* ws, int m, int n, int k, float* out, int64_t ldo, int32_t* oi,
+                     int64_t ldoi, hipStream_t stream);
+int launch_gemv_q8_k(int kind, const uint8_t* w, int64_t n, int nb, const uint8_t* q8k, int64_t ldq,
+                     int m, float* out, int64_t ldo, int32_t* isum, int32_t* msum, hipStream_t stream);
+}  // namespace rk
+
+namespace {
+
+bool aligned(const void* p, uintptr_t a) { return reinterpret_cast<uintptr_t>(p) % a == 0; }
+
+constexpr size_t kMaxGrid = 0x7fffffff;
+constexpr size_t kGemvLdsBytes = 64 * 1024;
+
+}  // namespace
+
+extern "C" int rocknpu_hip_repack_w8(uint32_t kind, const uint8_t* blocks, size_t blocks_bytes, size_t k,
+                                     size_t n, size_t k_pad, int8_t* w8, float* scales, void* stream) {
+    const size_t bb = rk::block_bytes(static_cast<int>(kind));
+    if (bb == 0 || !blocks || !w8 || !scales || k == 0 || n == 0 || k % rk::kQK != 0) return rk::kStatusInvalid;
+    if (k_pad < k || k_pad % 64 != 0 || blocks_bytes / bb / (k / rk::kQK) != n || blocks_bytes % bb != 0 ||
+        blocks_bytes != n * (k / rk::kQK) * bb)
+        return rk::kStatusInvalid;
+    if (!aligned(blocks, kind == 6 ? 2 : 16) || !aligned(w8, 16) || k / rk::kQK > INT_MAX ||
+        (n + 3) / 4 > kMaxGrid)
+        return rk::kStatusInvalid;
+    return rk::launch_repack_w8(static_cast<int>(kind), blocks, static_cast<int64_t>(n),
+                                static_cast<int>(k / rk::kQK), static_cast<int64_t>(k_pad), w8, scales,
+                                static_cast<hipStream_t>(stream));
+}
+
+extern "C" int rocknpu_hip_quantize_a8(const float* a, size_t m, size_t k, size_t lda, size_t k_pad,
+                                       int8_t* a8, float* scales, void* stream) {
+    if (!a || !a8 || !scales || m == 0 || k == 0 || lda < k || k_pad < k || m > kMaxGrid)
+        return rk::kStatusInvalid;
+    return rk::launch_quantize_a8(a, static_cast<int64_t>(m), static_cast<int64_t>(k),
+                                  static_cast<int64_t>(lda), static_cast<int64_t>(k_pad), a8, scales,
+                                  static_cast<hipStream_t>(stream));
+}
+
+extern "C" int rocknpu_hip_gemm_w8a8(const int8_t* a8, const float* a_scales, const int8_t* w8,
+                                     const float* w_scales, size_t m, size_t n, size_t k_pad, float* out,
+                                     size_t ldo, int32_t* out_i32, void* stream) {
+    if (!a8 || !a_scales || !w8 || !w_scales || !out || m == 0 || n == 0 || k_pad == 0 || k_pad % 64 != 0 ||
+        ldo < n || m > INT_MAX || n > INT_MAX || k_pad > INT_MAX)
+        return rk::kStatusInvalid;
+    if (!aligned(a8, 16) || !aligned(w8, 16)) return rk::kStatusInvalid;
+    // worst-case tile count (16-row tiles, 64-column tiles) must fit one grid
+    if (((m + 15) / 16) * ((n + 63) / 64) > kMaxGrid) return rk::kStatusInvalid;
+    return rk::launch_gemm_w8a8(a8, static_cast<int64_t>(k_pad), w8, static_cast<int64_t>(k_pad), a_scales,
+                                w_scales, static_cast<int>(m), static_cast<int>(n), static_cast<int>(k_pad),
+                                out, static_cast<int64_t>(ldo), out_i32, static_cast<int64_t>(n),
+                                static_cast<hipStream_t>(stream));
+}
+
+extern "C" int rocknpu_hip_quantize_q8_k(const float* x, size_t m, size_t k, size_t ldx, uint8_t* q8k,
+                                         void* stream) {
+    if (!x || !q8k || m == 0 || k == 0 || k % rk::kQK != 0 || ldx < k || !aligned(q8k, 4))
+        return rk::kStatusInvalid;
+    if ((m * (k / rk::kQK) + 3) / 4 > kMaxGrid) return rk::kStatusInvalid;
+    return rk::launch_quantize_q8_k(x, static_cast<int64_t>(m), static_cast<int64_t>(k),
+                                    static_cast<int64_t>(ldx), q8k, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int rocknpu_hip_gemv_q8_k(uint32_t kind, const uint8_t* w, size_t w_bytes, size_t k, size_t n,
+                                     const uint8_t* q8k, size_t m, float* out, size_t ldo, int32_t* isum,
+                                     int32_t* msum, void* stream) {
+    if ((kind != 4 && kind != 6) || !w || !q8k || !out || k == 0 || k % rk::kQK != 0 || n == 0 || m == 0 ||
+        ldo < n || n > INT_MAX)
+        return rk::kStatusInvalid;
+    const size_t bb = rk::block_bytes(static_cast<int>(kind)), nb = k / rk::kQK;
+    if (w_bytes != n * nb * bb || !aligned(w, kind == 4 ? 16 : 2) || !aligned(q8k, 4)) return rk::kStatusInvalid;
+    if ((isum == nullptr) != (msum == nullptr)) return rk::kStatusInvalid;
+    const size_t per_row = nb * rk::kQ8KBytes;
+    if (per_row > kGemvLdsBytes) return rk::kStatusInvalid;
+    // rows per launch: a power of two (the kernel's register tile) that fits LDS
+    size_t chunk = 8;
+    while (chunk > 1 && chunk * per_row > kGemvLdsBytes) chunk >>= 1;
+    const hipStream_t s = static_cast<hipStream_t>(stream);
+    for (size_t m0 = 0; m0 < m; m0 += chunk) {
+        const int mm = static_cast<int>(std::min(chunk, m - m0));
+        int32_t* is = isum ? isum + m0 * n * nb : nullptr;
+        int32_t* ms = msum ? msum + m0 * n * nb : nullptr;
+        const int st = rk::launch_gemv_q8_k(static_cast<int>(kind), w, static_cast<int64_t>(n),
+                                            static_cast<int>(nb), q8k + m0 * per_row,
+                                            static_cast<int64_t>(per_row), mm, out + m0 * ldo,
+                                            static_cast<int64_t>(ldo), is, ms, s);
+        if (st != rk::kStatusOk) return st;
+    }
+    return rk::kStatusOk;
+}

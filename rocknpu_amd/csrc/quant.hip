@@ -1,0 +1,168 @@
+// Kernel (b): per-token symmetric int8 activation quantisation, and the
+// Q8_K activation quantisation of the decode path.
+//
+// A8 (crates/rocknpu-capi/src/lib.rs:614-654, driven per row at :1776-1791):
+// scale = max|row| / 127 (1.0 for an all-zero row), q = clamp(round_half_away(
+// x / scale), -127, 127), int8 rows zero-padded to k_pad. A row holding a
+// non-finite value is rejected by the reference; here its scale is written as
+// NaN and its int8 row as zeros, and the host turns that into
+// ROCKNPU_STATUS_INVALID_ARGUMENT.
+//
+// Q8_K (ggml quantize_row_q8_K_ref, llama.cpp ggml-quants.c): per 256-value
+// block, the first value of largest magnitude `max` gives iscale = -127/max,
+// q = min(127, round_half_even(iscale * x)), bsums[16] = sums of 16 quants,
+// d = 1/iscale. An all-zero block stores d = 0, zero quants and zero bsums.
+#include "common.h"
+
+namespace rk {
+namespace {
+
+constexpr int kA8Threads = 256;
+
+__device__ __forceinline__ float block_max(float v, float* red) {
+    v = wave_max(v);
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    if (lane == 0) red[wave] = v;
+    __syncthreads();
+    float r = red[0];
+#pragma unroll
+    for (int w = 1; w < kA8Threads / 64; ++w) r = fmaxf(r, red[w]);
+    __syncthreads();
+    return r;
+}
+
+__device__ __forceinline__ uint32_t pack4(int a, int b, int c, int d) {
+    return (a & 0xFF) | (b & 0xFF) << 8 | (c & 0xFF) << 16 | static_cast<uint32_t>(d & 0xFF) << 24;
+}
+
+// One workgroup per activation row. VEC: k, lda and k_pad are multiples of 4
+// and both base pointers are 16-byte aligned.
+template <bool VEC>
+__global__ __launch_bounds__(kA8Threads) void quantize_a8_kernel(const float* __restrict__ a,
+                                                                 int64_t k, int64_t lda,
+                                                                 int64_t k_pad,
+                                                                 int8_t* __restrict__ a8,
+                                                                 float* __restrict__ scales) {
+    __shared__ float red[kA8Threads / 64];
+    const int64_t row = blockIdx.x;
+    const float* x = a + row * lda;
+    int8_t* q = a8 + row * k_pad;
+    const int t = threadIdx.x;
+
+    // Pass 1: max |x| over the row; a non-finite value poisons it to +inf
+    // (|x| > FLT_MAX, or NaN mapped to +inf) so one reduction serves both.
+    float vmax = 0.0f;
+    if constexpr (VEC) {
+        for (int64_t i = t; i < k / 4; i += kA8Threads) {
+            const float4 v = reinterpret_cast<const float4*>(x)[i];
+            const float e[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const float m = fabsf(e[j]);
+                vmax = fmaxf(vmax, (m <= 3.402823466e38f) ? m : __builtin_inff());
+            }
+        }
+    } else {
+        for (int64_t i = t; i < k; i += kA8Threads) {
+            const float m = fabsf(x[i]);
+            vmax = fmaxf(vmax, (m <= 3.402823466e38f) ? m : __builtin_inff());
+        }
+    }
+    vmax = block_max(vmax, red);
+    const bool bad = !(vmax <= 3.402823466e38f);
+    const float scale = vmax == 0.0f ? 1.0f : vmax / 127.0f;
+
+    // Pass 2: quantise (the row is cache-resident now) and zero the padding.
+    if constexpr (VEC) {
+        for (int64_t i = t; i < k / 4; i += kA8Threads) {
+            const float4 v = reinterpret_cast<const float4*>(x)[i];
+            uint32_t w = 0;
+            if (!bad) w = pack4(quant_sym(v.x, scale), quant_sym(v.y, scale), quant_sym(v.z, scale),
+                                quant_sym(v.w, scale));
+            reinterpret_cast<uint32_t*>(q)[i] = w;
+        }
+        for (int64_t i = k / 4 + t; i < k_pad / 4; i += kA8Threads) reinterpret_cast<uint32_t*>(q)[i] = 0;
+    } else {
+        for (int64_t i = t; i < k_pad; i += kA8Threads)
+            q[i] = (i < k && !bad) ? static_cast<int8_t>(quant_sym(x[i], scale)) : 0;
+    }
+    if (t == 0) scales[row] = bad ? __builtin_nanf("") : scale;
+}
+
+// One wave per 256-value block, 4 blocks per workgroup. VEC: ldx % 4 == 0 and
+// x is 16-byte aligned.
+template <bool VEC>
+__global__ __launch_bounds__(256) void quantize_q8_k_kernel(const float* __restrict__ x, int64_t m,
+                                                            int64_t nb, int64_t ldx,
+                                                            uint8_t* __restrict__ y) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int64_t gb = static_cast<int64_t>(blockIdx.x) * 4 + wave;
+    if (gb >= m * nb) return;
+    const int64_t r = gb / nb, b = gb % nb;
+    const float* xb = x + r * ldx + b * kQK;
+    float v[4];
+    if constexpr (VEC) {
+        const float4 f = reinterpret_cast<const float4*>(xb)[lane];
+        v[0] = f.x; v[1] = f.y; v[2] = f.z; v[3] = f.w;
+    } else {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) v[j] = xb[4 * lane + j];
+    }
+    // First index of the largest magnitude (strict '>' in index order, NaN
+    // never selected), reduced across the wave with ties to the lower index.
+    float best_abs = 0.0f, best_val = 0.0f;
+    int best_idx = 0x7fffffff;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const float ax = fabsf(v[j]);
+        if (ax > best_abs) { best_abs = ax; best_val = v[j]; best_idx = 4 * lane + j; }
+    }
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        const float oa = __shfl_xor(best_abs, o, 64);
+        const float ov = __shfl_xor(best_val, o, 64);
+        const int oi = __shfl_xor(best_idx, o, 64);
+        if (oa > best_abs || (oa == best_abs && oi < best_idx)) {
+            best_abs = oa; best_val = ov; best_idx = oi;
+        }
+    }
+    uint8_t* yb = y + gb * kQ8KBytes;
+    int q[4] = {0, 0, 0, 0};
+    float d = 0.0f;
+    if (best_abs != 0.0f) {
+        const float iscale = -127.0f / best_val;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) q[j] = min(127, static_cast<int>(__builtin_rintf(iscale * v[j])));
+        d = 1.0f / iscale;
+    }
+    int s = q[0] + q[1] + q[2] + q[3];
+    s += __shfl_xor(s, 1, 64);
+    s += __shfl_xor(s, 2, 64);
+    *reinterpret_cast<uint32_t*>(yb + 4 + 4 * lane) = pack4(q[0], q[1], q[2], q[3]);
+    if ((lane & 3) == 0) *reinterpret_cast<int16_t*>(yb + 260 + 2 * (lane >> 2)) = static_cast<int16_t>(s);
+    if (lane == 0) *reinterpret_cast<float*>(yb) = d;
+}
+
+}  // namespace
+
+int launch_quantize_a8(const float* a, int64_t m, int64_t k, int64_t lda, int64_t k_pad, int8_t* a8,
+                       float* scales, hipStream_t stream) {
+    const bool vec = k % 4 == 0 && lda % 4 == 0 && k_pad % 4 == 0 &&
+                     reinterpret_cast<uintptr_t>(a) % 16 == 0 && reinterpret_cast<uintptr_t>(a8) % 16 == 0;
+    const dim3 grid(static_cast<unsigned>(m)), block(kA8Threads);
+    if (vec) quantize_a8_kernel<true><<<grid, block, 0, stream>>>(a, k, lda, k_pad, a8, scales);
+    else quantize_a8_kernel<false><<<grid, block, 0, stream>>>(a, k, lda, k_pad, a8, scales);
+    return hipGetLastError() == hipSuccess ? kStatusOk : kStatusExec;
+}
+
+int launch_quantize_q8_k(const float* x, int64_t m, int64_t k, int64_t ldx, uint8_t* y,
+                         hipStream_t stream) {
+    const int64_t nb = k / kQK;
+    const bool vec = ldx % 4 == 0 && reinterpret_cast<uintptr_t>(x) % 16 == 0;
+    const dim3 grid(static_cast<unsigned>((m * nb + 3) / 4)), block(256);
+    if (vec) quantize_q8_k_kernel<true><<<grid, block, 0, stream>>>(x, m, nb, ldx, y);
+    else quantize_q8_k_kernel<false><<<grid, block, 0, stream>>>(x, m, nb, ldx, y);
+    return hipGetLastError() == hipSuccess ? kStatusOk : kStatusExec;
+}
+
+}  // namespace rk

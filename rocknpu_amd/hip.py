@@ -1,0 +1,100 @@
+"""Device-tensor wrappers of the launch layer (include/rocknpu_hip.h).
+
+Arguments are torch tensors already resident on the GPU; calls enqueue on the
+current torch stream and return immediately. torch is used only for device
+memory and streams; the computation is the gfx950 kernels of the library.
+"""
+from __future__ import annotations
+
+import ctypes
+
+import torch
+
+from . import _lib
+
+QK = 256
+Q8K_BYTES = 292
+BLOCK_BYTES = {4: 144, 5: 176, 6: 210}
+
+
+class LaunchError(RuntimeError):
+    pass
+
+
+def _stream() -> ctypes.c_void_p:
+    return ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+
+def _ptr(t):
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def _check(status: int, what: str) -> None:
+    if status != 0:
+        raise LaunchError(f"{what} returned status {status}")
+
+
+def k_pad_of(k: int) -> int:
+    return (k + 63) // 64 * 64
+
+
+def repack_w8(kind: int, blocks: torch.Tensor, k: int, n: int, w8: torch.Tensor | None = None,
+              scales: torch.Tensor | None = None):
+    """Kernel (a): K-quant blocks -> (W8 [n, k_pad] int8, scales [n] f32)."""
+    kp = k_pad_of(k)
+    if w8 is None:
+        w8 = torch.empty((n, kp), dtype=torch.int8, device=blocks.device)
+    if scales is None:
+        scales = torch.empty(n, dtype=torch.float32, device=blocks.device)
+    assert w8.shape == (n, kp) and w8.is_contiguous() and scales.numel() == n
+    _check(_lib.load().rocknpu_hip_repack_w8(kind, _ptr(blocks), blocks.numel(), k, n, kp, _ptr(w8),
+                                             _ptr(scales), _stream()), "repack_w8")
+    return w8, scales
+
+
+def quantize_a8(a: torch.Tensor, k_pad: int | None = None, a8: torch.Tensor | None = None,
+                scales: torch.Tensor | None = None):
+    """Kernel (b): f32 [m, k] -> (A8 [m, k_pad] int8, scales [m] f32)."""
+    m, k = a.shape
+    kp = k_pad_of(k) if k_pad is None else k_pad
+    if a8 is None:
+        a8 = torch.empty((m, kp), dtype=torch.int8, device=a.device)
+    if scales is None:
+        scales = torch.empty(m, dtype=torch.float32, device=a.device)
+    _check(_lib.load().rocknpu_hip_quantize_a8(_ptr(a), m, k, a.stride(0), kp, _ptr(a8), _ptr(scales),
+                                               _stream()), "quantize_a8")
+    return a8, scales
+
+
+def gemm_w8a8(a8: torch.Tensor, a_scales: torch.Tensor, w8: torch.Tensor, w_scales: torch.Tensor,
+              out: torch.Tensor | None = None, out_i32: torch.Tensor | None = None) -> torch.Tensor:
+    """Kernel (c): out[m, n] = (f32(A8 W8^T) * a_scales) * w_scales."""
+    m, kp = a8.shape
+    n = w8.shape[0]
+    assert w8.shape[1] == kp and a8.is_contiguous() and w8.is_contiguous()
+    if out is None:
+        out = torch.empty((m, n), dtype=torch.float32, device=a8.device)
+    _check(_lib.load().rocknpu_hip_gemm_w8a8(_ptr(a8), _ptr(a_scales), _ptr(w8), _ptr(w_scales), m, n, kp,
+                                             _ptr(out), out.stride(0), _ptr(out_i32), _stream()), "gemm_w8a8")
+    return out
+
+
+def quantize_q8_k(x: torch.Tensor, q8k: torch.Tensor | None = None) -> torch.Tensor:
+    """f32 [m, k] -> Q8_K rows, uint8 [m, (k/256)*292]."""
+    m, k = x.shape
+    if q8k is None:
+        q8k = torch.empty((m, (k // QK) * Q8K_BYTES), dtype=torch.uint8, device=x.device)
+    _check(_lib.load().rocknpu_hip_quantize_q8_k(_ptr(x), m, k, x.stride(0), _ptr(q8k), _stream()),
+           "quantize_q8_k")
+    return q8k
+
+
+def gemv_q8_k(kind: int, w: torch.Tensor, k: int, n: int, q8k: torch.Tensor, out: torch.Tensor | None = None,
+              isum: torch.Tensor | None = None, msum: torch.Tensor | None = None) -> torch.Tensor:
+    """Kernel (d): out[m, n] = vec_dot(W row, Q8_K row) for Q4_K / Q6_K weights."""
+    m = q8k.shape[0]
+    if out is None:
+        out = torch.empty((m, n), dtype=torch.float32, device=q8k.device)
+    _check(_lib.load().rocknpu_hip_gemv_q8_k(kind, _ptr(w), w.numel(), k, n, _ptr(q8k), m, _ptr(out),
+                                             out.stride(0), _ptr(isum), _ptr(msum), _stream()), "gemv_q8_k")
+    return out

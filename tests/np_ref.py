@@ -1,0 +1,155 @@
+"""Independent numpy restatement of the path's arithmetic, used only to
+cross-check the C oracle. Written from the format definitions (GGUF K-quant
+block layouts, the reference's symmetric quantiser in
+crates/rocknpu-capi/src/lib.rs:614-654) without sharing code with oracle.c:
+vectorised over whole blocks, scale fields unpacked bit-by-bit, rounding
+implemented from floor/abs rather than roundf."""
+import numpy as np
+
+QK = 256
+
+
+def f16(b: np.ndarray) -> np.ndarray:
+    return np.ascontiguousarray(b).view(np.float16).astype(np.float32).reshape(-1)
+
+
+def unpack_k4_scales(s: np.ndarray):
+    """Twelve bytes -> eight 6-bit scales and mins, bit by bit: scale j<4 is
+    bits 0-5 of byte j; min j<4 bits 0-5 of byte j+4; scale j>=4 takes its low
+    nibble from byte j+4 and bits 4-5 from bits 6-7 of byte j-4; min j>=4 takes
+    its low nibble from the high nibble of byte j+4 and bits 4-5 from bits 6-7
+    of byte j."""
+    s = s.astype(np.int32)
+    sc = np.zeros((s.shape[0], 8), np.int32)
+    mn = np.zeros((s.shape[0], 8), np.int32)
+    for j in range(8):
+        if j < 4:
+            sc[:, j] = s[:, j] % 64
+            mn[:, j] = s[:, j + 4] % 64
+        else:
+            sc[:, j] = (s[:, j + 4] % 16) + 16 * (s[:, j - 4] // 64)
+            mn[:, j] = (s[:, j + 4] // 16) + 16 * (s[:, j] // 64)
+    return sc, mn
+
+
+def q4_k_ints(blocks: np.ndarray):
+    """-> (d, dmin, sc[8], mn[8], q[256]) per block; q in value order."""
+    b = blocks.reshape(-1, 144)
+    d, dmin = f16(b[:, 0:2]), f16(b[:, 2:4])
+    sc, mn = unpack_k4_scales(b[:, 4:16])
+    qs = b[:, 16:].astype(np.int32).reshape(-1, 4, 32)
+    q = np.concatenate([qs % 16, qs // 16], axis=2).reshape(-1, 256)  # per 64-chunk: lows then highs
+    return d, dmin, sc, mn, q
+
+
+def dequant_q4_k(blocks: np.ndarray) -> np.ndarray:
+    d, dmin, sc, mn, q = q4_k_ints(blocks)
+    sub = np.arange(256) // 32
+    a = (d[:, None] * sc[:, sub].astype(np.float32)) * q.astype(np.float32)
+    return (a - dmin[:, None] * mn[:, sub].astype(np.float32)).astype(np.float32)
+
+
+def dequant_q5_k(blocks: np.ndarray) -> np.ndarray:
+    b = blocks.reshape(-1, 176)
+    d, dmin = f16(b[:, 0:2]), f16(b[:, 2:4])
+    sc, mn = unpack_k4_scales(b[:, 4:16])
+    qh = b[:, 16:48].astype(np.int32)
+    qs = b[:, 48:].astype(np.int32).reshape(-1, 4, 32)
+    q = np.empty((b.shape[0], 256), np.int32)
+    for j in range(4):
+        q[:, 64 * j:64 * j + 32] = qs[:, j] % 16 + 16 * ((qh >> (2 * j)) & 1)
+        q[:, 64 * j + 32:64 * j + 64] = qs[:, j] // 16 + 16 * ((qh >> (2 * j + 1)) & 1)
+    sub = np.arange(256) // 32
+    a = (d[:, None] * sc[:, sub].astype(np.float32)) * q.astype(np.float32)
+    return (a - dmin[:, None] * mn[:, sub].astype(np.float32)).astype(np.float32)
+
+
+def q6_k_ints(blocks: np.ndarray):
+    """-> (d, sc[16], q[256] in [-32, 31]) per block, q in value order."""
+    b = blocks.reshape(-1, 210)
+    ql = b[:, 0:128].astype(np.int32)
+    qh = b[:, 128:192].astype(np.int32)
+    sc = b[:, 192:208].view(np.int8).astype(np.int32)
+    d = f16(b[:, 208:210])
+    q = np.empty((b.shape[0], 256), np.int32)
+    for p in range(256):
+        half, r = divmod(p, 128)
+        quarter, l = divmod(r, 32)
+        byte = ql[:, 64 * half + l + 32 * (quarter % 2)]
+        low = byte % 16 if quarter < 2 else byte // 16
+        high = (qh[:, 32 * half + l] >> (2 * quarter)) & 3
+        q[:, p] = low + 16 * high - 32
+    return d, sc, q
+
+
+def dequant_q6_k(blocks: np.ndarray) -> np.ndarray:
+    d, sc, q = q6_k_ints(blocks)
+    sub = np.arange(256) // 16
+    return ((d[:, None] * sc[:, sub].astype(np.float32)) * q.astype(np.float32)).astype(np.float32)
+
+
+def dequant(kind, blocks, n, k):
+    f = {4: dequant_q4_k, 5: dequant_q5_k, 6: dequant_q6_k}[kind]
+    return f(blocks).reshape(n, k)
+
+
+def round_half_away(r: np.ndarray) -> np.ndarray:
+    a = np.abs(r)
+    f = np.floor(a)
+    up = (a - f) >= np.float32(0.5)
+    return np.sign(r) * (f + up)
+
+
+def quantize_symmetric(rows: np.ndarray):
+    rows = rows.astype(np.float32)
+    mx = np.max(np.abs(rows), axis=1)
+    scale = np.where(mx == 0, np.float32(1.0), mx / np.float32(127.0)).astype(np.float32)
+    r = (rows / scale[:, None]).astype(np.float32)
+    q = np.clip(round_half_away(r), -127, 127).astype(np.int8)
+    return q, scale
+
+
+def quantize_q8_k(x: np.ndarray):
+    """-> (d [nb] f32, qs [nb,256] int32, bsums [nb,16] int32) for one row."""
+    xb = x.astype(np.float32).reshape(-1, 256)
+    idx = np.argmax(np.abs(xb), axis=1)                   # first largest magnitude
+    mx = xb[np.arange(xb.shape[0]), idx]
+    d = np.zeros(xb.shape[0], np.float32)
+    qs = np.zeros(xb.shape, np.int32)
+    nz = mx != 0
+    iscale = (np.float32(-127.0) / mx[nz]).astype(np.float32)
+    qs[nz] = np.minimum(127, np.rint((iscale[:, None] * xb[nz]).astype(np.float32))).astype(np.int32)
+    d[nz] = (np.float32(1.0) / iscale).astype(np.float32)
+    bsums = qs.reshape(-1, 16, 16).sum(axis=2)
+    return d, qs, bsums
+
+
+def pack_q8_k(d, qs, bsums) -> np.ndarray:
+    out = np.zeros((d.size, 292), np.uint8)
+    out[:, 0:4] = d.astype(np.float32).view(np.uint8).reshape(-1, 4)
+    out[:, 4:260] = qs.astype(np.int8).view(np.uint8)
+    out[:, 260:292] = bsums.astype(np.int16).view(np.uint8).reshape(-1, 32)
+    return out.reshape(-1)
+
+
+def block_sums(kind, w: np.ndarray, n: int, k: int, x: np.ndarray):
+    """Exact per-(row, block) integer sums and the f64 row result."""
+    nb = k // QK
+    dq, qs, bs = quantize_q8_k(x)
+    if kind == 4:
+        d, dmin, sc, mn, q = q4_k_ints(w)
+        sub = np.arange(256) // 32
+        prod = q.reshape(n, nb, 256) * qs[None, :, :] * sc.reshape(n, nb, 8)[:, :, sub]
+        isum = prod.sum(axis=2)
+        pair = bs.reshape(nb, 8, 2).sum(axis=2)
+        msum = (mn.reshape(n, nb, 8) * pair[None]).sum(axis=2)
+        y = (d.reshape(n, nb).astype(np.float64) * dq[None] * isum -
+             dmin.reshape(n, nb).astype(np.float64) * dq[None] * msum).sum(axis=1)
+    else:
+        d, sc, q = q6_k_ints(w)
+        sub = np.arange(256) // 16
+        prod = q.reshape(n, nb, 256) * qs[None, :, :] * sc.reshape(n, nb, 16)[:, :, sub]
+        isum = prod.sum(axis=2)
+        msum = np.zeros_like(isum)
+        y = (d.reshape(n, nb).astype(np.float64) * dq[None] * isum).sum(axis=1)
+    return isum.astype(np.int32), msum.astype(np.int32), y

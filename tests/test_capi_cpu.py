@@ -1,0 +1,91 @@
+"""The C-ABI library on the CPU: it loads, exports every symbol include/*.h
+declares, and its argument guards answer before any device work (no compute
+calls here)."""
+import ctypes
+import re
+
+import numpy as np
+import pytest
+
+from rocknpu_amd import _lib
+
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parents[1]
+
+
+def _declared_symbols():
+    names = set()
+    for h in sorted((ROOT / "include").glob("*.h")):
+        text = re.sub(r"/\*.*?\*/", "", h.read_text(), flags=re.S)
+        names |= set(re.findall(r"\b(rocknpu_\w+)\s*\(", text))
+    return names
+
+
+def test_headers_declare_the_reference_abi():
+    ref_abi = {
+        "rocknpu_device_count", "rocknpu_context_create", "rocknpu_context_decode_cache_stats",
+        "rocknpu_context_destroy", "rocknpu_context_set_overlap", "rocknpu_matmul_q_concat_f32_f32_mtile",
+        "rocknpu_mtile_release", "rocknpu_prewarm_quantized_m16", "rocknpu_matmul_f16_f32_f32",
+        "rocknpu_matmul_w8a8_f32_f32_m1", "rocknpu_matmul_w8a8_f32_f32_m16",
+        "rocknpu_matmul_w8a8_f32_f32_m1_nsplit", "rocknpu_matmul_w8a8_swiglu_down_f32",
+        "rocknpu_matmul_w8a8_pair_f32_f32_m1", "rocknpu_matmul_q_pair_f32_f32_mtile",
+        "rocknpu_matmul_w8a8_triple_f32_f32_m1", "rocknpu_matmul_q_pair_f32_f32_m1",
+        "rocknpu_matmul_q_triple_f32_f32_m1", "rocknpu_matmul_q4_k_f32_f32", "rocknpu_matmul_q5_k_f32_f32",
+        "rocknpu_matmul_q6_k_f32_f32",
+    }
+    assert ref_abi <= _declared_symbols()  # the 21 symbols of crates/rocknpu-capi/include/rocknpu.h
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _lib.load()
+    declared = _declared_symbols()
+    missing = [s for s in declared if not hasattr(lib, s)]
+    assert not missing, missing
+    assert declared == set(_lib.SIGNATURES), "ctypes table out of sync with the headers"
+
+
+def test_library_is_gfx950_only():
+    data = _lib.LIB_PATH.read_bytes()
+    assert b"amdgcn-amd-amdhsa--gfx950" in data
+    for other in (b"gfx942", b"gfx90a", b"gfx1100"):
+        assert other not in data
+
+
+def test_null_context_guards():
+    lib = _lib.load()
+    # crates/rocknpu-capi/src/lib.rs:5791-5806: a null context is rejected before any pointer access
+    assert lib.rocknpu_matmul_f16_f32_f32(None, None, None, None, 4, 32, 16) == -1
+    assert lib.rocknpu_matmul_q4_k_f32_f32(None, None, 0, None, None, 1, 256, 1) == -1
+    assert lib.rocknpu_matmul_q6_k_f32_f32(None, None, 0, None, None, 1, 256, 1) == -1
+    assert lib.rocknpu_matmul_q5_k_f32_f32(None, None, 0, None, None, 2, 256, 1) == -1
+    assert lib.rocknpu_matmul_w8a8_f32_f32_m1(None, None, None, None, None, 64, 32) == -1
+    assert lib.rocknpu_mtile_release(None, 1, None) == -1
+    assert lib.rocknpu_context_set_overlap(None, None, None) == -1
+    assert lib.rocknpu_context_decode_cache_stats(None, None) == -1
+    assert lib.rocknpu_matmul_q_q8k_f32_f32(None, 4, None, 0, None, None, 1, 256, 1) == -1
+    lib.rocknpu_context_destroy(None)  # no-op
+
+
+def test_launch_layer_rejects_bad_shapes_before_launch():
+    lib = _lib.load()
+    buf = np.zeros(4096, np.uint8)
+    p = ctypes.c_void_p(buf.ctypes.data)
+    # k not a multiple of 256, wrong byte count, unaligned k_pad, bad kind
+    assert lib.rocknpu_hip_repack_w8(4, p, 144, 100, 1, 128, p, p, None) == -1
+    assert lib.rocknpu_hip_repack_w8(4, p, 143, 256, 1, 256, p, p, None) == -1
+    assert lib.rocknpu_hip_repack_w8(4, p, 144, 256, 1, 260, p, p, None) == -1
+    assert lib.rocknpu_hip_repack_w8(7, p, 144, 256, 1, 256, p, p, None) == -1
+    assert lib.rocknpu_hip_gemm_w8a8(p, p, p, p, 4, 4, 100, p, 4, None, None) == -1
+    assert lib.rocknpu_hip_quantize_q8_k(p, 1, 100, 100, p, None) == -1
+    assert lib.rocknpu_hip_gemv_q8_k(5, p, 144, 256, 1, p, 1, p, 1, None, None, None) == -1
+    assert lib.rocknpu_hip_gemv_q8_k(4, p, 144, 256, 1, p, 1, p, 1, p, None, None) == -1
+
+
+def test_no_device_means_no_context():
+    torch = pytest.importorskip("torch")
+    if torch.cuda.is_available():
+        pytest.skip("a GPU is visible")
+    lib = _lib.load()
+    assert lib.rocknpu_device_count() == 0
+    assert not lib.rocknpu_context_create()

@@ -1,0 +1,225 @@
+"""GPU parity of the four kernels (launch layer, device pointers) against the
+C oracle: int8 weights/activations, scales and int32 accumulators bit-exact,
+f32 GEMM outputs bit-exact (same operation order), decode GEMV f32 within
+1e-5 of the summed block-term magnitude (integer block sums bit-exact)."""
+import numpy as np
+import pytest
+import torch
+
+from oracle import oracle as orc
+from rocknpu_amd import hip, synth
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def _dev(a: np.ndarray) -> torch.Tensor:
+    return torch.from_numpy(np.ascontiguousarray(a)).to(DEV)
+
+
+def _bits(x: np.ndarray) -> np.ndarray:
+    return np.ascontiguousarray(x, np.float32).view(np.uint32)
+
+
+# ---------------------------------------------------------------- kernel (a)
+@pytest.mark.parametrize("kind,n,k", [
+    (4, 1, 256), (4, 67, 2048), (4, 130, 5632), (4, 5632, 2048),
+    (5, 48, 2048), (5, 9, 768),
+    (6, 1, 256), (6, 33, 2048), (6, 70, 5632), (6, 2048, 5632),
+])
+def test_repack_w8_bit_exact(kind, n, k):
+    print(f"repack kind={kind} n={n} k={k}", flush=True)
+    blocks = synth.kquant(kind, n, k, index=100 + kind * 7 + n)
+    w8_ref, sc_ref = orc.repack_w8(kind, blocks, k, n)
+    w8, sc = hip.repack_w8(kind, _dev(blocks), k, n)
+    torch.cuda.synchronize()
+    w8, sc = w8.cpu().numpy(), sc.cpu().numpy()
+    assert np.array_equal(w8[:, :k], w8_ref)
+    assert not w8[:, k:].any()
+    assert np.array_equal(_bits(sc), _bits(sc_ref))
+
+
+def test_repack_zero_and_nonfinite_rows():
+    k, n = 512, 3
+    blocks = synth.q4_k(n, k, index=7).reshape(n, -1, 144).copy()
+    blocks[0] = 0                      # all-zero row -> scale 1.0, zero int8
+    blocks[2, 1, 0:2] = [0x00, 0x7C]   # d = +inf in one block -> row rejected
+    flat = blocks.reshape(-1)
+    w8, sc = hip.repack_w8(4, _dev(flat), k, n)
+    torch.cuda.synchronize()
+    w8, sc = w8.cpu().numpy(), sc.cpu().numpy()
+    assert sc[0] == 1.0 and not w8[0].any()
+    assert np.isnan(sc[2])
+    w8_ref, sc_ref = orc.repack_w8(4, np.ascontiguousarray(blocks[:2].reshape(-1)), k, 2)
+    assert np.array_equal(w8[:2, :k], w8_ref) and np.array_equal(_bits(sc[:2]), _bits(sc_ref))
+
+
+# ---------------------------------------------------------------- kernel (b)
+def _rounding_kat_row() -> np.ndarray:
+    """The reference's rounding edge values plus its 2051 LCG values
+    (crates/rocknpu-capi/src/lib.rs:5680-5700)."""
+    vals = [-12.75, -7.5, -3.5, -1.5, -0.5, -0.49999997, 0.0, 0.49999997, 0.5, 1.5, 3.5, 7.5, 12.75]
+    state = 0x12345678
+    for _ in range(2051):
+        state = (state * 1664525 + 1013904223) & 0xFFFFFFFF
+        unit = np.float32(state >> 8) / np.float32((1 << 24) - 1)
+        vals.append((unit * np.float32(2.0) - np.float32(1.0)) * np.float32(17.0))
+    return np.array(vals, np.float32)
+
+
+@pytest.mark.parametrize("m,k,k_pad", [(1, 2048, 2048), (128, 2048, 2048), (7, 5632, 5632), (3, 300, 320),
+                                       (5, 1001, 1024), (2, 2064, 2112)])
+def test_quantize_a8_bit_exact(m, k, k_pad):
+    print(f"a8 m={m} k={k} k_pad={k_pad}", flush=True)
+    a = synth.activations(m, k, index=200 + m + k)
+    a8_ref, sc_ref = orc.quantize_a8(a, k_pad)
+    a8, sc = hip.quantize_a8(_dev(a), k_pad)
+    torch.cuda.synchronize()
+    assert np.array_equal(a8.cpu().numpy(), a8_ref)
+    assert np.array_equal(_bits(sc.cpu().numpy()), _bits(sc_ref))
+
+
+def test_quantize_a8_edge_rows():
+    kat = _rounding_kat_row()
+    k = kat.size
+    rows = np.zeros((6, k), np.float32)
+    rows[0] = kat
+    rows[1] = 0.0                                   # zero row: scale 1.0
+    rows[2] = kat * np.float32(1e-38)               # subnormal-range values
+    rows[3] = np.float32(127.0) * np.sign(kat)      # scale exactly 1: ties at +-0.5 not hit
+    # max 127 gives scale exactly 1.0, so x/scale hits exact ties at +-(j + 0.5)
+    ties = np.arange(-126.5, 127.0, 1.0, dtype=np.float32)
+    rows[4, 0] = 127.0
+    rows[4, 1:1 + ties.size] = ties
+    rows[5] = kat
+    rows[5, 100] = np.nan
+    a8, sc = hip.quantize_a8(_dev(rows), k)
+    torch.cuda.synchronize()
+    a8, sc = a8.cpu().numpy(), sc.cpu().numpy()
+    ref8, refs = orc.quantize_a8(rows[:5], k)
+    assert np.array_equal(a8[:5], ref8)
+    assert np.array_equal(_bits(sc[:5]), _bits(refs))
+    assert sc[1] == 1.0
+    assert np.isnan(sc[5]) and not a8[5].any()
+    rows[5, 100] = np.inf
+    _, sc = hip.quantize_a8(_dev(rows[5:6]), k)
+    torch.cuda.synchronize()
+    assert np.isnan(sc.cpu().numpy()[0])
+
+
+# ---------------------------------------------------------------- kernel (c)
+def _gemm_dev(a8, as_, w8, ws):
+    out_i32 = torch.empty((a8.shape[0], w8.shape[0]), dtype=torch.int32, device=DEV)
+    out = hip.gemm_w8a8(_dev(a8), _dev(as_), _dev(w8), _dev(ws), out_i32=out_i32)
+    torch.cuda.synchronize()
+    return out.cpu().numpy(), out_i32.cpu().numpy()
+
+
+@pytest.mark.parametrize("m,n,k", [(1, 64, 64), (4, 96, 256), (16, 256, 2048), (33, 130, 320),
+                                   (128, 5632, 2048), (200, 300, 640), (512, 2048, 2048),
+                                   (600, 520, 5632), (1, 5632, 2048), (257, 64, 128)])
+def test_gemm_w8a8_bit_exact(m, n, k):
+    print(f"gemm m={m} n={n} k={k}", flush=True)
+    g = np.random.default_rng(m * 1000 + n + k)
+    a8 = g.integers(-127, 128, (m, k), dtype=np.int8)
+    w8 = g.integers(-127, 128, (n, k), dtype=np.int8)
+    as_ = (g.random(m, dtype=np.float32) + np.float32(0.01)) / np.float32(127)
+    ws = (g.random(n, dtype=np.float32) + np.float32(0.01)) / np.float32(127)
+    out, c = _gemm_dev(a8, as_, w8, ws)
+    c_ref = orc.gemm_i32(a8, w8, threads=8)
+    assert np.array_equal(c, c_ref)
+    assert np.array_equal(_bits(out), _bits(orc.rescale(c_ref, as_, ws)))
+
+
+def test_gemm_reference_kats():
+    """Closed-form patterns of the reference's hardware gates."""
+    # uniform M-tile: input row%5+1, weights 1 -> K*(row%5+1) (int8_mtile.rs:28-37,71-82)
+    m, n, k = 128, 256, 2048
+    a8 = np.repeat((np.arange(m) % 5 + 1).astype(np.int8)[:, None], k, axis=1)
+    w8 = np.ones((n, k), np.int8)
+    _, c = _gemm_dev(a8, np.ones(m, np.float32), w8, np.ones(n, np.float32))
+    assert np.array_equal(c, np.repeat((k * (np.arange(m) % 5 + 1))[:, None], n, axis=1))
+    # M=1 pattern a=((i*7+3)%9)-4, b=((i*5+1)%11)-5 over N*K (int8_decode_m1.rs:35-45),
+    # its negation and a zero input (int8_projection_profile.rs:11-22,54-56)
+    k, n = 2048, 96
+    a = (((np.arange(k) * 7 + 3) % 9) - 4).astype(np.int8)
+    b = (((np.arange(n * k) * 5 + 1) % 11) - 5).astype(np.int8).reshape(n, k)
+    ref = b.astype(np.int64) @ a.astype(np.int64)
+    for sign in (1, -1, 0):
+        _, c = _gemm_dev((a * sign).astype(np.int8)[None, :], np.ones(1, np.float32), b, np.ones(n, np.float32))
+        assert np.array_equal(c[0], (ref * sign).astype(np.int32))
+    # K-split pattern ((row*7+kk*3+5)%13)-6 / ((col*5+kk*11+3)%17)-8 (int8_mtile_ksplit.rs:27-35)
+    m, n, k = 16, 64, 6144
+    r, kk = np.meshgrid(np.arange(m), np.arange(k), indexing="ij")
+    a8 = (((r * 7 + kk * 3 + 5) % 13) - 6).astype(np.int8)
+    cidx, kk = np.meshgrid(np.arange(n), np.arange(k), indexing="ij")
+    w8 = (((cidx * 5 + kk * 11 + 3) % 17) - 8).astype(np.int8)
+    _, c = _gemm_dev(a8, np.ones(m, np.float32), w8, np.ones(n, np.float32))
+    assert np.array_equal(c, (a8.astype(np.int64) @ w8.astype(np.int64).T).astype(np.int32))
+    # extreme magnitudes: |C| = 127^2 * K stays inside int32
+    m, n, k = 8, 64, 8192
+    a8 = np.full((m, k), -127, np.int8)
+    w8 = np.full((n, k), 127, np.int8)
+    w8[1::2] = -127
+    _, c = _gemm_dev(a8, np.ones(m, np.float32), w8, np.ones(n, np.float32))
+    exp = np.where(np.arange(n) % 2 == 0, -127 * 127 * k, 127 * 127 * k).astype(np.int32)
+    assert np.array_equal(c, np.broadcast_to(exp, (m, n)))
+
+
+def test_w8a8_pipeline_config0():
+    """Repack -> A8 quant -> GEMM for the 5632x2048 Q4_K weight and 128 tokens."""
+    m, k, n = 128, 2048, 5632
+    blocks = synth.q4_k(n, k, index=0)
+    a = synth.activations(m, k, index=1)
+    w8, ws = hip.repack_w8(4, _dev(blocks), k, n)
+    a8, as_ = hip.quantize_a8(_dev(a))
+    out = hip.gemm_w8a8(a8, as_, w8, ws)
+    torch.cuda.synchronize()
+    ref = orc.matmul_q_w8a8(4, blocks, a, n, threads=8)
+    assert np.array_equal(_bits(out.cpu().numpy()), _bits(ref))
+
+
+# ---------------------------------------------------------------- kernel (d)
+@pytest.mark.parametrize("m,k", [(1, 256), (1, 2048), (4, 2048), (3, 5632), (8, 2048), (11, 1024)])
+def test_quantize_q8_k_bit_exact(m, k):
+    x = synth.activations(m, k, index=300 + m + k)
+    if m > 2:
+        x[1, :256] = 0.0                   # all-zero block
+        x[2, 5] = -np.abs(x[2, :256]).max() - 1.0
+        x[2, 9] = -x[2, 5]                 # equal magnitudes: the first one wins
+    q = hip.quantize_q8_k(_dev(x))
+    torch.cuda.synchronize()
+    assert np.array_equal(q.cpu().numpy(), orc.quantize_q8_k(x))
+
+
+def _gemv_check(kind, n, k, m, index):
+    w = synth.kquant(kind, n, k, index=index)
+    x = synth.activations(m, k, index=index + 1)
+    q8 = orc.quantize_q8_k(x)
+    nb = k // 256
+    isum = torch.empty((m, n, nb), dtype=torch.int32, device=DEV)
+    msum = torch.empty((m, n, nb), dtype=torch.int32, device=DEV)
+    out = hip.gemv_q8_k(kind, _dev(w), k, n, _dev(q8), isum=isum, msum=msum)
+    torch.cuda.synchronize()
+    out, isum, msum = out.cpu().numpy(), isum.cpu().numpy(), msum.cpu().numpy()
+    ref = orc.gemv_q8_k(kind, w, k, n, q8, threads=8)
+    for mi in range(m):
+        ris, rms, mag = orc.gemv_block_sums(kind, w, k, n, q8[mi])
+        assert np.array_equal(isum[mi], ris), f"isum row {mi}"
+        assert np.array_equal(msum[mi], rms), f"msum row {mi}"
+        err = np.abs(out[mi].astype(np.float64) - ref[mi])
+        assert np.all(err <= 1e-5 * mag), f"row {mi}: max err/mag {np.max(err / mag)}"
+
+
+@pytest.mark.parametrize("kind,n,k,m", [
+    (4, 64, 256, 1), (4, 2048, 2048, 1), (4, 256, 2048, 4), (4, 5632, 2048, 1), (4, 300, 5632, 3),
+    (6, 64, 256, 1), (6, 2048, 5632, 1), (6, 2048, 5632, 4), (6, 100, 2048, 8), (4, 130, 14336, 2),
+])
+def test_gemv_q8_k(kind, n, k, m):
+    print(f"gemv kind={kind} n={n} k={k} m={m}", flush=True)
+    _gemv_check(kind, n, k, m, index=400 + kind + n + m)
+
+
+def test_gemv_m_chunking():
+    """m above one launch's 8 rows is split into launches; results unchanged."""
+    _gemv_check(4, 96, 2048, 13, index=500)
