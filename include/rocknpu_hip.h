@@ -65,6 +65,18 @@ int rocknpu_hip_gemv_q8_k(uint32_t kind, const uint8_t * w, size_t w_bytes, size
                           const uint8_t * q8k, size_t m, float * out, size_t ldo, int32_t * isum,
                           int32_t * msum, void * stream);
 
+/* Kernel (d), fused form: the same GEMV with the activations given as f32
+ * x [m, ldx] (ldx % 4 == 0, x 16-byte aligned) and quantised to Q8_K inside
+ * the kernel, for 1..4 projections of one kind that share x (q/k/v, gate/up):
+ * out[i][mi * ldo[i] + ni] for member i. Bit-identical to
+ * rocknpu_hip_quantize_q8_k followed by rocknpu_hip_gemv_q8_k per member.
+ * `w`, `w_bytes`, `n`, `out`, `ldo` are host arrays of `count` entries
+ * (device pointers inside). */
+int rocknpu_hip_gemv_q_f32(uint32_t kind, size_t count, const uint8_t * const * w,
+                           const size_t * w_bytes, const size_t * n, size_t k, const float * x,
+                           size_t ldx, size_t m, float * const * out, const size_t * ldo,
+                           void * stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -384,13 +384,15 @@ int or_gemv_block_sums(uint32_t kind, const uint8_t *w, size_t k, size_t n, cons
             int32_t aux32[8], sumi = 0, s = 0;
             if (kind == 4) q4k_block_ints(x, yb, aux32, &sumi);
             else q6k_block_ints(x, yb, aux32);
-            for (int l = 0; l < 8; ++l) s += aux32[l];
-            isum[r * nb + b] = s;
-            msum[r * nb + b] = sumi;
             float yd;
             memcpy(&yd, yb, 4);
             const double d = (double)or_fp16_to_f32(rd16(kind == 4 ? x : x + 208)) * yd;
-            total += fabs(d * s);
+            for (int l = 0; l < 8; ++l) {
+                s += aux32[l];
+                total += fabs(d * aux32[l]);  /* the generic dot rounds each d*aux32[l] */
+            }
+            isum[r * nb + b] = s;
+            msum[r * nb + b] = sumi;
             if (kind == 4) total += fabs((double)or_fp16_to_f32(rd16(x + 2)) * yd * sumi);
         }
         mag[r] = total;

@@ -94,7 +94,10 @@ int or_gemv_q8_k(uint32_t kind, const uint8_t *w, size_t k, size_t n, const uint
 /* Integer sub-sums of the decode dot for each (row, block):
  *   isum[r*nb+b] = sum_j scale_j * sum_{l in sub-block j} q8 * q
  *   msum[r*nb+b] = sum_j min_j * (bsum pair of sub-block j)   (Q4_K; 0 for Q6_K)
- * and mag[mi*n+ni] = sum_b |d*isum| + |dmin*msum| (the error-bound weight). */
+ * and mag[ni] = sum_b (sum_l |d*aux32_b[l]| + |dmin*msum_b|), the magnitude the
+ * generic ggml dot's f32 rounding error scales with (it rounds d*aux32[l] for
+ * its 8 lanes l of positions p % 8 == l): results of any f32 evaluation order
+ * agree with it to within a small multiple of 2^-24 * (8 + k/256) * mag. */
 int or_gemv_block_sums(uint32_t kind, const uint8_t *w, size_t k, size_t n, const uint8_t *q8k_row,
                        int32_t *isum, int32_t *msum, double *mag);
 

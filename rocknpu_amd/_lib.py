@@ -53,6 +53,7 @@ SIGNATURES = {
     "rocknpu_hip_gemm_w8a8": (_i, [_vp, _vp, _vp, _vp, _sz, _sz, _sz, _vp, _sz, _vp, _vp]),
     "rocknpu_hip_quantize_q8_k": (_i, [_vp, _sz, _sz, _sz, _vp, _vp]),
     "rocknpu_hip_gemv_q8_k": (_i, [_u32, _vp, _sz, _sz, _sz, _vp, _sz, _vp, _sz, _vp, _vp, _vp]),
+    "rocknpu_hip_gemv_q_f32": (_i, [_u32, _sz, _vp, _vp, _vp, _sz, _vp, _sz, _sz, _vp, _vp, _vp]),
 }
 
 

@@ -78,4 +78,26 @@ __device__ __forceinline__ int wave_or(int v) {
     return v;
 }
 
+
+// Decode GEMV launch description (kernel (d)): up to four projections that
+// share K and the activation rows, laid out back to back in a virtual row space.
+constexpr int kGemvMaxMembers = 4;
+struct GemvParams {
+    const uint8_t* w[kGemvMaxMembers];
+    float* out[kGemvMaxMembers];
+    int64_t ldo[kGemvMaxMembers];
+    int64_t row_end[kGemvMaxMembers];  // cumulative row counts of the members
+    int count;
+    const float* x;      // f32 activations [m, ldx] (quantised in-kernel), or
+    const uint8_t* q8k;  // Q8_K rows, ldx bytes apart
+    int64_t ldx;
+    int m;
+    int nb;              // super-blocks per row
+    int log2g;           // lanes per row = 1 << log2g
+    int iters;           // units per lane per row group
+    int64_t groups;      // row groups
+    int32_t* isum;       // optional exact per-(mi, row, block) sums (count == 1)
+    int32_t* msum;
+};
+
 }  // namespace rk

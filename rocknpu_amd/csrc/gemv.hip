@@ -2,19 +2,25 @@
 //
 // Replaces llama.cpp's CPU decode route that the reference plugin keeps for
 // M=1 (adapters/ggml-rocknpu/src/ggml-rocknpu.cpp:674-679 rejects M=1 under
-// ROCKNPU_DECODE=cpu): ggml_vec_dot_q4_K_q8_K / ggml_vec_dot_q6_K_q8_K. For
-// every (row, super-block) the integer sums are exact:
+// ROCKNPU_DECODE=cpu): ggml_vec_dot_q4_K_q8_K / ggml_vec_dot_q6_K_q8_K after
+// quantize_row_q8_K. For every (row, super-block) the integer sums are exact:
 //   isum = sum_j sc_j * sum_{l in sub-block j} q8[l] * q[l]
 //   msum = sum_j mn_j * (bsum pair of sub-block j)         (Q4_K only)
 // and the row result is sum_b (d_w*d_a) * isum - (dmin_w*d_a) * msum in f32.
 //
-// Mapping: the Q8_K activation rows are staged in LDS, split into aligned
-// quants / bsums / d arrays. A "unit" is 64 weight values of a Q4_K block
-// (4 per block: 32 qs bytes + the 16-byte header) or 32 values of a Q6_K block
-// (8 per block). Each wave works on 64/G rows at once, G lanes per row; lanes
-// of one block are adjacent, so a block's integer sums are reduced with lane
-// shuffles and converted to f32 once per block. Quant dot products use
-// v_dot4_i32_i8 (sdot4).
+// One launch serves up to four projections that share the activation rows
+// (q/k/v, gate/up): their rows are laid back to back in one virtual row space.
+// The activations are either f32 (quantised to Q8_K by every workgroup into
+// LDS: 16 lanes per 256-value block, DPP reductions) or Q8_K rows copied to
+// LDS. In LDS the quants are chunk-major ([row][16-value chunk][block]) so the
+// lanes reading consecutive blocks read consecutive 16-byte chunks.
+//
+// Work split: one lane owns one whole super-block (144 bytes of Q4_K, 210 of
+// Q6_K), so scales are unpacked once per block and the block's integer sums
+// never leave the lane. G lanes (G <= 16) share a weight row, a wave covers
+// 64/G rows at once, and a row group takes `iters` blocks per lane. Waves walk
+// their row groups grid-stride with D blocks of loads in flight per lane; the
+// row's G partial sums are combined with DPP lane moves.
 #include "common.h"
 
 namespace rk {
@@ -22,213 +28,489 @@ namespace {
 
 constexpr int kGemvWaves = 4;
 
-struct Q8Lds {
-    int8_t* qs;     // [m][nb][256]
-    int32_t* bs;    // [m][nb][8]  pairs of int16 bsums packed as words
-    float* d;       // [m][nb]
-};
+template <int CTRL>
+__device__ __forceinline__ int dpp(int v) {
+    return __builtin_amdgcn_mov_dpp(v, CTRL, 0xF, 0xF, false);
+}
+// DPP controls: quad_perm [1,0,3,2] and [2,3,0,1], row_half_mirror, row_mirror.
+// Applied in this order they combine aligned groups of 2, 4, 8 and 16 lanes.
+constexpr int kDppXor1 = 0xB1, kDppXor2 = 0x4E, kDppMirror8 = 0x141, kDppMirror16 = 0x140;
+
+__device__ __forceinline__ float max16(float v) {
+    v = fmaxf(v, __int_as_float(dpp<kDppXor1>(__float_as_int(v))));
+    v = fmaxf(v, __int_as_float(dpp<kDppXor2>(__float_as_int(v))));
+    v = fmaxf(v, __int_as_float(dpp<kDppMirror8>(__float_as_int(v))));
+    return fmaxf(v, __int_as_float(dpp<kDppMirror16>(__float_as_int(v))));
+}
+__device__ __forceinline__ int min16(int v) {
+    v = min(v, dpp<kDppXor1>(v));
+    v = min(v, dpp<kDppXor2>(v));
+    v = min(v, dpp<kDppMirror8>(v));
+    return min(v, dpp<kDppMirror16>(v));
+}
+// Sum over aligned groups of G lanes (G a power of two, at most 16).
+__device__ __forceinline__ float group_sum(float v, int G) {
+    if (G >= 2) v += __int_as_float(dpp<kDppXor1>(__float_as_int(v)));
+    if (G >= 4) v += __int_as_float(dpp<kDppXor2>(__float_as_int(v)));
+    if (G >= 8) v += __int_as_float(dpp<kDppMirror8>(__float_as_int(v)));
+    if (G >= 16) v += __int_as_float(dpp<kDppMirror16>(__float_as_int(v)));
+    return v;
+}
 
 __device__ __forceinline__ int dot4(uint32_t a, uint32_t b, int c) {
     return __builtin_amdgcn_sdot4(static_cast<int>(a), static_cast<int>(b), c, false);
 }
 
-template <int KIND, int MT>
-__global__ __launch_bounds__(kGemvWaves * 64) void gemv_q8_k_kernel(
-    const uint8_t* __restrict__ w, int64_t n, int nb, const uint8_t* __restrict__ q8k, int64_t ldq,
-    int m, int log2g, float* __restrict__ out, int64_t ldo, int32_t* __restrict__ isum_out,
-    int32_t* __restrict__ msum_out) {
-    constexpr int BB = block_bytes(KIND);
-    constexpr int UPB = KIND == 4 ? 4 : 8;  // units per block
-    extern __shared__ __align__(16) uint8_t smem[];
+// Global-memory (address space 1) views: addresses rebuilt from integers keep
+// global loads and stores instead of FLAT ones (which also count against the
+// LDS wait counter).
+typedef const __attribute__((address_space(1))) uint8_t* gbytes;
+typedef __attribute__((address_space(1))) float* gfloats;
+typedef unsigned v4u __attribute__((ext_vector_type(4)));
+
+// Branch-free choice among four 64-bit values (kept as register selects, so
+// the compiler cannot turn it into a table in private memory).
+__device__ __forceinline__ uint64_t select4(int i, uint64_t a, uint64_t b, uint64_t c, uint64_t d) {
+    const uint64_t m1 = 0ull - static_cast<uint64_t>(i == 1);
+    const uint64_t m2 = 0ull - static_cast<uint64_t>(i == 2);
+    const uint64_t m3 = 0ull - static_cast<uint64_t>(i == 3);
+    const uint64_t m0 = ~(m1 | m2 | m3);
+    return (a & m0) | (b & m1) | (c & m2) | (d & m3);
+}
+
+// Activation rows in LDS. Quant p (0..255) of block b of row mi lives at byte
+//   ((mi * 16 + p / 16) * nb + b) * 16 + p % 16
+// bsums 8h..8h+7 of that block at int16 index ((mi * 2 + h) * nb + b) * 8, and
+// its scale at d[mi * nb + b].
+struct Q8Lds {
+    int8_t* qs;
+    int16_t* bs;
+    float* d;
+};
+
+__device__ __forceinline__ Q8Lds q8_lds(uint8_t* smem, int mt, int nb) {
     Q8Lds a;
     a.qs = reinterpret_cast<int8_t*>(smem);
-    a.bs = reinterpret_cast<int32_t*>(smem + MT * nb * kQK);
-    a.d = reinterpret_cast<float*>(smem + MT * nb * (kQK + 32));
+    a.bs = reinterpret_cast<int16_t*>(smem + mt * nb * kQK);
+    a.d = reinterpret_cast<float*>(smem + mt * nb * (kQK + 32));
+    return a;
+}
 
-    // Stage the activation rows: word-granular copy, split by field.
+__device__ __forceinline__ int qs_offset(int mi, int nb, int b, int p) {
+    return ((mi * 16 + (p >> 4)) * nb + b) * 16 + (p & 15);
+}
+__device__ __forceinline__ int bs_index(int mi, int nb, int b, int j) {
+    return ((mi * 2 + (j >> 3)) * nb + b) * 8 + (j & 7);
+}
+
+// The 16 values of this lane for quantisation block qb.
+__device__ __forceinline__ void load_x16(const float* __restrict__ x, int64_t ldx, int nb, int qb, float4 (&f)[4]) {
+    const int sub = threadIdx.x & 15;
+    const int r = qb / nb, b = qb % nb;
+    const float4* src = reinterpret_cast<const float4*>(x + r * ldx + b * kQK + 16 * sub);
+#pragma unroll
+    for (int t = 0; t < 4; ++t) f[t] = src[t];
+}
+
+// Q8_K quantisation of rows [0, m) of x into LDS (ggml quantize_row_q8_K_ref
+// semantics, see quant.hip): 16 lanes per block, 16 values per lane. `first`
+// holds this lane's values of its first block, loaded by the caller ahead of
+// the weight loads so they return first.
+__device__ __forceinline__ void quantize_to_lds(const float* __restrict__ x, int64_t ldx, int m, int nb,
+                                                const float4 (&first)[4], const Q8Lds& a) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int sub = lane & 15;
+    const int slot = wave * 4 + (lane >> 4);
+    for (int qb = slot; qb < m * nb; qb += kGemvWaves * 4) {
+        const int r = qb / nb, b = qb % nb;
+        float4 f[4];
+        if (qb == slot) {
+#pragma unroll
+            for (int t = 0; t < 4; ++t) f[t] = first[t];
+        } else {
+            load_x16(x, ldx, nb, qb, f);
+        }
+        float v[16];
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            v[4 * t] = f[t].x; v[4 * t + 1] = f[t].y; v[4 * t + 2] = f[t].z; v[4 * t + 3] = f[t].w;
+        }
+        float amax = 0.0f;
+        int first_i = 0;
+        bool neg = false;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            const float ax = fabsf(v[i]);
+            if (ax > amax) { amax = ax; first_i = i; neg = v[i] < 0.0f; }
+        }
+        const float gmax = max16(amax);
+        int key = (amax == gmax && gmax > 0.0f) ? ((16 * sub + first_i) * 2 + (neg ? 1 : 0)) : 0x7fffffff;
+        key = min16(key);
+        int q[16];
+        float d = 0.0f;
+        if (gmax > 0.0f) {
+            const float mx = (key & 1) ? -gmax : gmax;  // the first value of largest magnitude
+            const float iscale = -127.0f / mx;
+#pragma unroll
+            for (int i = 0; i < 16; ++i) q[i] = min(127, static_cast<int>(__builtin_rintf(iscale * v[i])));
+            d = 1.0f / iscale;
+        } else {
+#pragma unroll
+            for (int i = 0; i < 16; ++i) q[i] = 0;
+        }
+        int s = 0;
+        uint32_t wq[4];
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            s += q[4 * t] + q[4 * t + 1] + q[4 * t + 2] + q[4 * t + 3];
+            wq[t] = (q[4 * t] & 0xFF) | (q[4 * t + 1] & 0xFF) << 8 | (q[4 * t + 2] & 0xFF) << 16 |
+                    static_cast<uint32_t>(q[4 * t + 3] & 0xFF) << 24;
+        }
+        *reinterpret_cast<uint4*>(a.qs + qs_offset(r, nb, b, 16 * sub)) = make_uint4(wq[0], wq[1], wq[2], wq[3]);
+        a.bs[bs_index(r, nb, b, sub)] = static_cast<int16_t>(s);
+        if (sub == 0) a.d[r * nb + b] = d;
+    }
+}
+
+// Copy Q8_K rows (292-byte blocks) into the LDS layout.
+__device__ __forceinline__ void stage_q8k(const uint8_t* __restrict__ q8k, int64_t ldq, int m, int nb,
+                                          const Q8Lds& a) {
     const int words = m * nb * (kQ8KBytes / 4);
     for (int i = threadIdx.x; i < words; i += blockDim.x) {
         const int blk = i / (kQ8KBytes / 4), wi = i % (kQ8KBytes / 4);
         const int mi = blk / nb, bi = blk % nb;
         const uint32_t v = *reinterpret_cast<const uint32_t*>(q8k + mi * ldq + bi * kQ8KBytes + 4 * wi);
-        const int flat = mi * nb + bi;
-        if (wi == 0) a.d[flat] = __uint_as_float(v);
-        else if (wi <= 64) reinterpret_cast<uint32_t*>(a.qs + flat * kQK)[wi - 1] = v;
-        else a.bs[flat * 8 + (wi - 65)] = static_cast<int32_t>(v);
+        if (wi == 0) a.d[mi * nb + bi] = __uint_as_float(v);
+        else if (wi <= 64) *reinterpret_cast<uint32_t*>(a.qs + qs_offset(mi, nb, bi, 4 * (wi - 1))) = v;
+        else *reinterpret_cast<uint32_t*>(a.bs + bs_index(mi, nb, bi, 2 * (wi - 65))) = v;
     }
-    __syncthreads();
+}
+
+// One super-block's raw bytes as 32-bit words.
+template <int KIND>
+struct Block;
+
+template <>
+struct Block<4> {
+    uint32_t w[36];  // [0] d|dmin, [1..3] packed scales, [4..35] qs
+    __device__ __forceinline__ void load(gbytes blk) {
+        typedef const __attribute__((address_space(1))) v4u* gu4;
+#pragma unroll
+        for (int t = 0; t < 9; ++t) {
+            const v4u x = reinterpret_cast<gu4>(blk)[t];
+            w[4 * t] = x.x; w[4 * t + 1] = x.y; w[4 * t + 2] = x.z; w[4 * t + 3] = x.w;
+        }
+    }
+};
+
+template <>
+struct Block<6> {
+    uint32_t w[53];  // [0..31] ql, [32..47] qh, [48..51] scales, [52] d (low 16 bits)
+    // Q6_K blocks are only 2-byte aligned; the hardware takes unaligned vector
+    // loads, so the first 208 bytes come in as 13 16-byte loads.
+    __device__ __forceinline__ void load(gbytes blk) {
+        typedef v4u v4u_a2 __attribute__((aligned(2)));
+        typedef const __attribute__((address_space(1))) v4u_a2* gu4;
+#pragma unroll
+        for (int t = 0; t < 13; ++t) {
+            const v4u x = reinterpret_cast<gu4>(blk)[t];
+            w[4 * t] = x.x; w[4 * t + 1] = x.y; w[4 * t + 2] = x.z; w[4 * t + 3] = x.w;
+        }
+        w[52] = *reinterpret_cast<const __attribute__((address_space(1))) uint16_t*>(blk + 208);
+    }
+};
+
+__device__ __forceinline__ v4u lds_chunk(const Q8Lds& a, int mi, int nb, int b, int c) {
+    return *reinterpret_cast<const v4u*>(a.qs + ((mi * 16 + c) * nb + b) * 16);
+}
+
+// Per-block decode shared by all activation rows: Q4_K 6-bit scales/mins;
+// Q6_K signed 6-bit quants (as packed int8 words) and int8 scales.
+template <int KIND>
+struct Decoded;
+
+template <>
+struct Decoded<4> {
+    int sc[8], mn[8];
+    __device__ __forceinline__ void decode(const Block<4>& k) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) scale_min_k4(j, k.w[1], k.w[2], k.w[3], sc[j], mn[j]);
+    }
+};
+
+template <>
+struct Decoded<6> {
+    uint32_t q[64];  // value words: q[(p / 4)] holds values p..p+3, minus 32, as int8
+    int sc[16];
+    __device__ __forceinline__ void decode(const Block<6>& k) {
+#pragma unroll
+        for (int half = 0; half < 2; ++half)
+#pragma unroll
+            for (int qd = 0; qd < 4; ++qd)
+#pragma unroll
+                for (int l = 0; l < 32; l += 4) {
+                    const uint32_t lb = k.w[(64 * half + 32 * (qd & 1) + l) / 4];
+                    const uint32_t lo = (qd < 2) ? (lb & 0x0F0F0F0Fu) : ((lb >> 4) & 0x0F0F0F0Fu);
+                    const uint32_t hi = (k.w[32 + (32 * half + l) / 4] >> (2 * qd)) & 0x03030303u;
+                    const uint32_t u6 = lo | (hi << 4);  // bytes in [0, 63]
+                    q[(128 * half + 32 * qd + l) / 4] = ((u6 | 0x80808080u) - 0x20202020u) ^ 0x80808080u;
+                }
+#pragma unroll
+        for (int si = 0; si < 16; ++si) sc[si] = static_cast<int8_t>((k.w[48 + si / 4] >> (8 * (si % 4))) & 0xFF);
+    }
+};
+
+// Exact integer sums of block b against activation row mi.
+__device__ __forceinline__ void block_sums(const Block<4>& k, const Decoded<4>& dc, int mi, int nb, int b,
+                                           const Q8Lds& a, int& isum, int& msum) {
+    int is = 0, ms = 0;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {  // 64-value group j: sub-blocks 2j (low nibbles), 2j+1 (high)
+        const v4u x0 = lds_chunk(a, mi, nb, b, 4 * j), x1 = lds_chunk(a, mi, nb, b, 4 * j + 1);
+        const v4u x2 = lds_chunk(a, mi, nb, b, 4 * j + 2), x3 = lds_chunk(a, mi, nb, b, 4 * j + 3);
+        const uint32_t lo8[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+        const uint32_t hi8[8] = {x2.x, x2.y, x2.z, x2.w, x3.x, x3.y, x3.z, x3.w};
+        int dlo = 0, dhi = 0;
+#pragma unroll
+        for (int t = 0; t < 8; ++t) {
+            const uint32_t q = k.w[4 + 8 * j + t];
+            dlo = dot4(q & 0x0F0F0F0Fu, lo8[t], dlo);
+            dhi = dot4((q >> 4) & 0x0F0F0F0Fu, hi8[t], dhi);
+        }
+        is += dc.sc[2 * j] * dlo + dc.sc[2 * j + 1] * dhi;
+        const uint2 bs = *reinterpret_cast<const uint2*>(a.bs + bs_index(mi, nb, b, 4 * j));
+        const int b_lo = static_cast<int16_t>(bs.x & 0xFFFF) + static_cast<int16_t>(bs.x >> 16);
+        const int b_hi = static_cast<int16_t>(bs.y & 0xFFFF) + static_cast<int16_t>(bs.y >> 16);
+        ms += dc.mn[2 * j] * b_lo + dc.mn[2 * j + 1] * b_hi;
+    }
+    isum = is;
+    msum = ms;
+}
+
+__device__ __forceinline__ void block_sums(const Block<6>&, const Decoded<6>& dc, int mi, int nb, int b,
+                                           const Q8Lds& a, int& isum, int& msum) {
+    int is = 0;
+#pragma unroll
+    for (int si = 0; si < 16; ++si) {  // 16-value sub-block si = chunk si
+        const v4u x = lds_chunk(a, mi, nb, b, si);
+        int dq = dot4(dc.q[4 * si], x.x, 0);
+        dq = dot4(dc.q[4 * si + 1], x.y, dq);
+        dq = dot4(dc.q[4 * si + 2], x.z, dq);
+        dq = dot4(dc.q[4 * si + 3], x.w, dq);
+        is += dc.sc[si] * dq;
+    }
+    isum = is;
+    msum = 0;
+}
+
+// Position of a lane's block: row group `gi`, iteration `it` inside the group.
+struct Pos {
+    int64_t gi;
+    int it;
+};
+
+template <int KIND, int MT, bool FUSED, int D>
+__global__ __launch_bounds__(kGemvWaves * 64) void gemv_kernel(const GemvParams p) {
+    constexpr int BB = block_bytes(KIND);
+    extern __shared__ __align__(16) uint8_t smem[];
+    const Q8Lds a = q8_lds(smem, MT, p.nb);
 
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    // argument block copied to locals (scalar registers): lanes choose among
+    // them with constant indices, never index the argument block by lane
+    const int count = p.count, iters = p.iters, nb = p.nb, m = p.m, log2g = p.log2g;
+    const int64_t e0 = p.row_end[0], e1 = p.row_end[1], e2 = p.row_end[2];
+    const int64_t total_rows = count == 1 ? e0 : count == 2 ? e1 : count == 3 ? e2 : p.row_end[3];
+    const uint8_t* const w0 = p.w[0];
+    const uint8_t* const w1 = p.w[1];
+    const uint8_t* const w2 = p.w[2];
+    const uint8_t* const w3 = p.w[3];
+    float* const out0 = p.out[0];
+    float* const out1 = p.out[1];
+    float* const out2 = p.out[2];
+    float* const out3 = p.out[3];
+    const int64_t ldo0 = p.ldo[0], ldo1 = p.ldo[1], ldo2 = p.ldo[2], ldo3 = p.ldo[3];
+    int32_t* const isum_out = p.isum;
+    int32_t* const msum_out = p.msum;
+
     const int G = 1 << log2g;
     const int gl = lane & (G - 1);
-    const int64_t row = (static_cast<int64_t>(blockIdx.x) * kGemvWaves + wave) * (64 >> log2g) + (lane >> log2g);
-    const bool row_ok = row < n;
-    const uint8_t* wrow = w + (row_ok ? row : 0) * static_cast<int64_t>(nb) * BB;
-    const int units = nb * UPB;
-    const int iters = (units + G - 1) / G;
+    const int slot = lane >> log2g;  // row inside the row group
+    const int rows_per_group = 64 >> log2g;
+    const int64_t row_bytes = static_cast<int64_t>(nb) * BB;
+    const int64_t wave_gid = static_cast<int64_t>(blockIdx.x) * kGemvWaves + wave;
+    const int64_t wave_stride = static_cast<int64_t>(gridDim.x) * kGemvWaves;
+    // this wave's blocks: row groups wave_gid + i*wave_stride, `iters` per lane each
+    const int64_t my_groups = wave_gid < p.groups ? (p.groups - 1 - wave_gid) / wave_stride + 1 : 0;
+    const int64_t S = my_groups * iters;
+
+    auto member_of = [=](int64_t row, int64_t& local) {
+        int mbr = 0;
+        int64_t start = 0;
+        if (count > 1 && row >= e0) { mbr = 1; start = e0; }
+        if (count > 2 && row >= e1) { mbr = 2; start = e1; }
+        if (count > 3 && row >= e2) { mbr = 3; start = e2; }
+        local = row - start;
+        return mbr;
+    };
+    auto advance = [=](Pos& q) {
+        if (++q.it == iters) { q.it = 0; q.gi += wave_stride; }
+    };
+    // Loads are issued unconditionally: a lane without a block re-reads a block
+    // of its wave's first row group (in bounds, cache-resident, private to the
+    // wave) and ignores it. Branch-free load sequences let the wait-count pass
+    // wait for exactly the loads a value depends on.
+    const int64_t home_row = min(wave_gid * rows_per_group + slot, total_rows - 1);
+    const int home_b = min(gl, nb - 1);
+    auto load_block = [=](const Pos& q, bool in_range, Block<KIND>& k) {
+        int64_t row = q.gi * rows_per_group + slot;
+        int b = gl + q.it * G;
+        if (!(in_range && row < total_rows && b < nb)) {
+            row = home_row;
+            b = home_b;
+        }
+        int64_t local;
+        const int mbr = member_of(row, local);
+        const gbytes base = reinterpret_cast<gbytes>(select4(mbr, reinterpret_cast<uint64_t>(w0),
+                                                             reinterpret_cast<uint64_t>(w1),
+                                                             reinterpret_cast<uint64_t>(w2),
+                                                             reinterpret_cast<uint64_t>(w3)));
+        k.load(base + local * row_bytes + static_cast<int64_t>(b) * BB);
+    };
+
+    // First activation values go out first (they return first), then D blocks.
+    float4 xfirst[4];
+    const int qslot = wave * 4 + (lane >> 4);
+    if constexpr (FUSED) load_x16(p.x, p.ldx, nb, qslot < m * nb ? qslot : 0, xfirst);
+    __builtin_amdgcn_sched_barrier(0);  // keep the activation loads ahead of the weight loads
+    Block<KIND> buf[D];
+    Pos lq{wave_gid, 0};  // next block to load
+#pragma unroll
+    for (int j = 0; j < D; ++j) {
+        load_block(lq, j < S, buf[j]);
+        advance(lq);
+    }
+    if constexpr (FUSED) quantize_to_lds(p.x, p.ldx, m, nb, xfirst, a);
+    else stage_q8k(p.q8k, p.ldx, m, nb, a);
+    __syncthreads();
 
     float acc[MT];
 #pragma unroll
     for (int mi = 0; mi < MT; ++mi) acc[mi] = 0.0f;
 
-    for (int it = 0; it < iters; ++it) {
-        const int u = gl + it * G;
-        const bool ok = row_ok && u < units;
-        const int b = ok ? u / UPB : 0, v = u % UPB;
-        const uint8_t* blk = wrow + b * BB;
-        int isum[MT], msum[MT];
+    Pos cq{wave_gid, 0};  // block being multiplied
+    for (int64_t base = 0; base < S; base += D) {
 #pragma unroll
-        for (int mi = 0; mi < MT; ++mi) { isum[mi] = 0; msum[mi] = 0; }
-        float dw = 0.0f, dminw = 0.0f;
-        if (ok) {
+        for (int j = 0; j < D; ++j) {
+            const int64_t s = base + j;
+            if (s >= S) break;  // uniform across the wave
+            const int64_t row = cq.gi * rows_per_group + slot;
+            const int b = gl + cq.it * G;
+            const bool ok = row < total_rows && b < nb;
+            float dw, dminw = 0.0f;
             if constexpr (KIND == 4) {
-                const uint4 hdr = *reinterpret_cast<const uint4*>(blk);
-                const uint4 qa = *reinterpret_cast<const uint4*>(blk + 16 + 32 * v);
-                const uint4 qb = *reinterpret_cast<const uint4*>(blk + 16 + 32 * v + 16);
-                dw = f16_bits_to_f32(static_cast<uint16_t>(hdr.x & 0xFFFF));
-                dminw = f16_bits_to_f32(static_cast<uint16_t>(hdr.x >> 16));
-                int sc_lo, mn_lo, sc_hi, mn_hi;
-                scale_min_k4(2 * v, hdr.y, hdr.z, hdr.w, sc_lo, mn_lo);
-                scale_min_k4(2 * v + 1, hdr.y, hdr.z, hdr.w, sc_hi, mn_hi);
-                const uint32_t qw[8] = {qa.x, qa.y, qa.z, qa.w, qb.x, qb.y, qb.z, qb.w};
-#pragma unroll
-                for (int mi = 0; mi < MT; ++mi) {
-                    if (mi >= m) break;
-                    const int flat = mi * nb + b;
-                    const uint4* q8 = reinterpret_cast<const uint4*>(a.qs + flat * kQK + 64 * v);
-                    const uint4 x0 = q8[0], x1 = q8[1], x2 = q8[2], x3 = q8[3];
-                    const uint32_t lo8[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
-                    const uint32_t hi8[8] = {x2.x, x2.y, x2.z, x2.w, x3.x, x3.y, x3.z, x3.w};
-                    int dlo = 0, dhi = 0;
-#pragma unroll
-                    for (int t = 0; t < 8; ++t) {
-                        dlo = dot4(qw[t] & 0x0F0F0F0Fu, lo8[t], dlo);
-                        dhi = dot4((qw[t] >> 4) & 0x0F0F0F0Fu, hi8[t], dhi);
-                    }
-                    isum[mi] = sc_lo * dlo + sc_hi * dhi;
-                    const int32_t p0 = a.bs[flat * 8 + 2 * v], p1 = a.bs[flat * 8 + 2 * v + 1];
-                    const int bs_lo = static_cast<int16_t>(p0 & 0xFFFF) + static_cast<int16_t>(p0 >> 16);
-                    const int bs_hi = static_cast<int16_t>(p1 & 0xFFFF) + static_cast<int16_t>(p1 >> 16);
-                    msum[mi] = mn_lo * bs_lo + mn_hi * bs_hi;
-                }
+                dw = f16_bits_to_f32(static_cast<uint16_t>(buf[j].w[0] & 0xFFFF));
+                dminw = f16_bits_to_f32(static_cast<uint16_t>(buf[j].w[0] >> 16));
             } else {
-                const int half = v >> 2, g = v & 3;
-                uint32_t l0[2], l1[2], h[2];
-#pragma unroll
-                for (int t = 0; t < 2; ++t) {
-                    const uint8_t* p0 = blk + 64 * half + 8 * g + 4 * t;
-                    const uint8_t* p1 = p0 + 32;
-                    const uint8_t* ph = blk + 128 + 32 * half + 8 * g + 4 * t;
-                    l0[t] = ld_u16(p0) | static_cast<uint32_t>(ld_u16(p0 + 2)) << 16;
-                    l1[t] = ld_u16(p1) | static_cast<uint32_t>(ld_u16(p1 + 2)) << 16;
-                    h[t] = ld_u16(ph) | static_cast<uint32_t>(ld_u16(ph + 2)) << 16;
-                }
-                const uint32_t sw0 = ld_u16(blk + 192 + 8 * half) | static_cast<uint32_t>(ld_u16(blk + 194 + 8 * half)) << 16;
-                const uint32_t sw1 = ld_u16(blk + 196 + 8 * half) | static_cast<uint32_t>(ld_u16(blk + 198 + 8 * half)) << 16;
-                dw = f16_bits_to_f32(ld_u16(blk + 208));
-                // scale of quarter qd is byte (g/2 + 2*qd) of the 8 half-block scales
-                const uint64_t sw = sw0 | static_cast<uint64_t>(sw1) << 32;
-                int sc[4];
-#pragma unroll
-                for (int qd = 0; qd < 4; ++qd) sc[qd] = static_cast<int8_t>((sw >> (8 * ((g >> 1) + 2 * qd))) & 0xFF);
-                uint32_t qv[4][2];
-#pragma unroll
-                for (int qd = 0; qd < 4; ++qd)
-#pragma unroll
-                    for (int t = 0; t < 2; ++t) {
-                        const uint32_t lb = (qd & 1) ? l1[t] : l0[t];
-                        const uint32_t lo = (qd < 2) ? (lb & 0x0F0F0F0Fu) : ((lb >> 4) & 0x0F0F0F0Fu);
-                        const uint32_t hi = (h[t] >> (2 * qd)) & 0x03030303u;
-                        const uint32_t u6 = lo | (hi << 4);  // bytes in [0, 63]
-                        qv[qd][t] = ((u6 | 0x80808080u) - 0x20202020u) ^ 0x80808080u;  // bytes - 32
-                    }
-#pragma unroll
-                for (int mi = 0; mi < MT; ++mi) {
-                    if (mi >= m) break;
-                    const int8_t* q8 = a.qs + (mi * nb + b) * kQK + 128 * half + 8 * g;
-                    int s = 0;
-#pragma unroll
-                    for (int qd = 0; qd < 4; ++qd) {
-                        const uint2 x = *reinterpret_cast<const uint2*>(q8 + 32 * qd);
-                        const int dq = dot4(qv[qd][1], x.y, dot4(qv[qd][0], x.x, 0));
-                        s += sc[qd] * dq;
-                    }
-                    isum[mi] = s;
-                }
+                dw = f16_bits_to_f32(static_cast<uint16_t>(buf[j].w[52]));
             }
-        }
-        // Reduce the UPB lanes of each block (adjacent lanes), exactly in int.
-#pragma unroll
-        for (int mi = 0; mi < MT; ++mi) {
-#pragma unroll
-            for (int o = 1; o < UPB; o <<= 1) {
-                isum[mi] += __shfl_xor(isum[mi], o, 64);
-                if constexpr (KIND == 4) msum[mi] += __shfl_xor(msum[mi], o, 64);
-            }
-        }
-        if (ok && v == 0) {
+            // Every lane computes (a lane without a block holds its home block)
+            // and discards the result: straight-line code for all rows mi.
+            const int bs = ok ? b : home_b;
+            Decoded<KIND> dc;
+            dc.decode(buf[j]);
 #pragma unroll
             for (int mi = 0; mi < MT; ++mi) {
                 if (mi >= m) break;
-                const float da = a.d[mi * nb + b];
-                float term = (dw * da) * static_cast<float>(isum[mi]);
-                if constexpr (KIND == 4) term = term - (dminw * da) * static_cast<float>(msum[mi]);
-                acc[mi] += term;
-                if (isum_out) {
-                    const int64_t idx = (static_cast<int64_t>(mi) * n + row) * nb + b;
-                    isum_out[idx] = isum[mi];
-                    msum_out[idx] = msum[mi];
+                int isum, msum;
+                block_sums(buf[j], dc, mi, nb, bs, a, isum, msum);
+                const float da = a.d[mi * nb + bs];
+                float term = (dw * da) * static_cast<float>(isum);
+                if constexpr (KIND == 4) term = term - (dminw * da) * static_cast<float>(msum);
+                acc[mi] += ok ? term : 0.0f;
+                if (isum_out && ok) {
+                    const int64_t idx = (static_cast<int64_t>(mi) * total_rows + row) * nb + b;
+                    isum_out[idx] = isum;
+                    msum_out[idx] = msum;
                 }
             }
-        }
-    }
-    // Sum the row's per-lane partials across its G lanes.
+            // refill this slot with the block D ahead
+            load_block(lq, s + D < S, buf[j]);
+            advance(lq);
+            if (cq.it == iters - 1) {
+                // row group done: combine the row's G lanes and store
+                int64_t local;
+                const int mbr = member_of(row, local);
+                const gfloats out = reinterpret_cast<gfloats>(select4(mbr, reinterpret_cast<uint64_t>(out0),
+                                                                      reinterpret_cast<uint64_t>(out1),
+                                                                      reinterpret_cast<uint64_t>(out2),
+                                                                      reinterpret_cast<uint64_t>(out3)));
+                const int64_t ldo = static_cast<int64_t>(select4(mbr, ldo0, ldo1, ldo2, ldo3));
 #pragma unroll
-    for (int mi = 0; mi < MT; ++mi) {
-        for (int o = 1; o < G; o <<= 1) acc[mi] += __shfl_xor(acc[mi], o, 64);
-    }
-    if (row_ok && gl == 0) {
-#pragma unroll
-        for (int mi = 0; mi < MT; ++mi) {
-            if (mi >= m) break;
-            out[mi * ldo + row] = acc[mi];
+                for (int mi = 0; mi < MT; ++mi) {
+                    const float r = group_sum(acc[mi], G);
+                    if (gl == 0 && row < total_rows && mi < m) out[mi * ldo + local] = r;
+                    acc[mi] = 0.0f;
+                }
+            }
+            advance(cq);
         }
     }
 }
 
-template <int KIND>
-int launch_kind(const uint8_t* w, int64_t n, int nb, const uint8_t* q8k, int64_t ldq, int m,
-                float* out, int64_t ldo, int32_t* isum, int32_t* msum, hipStream_t stream) {
-    constexpr int UPB = KIND == 4 ? 4 : 8;
-    const int units = nb * UPB;
-    int log2g = 0;
-    while ((1 << log2g) < units && log2g < 6) ++log2g;
-    const int64_t rows_per_wg = static_cast<int64_t>(kGemvWaves) * (64 >> log2g);
-    const dim3 grid(static_cast<unsigned>((n + rows_per_wg - 1) / rows_per_wg)), block(kGemvWaves * 64);
-    int mt = m <= 1 ? 1 : m <= 2 ? 2 : m <= 4 ? 4 : 8;
-    const size_t lds = static_cast<size_t>(mt) * nb * (kQK + 32 + 4);
-#define RK_GEMV_CASE(MTV)                                                                     \
-    case MTV:                                                                                 \
-        gemv_q8_k_kernel<KIND, MTV><<<grid, block, lds, stream>>>(w, n, nb, q8k, ldq, m, log2g, \
-                                                                  out, ldo, isum, msum);      \
-        break;
+template <int KIND, bool FUSED, int D>
+void launch_d(const GemvParams& p, int mt, dim3 grid, size_t lds, hipStream_t stream) {
+    const dim3 block(kGemvWaves * 64);
     switch (mt) {
-        RK_GEMV_CASE(1)
-        RK_GEMV_CASE(2)
-        RK_GEMV_CASE(4)
-        RK_GEMV_CASE(8)
+    case 1: gemv_kernel<KIND, 1, FUSED, D><<<grid, block, lds, stream>>>(p); break;
+    case 2: gemv_kernel<KIND, 2, FUSED, D><<<grid, block, lds, stream>>>(p); break;
+    case 4: gemv_kernel<KIND, 4, FUSED, D><<<grid, block, lds, stream>>>(p); break;
+    default: gemv_kernel<KIND, 8, FUSED, D><<<grid, block, lds, stream>>>(p); break;
     }
-#undef RK_GEMV_CASE
+}
+
+// Lanes per row: the largest power of two <= min(16, nb) whose last pass over
+// the row's blocks keeps at least 85% of the lanes busy.
+int lanes_per_row_log2(int nb) {
+    int lg = 0;
+    while ((2 << lg) <= 16 && (2 << lg) <= nb) ++lg;
+    while (lg > 0) {
+        const int g = 1 << lg, it = (nb + g - 1) / g;
+        if (nb * 100 >= 85 * g * it) break;
+        --lg;
+    }
+    return lg;
+}
+
+template <int KIND, bool FUSED>
+int launch_kind(GemvParams& p, hipStream_t stream) {
+    p.log2g = lanes_per_row_log2(p.nb);
+    const int G = 1 << p.log2g;
+    p.iters = (p.nb + G - 1) / G;
+    const int64_t rows = p.row_end[p.count - 1];
+    const int64_t rows_per_group = 64 / G;
+    p.groups = (rows + rows_per_group - 1) / rows_per_group;
+    // D blocks per lane in flight; the grid gives every wave about D blocks
+    // (one round) while keeping at least ~256 workgroups when there is work.
+    const int64_t wave_blocks = p.groups * p.iters;
+    const int d = wave_blocks >= 2 * kGemvWaves * 256 ? 2 : 1;
+    int64_t wgs = (wave_blocks + static_cast<int64_t>(d) * kGemvWaves - 1) / (static_cast<int64_t>(d) * kGemvWaves);
+    if (wgs > 2048) wgs = 2048;
+    if (wgs < 1) wgs = 1;
+    const int mt = p.m <= 1 ? 1 : p.m <= 2 ? 2 : p.m <= 4 ? 4 : 8;
+    const size_t lds = static_cast<size_t>(mt) * p.nb * (kQK + 32 + 4);
+    const dim3 grid(static_cast<unsigned>(wgs));
+    if (d == 2) launch_d<KIND, FUSED, 2>(p, mt, grid, lds, stream);
+    else launch_d<KIND, FUSED, 1>(p, mt, grid, lds, stream);
     return hipGetLastError() == hipSuccess ? kStatusOk : kStatusExec;
 }
 
 }  // namespace
 
-// m <= 8 rows per launch; LDS holds m * nb * 292 bytes (callers keep it <= 64 KiB).
-int launch_gemv_q8_k(int kind, const uint8_t* w, int64_t n, int nb, const uint8_t* q8k, int64_t ldq,
-                     int m, float* out, int64_t ldo, int32_t* isum, int32_t* msum, hipStream_t stream) {
-    if (kind == 4) return launch_kind<4>(w, n, nb, q8k, ldq, m, out, ldo, isum, msum, stream);
-    if (kind == 6) return launch_kind<6>(w, n, nb, q8k, ldq, m, out, ldo, isum, msum, stream);
+// p.m <= 8 activation rows; LDS holds m * nb * 292 bytes (callers keep it <= 64 KiB).
+int launch_gemv(int kind, bool fused, GemvParams& p, hipStream_t stream) {
+    if (kind == 4) return fused ? launch_kind<4, true>(p, stream) : launch_kind<4, false>(p, stream);
+    if (kind == 6) return fused ? launch_kind<6, true>(p, stream) : launch_kind<6, false>(p, stream);
     return kStatusInvalid;
 }
 

@@ -17,8 +17,7 @@ int launch_quantize_q8_k(const float* x, int64_t m, int64_t k, int64_t ldx, uint
 int launch_gemm_w8a8(const int8_t* a8, int64_t lda, const int8_t* w8, int64_t ldw, const float* as,
                      const float* ws, int m, int n, int k, float* out, int64_t ldo, int32_t* oi,
                      int64_t ldoi, hipStream_t stream);
-int launch_gemv_q8_k(int kind, const uint8_t* w, int64_t n, int nb, const uint8_t* q8k, int64_t ldq,
-                     int m, float* out, int64_t ldo, int32_t* isum, int32_t* msum, hipStream_t stream);
+int launch_gemv(int kind, bool fused, GemvParams& p, hipStream_t stream);
 }  // namespace rk
 
 namespace {
@@ -78,6 +77,14 @@ extern "C" int rocknpu_hip_quantize_q8_k(const float* x, size_t m, size_t k, siz
                                     static_cast<int64_t>(ldx), q8k, static_cast<hipStream_t>(stream));
 }
 
+// rows per launch: a power of two (the kernel's register tile) whose Q8_K
+// blocks fit the 64 KiB of LDS a workgroup stages them in
+size_t gemv_rows_per_launch(size_t nb) {
+    size_t chunk = 8;
+    while (chunk > 1 && chunk * nb * rk::kQ8KBytes > kGemvLdsBytes) chunk >>= 1;
+    return chunk;
+}
+
 extern "C" int rocknpu_hip_gemv_q8_k(uint32_t kind, const uint8_t* w, size_t w_bytes, size_t k, size_t n,
                                      const uint8_t* q8k, size_t m, float* out, size_t ldo, int32_t* isum,
                                      int32_t* msum, void* stream) {
@@ -89,18 +96,62 @@ extern "C" int rocknpu_hip_gemv_q8_k(uint32_t kind, const uint8_t* w, size_t w_b
     if ((isum == nullptr) != (msum == nullptr)) return rk::kStatusInvalid;
     const size_t per_row = nb * rk::kQ8KBytes;
     if (per_row > kGemvLdsBytes) return rk::kStatusInvalid;
-    // rows per launch: a power of two (the kernel's register tile) that fits LDS
-    size_t chunk = 8;
-    while (chunk > 1 && chunk * per_row > kGemvLdsBytes) chunk >>= 1;
+    const size_t chunk = gemv_rows_per_launch(nb);
     const hipStream_t s = static_cast<hipStream_t>(stream);
     for (size_t m0 = 0; m0 < m; m0 += chunk) {
-        const int mm = static_cast<int>(std::min(chunk, m - m0));
-        int32_t* is = isum ? isum + m0 * n * nb : nullptr;
-        int32_t* ms = msum ? msum + m0 * n * nb : nullptr;
-        const int st = rk::launch_gemv_q8_k(static_cast<int>(kind), w, static_cast<int64_t>(n),
-                                            static_cast<int>(nb), q8k + m0 * per_row,
-                                            static_cast<int64_t>(per_row), mm, out + m0 * ldo,
-                                            static_cast<int64_t>(ldo), is, ms, s);
+        rk::GemvParams p{};
+        p.count = 1;
+        p.w[0] = w;
+        p.out[0] = out + m0 * ldo;
+        p.ldo[0] = static_cast<int64_t>(ldo);
+        p.row_end[0] = static_cast<int64_t>(n);
+        p.q8k = q8k + m0 * per_row;
+        p.ldx = static_cast<int64_t>(per_row);
+        p.m = static_cast<int>(std::min(chunk, m - m0));
+        p.nb = static_cast<int>(nb);
+        p.isum = isum ? isum + m0 * n * nb : nullptr;
+        p.msum = msum ? msum + m0 * n * nb : nullptr;
+        const int st = rk::launch_gemv(static_cast<int>(kind), false, p, s);
+        if (st != rk::kStatusOk) return st;
+    }
+    return rk::kStatusOk;
+}
+
+extern "C" int rocknpu_hip_gemv_q_f32(uint32_t kind, size_t count, const uint8_t* const* w, const size_t* w_bytes,
+                                      const size_t* n, size_t k, const float* x, size_t ldx, size_t m,
+                                      float* const* out, const size_t* ldo, void* stream) {
+    if ((kind != 4 && kind != 6) || count < 1 || count > static_cast<size_t>(rk::kGemvMaxMembers) || !w ||
+        !w_bytes || !n || !x || !out || !ldo || k == 0 || k % rk::kQK != 0 || m == 0 || ldx < k)
+        return rk::kStatusInvalid;
+    if (ldx % 4 != 0 || !aligned(x, 16)) return rk::kStatusInvalid;
+    const size_t bb = rk::block_bytes(static_cast<int>(kind)), nb = k / rk::kQK;
+    if (nb * rk::kQ8KBytes > kGemvLdsBytes) return rk::kStatusInvalid;
+    size_t total = 0;
+    for (size_t i = 0; i < count; ++i) {
+        if (!w[i] || !out[i] || n[i] == 0 || ldo[i] < n[i] || w_bytes[i] != n[i] * nb * bb ||
+            !aligned(w[i], kind == 4 ? 16 : 2))
+            return rk::kStatusInvalid;
+        total += n[i];
+    }
+    if (total > INT_MAX) return rk::kStatusInvalid;
+    const size_t chunk = gemv_rows_per_launch(nb);
+    const hipStream_t s = static_cast<hipStream_t>(stream);
+    for (size_t m0 = 0; m0 < m; m0 += chunk) {
+        rk::GemvParams p{};
+        p.count = static_cast<int>(count);
+        int64_t end = 0;
+        for (size_t i = 0; i < count; ++i) {
+            p.w[i] = w[i];
+            p.out[i] = out[i] + m0 * ldo[i];
+            p.ldo[i] = static_cast<int64_t>(ldo[i]);
+            end += static_cast<int64_t>(n[i]);
+            p.row_end[i] = end;
+        }
+        p.x = x + m0 * ldx;
+        p.ldx = static_cast<int64_t>(ldx);
+        p.m = static_cast<int>(std::min(chunk, m - m0));
+        p.nb = static_cast<int>(nb);
+        const int st = rk::launch_gemv(static_cast<int>(kind), true, p, s);
         if (st != rk::kStatusOk) return st;
     }
     return rk::kStatusOk;

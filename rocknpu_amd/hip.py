@@ -98,3 +98,20 @@ def gemv_q8_k(kind: int, w: torch.Tensor, k: int, n: int, q8k: torch.Tensor, out
     _check(_lib.load().rocknpu_hip_gemv_q8_k(kind, _ptr(w), w.numel(), k, n, _ptr(q8k), m, _ptr(out),
                                              out.stride(0), _ptr(isum), _ptr(msum), _stream()), "gemv_q8_k")
     return out
+
+
+def gemv_q_f32(kind: int, weights, k: int, ns, x: torch.Tensor, outs=None):
+    """Kernel (d), fused: f32 activations x [m, k] quantised to Q8_K in-kernel,
+    times 1..4 same-kind projections sharing x. Returns the list of outputs."""
+    m = x.shape[0]
+    count = len(weights)
+    if outs is None:
+        outs = [torch.empty((m, n), dtype=torch.float32, device=x.device) for n in ns]
+    w_arr = (ctypes.c_void_p * count)(*[w.data_ptr() for w in weights])
+    b_arr = (ctypes.c_size_t * count)(*[w.numel() for w in weights])
+    n_arr = (ctypes.c_size_t * count)(*ns)
+    o_arr = (ctypes.c_void_p * count)(*[o.data_ptr() for o in outs])
+    l_arr = (ctypes.c_size_t * count)(*[o.stride(0) for o in outs])
+    _check(_lib.load().rocknpu_hip_gemv_q_f32(kind, count, w_arr, b_arr, n_arr, k, _ptr(x), x.stride(0), m,
+                                              o_arr, l_arr, _stream()), "gemv_q_f32")
+    return outs

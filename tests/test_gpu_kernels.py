@@ -223,3 +223,32 @@ def test_gemv_q8_k(kind, n, k, m):
 def test_gemv_m_chunking():
     """m above one launch's 8 rows is split into launches; results unchanged."""
     _gemv_check(4, 96, 2048, 13, index=500)
+
+
+@pytest.mark.parametrize("kind,ns,k,m", [
+    (4, (2048, 256, 256), 2048, 1), (4, (2048, 256, 256), 2048, 4), (4, (5632, 5632), 2048, 1),
+    (4, (5632, 5632), 2048, 4), (6, (2048,), 5632, 1), (6, (2048,), 5632, 4), (4, (96, 160, 32, 64), 1024, 8),
+    (6, (130, 70), 2048, 3), (4, (40,), 14336, 2), (4, (33,), 256, 11),
+    (6, (300000,), 256, 1),  # grid capped: several prefetch rounds per wave
+])
+def test_gemv_fused_grouped(kind, ns, k, m):
+    """Fused Q8_K quant + grouped GEMV == separate quant + per-member GEMV, bit for bit,
+    and within tolerance of the oracle."""
+    print(f"fused gemv kind={kind} ns={ns} k={k} m={m}", flush=True)
+    ws = [synth.kquant(kind, n, k, index=600 + i + n) for i, n in enumerate(ns)]
+    x = synth.activations(m, k, index=700 + m + k)
+    dx = _dev(x)
+    outs = hip.gemv_q_f32(kind, [_dev(w) for w in ws], k, ns, dx)
+    q8 = hip.quantize_q8_k(dx)
+    torch.cuda.synchronize()
+    q8_ref = orc.quantize_q8_k(x)
+    assert np.array_equal(q8.cpu().numpy(), q8_ref)
+    for w, n, o in zip(ws, ns, outs):
+        sep = hip.gemv_q8_k(kind, _dev(w), k, n, q8)
+        torch.cuda.synchronize()
+        got = o.cpu().numpy()
+        assert np.array_equal(got.view(np.uint32), sep.cpu().numpy().view(np.uint32))
+        ref = orc.gemv_q8_k(kind, w, k, n, q8_ref, threads=8)
+        for mi in range(m):
+            _, _, mag = orc.gemv_block_sums(kind, w, k, n, q8_ref[mi])
+            assert np.all(np.abs(got[mi].astype(np.float64) - ref[mi]) <= 1e-5 * mag)
