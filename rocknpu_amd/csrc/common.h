@@ -80,13 +80,20 @@ __device__ __forceinline__ int wave_or(int v) {
 
 
 // Decode GEMV launch description (kernel (d)): up to four projections that
-// share K and the activation rows, laid out back to back in a virtual row space.
+// share K and the activation rows. Each workgroup serves one projection:
+// workgroups [wg_end[i-1], wg_end[i]) belong to member i.
 constexpr int kGemvMaxMembers = 4;
+// LDS bytes per activation row and super-block: quants with a 272-byte block
+// stride, bsums with a 48-byte stride, one f32 scale.
+constexpr int kGemvLdsQsStride = 272;
+constexpr int kGemvLdsBsStride = 48;
+constexpr int kGemvLdsPerBlock = kGemvLdsQsStride + kGemvLdsBsStride + 4;
 struct GemvParams {
     const uint8_t* w[kGemvMaxMembers];
     float* out[kGemvMaxMembers];
     int64_t ldo[kGemvMaxMembers];
-    int64_t row_end[kGemvMaxMembers];  // cumulative row counts of the members
+    int64_t rows[kGemvMaxMembers];     // rows (output columns) of each member
+    int64_t wg_end[kGemvMaxMembers];   // cumulative workgroup counts
     int count;
     const float* x;      // f32 activations [m, ldx] (quantised in-kernel), or
     const uint8_t* q8k;  // Q8_K rows, ldx bytes apart
@@ -94,8 +101,7 @@ struct GemvParams {
     int m;
     int nb;              // super-blocks per row
     int log2g;           // lanes per row = 1 << log2g
-    int iters;           // units per lane per row group
-    int64_t groups;      // row groups
+    int iters;           // blocks per lane per row group
     int32_t* isum;       // optional exact per-(mi, row, block) sums (count == 1)
     int32_t* msum;
 };

@@ -9,11 +9,10 @@
 // and the row result is sum_b (d_w*d_a) * isum - (dmin_w*d_a) * msum in f32.
 //
 // One launch serves up to four projections that share the activation rows
-// (q/k/v, gate/up): their rows are laid back to back in one virtual row space.
-// The activations are either f32 (quantised to Q8_K by every workgroup into
-// LDS: 16 lanes per 256-value block, DPP reductions) or Q8_K rows copied to
-// LDS. In LDS the quants are chunk-major ([row][16-value chunk][block]) so the
-// lanes reading consecutive blocks read consecutive 16-byte chunks.
+// (q/k/v, gate/up); each workgroup serves one of them, so every per-projection
+// value is wave-uniform. The activations are either f32 (quantised to Q8_K by
+// every workgroup into LDS: 16 lanes per 256-value block, DPP reductions) or
+// Q8_K rows copied to LDS.
 //
 // Work split: one lane owns one whole super-block (144 bytes of Q4_K, 210 of
 // Q6_K), so scales are unpacked once per block and the block's integer sums
@@ -61,46 +60,38 @@ __device__ __forceinline__ int dot4(uint32_t a, uint32_t b, int c) {
     return __builtin_amdgcn_sdot4(static_cast<int>(a), static_cast<int>(b), c, false);
 }
 
-// Global-memory (address space 1) views: addresses rebuilt from integers keep
-// global loads and stores instead of FLAT ones (which also count against the
-// LDS wait counter).
+// Global-memory (address space 1) views keep global loads and stores even for
+// addresses the compiler cannot trace back to a kernel argument.
 typedef const __attribute__((address_space(1))) uint8_t* gbytes;
 typedef __attribute__((address_space(1))) float* gfloats;
 typedef unsigned v4u __attribute__((ext_vector_type(4)));
 
-// Branch-free choice among four 64-bit values (kept as register selects, so
-// the compiler cannot turn it into a table in private memory).
-__device__ __forceinline__ uint64_t select4(int i, uint64_t a, uint64_t b, uint64_t c, uint64_t d) {
-    const uint64_t m1 = 0ull - static_cast<uint64_t>(i == 1);
-    const uint64_t m2 = 0ull - static_cast<uint64_t>(i == 2);
-    const uint64_t m3 = 0ull - static_cast<uint64_t>(i == 3);
-    const uint64_t m0 = ~(m1 | m2 | m3);
-    return (a & m0) | (b & m1) | (c & m2) | (d & m3);
-}
-
-// Activation rows in LDS. Quant p (0..255) of block b of row mi lives at byte
-//   ((mi * 16 + p / 16) * nb + b) * 16 + p % 16
-// bsums 8h..8h+7 of that block at int16 index ((mi * 2 + h) * nb + b) * 8, and
-// its scale at d[mi * nb + b].
+// Activation rows in LDS (regions sized for MT rows):
+//   quants of block b of row mi: 256 bytes at qs + (mi*nb + b) * 272
+//   its bsums:                   16 x int16 at bs + (mi*nb + b) * 48
+//   its scale:                   d[mi*nb + b]
+// The 272- and 48-byte strides put consecutive blocks in different LDS banks,
+// and the 16 chunk reads of a block use immediate offsets.
 struct Q8Lds {
-    int8_t* qs;
-    int16_t* bs;
+    uint8_t* qs;
+    uint8_t* bs;
     float* d;
+    int nb;
+    __device__ __forceinline__ const uint8_t* quants(int mi, int b) const {
+        return qs + (mi * nb + b) * kGemvLdsQsStride;
+    }
+    __device__ __forceinline__ const int16_t* bsums(int mi, int b) const {
+        return reinterpret_cast<const int16_t*>(bs + (mi * nb + b) * kGemvLdsBsStride);
+    }
 };
 
 __device__ __forceinline__ Q8Lds q8_lds(uint8_t* smem, int mt, int nb) {
     Q8Lds a;
-    a.qs = reinterpret_cast<int8_t*>(smem);
-    a.bs = reinterpret_cast<int16_t*>(smem + mt * nb * kQK);
-    a.d = reinterpret_cast<float*>(smem + mt * nb * (kQK + 32));
+    a.qs = smem;
+    a.bs = smem + mt * nb * kGemvLdsQsStride;
+    a.d = reinterpret_cast<float*>(a.bs + mt * nb * kGemvLdsBsStride);
+    a.nb = nb;
     return a;
-}
-
-__device__ __forceinline__ int qs_offset(int mi, int nb, int b, int p) {
-    return ((mi * 16 + (p >> 4)) * nb + b) * 16 + (p & 15);
-}
-__device__ __forceinline__ int bs_index(int mi, int nb, int b, int j) {
-    return ((mi * 2 + (j >> 3)) * nb + b) * 8 + (j & 7);
 }
 
 // The 16 values of this lane for quantisation block qb.
@@ -166,8 +157,9 @@ __device__ __forceinline__ void quantize_to_lds(const float* __restrict__ x, int
             wq[t] = (q[4 * t] & 0xFF) | (q[4 * t + 1] & 0xFF) << 8 | (q[4 * t + 2] & 0xFF) << 16 |
                     static_cast<uint32_t>(q[4 * t + 3] & 0xFF) << 24;
         }
-        *reinterpret_cast<uint4*>(a.qs + qs_offset(r, nb, b, 16 * sub)) = make_uint4(wq[0], wq[1], wq[2], wq[3]);
-        a.bs[bs_index(r, nb, b, sub)] = static_cast<int16_t>(s);
+        uint8_t* qdst = a.qs + (r * nb + b) * kGemvLdsQsStride + 16 * sub;
+        *reinterpret_cast<uint4*>(qdst) = make_uint4(wq[0], wq[1], wq[2], wq[3]);
+        reinterpret_cast<int16_t*>(a.bs + (r * nb + b) * kGemvLdsBsStride)[sub] = static_cast<int16_t>(s);
         if (sub == 0) a.d[r * nb + b] = d;
     }
 }
@@ -181,8 +173,8 @@ __device__ __forceinline__ void stage_q8k(const uint8_t* __restrict__ q8k, int64
         const int mi = blk / nb, bi = blk % nb;
         const uint32_t v = *reinterpret_cast<const uint32_t*>(q8k + mi * ldq + bi * kQ8KBytes + 4 * wi);
         if (wi == 0) a.d[mi * nb + bi] = __uint_as_float(v);
-        else if (wi <= 64) *reinterpret_cast<uint32_t*>(a.qs + qs_offset(mi, nb, bi, 4 * (wi - 1))) = v;
-        else *reinterpret_cast<uint32_t*>(a.bs + bs_index(mi, nb, bi, 2 * (wi - 65))) = v;
+        else if (wi <= 64) reinterpret_cast<uint32_t*>(a.qs + (mi * nb + bi) * kGemvLdsQsStride)[wi - 1] = v;
+        else reinterpret_cast<uint32_t*>(a.bs + (mi * nb + bi) * kGemvLdsBsStride)[wi - 65] = v;
     }
 }
 
@@ -220,12 +212,7 @@ struct Block<6> {
     }
 };
 
-__device__ __forceinline__ v4u lds_chunk(const Q8Lds& a, int mi, int nb, int b, int c) {
-    return *reinterpret_cast<const v4u*>(a.qs + ((mi * 16 + c) * nb + b) * 16);
-}
-
-// Per-block decode shared by all activation rows: Q4_K 6-bit scales/mins;
-// Q6_K signed 6-bit quants (as packed int8 words) and int8 scales.
+// Per-block decode shared by all activation rows.
 template <int KIND>
 struct Decoded;
 
@@ -240,7 +227,7 @@ struct Decoded<4> {
 
 template <>
 struct Decoded<6> {
-    uint32_t q[64];  // value words: q[(p / 4)] holds values p..p+3, minus 32, as int8
+    uint32_t u[64];  // u[p/4]: values p..p+3 as unsigned 6-bit quants (0..63)
     int sc[16];
     __device__ __forceinline__ void decode(const Block<6>& k) {
 #pragma unroll
@@ -252,8 +239,7 @@ struct Decoded<6> {
                     const uint32_t lb = k.w[(64 * half + 32 * (qd & 1) + l) / 4];
                     const uint32_t lo = (qd < 2) ? (lb & 0x0F0F0F0Fu) : ((lb >> 4) & 0x0F0F0F0Fu);
                     const uint32_t hi = (k.w[32 + (32 * half + l) / 4] >> (2 * qd)) & 0x03030303u;
-                    const uint32_t u6 = lo | (hi << 4);  // bytes in [0, 63]
-                    q[(128 * half + 32 * qd + l) / 4] = ((u6 | 0x80808080u) - 0x20202020u) ^ 0x80808080u;
+                    u[(128 * half + 32 * qd + l) / 4] = lo | (hi << 4);
                 }
 #pragma unroll
         for (int si = 0; si < 16; ++si) sc[si] = static_cast<int8_t>((k.w[48 + si / 4] >> (8 * (si % 4))) & 0xFF);
@@ -261,13 +247,14 @@ struct Decoded<6> {
 };
 
 // Exact integer sums of block b against activation row mi.
-__device__ __forceinline__ void block_sums(const Block<4>& k, const Decoded<4>& dc, int mi, int nb, int b,
-                                           const Q8Lds& a, int& isum, int& msum) {
+__device__ __forceinline__ void block_sums(const Block<4>& k, const Decoded<4>& dc, int mi, int b, const Q8Lds& a,
+                                           int& isum, int& msum) {
+    const v4u* q8 = reinterpret_cast<const v4u*>(a.quants(mi, b));
+    const int16_t* bs = a.bsums(mi, b);
     int is = 0, ms = 0;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {  // 64-value group j: sub-blocks 2j (low nibbles), 2j+1 (high)
-        const v4u x0 = lds_chunk(a, mi, nb, b, 4 * j), x1 = lds_chunk(a, mi, nb, b, 4 * j + 1);
-        const v4u x2 = lds_chunk(a, mi, nb, b, 4 * j + 2), x3 = lds_chunk(a, mi, nb, b, 4 * j + 3);
+        const v4u x0 = q8[4 * j], x1 = q8[4 * j + 1], x2 = q8[4 * j + 2], x3 = q8[4 * j + 3];
         const uint32_t lo8[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
         const uint32_t hi8[8] = {x2.x, x2.y, x2.z, x2.w, x3.x, x3.y, x3.z, x3.w};
         int dlo = 0, dhi = 0;
@@ -278,26 +265,33 @@ __device__ __forceinline__ void block_sums(const Block<4>& k, const Decoded<4>& 
             dhi = dot4((q >> 4) & 0x0F0F0F0Fu, hi8[t], dhi);
         }
         is += dc.sc[2 * j] * dlo + dc.sc[2 * j + 1] * dhi;
-        const uint2 bs = *reinterpret_cast<const uint2*>(a.bs + bs_index(mi, nb, b, 4 * j));
-        const int b_lo = static_cast<int16_t>(bs.x & 0xFFFF) + static_cast<int16_t>(bs.x >> 16);
-        const int b_hi = static_cast<int16_t>(bs.y & 0xFFFF) + static_cast<int16_t>(bs.y >> 16);
+        const uint2 pair = *reinterpret_cast<const uint2*>(bs + 4 * j);
+        const int b_lo = static_cast<int16_t>(pair.x & 0xFFFF) + static_cast<int16_t>(pair.x >> 16);
+        const int b_hi = static_cast<int16_t>(pair.y & 0xFFFF) + static_cast<int16_t>(pair.y >> 16);
         ms += dc.mn[2 * j] * b_lo + dc.mn[2 * j + 1] * b_hi;
     }
     isum = is;
     msum = ms;
 }
 
-__device__ __forceinline__ void block_sums(const Block<6>&, const Decoded<6>& dc, int mi, int nb, int b,
-                                           const Q8Lds& a, int& isum, int& msum) {
+// Q6_K: the quants are q - 32 with q = 0..63, and bsums hold the sums of the
+// 16 activation quants of each sub-block, so sum (q-32)*x = sum q*x - 32*bsum.
+__device__ __forceinline__ void block_sums(const Block<6>&, const Decoded<6>& dc, int mi, int b, const Q8Lds& a,
+                                           int& isum, int& msum) {
+    const v4u* q8 = reinterpret_cast<const v4u*>(a.quants(mi, b));
+    const v4u* bsv = reinterpret_cast<const v4u*>(a.bsums(mi, b));
+    const v4u b0 = bsv[0], b1 = bsv[1];
+    const uint32_t bw[8] = {b0.x, b0.y, b0.z, b0.w, b1.x, b1.y, b1.z, b1.w};
     int is = 0;
 #pragma unroll
     for (int si = 0; si < 16; ++si) {  // 16-value sub-block si = chunk si
-        const v4u x = lds_chunk(a, mi, nb, b, si);
-        int dq = dot4(dc.q[4 * si], x.x, 0);
-        dq = dot4(dc.q[4 * si + 1], x.y, dq);
-        dq = dot4(dc.q[4 * si + 2], x.z, dq);
-        dq = dot4(dc.q[4 * si + 3], x.w, dq);
-        is += dc.sc[si] * dq;
+        const v4u x = q8[si];
+        int dq = dot4(dc.u[4 * si], x.x, 0);
+        dq = dot4(dc.u[4 * si + 1], x.y, dq);
+        dq = dot4(dc.u[4 * si + 2], x.z, dq);
+        dq = dot4(dc.u[4 * si + 3], x.w, dq);
+        const int bsum = static_cast<int16_t>((bw[si / 2] >> (16 * (si % 2))) & 0xFFFF);
+        is += dc.sc[si] * (dq - 32 * bsum);
     }
     isum = is;
     msum = 0;
@@ -313,23 +307,20 @@ template <int KIND, int MT, bool FUSED, int D>
 __global__ __launch_bounds__(kGemvWaves * 64) void gemv_kernel(const GemvParams p) {
     constexpr int BB = block_bytes(KIND);
     extern __shared__ __align__(16) uint8_t smem[];
-    const Q8Lds a = q8_lds(smem, MT, p.nb);
-
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    // argument block copied to locals (scalar registers): lanes choose among
-    // them with constant indices, never index the argument block by lane
-    const int count = p.count, iters = p.iters, nb = p.nb, m = p.m, log2g = p.log2g;
-    const int64_t e0 = p.row_end[0], e1 = p.row_end[1], e2 = p.row_end[2];
-    const int64_t total_rows = count == 1 ? e0 : count == 2 ? e1 : count == 3 ? e2 : p.row_end[3];
-    const uint8_t* const w0 = p.w[0];
-    const uint8_t* const w1 = p.w[1];
-    const uint8_t* const w2 = p.w[2];
-    const uint8_t* const w3 = p.w[3];
-    float* const out0 = p.out[0];
-    float* const out1 = p.out[1];
-    float* const out2 = p.out[2];
-    float* const out3 = p.out[3];
-    const int64_t ldo0 = p.ldo[0], ldo1 = p.ldo[1], ldo2 = p.ldo[2], ldo3 = p.ldo[3];
+    const int nb = p.nb, m = p.m, iters = p.iters, log2g = p.log2g;
+    const Q8Lds a = q8_lds(smem, MT, nb);
+
+    // the projection this workgroup serves (wave-uniform)
+    const int64_t wg = blockIdx.x;
+    const uint8_t* w = p.w[0];
+    float* out = p.out[0];
+    int64_t ldo = p.ldo[0], rows = p.rows[0], wg0 = 0, wg1 = p.wg_end[0];
+    if (p.count > 1 && wg >= p.wg_end[0]) { w = p.w[1]; out = p.out[1]; ldo = p.ldo[1]; rows = p.rows[1]; wg0 = p.wg_end[0]; wg1 = p.wg_end[1]; }
+    if (p.count > 2 && wg >= p.wg_end[1]) { w = p.w[2]; out = p.out[2]; ldo = p.ldo[2]; rows = p.rows[2]; wg0 = p.wg_end[1]; wg1 = p.wg_end[2]; }
+    if (p.count > 3 && wg >= p.wg_end[2]) { w = p.w[3]; out = p.out[3]; ldo = p.ldo[3]; rows = p.rows[3]; wg0 = p.wg_end[2]; wg1 = p.wg_end[3]; }
+    const gbytes wg_w = reinterpret_cast<gbytes>(reinterpret_cast<uint64_t>(w));
+    const gfloats wg_out = reinterpret_cast<gfloats>(reinterpret_cast<uint64_t>(out));
     int32_t* const isum_out = p.isum;
     int32_t* const msum_out = p.msum;
 
@@ -338,21 +329,13 @@ __global__ __launch_bounds__(kGemvWaves * 64) void gemv_kernel(const GemvParams 
     const int slot = lane >> log2g;  // row inside the row group
     const int rows_per_group = 64 >> log2g;
     const int64_t row_bytes = static_cast<int64_t>(nb) * BB;
-    const int64_t wave_gid = static_cast<int64_t>(blockIdx.x) * kGemvWaves + wave;
-    const int64_t wave_stride = static_cast<int64_t>(gridDim.x) * kGemvWaves;
+    const int64_t groups = (rows + rows_per_group - 1) / rows_per_group;
+    const int64_t wave_gid = (wg - wg0) * kGemvWaves + wave;
+    const int64_t wave_stride = (wg1 - wg0) * kGemvWaves;
     // this wave's blocks: row groups wave_gid + i*wave_stride, `iters` per lane each
-    const int64_t my_groups = wave_gid < p.groups ? (p.groups - 1 - wave_gid) / wave_stride + 1 : 0;
+    const int64_t my_groups = wave_gid < groups ? (groups - 1 - wave_gid) / wave_stride + 1 : 0;
     const int64_t S = my_groups * iters;
 
-    auto member_of = [=](int64_t row, int64_t& local) {
-        int mbr = 0;
-        int64_t start = 0;
-        if (count > 1 && row >= e0) { mbr = 1; start = e0; }
-        if (count > 2 && row >= e1) { mbr = 2; start = e1; }
-        if (count > 3 && row >= e2) { mbr = 3; start = e2; }
-        local = row - start;
-        return mbr;
-    };
     auto advance = [=](Pos& q) {
         if (++q.it == iters) { q.it = 0; q.gi += wave_stride; }
     };
@@ -360,22 +343,16 @@ __global__ __launch_bounds__(kGemvWaves * 64) void gemv_kernel(const GemvParams 
     // of its wave's first row group (in bounds, cache-resident, private to the
     // wave) and ignores it. Branch-free load sequences let the wait-count pass
     // wait for exactly the loads a value depends on.
-    const int64_t home_row = min(wave_gid * rows_per_group + slot, total_rows - 1);
+    const int64_t home_row = min(wave_gid * rows_per_group + slot, rows - 1);
     const int home_b = min(gl, nb - 1);
     auto load_block = [=](const Pos& q, bool in_range, Block<KIND>& k) {
         int64_t row = q.gi * rows_per_group + slot;
         int b = gl + q.it * G;
-        if (!(in_range && row < total_rows && b < nb)) {
+        if (!(in_range && row < rows && b < nb)) {
             row = home_row;
             b = home_b;
         }
-        int64_t local;
-        const int mbr = member_of(row, local);
-        const gbytes base = reinterpret_cast<gbytes>(select4(mbr, reinterpret_cast<uint64_t>(w0),
-                                                             reinterpret_cast<uint64_t>(w1),
-                                                             reinterpret_cast<uint64_t>(w2),
-                                                             reinterpret_cast<uint64_t>(w3)));
-        k.load(base + local * row_bytes + static_cast<int64_t>(b) * BB);
+        k.load(wg_w + row * row_bytes + static_cast<int64_t>(b) * BB);
     };
 
     // First activation values go out first (they return first), then D blocks.
@@ -406,7 +383,10 @@ __global__ __launch_bounds__(kGemvWaves * 64) void gemv_kernel(const GemvParams 
             if (s >= S) break;  // uniform across the wave
             const int64_t row = cq.gi * rows_per_group + slot;
             const int b = gl + cq.it * G;
-            const bool ok = row < total_rows && b < nb;
+            const bool ok = row < rows && b < nb;
+            // Every lane computes (a lane without a block holds its home block)
+            // and discards the result: straight-line code for all rows mi.
+            const int bk = ok ? b : home_b;
             float dw, dminw = 0.0f;
             if constexpr (KIND == 4) {
                 dw = f16_bits_to_f32(static_cast<uint16_t>(buf[j].w[0] & 0xFFFF));
@@ -414,22 +394,19 @@ __global__ __launch_bounds__(kGemvWaves * 64) void gemv_kernel(const GemvParams 
             } else {
                 dw = f16_bits_to_f32(static_cast<uint16_t>(buf[j].w[52]));
             }
-            // Every lane computes (a lane without a block holds its home block)
-            // and discards the result: straight-line code for all rows mi.
-            const int bs = ok ? b : home_b;
             Decoded<KIND> dc;
             dc.decode(buf[j]);
 #pragma unroll
             for (int mi = 0; mi < MT; ++mi) {
                 if (mi >= m) break;
                 int isum, msum;
-                block_sums(buf[j], dc, mi, nb, bs, a, isum, msum);
-                const float da = a.d[mi * nb + bs];
+                block_sums(buf[j], dc, mi, bk, a, isum, msum);
+                const float da = a.d[mi * nb + bk];
                 float term = (dw * da) * static_cast<float>(isum);
                 if constexpr (KIND == 4) term = term - (dminw * da) * static_cast<float>(msum);
                 acc[mi] += ok ? term : 0.0f;
                 if (isum_out && ok) {
-                    const int64_t idx = (static_cast<int64_t>(mi) * total_rows + row) * nb + b;
+                    const int64_t idx = (static_cast<int64_t>(mi) * rows + row) * nb + b;
                     isum_out[idx] = isum;
                     msum_out[idx] = msum;
                 }
@@ -439,17 +416,10 @@ __global__ __launch_bounds__(kGemvWaves * 64) void gemv_kernel(const GemvParams 
             advance(lq);
             if (cq.it == iters - 1) {
                 // row group done: combine the row's G lanes and store
-                int64_t local;
-                const int mbr = member_of(row, local);
-                const gfloats out = reinterpret_cast<gfloats>(select4(mbr, reinterpret_cast<uint64_t>(out0),
-                                                                      reinterpret_cast<uint64_t>(out1),
-                                                                      reinterpret_cast<uint64_t>(out2),
-                                                                      reinterpret_cast<uint64_t>(out3)));
-                const int64_t ldo = static_cast<int64_t>(select4(mbr, ldo0, ldo1, ldo2, ldo3));
 #pragma unroll
                 for (int mi = 0; mi < MT; ++mi) {
                     const float r = group_sum(acc[mi], G);
-                    if (gl == 0 && row < total_rows && mi < m) out[mi * ldo + local] = r;
+                    if (gl == 0 && row < rows && mi < m) wg_out[mi * ldo + row] = r;
                     acc[mi] = 0.0f;
                 }
             }
@@ -487,18 +457,23 @@ int launch_kind(GemvParams& p, hipStream_t stream) {
     p.log2g = lanes_per_row_log2(p.nb);
     const int G = 1 << p.log2g;
     p.iters = (p.nb + G - 1) / G;
-    const int64_t rows = p.row_end[p.count - 1];
     const int64_t rows_per_group = 64 / G;
-    p.groups = (rows + rows_per_group - 1) / rows_per_group;
-    // D blocks per lane in flight; the grid gives every wave about D blocks
-    // (one round) while keeping at least ~256 workgroups when there is work.
-    const int64_t wave_blocks = p.groups * p.iters;
-    const int d = wave_blocks >= 2 * kGemvWaves * 256 ? 2 : 1;
-    int64_t wgs = (wave_blocks + static_cast<int64_t>(d) * kGemvWaves - 1) / (static_cast<int64_t>(d) * kGemvWaves);
-    if (wgs > 2048) wgs = 2048;
-    if (wgs < 1) wgs = 1;
+    // D blocks per lane in flight; each projection gets about D blocks per
+    // lane (one round) worth of workgroups.
+    int64_t total_wave_blocks = 0;
+    for (int i = 0; i < p.count; ++i) total_wave_blocks += (p.rows[i] + rows_per_group - 1) / rows_per_group * p.iters;
+    const int d = total_wave_blocks >= 2 * kGemvWaves * 256 ? 2 : 1;
+    int64_t wgs = 0;
+    for (int i = 0; i < p.count; ++i) {
+        const int64_t wave_blocks = (p.rows[i] + rows_per_group - 1) / rows_per_group * p.iters;
+        int64_t n = (wave_blocks + static_cast<int64_t>(d) * kGemvWaves - 1) / (static_cast<int64_t>(d) * kGemvWaves);
+        if (n > 2048) n = 2048;
+        if (n < 1) n = 1;
+        wgs += n;
+        p.wg_end[i] = wgs;
+    }
     const int mt = p.m <= 1 ? 1 : p.m <= 2 ? 2 : p.m <= 4 ? 4 : 8;
-    const size_t lds = static_cast<size_t>(mt) * p.nb * (kQK + 32 + 4);
+    const size_t lds = static_cast<size_t>(mt) * p.nb * kGemvLdsPerBlock;
     const dim3 grid(static_cast<unsigned>(wgs));
     if (d == 2) launch_d<KIND, FUSED, 2>(p, mt, grid, lds, stream);
     else launch_d<KIND, FUSED, 1>(p, mt, grid, lds, stream);
@@ -507,7 +482,8 @@ int launch_kind(GemvParams& p, hipStream_t stream) {
 
 }  // namespace
 
-// p.m <= 8 activation rows; LDS holds m * nb * 292 bytes (callers keep it <= 64 KiB).
+// p.m <= 8 activation rows; LDS holds m * nb * kGemvLdsPerBlock bytes (callers
+// keep it <= 64 KiB).
 int launch_gemv(int kind, bool fused, GemvParams& p, hipStream_t stream) {
     if (kind == 4) return fused ? launch_kind<4, true>(p, stream) : launch_kind<4, false>(p, stream);
     if (kind == 6) return fused ? launch_kind<6, true>(p, stream) : launch_kind<6, false>(p, stream);

@@ -81,7 +81,7 @@ extern "C" int rocknpu_hip_quantize_q8_k(const float* x, size_t m, size_t k, siz
 // blocks fit the 64 KiB of LDS a workgroup stages them in
 size_t gemv_rows_per_launch(size_t nb) {
     size_t chunk = 8;
-    while (chunk > 1 && chunk * nb * rk::kQ8KBytes > kGemvLdsBytes) chunk >>= 1;
+    while (chunk > 1 && chunk * nb * rk::kGemvLdsPerBlock > kGemvLdsBytes) chunk >>= 1;
     return chunk;
 }
 
@@ -95,7 +95,7 @@ extern "C" int rocknpu_hip_gemv_q8_k(uint32_t kind, const uint8_t* w, size_t w_b
     if (w_bytes != n * nb * bb || !aligned(w, kind == 4 ? 16 : 2) || !aligned(q8k, 4)) return rk::kStatusInvalid;
     if ((isum == nullptr) != (msum == nullptr)) return rk::kStatusInvalid;
     const size_t per_row = nb * rk::kQ8KBytes;
-    if (per_row > kGemvLdsBytes) return rk::kStatusInvalid;
+    if (nb * rk::kGemvLdsPerBlock > kGemvLdsBytes) return rk::kStatusInvalid;
     const size_t chunk = gemv_rows_per_launch(nb);
     const hipStream_t s = static_cast<hipStream_t>(stream);
     for (size_t m0 = 0; m0 < m; m0 += chunk) {
@@ -104,7 +104,7 @@ extern "C" int rocknpu_hip_gemv_q8_k(uint32_t kind, const uint8_t* w, size_t w_b
         p.w[0] = w;
         p.out[0] = out + m0 * ldo;
         p.ldo[0] = static_cast<int64_t>(ldo);
-        p.row_end[0] = static_cast<int64_t>(n);
+        p.rows[0] = static_cast<int64_t>(n);
         p.q8k = q8k + m0 * per_row;
         p.ldx = static_cast<int64_t>(per_row);
         p.m = static_cast<int>(std::min(chunk, m - m0));
@@ -125,7 +125,7 @@ extern "C" int rocknpu_hip_gemv_q_f32(uint32_t kind, size_t count, const uint8_t
         return rk::kStatusInvalid;
     if (ldx % 4 != 0 || !aligned(x, 16)) return rk::kStatusInvalid;
     const size_t bb = rk::block_bytes(static_cast<int>(kind)), nb = k / rk::kQK;
-    if (nb * rk::kQ8KBytes > kGemvLdsBytes) return rk::kStatusInvalid;
+    if (nb * rk::kGemvLdsPerBlock > kGemvLdsBytes) return rk::kStatusInvalid;
     size_t total = 0;
     for (size_t i = 0; i < count; ++i) {
         if (!w[i] || !out[i] || n[i] == 0 || ldo[i] < n[i] || w_bytes[i] != n[i] * nb * bb ||
@@ -139,13 +139,11 @@ extern "C" int rocknpu_hip_gemv_q_f32(uint32_t kind, size_t count, const uint8_t
     for (size_t m0 = 0; m0 < m; m0 += chunk) {
         rk::GemvParams p{};
         p.count = static_cast<int>(count);
-        int64_t end = 0;
         for (size_t i = 0; i < count; ++i) {
             p.w[i] = w[i];
             p.out[i] = out[i] + m0 * ldo[i];
             p.ldo[i] = static_cast<int64_t>(ldo[i]);
-            end += static_cast<int64_t>(n[i]);
-            p.row_end[i] = end;
+            p.rows[i] = static_cast<int64_t>(n[i]);
         }
         p.x = x + m0 * ldx;
         p.ldx = static_cast<int64_t>(ldx);

@@ -1,0 +1,205 @@
+"""GPU tests of the reference C ABI (include/rocknpu.h) through host buffers,
+mirroring how the ggml adapter calls it: every matmul entry point against
+the oracle, grouping == separate calls, cache release/prewarm/stats, the
+overlap callback, and the reference's error codes."""
+import numpy as np
+import pytest
+
+from oracle import oracle as orc
+from rocknpu_amd import synth
+from rocknpu_amd.capi import STATUS_INVALID_ARGUMENT, STATUS_OK, Context
+
+pytestmark = pytest.mark.gpu
+
+
+def _bits(x):
+    return np.ascontiguousarray(x, np.float32).view(np.uint32)
+
+
+@pytest.fixture(scope="module")
+def ctx():
+    c = Context()
+    yield c
+    c.close()
+
+
+def _w8a8_ref(kind, blocks, a, n):
+    return orc.matmul_q_w8a8(kind, blocks, a, n, threads=8)
+
+
+@pytest.mark.parametrize("kind,m,k,n", [(4, 128, 2048, 5632), (4, 1, 2048, 256), (4, 7, 512, 96), (6, 16, 5632, 2048),
+                                        (6, 1, 2048, 128), (5, 12, 1024, 64), (4, 300, 768, 200), (6, 4, 256, 33)])
+def test_matmul_q_matches_oracle(ctx, kind, m, k, n):
+    blocks = synth.kquant(kind, n, k, index=800 + kind + m + n)
+    a = synth.activations(m, k, index=900 + m)
+    out = np.empty((m, n), np.float32)
+    assert ctx.matmul_q(kind, blocks, a, out, k, n) == STATUS_OK
+    assert np.array_equal(_bits(out), _bits(_w8a8_ref(kind, blocks, a, n)))
+    # second call hits the resident cache and gives the same bits
+    out2 = np.empty_like(out)
+    assert ctx.matmul_q(kind, blocks, a, out2, k, n) == STATUS_OK
+    assert np.array_equal(_bits(out2), _bits(out))
+
+
+def test_matmul_q_error_codes(ctx):
+    k, n = 512, 32
+    blocks = synth.q4_k(n, k, index=1)
+    a = synth.activations(4, k, index=2)
+    out = np.empty((4, n), np.float32)
+    assert ctx.matmul_q(4, blocks[:-1], a, out, k, n) == STATUS_INVALID_ARGUMENT      # byte count
+    assert ctx.matmul_q(4, blocks, a[:, :300].copy(), out, 300, n) == STATUS_INVALID_ARGUMENT  # k % 256
+    bad = a.copy()
+    bad[2, 17] = np.nan
+    sentinel = np.full((4, n), 7.0, np.float32)
+    assert ctx.matmul_q(4, blocks, bad, sentinel, k, n) == STATUS_INVALID_ARGUMENT   # non-finite row
+    assert np.all(sentinel == 7.0)                                                     # output untouched
+    bad[2, 17] = np.inf
+    assert ctx.matmul_q(4, blocks, bad, out, k, n) == STATUS_INVALID_ARGUMENT
+    assert ctx.matmul_q(5, synth.q5_k(n, k, index=3), a[:1].copy(), out[:1], k, n) == STATUS_INVALID_ARGUMENT  # Q5_K M=1
+    # a weight whose dequantised row is non-finite is rejected, not cached
+    wb = synth.q4_k(n, k, index=4).reshape(n, -1, 144).copy()
+    wb[5, 0, 0:2] = [0x00, 0x7C]
+    assert ctx.matmul_q(4, wb.reshape(-1), a, out, k, n) == STATUS_INVALID_ARGUMENT
+
+
+def test_zero_activation_row_gives_zero_output(ctx):
+    k, n = 512, 64
+    blocks = synth.q6_k(n, k, index=5)
+    a = synth.activations(3, k, index=6)
+    a[1] = 0.0
+    out = np.empty((3, n), np.float32)
+    assert ctx.matmul_q(6, blocks, a, out, k, n) == STATUS_OK
+    assert not out[1].any()
+    assert np.array_equal(_bits(out), _bits(_w8a8_ref(6, blocks, a, n)))
+
+
+def test_concat_pair_equal_separate_calls(ctx):
+    m, k = 128, 2048
+    ns = (2048, 256, 256)
+    ws = [synth.q4_k(n, k, index=1000 + i) for i, n in enumerate(ns)]
+    a = synth.activations(m, k, index=1100)
+    outs = [np.empty((m, n), np.float32) for n in ns]
+    assert ctx.matmul_q_concat(ws, [4, 4, 4], ns, a, outs, k) == STATUS_OK
+    for w, n, o in zip(ws, ns, outs):
+        assert np.array_equal(_bits(o), _bits(_w8a8_ref(4, w, a, n)))
+    o1, o2 = np.empty((m, ns[1]), np.float32), np.empty((m, ns[2]), np.float32)
+    assert ctx.matmul_q_pair_mtile(ws[1], 4, ns[1], ws[2], 4, ns[2], a, o1, o2, k) == STATUS_OK
+    assert np.array_equal(_bits(o1), _bits(outs[1])) and np.array_equal(_bits(o2), _bits(outs[2]))
+    # mixed kinds in a group
+    w6 = synth.q6_k(96, k, index=1200)
+    oa, ob = np.empty((m, 256), np.float32), np.empty((m, 96), np.float32)
+    assert ctx.matmul_q_concat([ws[1], w6], [4, 6], [256, 96], a, [oa, ob], k) == STATUS_OK
+    assert np.array_equal(_bits(ob), _bits(_w8a8_ref(6, w6, a, 96)))
+    assert ctx.matmul_q_concat([ws[1]] * 5, [4] * 5, [256] * 5, a, [oa] * 5, k) == STATUS_INVALID_ARGUMENT
+
+
+def test_m1_groups_and_w8a8_entries(ctx):
+    k = 2048
+    ns = (512, 128, 64)
+    ws = [synth.q4_k(n, k, index=1300 + i) for i, n in enumerate(ns)]
+    x = synth.activations(1, k, index=1400)
+    refs = [_w8a8_ref(4, w, x, n)[0] for w, n in zip(ws, ns)]
+    outs = [np.empty(n, np.float32) for n in ns]
+    assert ctx.matmul_q_triple_m1(ws[0], 4, ns[0], ws[1], 4, ns[1], ws[2], 4, ns[2], x[0], *outs, k) == STATUS_OK
+    for o, r in zip(outs, refs):
+        assert np.array_equal(_bits(o), _bits(r))
+    o1, o2 = np.empty(ns[0], np.float32), np.empty(ns[1], np.float32)
+    assert ctx.matmul_q_pair_m1(ws[0], 4, ns[0], ws[1], 4, ns[1], x[0], o1, o2, k) == STATUS_OK
+    assert np.array_equal(_bits(o1), _bits(refs[0])) and np.array_equal(_bits(o2), _bits(refs[1]))
+    # caller-quantised W8 entries
+    w8s = [orc.repack_w8(4, w, k, n) for w, n in zip(ws, ns)]
+    o = np.empty(ns[0], np.float32)
+    assert ctx.matmul_w8a8_m1(w8s[0][0], w8s[0][1], x[0], o, k, ns[0]) == STATUS_OK
+    assert np.array_equal(_bits(o), _bits(refs[0]))
+    o = np.empty(ns[0], np.float32)
+    assert ctx.matmul_w8a8_m1_nsplit(w8s[0][0], w8s[0][1], x[0], o, k, ns[0], 96) == STATUS_OK
+    assert np.array_equal(_bits(o), _bits(refs[0]))
+    p1, p2 = np.empty(ns[0], np.float32), np.empty(ns[1], np.float32)
+    assert ctx.matmul_w8a8_pair_m1(w8s[0][0], w8s[0][1], ns[0], w8s[1][0], w8s[1][1], ns[1], x[0], p1, p2,
+                                   k) == STATUS_OK
+    assert np.array_equal(_bits(p1), _bits(refs[0])) and np.array_equal(_bits(p2), _bits(refs[1]))
+    t = [np.empty(n, np.float32) for n in ns]
+    assert ctx.matmul_w8a8_triple_m1(w8s[0][0], w8s[0][1], ns[0], w8s[1][0], w8s[1][1], ns[1], w8s[2][0],
+                                     w8s[2][1], ns[2], x[0], *t, k) == STATUS_OK
+    for o, r in zip(t, refs):
+        assert np.array_equal(_bits(o), _bits(r))
+    a16 = synth.activations(16, k, index=1500)
+    o16 = np.empty((16, ns[1]), np.float32)
+    assert ctx.matmul_w8a8_m16(w8s[1][0], w8s[1][1], a16, o16, k, ns[1]) == STATUS_OK
+    assert np.array_equal(_bits(o16), _bits(_w8a8_ref(4, ws[1], a16, ns[1])))
+    bad_scales = w8s[1][1].copy()
+    bad_scales[3] = 0.0
+    assert ctx.matmul_w8a8_m1(w8s[1][0], bad_scales, x[0], np.empty(ns[1], np.float32), k,
+                              ns[1]) == STATUS_INVALID_ARGUMENT
+
+
+def test_swiglu_down(ctx):
+    k, ffn, out_n = 512, 256, 128
+    gw, uw = synth.q4_k(ffn, k, index=1600), synth.q4_k(ffn, k, index=1601)
+    dw = synth.q4_k(out_n, ffn, index=1602)
+    (g8, gs), (u8, us), (d8, ds) = (orc.repack_w8(4, gw, k, ffn), orc.repack_w8(4, uw, k, ffn),
+                                    orc.repack_w8(4, dw, ffn, out_n))
+    x = synth.activations(1, k, index=1603)
+    out = np.empty(out_n, np.float32)
+    assert ctx.matmul_w8a8_swiglu_down(g8, gs, u8, us, d8, ds, x[0], out, k, ffn, out_n) == STATUS_OK
+    gate = _w8a8_ref(4, gw, x, ffn)[0]
+    up = _w8a8_ref(4, uw, x, ffn)[0]
+    sig = (np.float32(1.0) / (np.float32(1.0) + np.exp(-gate))).astype(np.float32)
+    h = (gate * sig * up).astype(np.float32)
+    ref = _w8a8_ref(4, dw, h[None, :], out_n)[0]
+    # SwiGLU's exp is the platform libm on both sides; allow its last-ulp freedom
+    np.testing.assert_allclose(out, ref, rtol=1e-3, atol=1e-3 * np.abs(ref).max())
+
+
+def test_cache_stats_release_prewarm_overlap(ctx):
+    k, n = 1024, 128
+    w = synth.q4_k(n, k, index=1700)
+    x = synth.activations(1, k, index=1701)
+    before = ctx.decode_cache_stats()
+    out = np.empty(n, np.float32)
+    ran = []
+    assert ctx.set_overlap(lambda: ran.append(1)) == STATUS_OK
+    assert ctx.matmul_q(4, w, x, out, k, n) == STATUS_OK
+    assert ran == [1]                                  # one-shot, run during the M=1 call
+    assert ctx.matmul_q(4, w, x, out, k, n) == STATUS_OK
+    assert ran == [1]
+    after = ctx.decode_cache_stats()
+    assert after.misses == before.misses + 1 and after.hits == before.hits + 1
+    assert after.entries >= before.entries + 1 and after.resident_bytes > before.resident_bytes
+    # prewarm fills the prompt cache; release drops it without touching decode caches
+    assert ctx.prewarm_quantized_m16(w, 4, k, n) == STATUS_OK
+    assert ctx.mtile_release([w]) == STATUS_OK
+    assert ctx.decode_cache_stats().entries == after.entries
+    a = synth.activations(4, k, index=1702)
+    o4 = np.empty((4, n), np.float32)
+    assert ctx.matmul_q(4, w, a, o4, k, n) == STATUS_OK
+    assert np.array_equal(_bits(o4), _bits(_w8a8_ref(4, w, a, n)))
+    assert ctx.mtile_release([]) == STATUS_INVALID_ARGUMENT
+
+
+def test_decode_q8k_entry(ctx):
+    for kind, k, n, m in ((4, 2048, 256, 1), (6, 5632, 128, 4), (4, 2048, 5632, 2)):
+        w = synth.kquant(kind, n, k, index=1800 + kind + m)
+        x = synth.activations(m, k, index=1900 + m)
+        out = np.empty((m, n), np.float32)
+        assert ctx.matmul_q_q8k(kind, w, x, out, k, n) == STATUS_OK
+        q8 = orc.quantize_q8_k(x)
+        ref = orc.gemv_q8_k(kind, w, k, n, q8, threads=8)
+        for mi in range(m):
+            _, _, mag = orc.gemv_block_sums(kind, w, k, n, q8[mi])
+            assert np.all(np.abs(out[mi].astype(np.float64) - ref[mi]) <= 1e-5 * mag)
+    bad = synth.activations(1, 256, index=1)
+    bad[0, 3] = np.inf
+    assert ctx.matmul_q_q8k(4, synth.q4_k(8, 256, index=2), bad, np.empty((1, 8), np.float32), 256,
+                            8) == STATUS_INVALID_ARGUMENT
+
+
+def test_f16_bridge(ctx):
+    m, k, n = 5, 96, 40
+    g = np.random.default_rng(3)
+    w = (g.standard_normal((n, k)) * 0.1).astype(np.float16)
+    a = g.standard_normal((m, k)).astype(np.float32)
+    out = np.empty((m, n), np.float32)
+    assert ctx.matmul_f16(w.view(np.uint16), a, out, k, n) == STATUS_OK
+    ref = a.astype(np.float16).astype(np.float64) @ w.astype(np.float64).T
+    np.testing.assert_allclose(out, ref, rtol=1e-4, atol=1e-4)
