@@ -100,8 +100,8 @@ struct GemvParams {
     int64_t ldx;
     int m;
     int nb;              // super-blocks per row
-    int log2g;           // lanes per row = 1 << log2g
-    int iters;           // blocks per lane per row group
+    int log2g;           // block slots per row = 1 << log2g
+    int iters;           // blocks per slot per row group
     int32_t* isum;       // optional exact per-(mi, row, block) sums (count == 1)
     int32_t* msum;
 };

@@ -12,27 +12,38 @@
 // (q/k/v, gate/up); each workgroup serves one of them, so every per-projection
 // value is wave-uniform. The activations are either f32 (quantised to Q8_K by
 // every workgroup into LDS: 16 lanes per 256-value block, DPP reductions) or
-// Q8_K rows copied to LDS.
+// Q8_K rows copied to LDS. Workgroups hold 16 waves and there is at most one
+// per CU, so that quantisation is repeated at most once per CU.
 //
-// Work split: one lane owns one whole super-block (144 bytes of Q4_K, 210 of
-// Q6_K), so scales are unpacked once per block and the block's integer sums
-// never leave the lane. G lanes (G <= 16) share a weight row, a wave covers
-// 64/G rows at once, and a row group takes `iters` blocks per lane. Waves walk
-// their row groups grid-stride with D blocks of loads in flight per lane; the
-// row's G partial sums are combined with DPP lane moves.
+// Work split: L lanes (1, 2, 4 or 8) share a super-block; lane p of the L
+// takes 16-byte "units" [8p/L, 8(p+1)/L) of the block's 128 quant bytes (plus
+// the scale bytes every lane of the block reads). A wave therefore holds 64/L
+// block slots; G slots share a weight row, and a row group of 64/(L*G) rows
+// takes `iters` = ceil(nb/G) blocks per slot. Waves walk their row groups
+// grid-stride with D blocks of loads in flight per lane. A block's integer
+// sums are added over its L lanes with DPP moves before the f32 scaling, so
+// every block contributes one f32 term; a row's G slot sums are added when the
+// row group ends. Small launches use large L (short per-lane work, many lanes
+// busy); large launches use L = 1, which spends the fewest instructions per
+// block.
 #include "common.h"
+
+#include <algorithm>
 
 namespace rk {
 namespace {
 
-constexpr int kGemvWaves = 4;
+// Waves per workgroup: 16, or 8 where 8 waves per CU cover the launch and one
+// 8-wave pass quantises the activations.
+constexpr int kGemvMaxWaves = 16;
 
 template <int CTRL>
 __device__ __forceinline__ int dpp(int v) {
     return __builtin_amdgcn_mov_dpp(v, CTRL, 0xF, 0xF, false);
 }
 // DPP controls: quad_perm [1,0,3,2] and [2,3,0,1], row_half_mirror, row_mirror.
-// Applied in this order they combine aligned groups of 2, 4, 8 and 16 lanes.
+// Applied in this order to a value that is uniform over the lower lane-index
+// bits, they exchange across lane-index bits 0, 1, 2 and 3.
 constexpr int kDppXor1 = 0xB1, kDppXor2 = 0x4E, kDppMirror8 = 0x141, kDppMirror16 = 0x140;
 
 __device__ __forceinline__ float max16(float v) {
@@ -47,12 +58,22 @@ __device__ __forceinline__ int min16(int v) {
     v = min(v, dpp<kDppMirror8>(v));
     return min(v, dpp<kDppMirror16>(v));
 }
-// Sum over aligned groups of G lanes (G a power of two, at most 16).
-__device__ __forceinline__ float group_sum(float v, int G) {
-    if (G >= 2) v += __int_as_float(dpp<kDppXor1>(__float_as_int(v)));
-    if (G >= 4) v += __int_as_float(dpp<kDppXor2>(__float_as_int(v)));
-    if (G >= 8) v += __int_as_float(dpp<kDppMirror8>(__float_as_int(v)));
-    if (G >= 16) v += __int_as_float(dpp<kDppMirror16>(__float_as_int(v)));
+// Integer sum over aligned groups of L lanes (L <= 8), in every lane of the group.
+template <int L>
+__device__ __forceinline__ int sum_lanes(int v) {
+    if constexpr (L >= 2) v += dpp<kDppXor1>(v);
+    if constexpr (L >= 4) v += dpp<kDppXor2>(v);
+    if constexpr (L >= 8) v += dpp<kDppMirror8>(v);
+    return v;
+}
+// Sum over lane-index bits [lo, hi) of a value uniform over bits below lo.
+__device__ __forceinline__ float sum_bits(float v, int lo, int hi) {
+    if (lo <= 0 && hi > 0) v += __int_as_float(dpp<kDppXor1>(__float_as_int(v)));
+    if (lo <= 1 && hi > 1) v += __int_as_float(dpp<kDppXor2>(__float_as_int(v)));
+    if (lo <= 2 && hi > 2) v += __int_as_float(dpp<kDppMirror8>(__float_as_int(v)));
+    if (lo <= 3 && hi > 3) v += __int_as_float(dpp<kDppMirror16>(__float_as_int(v)));
+    if (lo <= 4 && hi > 4) v += __shfl_xor(v, 16);
+    if (lo <= 5 && hi > 5) v += __shfl_xor(v, 32);
     return v;
 }
 
@@ -65,23 +86,22 @@ __device__ __forceinline__ int dot4(uint32_t a, uint32_t b, int c) {
 typedef const __attribute__((address_space(1))) uint8_t* gbytes;
 typedef __attribute__((address_space(1))) float* gfloats;
 typedef unsigned v4u __attribute__((ext_vector_type(4)));
+typedef v4u v4u_a2 __attribute__((aligned(2)));
+typedef const __attribute__((address_space(1))) v4u* gv4u;
+typedef const __attribute__((address_space(1))) v4u_a2* gv4u_a2;
 
-// Activation rows in LDS (regions sized for MT rows):
-//   quants of block b of row mi: 256 bytes at qs + (mi*nb + b) * 272
-//   its bsums:                   16 x int16 at bs + (mi*nb + b) * 48
-//   its scale:                   d[mi*nb + b]
-// The 272- and 48-byte strides put consecutive blocks in different LDS banks,
-// and the 16 chunk reads of a block use immediate offsets.
+// Activation rows in LDS (regions sized for MT rows; blk = mi*nb + b):
+//   quants of block blk: 256 bytes at qs + blk * 272
+//   its bsums:           16 x int16 at bs + blk * 48
+//   its scale:           d[blk]
+// The 272- and 48-byte strides put consecutive blocks in different LDS banks.
 struct Q8Lds {
     uint8_t* qs;
     uint8_t* bs;
     float* d;
-    int nb;
-    __device__ __forceinline__ const uint8_t* quants(int mi, int b) const {
-        return qs + (mi * nb + b) * kGemvLdsQsStride;
-    }
-    __device__ __forceinline__ const int16_t* bsums(int mi, int b) const {
-        return reinterpret_cast<const int16_t*>(bs + (mi * nb + b) * kGemvLdsBsStride);
+    __device__ __forceinline__ const uint8_t* quants(int blk) const { return qs + blk * kGemvLdsQsStride; }
+    __device__ __forceinline__ const int16_t* bsums(int blk) const {
+        return reinterpret_cast<const int16_t*>(bs + blk * kGemvLdsBsStride);
     }
 };
 
@@ -90,7 +110,6 @@ __device__ __forceinline__ Q8Lds q8_lds(uint8_t* smem, int mt, int nb) {
     a.qs = smem;
     a.bs = smem + mt * nb * kGemvLdsQsStride;
     a.d = reinterpret_cast<float*>(a.bs + mt * nb * kGemvLdsBsStride);
-    a.nb = nb;
     return a;
 }
 
@@ -104,16 +123,15 @@ __device__ __forceinline__ void load_x16(const float* __restrict__ x, int64_t ld
 }
 
 // Q8_K quantisation of rows [0, m) of x into LDS (ggml quantize_row_q8_K_ref
-// semantics, see quant.hip): 16 lanes per block, 16 values per lane. `first`
-// holds this lane's values of its first block, loaded by the caller ahead of
-// the weight loads so they return first.
+// semantics, see quant.hip): 16 lanes per block, 16 values per lane, run by
+// the first waves of the workgroup. `first` holds this lane's values of its
+// first block.
+template <int THREADS>
 __device__ __forceinline__ void quantize_to_lds(const float* __restrict__ x, int64_t ldx, int m, int nb,
                                                 const float4 (&first)[4], const Q8Lds& a) {
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int sub = lane & 15;
-    const int slot = wave * 4 + (lane >> 4);
-    for (int qb = slot; qb < m * nb; qb += kGemvWaves * 4) {
-        const int r = qb / nb, b = qb % nb;
+    const int sub = threadIdx.x & 15;
+    const int slot = threadIdx.x >> 4;
+    for (int qb = slot; qb < m * nb; qb += THREADS / 16) {
         float4 f[4];
         if (qb == slot) {
 #pragma unroll
@@ -157,157 +175,213 @@ __device__ __forceinline__ void quantize_to_lds(const float* __restrict__ x, int
             wq[t] = (q[4 * t] & 0xFF) | (q[4 * t + 1] & 0xFF) << 8 | (q[4 * t + 2] & 0xFF) << 16 |
                     static_cast<uint32_t>(q[4 * t + 3] & 0xFF) << 24;
         }
-        uint8_t* qdst = a.qs + (r * nb + b) * kGemvLdsQsStride + 16 * sub;
-        *reinterpret_cast<uint4*>(qdst) = make_uint4(wq[0], wq[1], wq[2], wq[3]);
-        reinterpret_cast<int16_t*>(a.bs + (r * nb + b) * kGemvLdsBsStride)[sub] = static_cast<int16_t>(s);
-        if (sub == 0) a.d[r * nb + b] = d;
+        *reinterpret_cast<uint4*>(a.qs + qb * kGemvLdsQsStride + 16 * sub) = make_uint4(wq[0], wq[1], wq[2], wq[3]);
+        reinterpret_cast<int16_t*>(a.bs + qb * kGemvLdsBsStride)[sub] = static_cast<int16_t>(s);
+        if (sub == 0) a.d[qb] = d;
     }
 }
 
-// Copy Q8_K rows (292-byte blocks) into the LDS layout.
+// Copy Q8_K rows (292-byte blocks: f32 d, 256 quants, 16 int16 bsums) into
+// the LDS layout, one 32-bit word per thread and step.
+template <int THREADS>
 __device__ __forceinline__ void stage_q8k(const uint8_t* __restrict__ q8k, int64_t ldq, int m, int nb,
                                           const Q8Lds& a) {
     const int words = m * nb * (kQ8KBytes / 4);
-    for (int i = threadIdx.x; i < words; i += blockDim.x) {
+    for (int i = threadIdx.x; i < words; i += THREADS) {
         const int blk = i / (kQ8KBytes / 4), wi = i % (kQ8KBytes / 4);
         const int mi = blk / nb, bi = blk % nb;
         const uint32_t v = *reinterpret_cast<const uint32_t*>(q8k + mi * ldq + bi * kQ8KBytes + 4 * wi);
-        if (wi == 0) a.d[mi * nb + bi] = __uint_as_float(v);
-        else if (wi <= 64) reinterpret_cast<uint32_t*>(a.qs + (mi * nb + bi) * kGemvLdsQsStride)[wi - 1] = v;
-        else reinterpret_cast<uint32_t*>(a.bs + (mi * nb + bi) * kGemvLdsBsStride)[wi - 65] = v;
+        if (wi == 0) a.d[blk] = __uint_as_float(v);
+        else if (wi <= 64) reinterpret_cast<uint32_t*>(a.qs + blk * kGemvLdsQsStride)[wi - 1] = v;
+        else reinterpret_cast<uint32_t*>(a.bs + blk * kGemvLdsBsStride)[wi - 65] = v;
     }
 }
 
-// One super-block's raw bytes as 32-bit words.
-template <int KIND>
-struct Block;
+// The bytes lane p of a block's L lanes loads.
+template <int KIND, int L>
+struct Piece;
 
-template <>
-struct Block<4> {
-    uint32_t w[36];  // [0] d|dmin, [1..3] packed scales, [4..35] qs
-    __device__ __forceinline__ void load(gbytes blk) {
-        typedef const __attribute__((address_space(1))) v4u* gu4;
+// Q4_K (144 bytes): d|dmin, 12 packed scale bytes, 128 quant bytes. Unit u
+// (16 quant bytes 32j + 16h ..) holds values 64j + 16h + t (low nibbles,
+// sub-block 2j) and 64j + 32 + 16h + t (high nibbles, sub-block 2j + 1).
+template <int L>
+struct Piece<4, L> {
+    static constexpr int NU = 8 / L;
+    v4u h;
+    v4u q[NU];
+    __device__ __forceinline__ void load(gbytes blk, int p) {
+        h = reinterpret_cast<gv4u>(blk)[0];
 #pragma unroll
-        for (int t = 0; t < 9; ++t) {
-            const v4u x = reinterpret_cast<gu4>(blk)[t];
-            w[4 * t] = x.x; w[4 * t + 1] = x.y; w[4 * t + 2] = x.z; w[4 * t + 3] = x.w;
-        }
+        for (int u = 0; u < NU; ++u) q[u] = reinterpret_cast<gv4u>(blk)[1 + NU * p + u];
     }
 };
 
-template <>
-struct Block<6> {
-    uint32_t w[53];  // [0..31] ql, [32..47] qh, [48..51] scales, [52] d (low 16 bits)
-    // Q6_K blocks are only 2-byte aligned; the hardware takes unaligned vector
-    // loads, so the first 208 bytes come in as 13 16-byte loads.
-    __device__ __forceinline__ void load(gbytes blk) {
-        typedef v4u v4u_a2 __attribute__((aligned(2)));
-        typedef const __attribute__((address_space(1))) v4u_a2* gu4;
+// Q6_K (210 bytes, so only 2-byte aligned; the hardware takes unaligned
+// loads): ql[128], qh[64], 16 int8 scales, f16 d. Unit u (16 ql bytes at 16u,
+// half h = u/4, quarter a = u/2 % 2, c = u % 2) with qh bytes 32h + 16c .. holds
+// values 128h + 32a + 16c + t (low nibbles) and that + 64 (high nibbles), of
+// sub-blocks 8h + 2a + c and 8h + 2a + c + 4. The scale comes with a 32-bit
+// load of bytes 206..209, so that no extension of a 16-bit load result sits
+// between the loads and their use.
+template <int L>
+struct Piece<6, L> {
+    static constexpr int NU = 8 / L;
+    static constexpr int NH = L == 1 ? 4 : (L == 8 ? 1 : 2);  // qh pieces of the lane's units
+    v4u ql[NU];
+    v4u qh[NH];
+    v4u sc;
+    uint32_t d;
+    // first qh piece (index 2h + c) of lane p
+    __device__ __forceinline__ static int qh_first(int p) {
+        if constexpr (L == 1) return 0;
+        else if constexpr (L == 2) return 2 * p;
+        else if constexpr (L == 4) return 2 * (p >> 1);
+        else return 2 * (p >> 2) + (p & 1);
+    }
+    __device__ __forceinline__ void load(gbytes blk, int p) {
+        typedef uint32_t u32_a2 __attribute__((aligned(2)));
 #pragma unroll
-        for (int t = 0; t < 13; ++t) {
-            const v4u x = reinterpret_cast<gu4>(blk)[t];
-            w[4 * t] = x.x; w[4 * t + 1] = x.y; w[4 * t + 2] = x.z; w[4 * t + 3] = x.w;
-        }
-        w[52] = *reinterpret_cast<const __attribute__((address_space(1))) uint16_t*>(blk + 208);
+        for (int u = 0; u < NU; ++u) ql[u] = reinterpret_cast<gv4u_a2>(blk)[NU * p + u];
+#pragma unroll
+        for (int i = 0; i < NH; ++i) qh[i] = reinterpret_cast<gv4u_a2>(blk + 128)[qh_first(p) + i];
+        sc = reinterpret_cast<gv4u_a2>(blk + 192)[0];
+        d = *reinterpret_cast<const __attribute__((address_space(1))) u32_a2*>(blk + 206);
     }
 };
 
-// Per-block decode shared by all activation rows.
-template <int KIND>
-struct Decoded;
-
-template <>
-struct Decoded<4> {
-    int sc[8], mn[8];
-    __device__ __forceinline__ void decode(const Block<4>& k) {
-#pragma unroll
-        for (int j = 0; j < 8; ++j) scale_min_k4(j, k.w[1], k.w[2], k.w[3], sc[j], mn[j]);
-    }
-};
-
-template <>
-struct Decoded<6> {
-    uint32_t u[64];  // u[p/4]: values p..p+3 as unsigned 6-bit quants (0..63)
-    int sc[16];
-    __device__ __forceinline__ void decode(const Block<6>& k) {
-#pragma unroll
-        for (int half = 0; half < 2; ++half)
-#pragma unroll
-            for (int qd = 0; qd < 4; ++qd)
-#pragma unroll
-                for (int l = 0; l < 32; l += 4) {
-                    const uint32_t lb = k.w[(64 * half + 32 * (qd & 1) + l) / 4];
-                    const uint32_t lo = (qd < 2) ? (lb & 0x0F0F0F0Fu) : ((lb >> 4) & 0x0F0F0F0Fu);
-                    const uint32_t hi = (k.w[32 + (32 * half + l) / 4] >> (2 * qd)) & 0x03030303u;
-                    u[(128 * half + 32 * qd + l) / 4] = lo | (hi << 4);
-                }
-#pragma unroll
-        for (int si = 0; si < 16; ++si) sc[si] = static_cast<int8_t>((k.w[48 + si / 4] >> (8 * (si % 4))) & 0xFF);
-    }
-};
-
-// Exact integer sums of block b against activation row mi.
-__device__ __forceinline__ void block_sums(const Block<4>& k, const Decoded<4>& dc, int mi, int b, const Q8Lds& a,
-                                           int& isum, int& msum) {
-    const v4u* q8 = reinterpret_cast<const v4u*>(a.quants(mi, b));
-    const int16_t* bs = a.bsums(mi, b);
-    int is = 0, ms = 0;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {  // 64-value group j: sub-blocks 2j (low nibbles), 2j+1 (high)
-        const v4u x0 = q8[4 * j], x1 = q8[4 * j + 1], x2 = q8[4 * j + 2], x3 = q8[4 * j + 3];
-        const uint32_t lo8[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
-        const uint32_t hi8[8] = {x2.x, x2.y, x2.z, x2.w, x3.x, x3.y, x3.z, x3.w};
-        int dlo = 0, dhi = 0;
-#pragma unroll
-        for (int t = 0; t < 8; ++t) {
-            const uint32_t q = k.w[4 + 8 * j + t];
-            dlo = dot4(q & 0x0F0F0F0Fu, lo8[t], dlo);
-            dhi = dot4((q >> 4) & 0x0F0F0F0Fu, hi8[t], dhi);
-        }
-        is += dc.sc[2 * j] * dlo + dc.sc[2 * j + 1] * dhi;
-        const uint2 pair = *reinterpret_cast<const uint2*>(bs + 4 * j);
-        const int b_lo = static_cast<int16_t>(pair.x & 0xFFFF) + static_cast<int16_t>(pair.x >> 16);
-        const int b_hi = static_cast<int16_t>(pair.y & 0xFFFF) + static_cast<int16_t>(pair.y >> 16);
-        ms += dc.mn[2 * j] * b_lo + dc.mn[2 * j + 1] * b_hi;
-    }
-    isum = is;
-    msum = ms;
+// Sub-block scale/min pairs (2j, 2j+1) of a Q4_K block (ggml get_scale_min_k4).
+__device__ __forceinline__ void q4_scales(const v4u& h, int j, int& sc0, int& sc1, int& mn0, int& mn1) {
+    const int sh = 16 * (j & 1);
+    const uint32_t y = h.y >> sh, z = h.z >> sh, w = h.w >> sh;
+    const uint32_t scp = j < 2 ? (y & 0x3F3Fu) : ((w & 0x0F0Fu) | ((y >> 2) & 0x3030u));
+    const uint32_t mnp = j < 2 ? (z & 0x3F3Fu) : (((w >> 4) & 0x0F0Fu) | ((z >> 2) & 0x3030u));
+    sc0 = scp & 0xFF;
+    sc1 = scp >> 8;
+    mn0 = mnp & 0xFF;
+    mn1 = mnp >> 8;
 }
 
-// Q6_K: the quants are q - 32 with q = 0..63, and bsums hold the sums of the
-// 16 activation quants of each sub-block, so sum (q-32)*x = sum q*x - 32*bsum.
-__device__ __forceinline__ void block_sums(const Block<6>&, const Decoded<6>& dc, int mi, int b, const Q8Lds& a,
-                                           int& isum, int& msum) {
-    const v4u* q8 = reinterpret_cast<const v4u*>(a.quants(mi, b));
-    const v4u* bsv = reinterpret_cast<const v4u*>(a.bsums(mi, b));
-    const v4u b0 = bsv[0], b1 = bsv[1];
-    const uint32_t bw[8] = {b0.x, b0.y, b0.z, b0.w, b1.x, b1.y, b1.z, b1.w};
-    int is = 0;
-#pragma unroll
-    for (int si = 0; si < 16; ++si) {  // 16-value sub-block si = chunk si
-        const v4u x = q8[si];
-        int dq = dot4(dc.u[4 * si], x.x, 0);
-        dq = dot4(dc.u[4 * si + 1], x.y, dq);
-        dq = dot4(dc.u[4 * si + 2], x.z, dq);
-        dq = dot4(dc.u[4 * si + 3], x.w, dq);
-        const int bsum = static_cast<int16_t>((bw[si / 2] >> (16 * (si % 2))) & 0xFFFF);
-        is += dc.sc[si] * (dq - 32 * bsum);
-    }
-    isum = is;
-    msum = 0;
+__device__ __forceinline__ int sbyte(const v4u& v, int i) {
+    const uint32_t w = i < 8 ? (i < 4 ? v.x : v.y) : (i < 12 ? v.z : v.w);
+    return static_cast<int8_t>((w >> (8 * (i & 3))) & 0xFF);
 }
 
-// Position of a lane's block: row group `gi`, iteration `it` inside the group.
+// This lane's share of the exact integer sums of block b against the
+// activation rows [0, m): is[mi], ms[mi].
+template <int L, int MT>
+__device__ __forceinline__ void lane_sums(const Piece<4, L>& k, int p, const Q8Lds& a, int nb, int b, int m,
+                                          int (&is)[MT], int (&ms)[MT]) {
+    constexpr int NU = Piece<4, L>::NU;
+#pragma unroll
+    for (int mi = 0; mi < MT; ++mi) { is[mi] = 0; ms[mi] = 0; }
+#pragma unroll
+    for (int u = 0; u < NU; ++u) {
+        const int gu = NU * p + u;
+        const int j = gu >> 1, hh = gu & 1;
+        int sc0, sc1, mn0, mn1;
+        q4_scales(k.h, j, sc0, sc1, mn0, mn1);
+        const uint32_t q[4] = {k.q[u].x, k.q[u].y, k.q[u].z, k.q[u].w};
+        uint32_t lo[4], hi[4];
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            lo[t] = q[t] & 0x0F0F0F0Fu;
+            hi[t] = (q[t] >> 4) & 0x0F0F0F0Fu;
+        }
+#pragma unroll
+        for (int mi = 0; mi < MT; ++mi) {
+            if (mi >= m) break;
+            const int blk = mi * nb + b;
+            const uint8_t* xq = a.quants(blk);
+            const v4u x0 = *reinterpret_cast<const v4u*>(xq + 64 * j + 16 * hh);
+            const v4u x1 = *reinterpret_cast<const v4u*>(xq + 64 * j + 32 + 16 * hh);
+            int d0 = dot4(lo[0], x0.x, 0);
+            d0 = dot4(lo[1], x0.y, d0);
+            d0 = dot4(lo[2], x0.z, d0);
+            d0 = dot4(lo[3], x0.w, d0);
+            int d1 = dot4(hi[0], x1.x, 0);
+            d1 = dot4(hi[1], x1.y, d1);
+            d1 = dot4(hi[2], x1.z, d1);
+            d1 = dot4(hi[3], x1.w, d1);
+            const int16_t* bs = a.bsums(blk);
+            is[mi] += sc0 * d0 + sc1 * d1;
+            ms[mi] += mn0 * bs[4 * j + hh] + mn1 * bs[4 * j + 2 + hh];
+        }
+    }
+}
+
+// Q6_K quants are q - 32 with q = 0..63; bsums hold the sums of the 16
+// activation quants of each sub-block, so sum (q-32)*x = sum q*x - 32*bsum.
+template <int L, int MT>
+__device__ __forceinline__ void lane_sums(const Piece<6, L>& k, int p, const Q8Lds& a, int nb, int b, int m,
+                                          int (&is)[MT], int (&ms)[MT]) {
+    constexpr int NU = Piece<6, L>::NU;
+#pragma unroll
+    for (int mi = 0; mi < MT; ++mi) { is[mi] = 0; ms[mi] = 0; }
+#pragma unroll
+    for (int u = 0; u < NU; ++u) {
+        const int gu = NU * p + u;
+        const int h = gu >> 2, qa = (gu >> 1) & 1, c = gu & 1;
+        const int hq = L == 1 ? 2 * h + c : (L == 8 ? 0 : c);
+        const int s0 = 8 * h + 2 * qa + c;
+        const int sc0 = sbyte(k.sc, s0), sc1 = sbyte(k.sc, s0 + 4);
+        const uint32_t ql[4] = {k.ql[u].x, k.ql[u].y, k.ql[u].z, k.ql[u].w};
+        const v4u qhv = k.qh[hq];
+        const uint32_t qh[4] = {qhv.x, qhv.y, qhv.z, qhv.w};
+        const int sh = 2 * qa;
+        uint32_t u0[4], u1[4];
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            u0[t] = (ql[t] & 0x0F0F0F0Fu) | (((qh[t] >> sh) & 0x03030303u) << 4);
+            u1[t] = ((ql[t] >> 4) & 0x0F0F0F0Fu) | (((qh[t] >> (sh + 4)) & 0x03030303u) << 4);
+        }
+#pragma unroll
+        for (int mi = 0; mi < MT; ++mi) {
+            if (mi >= m) break;
+            const int blk = mi * nb + b;
+            const uint8_t* xq = a.quants(blk) + 128 * h + 32 * qa + 16 * c;
+            const v4u x0 = *reinterpret_cast<const v4u*>(xq);
+            const v4u x1 = *reinterpret_cast<const v4u*>(xq + 64);
+            int d0 = dot4(u0[0], x0.x, 0);
+            d0 = dot4(u0[1], x0.y, d0);
+            d0 = dot4(u0[2], x0.z, d0);
+            d0 = dot4(u0[3], x0.w, d0);
+            int d1 = dot4(u1[0], x1.x, 0);
+            d1 = dot4(u1[1], x1.y, d1);
+            d1 = dot4(u1[2], x1.z, d1);
+            d1 = dot4(u1[3], x1.w, d1);
+            const int16_t* bs = a.bsums(blk);
+            is[mi] += sc0 * (d0 - 32 * bs[s0]) + sc1 * (d1 - 32 * bs[s0 + 4]);
+        }
+    }
+}
+
+template <int L>
+__device__ __forceinline__ void block_scales(const Piece<4, L>& k, float& d, float& dmin) {
+    d = f16_bits_to_f32(static_cast<uint16_t>(k.h.x & 0xFFFF));
+    dmin = f16_bits_to_f32(static_cast<uint16_t>(k.h.x >> 16));
+}
+template <int L>
+__device__ __forceinline__ void block_scales(const Piece<6, L>& k, float& d, float& dmin) {
+    d = f16_bits_to_f32(static_cast<uint16_t>(k.d >> 16));
+    dmin = 0.0f;
+}
+
+// A slot's block: row group `gi`, iteration `it` inside the group.
 struct Pos {
     int64_t gi;
     int it;
 };
 
-template <int KIND, int MT, bool FUSED, int D>
-__global__ __launch_bounds__(kGemvWaves * 64) void gemv_kernel(const GemvParams p) {
+// SUMS: also write every block's exact integer sums (p.isum / p.msum).
+template <int KIND, int L, int MT, bool FUSED, int D, bool SUMS, int W>
+__global__ __launch_bounds__(W * 64) void gemv_kernel(const GemvParams p) {
     constexpr int BB = block_bytes(KIND);
+    constexpr int SW = 64 / L;  // block slots per wave
+    constexpr int LOG2L = L == 1 ? 0 : L == 2 ? 1 : L == 4 ? 2 : 3;
     extern __shared__ __align__(16) uint8_t smem[];
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    __shared__ int q8_ready;  // waves done quantising the activations (fused launches)
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // uniform: keeps row math scalar
     const int nb = p.nb, m = p.m, iters = p.iters, log2g = p.log2g;
     const Q8Lds a = q8_lds(smem, MT, nb);
 
@@ -321,55 +395,83 @@ __global__ __launch_bounds__(kGemvWaves * 64) void gemv_kernel(const GemvParams 
     if (p.count > 3 && wg >= p.wg_end[2]) { w = p.w[3]; out = p.out[3]; ldo = p.ldo[3]; rows = p.rows[3]; wg0 = p.wg_end[2]; wg1 = p.wg_end[3]; }
     const gbytes wg_w = reinterpret_cast<gbytes>(reinterpret_cast<uint64_t>(w));
     const gfloats wg_out = reinterpret_cast<gfloats>(reinterpret_cast<uint64_t>(out));
-    int32_t* const isum_out = p.isum;
-    int32_t* const msum_out = p.msum;
 
+    const int sl = lane >> LOG2L, pc = lane & (L - 1);  // block slot, lane inside the block
     const int G = 1 << log2g;
-    const int gl = lane & (G - 1);
-    const int slot = lane >> log2g;  // row inside the row group
-    const int rows_per_group = 64 >> log2g;
+    const int gl = sl & (G - 1);                         // slot inside the row
+    const int rs = sl >> log2g;                          // row inside the row group
+    const int rows_per_group = SW >> log2g;
     const int64_t row_bytes = static_cast<int64_t>(nb) * BB;
     const int64_t groups = (rows + rows_per_group - 1) / rows_per_group;
-    const int64_t wave_gid = (wg - wg0) * kGemvWaves + wave;
-    const int64_t wave_stride = (wg1 - wg0) * kGemvWaves;
-    // this wave's blocks: row groups wave_gid + i*wave_stride, `iters` per lane each
+    const int64_t wave_gid = (wg - wg0) * W + wave;
+    const int64_t wave_stride = (wg1 - wg0) * W;
+    // this wave's blocks: row groups wave_gid + i*wave_stride, `iters` per slot each
     const int64_t my_groups = wave_gid < groups ? (groups - 1 - wave_gid) / wave_stride + 1 : 0;
     const int64_t S = my_groups * iters;
 
     auto advance = [=](Pos& q) {
         if (++q.it == iters) { q.it = 0; q.gi += wave_stride; }
     };
-    // Loads are issued unconditionally: a lane without a block re-reads a block
-    // of its wave's first row group (in bounds, cache-resident, private to the
-    // wave) and ignores it. Branch-free load sequences let the wait-count pass
-    // wait for exactly the loads a value depends on.
-    const int64_t home_row = min(wave_gid * rows_per_group + slot, rows - 1);
+    // Loads are issued unconditionally: a slot without a block re-reads a
+    // block of the wave's first row group (in bounds, cache-resident) and
+    // ignores it. Branch-free load sequences let the wait-count pass wait for
+    // exactly the loads a value depends on.
+    const int64_t home_row = min(wave_gid * rows_per_group + rs, rows - 1);
     const int home_b = min(gl, nb - 1);
-    auto load_block = [=](const Pos& q, bool in_range, Block<KIND>& k) {
-        int64_t row = q.gi * rows_per_group + slot;
+    auto load_block = [=](const Pos& q, bool in_range, Piece<KIND, L>& k) {
+        int64_t row = q.gi * rows_per_group + rs;
         int b = gl + q.it * G;
         if (!(in_range && row < rows && b < nb)) {
             row = home_row;
             b = home_b;
         }
-        k.load(wg_w + row * row_bytes + static_cast<int64_t>(b) * BB);
+        k.load(wg_w + row * row_bytes + static_cast<int64_t>(b) * BB, pc);
     };
 
-    // First activation values go out first (they return first), then D blocks.
-    float4 xfirst[4];
-    const int qslot = wave * 4 + (lane >> 4);
-    if constexpr (FUSED) load_x16(p.x, p.ldx, nb, qslot < m * nb ? qslot : 0, xfirst);
-    __builtin_amdgcn_sched_barrier(0);  // keep the activation loads ahead of the weight loads
-    Block<KIND> buf[D];
+    // Fused activations: the waves that own quantisation blocks issue their
+    // activation loads, then one barrier (which also publishes the cleared
+    // q8_ready) puts those loads ahead of every weight load of the workgroup.
+    // The owners quantise and count themselves in q8_ready; every wave issues
+    // its weight loads and waits for that count. Only the owners' progress
+    // gates the rest, so no wave waits for another wave's weight loads to be
+    // issued (a barrier after them would, and under a saturated memory pipe
+    // that costs microseconds).
+    const int quant_waves = FUSED ? min(W, (m * nb + 3) / 4) : 0;
+    const bool quant_wave = wave < quant_waves;
+    if constexpr (FUSED) {
+        float4 xfirst[4];
+        if (quant_wave) {
+            const int qslot = threadIdx.x >> 4;
+            load_x16(p.x, p.ldx, nb, qslot < m * nb ? qslot : 0, xfirst);
+        }
+        if (threadIdx.x == 0) q8_ready = 0;
+        __syncthreads();
+        if (quant_wave) {
+            quantize_to_lds<W * 64>(p.x, p.ldx, m, nb, xfirst, a);
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+            if (lane == 0) __hip_atomic_fetch_add(&q8_ready, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+        }
+    }
+    Piece<KIND, L> buf[D];
     Pos lq{wave_gid, 0};  // next block to load
 #pragma unroll
     for (int j = 0; j < D; ++j) {
         load_block(lq, j < S, buf[j]);
         advance(lq);
     }
-    if constexpr (FUSED) quantize_to_lds(p.x, p.ldx, m, nb, xfirst, a);
-    else stage_q8k(p.q8k, p.ldx, m, nb, a);
-    __syncthreads();
+    if constexpr (FUSED) {
+        // Every wave (owners too: each reads all blocks) waits for the count.
+        // Bounded for safety only: the owners depend on nothing but their own
+        // activation loads, so the count arrives.
+        for (int spin = 0; spin < (1 << 24); ++spin) {
+            if (__hip_atomic_load(&q8_ready, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) >= quant_waves) break;
+            __builtin_amdgcn_s_sleep(1);
+        }
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+    } else {
+        stage_q8k<W * 64>(p.q8k, p.ldx, m, nb, a);
+        __syncthreads();
+    }
 
     float acc[MT];
 #pragma unroll
@@ -380,46 +482,43 @@ __global__ __launch_bounds__(kGemvWaves * 64) void gemv_kernel(const GemvParams 
 #pragma unroll
         for (int j = 0; j < D; ++j) {
             const int64_t s = base + j;
-            if (s >= S) break;  // uniform across the wave
-            const int64_t row = cq.gi * rows_per_group + slot;
+            const bool live = s < S;  // uniform across the wave
+            const int64_t row = cq.gi * rows_per_group + rs;
             const int b = gl + cq.it * G;
-            const bool ok = row < rows && b < nb;
-            // Every lane computes (a lane without a block holds its home block)
-            // and discards the result: straight-line code for all rows mi.
-            const int bk = ok ? b : home_b;
-            float dw, dminw = 0.0f;
-            if constexpr (KIND == 4) {
-                dw = f16_bits_to_f32(static_cast<uint16_t>(buf[j].w[0] & 0xFFFF));
-                dminw = f16_bits_to_f32(static_cast<uint16_t>(buf[j].w[0] >> 16));
-            } else {
-                dw = f16_bits_to_f32(static_cast<uint16_t>(buf[j].w[52]));
-            }
-            Decoded<KIND> dc;
-            dc.decode(buf[j]);
+            const bool have = row < rows && b < nb;  // uniform inside each block's L lanes
+            if (live) {
+                const int bk = have ? b : home_b;
+                int is[MT], ms[MT];
+                lane_sums<L, MT>(buf[j], pc, a, nb, bk, m, is, ms);
+                float dw, dminw;
+                block_scales<L>(buf[j], dw, dminw);
 #pragma unroll
-            for (int mi = 0; mi < MT; ++mi) {
-                if (mi >= m) break;
-                int isum, msum;
-                block_sums(buf[j], dc, mi, bk, a, isum, msum);
-                const float da = a.d[mi * nb + bk];
-                float term = (dw * da) * static_cast<float>(isum);
-                if constexpr (KIND == 4) term = term - (dminw * da) * static_cast<float>(msum);
-                acc[mi] += ok ? term : 0.0f;
-                if (isum_out && ok) {
-                    const int64_t idx = (static_cast<int64_t>(mi) * rows + row) * nb + b;
-                    isum_out[idx] = isum;
-                    msum_out[idx] = msum;
+                for (int mi = 0; mi < MT; ++mi) {
+                    if (mi >= m) break;
+                    const int isum = sum_lanes<L>(is[mi]);
+                    const int msum = KIND == 4 ? sum_lanes<L>(ms[mi]) : 0;
+                    const float da = a.d[mi * nb + bk];
+                    float term = (dw * da) * static_cast<float>(isum);
+                    if constexpr (KIND == 4) term = term - (dminw * da) * static_cast<float>(msum);
+                    acc[mi] += have ? term : 0.0f;
+                    if constexpr (SUMS) {
+                        if (have && pc == 0) {
+                            const int64_t idx = (static_cast<int64_t>(mi) * rows + row) * nb + b;
+                            p.isum[idx] = isum;
+                            p.msum[idx] = msum;
+                        }
+                    }
                 }
             }
             // refill this slot with the block D ahead
             load_block(lq, s + D < S, buf[j]);
             advance(lq);
-            if (cq.it == iters - 1) {
-                // row group done: combine the row's G lanes and store
+            if (live && cq.it == iters - 1) {
+                // row group done: add each row's G slot sums and store
 #pragma unroll
                 for (int mi = 0; mi < MT; ++mi) {
-                    const float r = group_sum(acc[mi], G);
-                    if (gl == 0 && row < rows && mi < m) wg_out[mi * ldo + row] = r;
+                    const float r = sum_bits(acc[mi], LOG2L, LOG2L + log2g);
+                    if (gl == 0 && pc == 0 && row < rows && mi < m) wg_out[mi * ldo + row] = r;
                     acc[mi] = 0.0f;
                 }
             }
@@ -428,22 +527,65 @@ __global__ __launch_bounds__(kGemvWaves * 64) void gemv_kernel(const GemvParams 
     }
 }
 
-template <int KIND, bool FUSED, int D>
-void launch_d(const GemvParams& p, int mt, dim3 grid, size_t lds, hipStream_t stream) {
-    const dim3 block(kGemvWaves * 64);
+// Most blocks in flight per lane, by kind and lanes per block: 64-150 bytes
+// of weights per lane, within the 128 VGPRs a 1024-thread workgroup allows
+// (halved for eight activation rows).
+template <int KIND, int L>
+constexpr int max_depth() {
+    if constexpr (KIND == 4) return L <= 2 ? 2 : 4;
+    else return L == 1 ? 1 : L == 8 ? 4 : 2;
+}
+
+template <int KIND, int L, int MT, bool FUSED, bool SUMS, int W>
+void launch_mt(const GemvParams& p, int d, dim3 grid, size_t lds, hipStream_t stream) {
+    constexpr int DM = SUMS ? 1 : (MT == 8 ? (max_depth<KIND, L>() > 1 ? max_depth<KIND, L>() / 2 : 1)
+                                           : max_depth<KIND, L>());
+    const dim3 block(W * 64);
+    if (DM >= 4 && d >= 3) gemv_kernel<KIND, L, MT, FUSED, (DM >= 4 ? 4 : 1), SUMS, W><<<grid, block, lds, stream>>>(p);
+    else if (DM >= 2 && d >= 2) gemv_kernel<KIND, L, MT, FUSED, (DM >= 2 ? 2 : 1), SUMS, W><<<grid, block, lds, stream>>>(p);
+    else gemv_kernel<KIND, L, MT, FUSED, 1, SUMS, W><<<grid, block, lds, stream>>>(p);
+}
+
+template <int KIND, int L, bool FUSED, bool SUMS, int W>
+void launch_w(const GemvParams& p, int mt, int d, dim3 grid, size_t lds, hipStream_t stream) {
     switch (mt) {
-    case 1: gemv_kernel<KIND, 1, FUSED, D><<<grid, block, lds, stream>>>(p); break;
-    case 2: gemv_kernel<KIND, 2, FUSED, D><<<grid, block, lds, stream>>>(p); break;
-    case 4: gemv_kernel<KIND, 4, FUSED, D><<<grid, block, lds, stream>>>(p); break;
-    default: gemv_kernel<KIND, 8, FUSED, D><<<grid, block, lds, stream>>>(p); break;
+    case 1: launch_mt<KIND, L, 1, FUSED, SUMS, W>(p, d, grid, lds, stream); break;
+    case 2: launch_mt<KIND, L, 2, FUSED, SUMS, W>(p, d, grid, lds, stream); break;
+    case 4: launch_mt<KIND, L, 4, FUSED, SUMS, W>(p, d, grid, lds, stream); break;
+    default:
+        // eight rows run with L <= 2 only (more lanes per block would spill)
+        if constexpr (L <= 2) launch_mt<KIND, L, 8, FUSED, SUMS, W>(p, d, grid, lds, stream);
+        break;
     }
 }
 
-// Lanes per row: the largest power of two <= min(16, nb) whose last pass over
-// the row's blocks keeps at least 85% of the lanes busy.
-int lanes_per_row_log2(int nb) {
+// 8-wave workgroups serve fused launches only.
+template <int KIND, int L, bool FUSED, bool SUMS>
+void launch_l(const GemvParams& p, int w, int mt, int d, dim3 grid, size_t lds, hipStream_t stream) {
+    if constexpr (FUSED && !SUMS) {
+        if (w == 8) return launch_w<KIND, L, FUSED, SUMS, 8>(p, mt, d, grid, lds, stream);
+    }
+    launch_w<KIND, L, FUSED, SUMS, 16>(p, mt, d, grid, lds, stream);
+}
+
+// Compute units of the current device (cached per device).
+int device_cus() {
+    static int cached[64] = {};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+    if (cached[dev] == 0) {
+        int n = 0;
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+        cached[dev] = n;
+    }
+    return cached[dev];
+}
+
+// Slots per row: the largest power of two <= min(slots, nb) whose last pass
+// over the row's blocks keeps at least 85% of the slots busy.
+int slots_per_row_log2(int nb, int slots) {
     int lg = 0;
-    while ((2 << lg) <= 16 && (2 << lg) <= nb) ++lg;
+    while ((2 << lg) <= slots && (2 << lg) <= nb) ++lg;
     while (lg > 0) {
         const int g = 1 << lg, it = (nb + g - 1) / g;
         if (nb * 100 >= 85 * g * it) break;
@@ -454,29 +596,59 @@ int lanes_per_row_log2(int nb) {
 
 template <int KIND, bool FUSED>
 int launch_kind(GemvParams& p, hipStream_t stream) {
-    p.log2g = lanes_per_row_log2(p.nb);
+    const bool sums = !FUSED && p.isum != nullptr;
+    const int cus = device_cus();
+    const int mt = p.m <= 1 ? 1 : p.m <= 2 ? 2 : p.m <= 4 ? 4 : 8;
+    // At most 8 slots per row whatever L is: a row's f32 sum then runs in the
+    // same order for every L and every grouping of projections.
+    p.log2g = slots_per_row_log2(p.nb, 8);
     const int G = 1 << p.log2g;
     p.iters = (p.nb + G - 1) / G;
-    const int64_t rows_per_group = 64 / G;
-    // D blocks per lane in flight; each projection gets about D blocks per
-    // lane (one round) worth of workgroups.
-    int64_t total_wave_blocks = 0;
-    for (int i = 0; i < p.count; ++i) total_wave_blocks += (p.rows[i] + rows_per_group - 1) / rows_per_group * p.iters;
-    const int d = total_wave_blocks >= 2 * kGemvWaves * 256 ? 2 : 1;
-    int64_t wgs = 0;
+    auto row_groups = [&](int lanes_per_block) {
+        const int64_t rpg = 64 / lanes_per_block / G;
+        int64_t n = 0;
+        for (int i = 0; i < p.count; ++i) n += (p.rows[i] + rpg - 1) / rpg;
+        return n;
+    };
+    // Lanes per block: the fewest that still give half of the device's waves
+    // a row group (eight activation rows: at most 2, more would spill).
+    const int max_l = sums ? 1 : mt == 8 ? 2 : 8;
+    int L = 1;
+    while (L < max_l && row_groups(L) * 2 < static_cast<int64_t>(cus) * kGemvMaxWaves) L <<= 1;
+    // One workgroup per CU: 8 waves where that covers the row groups and one
+    // 8-wave pass quantises the activations, else 16.
+    const int W = FUSED && !sums && p.m * p.nb <= 32 && row_groups(L) <= static_cast<int64_t>(cus) * 8 ? 8 : 16;
+    const int64_t max_wgs = cus;
+    const int64_t rows_per_group = 64 / L / G;
+    // Workgroups: at most one per CU and one per W row groups, split between
+    // the projections in proportion to their row groups; blocks in flight per
+    // lane = the blocks a wave ends up with, up to the kernel's most.
+    int64_t total_groups = 0;
+    for (int i = 0; i < p.count; ++i) total_groups += (p.rows[i] + rows_per_group - 1) / rows_per_group;
+    const int64_t budget = std::max<int64_t>(p.count, std::min<int64_t>(max_wgs, (total_groups + W - 1) / W));
+    int64_t wgs = 0, per_wave = 1;
     for (int i = 0; i < p.count; ++i) {
-        const int64_t wave_blocks = (p.rows[i] + rows_per_group - 1) / rows_per_group * p.iters;
-        int64_t n = (wave_blocks + static_cast<int64_t>(d) * kGemvWaves - 1) / (static_cast<int64_t>(d) * kGemvWaves);
-        if (n > 2048) n = 2048;
-        if (n < 1) n = 1;
+        const int64_t groups = (p.rows[i] + rows_per_group - 1) / rows_per_group;
+        int64_t n = (budget * groups + total_groups / 2) / total_groups;
+        n = std::max<int64_t>(1, std::min(n, (groups + W - 1) / W));
         wgs += n;
         p.wg_end[i] = wgs;
+        per_wave = std::max(per_wave, (groups + n * W - 1) / (n * W) * p.iters);
     }
-    const int mt = p.m <= 1 ? 1 : p.m <= 2 ? 2 : p.m <= 4 ? 4 : 8;
+    const int d = static_cast<int>(std::min<int64_t>(per_wave, 4));
     const size_t lds = static_cast<size_t>(mt) * p.nb * kGemvLdsPerBlock;
     const dim3 grid(static_cast<unsigned>(wgs));
-    if (d == 2) launch_d<KIND, FUSED, 2>(p, mt, grid, lds, stream);
-    else launch_d<KIND, FUSED, 1>(p, mt, grid, lds, stream);
+    if (sums) {
+        if constexpr (!FUSED) launch_l<KIND, 1, FUSED, true>(p, W, mt, d, grid, lds, stream);
+    } else if (L == 1) {
+        launch_l<KIND, 1, FUSED, false>(p, W, mt, d, grid, lds, stream);
+    } else if (L == 2) {
+        launch_l<KIND, 2, FUSED, false>(p, W, mt, d, grid, lds, stream);
+    } else if (L == 4) {
+        launch_l<KIND, 4, FUSED, false>(p, W, mt, d, grid, lds, stream);
+    } else {
+        launch_l<KIND, 8, FUSED, false>(p, W, mt, d, grid, lds, stream);
+    }
     return hipGetLastError() == hipSuccess ? kStatusOk : kStatusExec;
 }
 
