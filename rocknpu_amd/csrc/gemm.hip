@@ -15,10 +15,13 @@
 // on the 16-byte chunk index so fragment reads are bank-conflict free.
 #include "common.h"
 
+#include <type_traits>
+
 namespace rk {
 namespace {
 
 typedef int v4i __attribute__((ext_vector_type(4)));
+typedef int v16i __attribute__((ext_vector_type(16)));
 
 constexpr int kBK = 64;
 
@@ -126,6 +129,280 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_w8a8_kernel(
         }
 }
 
+// Large tiles: the same product with a four-stage pipeline of LDS buffers
+// filled by direct global->LDS loads (global_load_lds_dwordx4, no register
+// staging). Each wave issues its share of a stage as 1 KiB segments (16 rows
+// x 64 bytes; lane i's 16 bytes land at segment + 16*i, so the lane loads the
+// global chunk that the swizzled layout puts there). Stage s+3 is issued while
+// stage s is multiplied; one barrier per K step both publishes stage s (after
+// each wave's own wait for its loads) and frees stage s-1 for reuse. The
+// barrier is a bare s_barrier: a fenced one would wait for every load in
+// flight, stages ahead included.
+constexpr int kStages = 4;
+
+template <int ROWS>
+struct StageBuf {
+    int8_t a[ROWS * kBK];
+};
+
+template <int BM, int BN, int WM, int WN>
+struct DmaTile {
+    static constexpr int T = WM * WN * 64;
+    static constexpr int W = WM * WN;
+    static constexpr int A_SEG = BM / 16 / W, B_SEG = BN / 16 / W;  // 1 KiB segments per wave and stage
+    static_assert(A_SEG * W * 16 == BM && B_SEG * W * 16 == BN, "tile rows must split into 16-row segments per wave");
+};
+
+// s_waitcnt with only vmcnt constrained (gfx9 encoding: vmcnt[3:0] | expcnt[6:4]
+// | lgkmcnt[11:8] | vmcnt[5:4] at bits 15:14).
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+    __builtin_amdgcn_s_waitcnt((N & 0xF) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
+}
+__device__ __forceinline__ void wait_lgkm0() { __builtin_amdgcn_s_waitcnt(0xF | (7 << 4) | ((0x3) << 14)); }
+
+// One 16-byte direct global->LDS load per lane; `lds` must be wave-uniform
+// (the 64 lanes fill lds .. lds + 1023).
+__device__ __forceinline__ void dma16(const int8_t* src, int8_t* lds) {
+    __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void*)(lds), 16, 0, 0);
+}
+
+template <int BM, int BN, int WM, int WN>
+__global__ __launch_bounds__(WM* WN * 64) void gemm_w8a8_dma_kernel(
+    const int8_t* __restrict__ a8, int64_t lda, const int8_t* __restrict__ w8, int64_t ldw,
+    const float* __restrict__ a_scales, const float* __restrict__ w_scales, int m, int n, int k,
+    float* __restrict__ out, int64_t ldo, int32_t* __restrict__ out_i32, int64_t ldo_i32) {
+    using Cfg = DmaTile<BM, BN, WM, WN>;
+    constexpr int TM = BM / WM, TN = BN / WN;
+    constexpr int FM = TM / 32, FN = TN / 32;  // 32x32 fragments
+    // One array per stage, always indexed by a compile-time stage: the
+    // wait-count pass then sees which LDS buffer a direct load writes and does
+    // not wait for every load in flight before each LDS read.
+    __shared__ __align__(16) int8_t la0[BM * kBK], la1[BM * kBK], la2[BM * kBK], la3[BM * kBK];
+    __shared__ __align__(16) int8_t lb0[BN * kBK], lb1[BN * kBK], lb2[BN * kBK], lb3[BN * kBK];
+    static_assert(kStages == 4, "four stage buffers");
+    auto stage_a = [&](auto st) -> int8_t* {
+        constexpr int S = decltype(st)::value;
+        if constexpr (S == 0) return la0; else if constexpr (S == 1) return la1;
+        else if constexpr (S == 2) return la2; else return la3;
+    };
+    auto stage_b = [&](auto st) -> int8_t* {
+        constexpr int S = decltype(st)::value;
+        if constexpr (S == 0) return lb0; else if constexpr (S == 1) return lb1;
+        else if constexpr (S == 2) return lb2; else return lb3;
+    };
+
+    // XCD-aware tile order: workgroup b runs on XCD b % 8, so each XCD takes a
+    // contiguous range of tile indices, walked in groups of 4 tile rows; the
+    // 32 tiles an XCD runs at once then share A rows and W rows in its L2.
+    const int tiles_m = (m + BM - 1) / BM, tiles_n = (n + BN - 1) / BN;
+    const int tiles = tiles_m * tiles_n;
+    const int bid = blockIdx.x, xcd = bid & 7, per = tiles >> 3, rem = tiles & 7;
+    const int t = xcd * per + min(xcd, rem) + (bid >> 3);
+    constexpr int GM = 4;
+    const int group = t / (GM * tiles_n), first_m = group * GM;
+    const int gsize = min(tiles_m - first_m, GM);
+    const int tm = first_m + (t % (GM * tiles_n)) % gsize, tn = (t % (GM * tiles_n)) / gsize;
+    const int m0 = tm * BM, n0 = tn * BN;
+
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int wm = wave / WN, wn = wave % WN;
+
+    // This lane's source row and chunk for each of its segments. Rows past the
+    // matrix re-read its last row (their products land in rows/columns that
+    // are never stored).
+    const int8_t* asrc[Cfg::A_SEG];
+    const int8_t* bsrc[Cfg::B_SEG];
+#pragma unroll
+    for (int q = 0; q < Cfg::A_SEG; ++q) {
+        const int r = (wave * Cfg::A_SEG + q) * 16 + (lane >> 2);
+        const int c = (lane & 3) ^ ((r >> 1) & 3);
+        asrc[q] = a8 + static_cast<int64_t>(min(m0 + r, m - 1)) * lda + c * 16;
+    }
+#pragma unroll
+    for (int q = 0; q < Cfg::B_SEG; ++q) {
+        const int r = (wave * Cfg::B_SEG + q) * 16 + (lane >> 2);
+        const int c = (lane & 3) ^ ((r >> 1) & 3);
+        bsrc[q] = w8 + static_cast<int64_t>(min(n0 + r, n - 1)) * ldw + c * 16;
+    }
+    auto issue = [&](auto st, int kt) {
+        int8_t* la = stage_a(st);
+        int8_t* lb = stage_b(st);
+#pragma unroll
+        for (int q = 0; q < Cfg::A_SEG; ++q) dma16(asrc[q] + kt * kBK, la + (wave * Cfg::A_SEG + q) * 1024);
+#pragma unroll
+        for (int q = 0; q < Cfg::B_SEG; ++q) dma16(bsrc[q] + kt * kBK, lb + (wave * Cfg::B_SEG + q) * 1024);
+    };
+
+    v16i acc[FM][FN];
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j) acc[i][j] = v16i{};
+
+    const int KT = k / kBK;
+    using S0 = std::integral_constant<int, 0>;
+    using S1 = std::integral_constant<int, 1>;
+    using S2 = std::integral_constant<int, 2>;
+    using S3 = std::integral_constant<int, 3>;
+    // Pipeline per K step s (stage s's fragments were read in step s-1):
+    //   wait for those reads and for this wave's loads of stage s+1; barrier
+    //   (every wave's stage s+1 is in, and every wave holds stage s in
+    //   registers, so its buffer is free); issue stage s+4 into that buffer;
+    //   read stage s+1's fragments into the other register set; then the
+    //   MFMAs of stage s, which run while those reads complete.
+    // Past the last K step the issue re-reads the last step into a buffer no
+    // step reads, so the count of loads in flight stays fixed.
+    constexpr int PER_STAGE = Cfg::A_SEG + Cfg::B_SEG;  // loads per wave and stage
+    v4i fa[2][2][FM], fb[2][2][FN];  // [register set][32-deep half][fragment]
+    // lane l supplies row l%32 and the 16 bytes of chunk 2*h + l/32
+    auto read_half = [&](auto st, auto set, auto half) {
+        constexpr int R = decltype(set)::value, H = decltype(half)::value;
+        const int8_t* la = stage_a(st);
+        const int8_t* lb = stage_b(st);
+#pragma unroll
+        for (int i = 0; i < FM; ++i)
+            fa[R][H][i] = *reinterpret_cast<const v4i*>(la + swz(wm * TM + i * 32 + (lane & 31), 2 * H + (lane >> 5)));
+#pragma unroll
+        for (int j = 0; j < FN; ++j)
+            fb[R][H][j] = *reinterpret_cast<const v4i*>(lb + swz(wn * TN + j * 32 + (lane & 31), 2 * H + (lane >> 5)));
+    };
+    using H0 = std::integral_constant<int, 0>;
+    using H1 = std::integral_constant<int, 1>;
+    auto read_frags = [&](auto st, auto set) {
+        read_half(st, set, H0{});
+        read_half(st, set, H1{});
+    };
+    auto mfma_half = [&](auto set, auto half) {
+        constexpr int R = decltype(set)::value, H = decltype(half)::value;
+#pragma unroll
+        for (int j = 0; j < FN; ++j)
+#pragma unroll
+            for (int i = 0; i < FM; ++i)
+                acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa[R][H][i], fb[R][H][j], acc[i][j], 0, 0, 0);
+    };
+    using R0 = std::integral_constant<int, 0>;
+    using R1 = std::integral_constant<int, 1>;
+    issue(S0{}, 0);
+    issue(S1{}, min(1, KT - 1));
+    issue(S2{}, min(2, KT - 1));
+    wait_vm<2 * PER_STAGE>();
+    __builtin_amdgcn_s_barrier();
+    issue(S3{}, min(3, KT - 1));
+    read_frags(S0{}, R0{});
+    // step s: stage s in register set s%2; S1N = stage of s+1
+    // Each step is one basic block: the barrier, the direct loads of stage
+    // s+4 and the fragment reads of stage s+1 are spread between the MFMAs of
+    // stage s (scheduling groups of one load, its share of the reads and of
+    // the MFMAs), so the LDS and memory traffic overlaps the matrix cores
+    // instead of stalling them. After the last K step the barrier, loads and reads
+    // still run (on buffers no step reads), which keeps the block branch-free.
+    auto step = [&](auto set, auto next_st, auto refill_st, int kt) {
+        using NSET = std::integral_constant<int, 1 - decltype(set)::value>;
+        wait_lgkm0();
+        wait_vm<2 * PER_STAGE>();  // stage s+1 done (s+2 and s+3 may be in flight)
+        __builtin_amdgcn_s_barrier();
+        issue(refill_st, min(kt + 4, KT - 1));
+        read_frags(next_st, NSET{});
+        mfma_half(set, H0{});
+        mfma_half(set, H1{});
+        constexpr int READS = 2 * (FM + FN), MFMAS = 2 * FM * FN;
+        static_assert(READS % PER_STAGE == 0 && MFMAS % PER_STAGE == 0, "schedule groups split evenly");
+#pragma unroll
+        for (int q = 0; q < PER_STAGE; ++q) {
+            __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);                  // VMEM read (direct load)
+            __builtin_amdgcn_sched_group_barrier(0x100, READS / PER_STAGE, 0);  // DS read
+            __builtin_amdgcn_sched_group_barrier(0x008, MFMAS / PER_STAGE, 0);  // MFMA
+        }
+    };
+    const int KT4 = KT & ~(kStages - 1);
+    for (int kt = 0; kt < KT4; kt += kStages) {
+        step(R0{}, S1{}, S0{}, kt);
+        step(R1{}, S2{}, S1{}, kt + 1);
+        step(R0{}, S3{}, S2{}, kt + 2);
+        step(R1{}, S0{}, S3{}, kt + 3);
+    }
+    if (KT4 < KT) step(R0{}, S1{}, S0{}, KT4);
+    if (KT4 + 1 < KT) step(R1{}, S2{}, S1{}, KT4 + 1);
+    if (KT4 + 2 < KT) step(R0{}, S3{}, S2{}, KT4 + 2);
+    // Every wave's direct loads and fragment reads are done before any wave
+    // reuses the stage buffers below.
+    wait_vm<0>();
+    wait_lgkm0();
+    __builtin_amdgcn_s_barrier();
+
+    // Epilogue. lane l holds column l%32 of each 32x32 fragment, rows
+    // (e%4) + 4*(l/32) + 8*(e/4). Each fragment is scaled, written to a 32x40
+    // f32 tile of the wave's own stage buffer, and read back as 4 rows x 32
+    // columns per pass, so every lane stores 16 contiguous bytes and eight
+    // lanes fill a 128-byte row segment.
+    constexpr int TS = 40;  // tile row stride in floats: 16-byte aligned rows, rows 4 apart 32 banks apart
+    static_assert(32 * TS * 4 <= BM * kBK, "epilogue tile fits a stage buffer");
+    float* tile = reinterpret_cast<float*>(wave == 0 ? la0 : wave == 1 ? la1 : wave == 2 ? la2 : la3);
+    typedef float f4u __attribute__((ext_vector_type(4), aligned(4)));  // scales and outputs: 4-byte alignment
+#pragma unroll
+    for (int i = 0; i < FM; ++i) {
+        const int rbase = m0 + wm * TM + i * 32 + 4 * (lane >> 5);
+        float rs[16];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const int r = rbase + 8 * q;
+            if (r + 3 < m) {
+                const f4u v = *reinterpret_cast<const f4u*>(a_scales + r);
+                rs[4 * q] = v.x; rs[4 * q + 1] = v.y; rs[4 * q + 2] = v.z; rs[4 * q + 3] = v.w;
+            } else {
+#pragma unroll
+                for (int e = 0; e < 4; ++e) rs[4 * q + e] = r + e < m ? a_scales[r + e] : 0.0f;
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < FN; ++j) {
+            const int c0 = n0 + wn * TN + j * 32;
+            const float ws = w_scales[min(c0 + (lane & 31), n - 1)];
+#pragma unroll
+            for (int e = 0; e < 16; ++e) {
+                const int lr = (e & 3) + 4 * (lane >> 5) + 8 * (e >> 2);
+                tile[lr * TS + (lane & 31)] = (static_cast<float>(acc[i][j][e]) * rs[e]) * ws;
+            }
+            // same wave: its LDS writes land before its reads
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                const int lr = (lane >> 3) + 8 * t, lc = 4 * (lane & 7);
+                const f4u v = *reinterpret_cast<const f4u*>(tile + lr * TS + lc);
+                const int row = m0 + wm * TM + i * 32 + lr, col = c0 + lc;
+                if (row < m) {
+                    float* dst = out + static_cast<int64_t>(row) * ldo + col;
+                    if (col + 3 < n) {
+                        *reinterpret_cast<f4u*>(dst) = v;
+                    } else {
+                        if (col < n) dst[0] = v.x;
+                        if (col + 1 < n) dst[1] = v.y;
+                        if (col + 2 < n) dst[2] = v.z;
+                    }
+                }
+            }
+            if (out_i32) {
+#pragma unroll
+                for (int e = 0; e < 16; ++e) {
+                    const int row = rbase + (e & 3) + 8 * (e >> 2), col = c0 + (lane & 31);
+                    if (row < m && col < n) out_i32[row * ldo_i32 + col] = acc[i][j][e];
+                }
+            }
+        }
+    }
+}
+
+template <int BM, int BN, int WM, int WN>
+int launch_dma(const int8_t* a8, int64_t lda, const int8_t* w8, int64_t ldw, const float* as,
+               const float* ws, int m, int n, int k, float* out, int64_t ldo, int32_t* oi,
+               int64_t ldoi, hipStream_t stream) {
+    const int64_t tiles = static_cast<int64_t>((m + BM - 1) / BM) * ((n + BN - 1) / BN);
+    gemm_w8a8_dma_kernel<BM, BN, WM, WN><<<dim3(static_cast<unsigned>(tiles)), dim3(WM * WN * 64), 0, stream>>>(
+        a8, lda, w8, ldw, as, ws, m, n, k, out, ldo, oi, ldoi);
+    return hipGetLastError() == hipSuccess ? kStatusOk : kStatusExec;
+}
+
 template <int BM, int BN, int WM, int WN>
 int launch_cfg(const int8_t* a8, int64_t lda, const int8_t* w8, int64_t ldw, const float* as,
                const float* ws, int m, int n, int k, float* out, int64_t ldo, int32_t* oi,
@@ -144,7 +421,9 @@ int launch_gemm_w8a8(const int8_t* a8, int64_t lda, const int8_t* w8, int64_t ld
     if (m <= 16) return launch_cfg<16, 64, 1, 4>(a8, lda, w8, ldw, as, ws, m, n, k, out, ldo, oi, ldoi, stream);
     if (m <= 32) return launch_cfg<32, 64, 1, 4>(a8, lda, w8, ldw, as, ws, m, n, k, out, ldo, oi, ldoi, stream);
     if (m <= 256) return launch_cfg<64, 64, 2, 2>(a8, lda, w8, ldw, as, ws, m, n, k, out, ldo, oi, ldoi, stream);
-    return launch_cfg<128, 128, 2, 2>(a8, lda, w8, ldw, as, ws, m, n, k, out, ldo, oi, ldoi, stream);
+    const int64_t big_tiles = static_cast<int64_t>((m + 255) / 256) * ((n + 255) / 256);
+    if (big_tiles >= 256) return launch_dma<256, 256, 2, 2>(a8, lda, w8, ldw, as, ws, m, n, k, out, ldo, oi, ldoi, stream);
+    return launch_dma<128, 128, 2, 2>(a8, lda, w8, ldw, as, ws, m, n, k, out, ldo, oi, ldoi, stream);
 }
 
 }  // namespace rk

@@ -117,7 +117,10 @@ def _gemm_dev(a8, as_, w8, ws):
 
 @pytest.mark.parametrize("m,n,k", [(1, 64, 64), (4, 96, 256), (16, 256, 2048), (33, 130, 320),
                                    (128, 5632, 2048), (200, 300, 640), (512, 2048, 2048),
-                                   (600, 520, 5632), (1, 5632, 2048), (257, 64, 128)])
+                                   (600, 520, 5632), (1, 5632, 2048), (257, 64, 128),
+                                   (300, 300, 64),        # one K step: pipeline prologue only
+                                   (4096, 4096, 256),     # 256x256 tiles
+                                   (4100, 4000, 192)])    # 256x256 tiles, ragged edges, 3 K steps
 def test_gemm_w8a8_bit_exact(m, n, k):
     print(f"gemm m={m} n={n} k={k}", flush=True)
     g = np.random.default_rng(m * 1000 + n + k)
