@@ -34,6 +34,13 @@ def _check(status: int, what: str) -> None:
         raise LaunchError(f"{what} returned status {status}")
 
 
+def _ld(t: torch.Tensor) -> int:
+    """Row stride in elements for the C ABI. A single row's stride is
+    arbitrary in torch (0 for a row added with [None]), so it is the row
+    length there."""
+    return t.stride(0) if t.shape[0] > 1 else t.shape[1]
+
+
 def k_pad_of(k: int) -> int:
     return (k + 63) // 64 * 64
 
@@ -61,7 +68,7 @@ def quantize_a8(a: torch.Tensor, k_pad: int | None = None, a8: torch.Tensor | No
         a8 = torch.empty((m, kp), dtype=torch.int8, device=a.device)
     if scales is None:
         scales = torch.empty(m, dtype=torch.float32, device=a.device)
-    _check(_lib.load().rocknpu_hip_quantize_a8(_ptr(a), m, k, a.stride(0), kp, _ptr(a8), _ptr(scales),
+    _check(_lib.load().rocknpu_hip_quantize_a8(_ptr(a), m, k, _ld(a), kp, _ptr(a8), _ptr(scales),
                                                _stream()), "quantize_a8")
     return a8, scales
 
@@ -75,7 +82,7 @@ def gemm_w8a8(a8: torch.Tensor, a_scales: torch.Tensor, w8: torch.Tensor, w_scal
     if out is None:
         out = torch.empty((m, n), dtype=torch.float32, device=a8.device)
     _check(_lib.load().rocknpu_hip_gemm_w8a8(_ptr(a8), _ptr(a_scales), _ptr(w8), _ptr(w_scales), m, n, kp,
-                                             _ptr(out), out.stride(0), _ptr(out_i32), _stream()), "gemm_w8a8")
+                                             _ptr(out), _ld(out), _ptr(out_i32), _stream()), "gemm_w8a8")
     return out
 
 
@@ -84,7 +91,7 @@ def quantize_q8_k(x: torch.Tensor, q8k: torch.Tensor | None = None) -> torch.Ten
     m, k = x.shape
     if q8k is None:
         q8k = torch.empty((m, (k // QK) * Q8K_BYTES), dtype=torch.uint8, device=x.device)
-    _check(_lib.load().rocknpu_hip_quantize_q8_k(_ptr(x), m, k, x.stride(0), _ptr(q8k), _stream()),
+    _check(_lib.load().rocknpu_hip_quantize_q8_k(_ptr(x), m, k, _ld(x), _ptr(q8k), _stream()),
            "quantize_q8_k")
     return q8k
 
@@ -96,7 +103,7 @@ def gemv_q8_k(kind: int, w: torch.Tensor, k: int, n: int, q8k: torch.Tensor, out
     if out is None:
         out = torch.empty((m, n), dtype=torch.float32, device=q8k.device)
     _check(_lib.load().rocknpu_hip_gemv_q8_k(kind, _ptr(w), w.numel(), k, n, _ptr(q8k), m, _ptr(out),
-                                             out.stride(0), _ptr(isum), _ptr(msum), _stream()), "gemv_q8_k")
+                                             _ld(out), _ptr(isum), _ptr(msum), _stream()), "gemv_q8_k")
     return out
 
 
@@ -111,7 +118,7 @@ def gemv_q_f32(kind: int, weights, k: int, ns, x: torch.Tensor, outs=None):
     b_arr = (ctypes.c_size_t * count)(*[w.numel() for w in weights])
     n_arr = (ctypes.c_size_t * count)(*ns)
     o_arr = (ctypes.c_void_p * count)(*[o.data_ptr() for o in outs])
-    l_arr = (ctypes.c_size_t * count)(*[o.stride(0) for o in outs])
-    _check(_lib.load().rocknpu_hip_gemv_q_f32(kind, count, w_arr, b_arr, n_arr, k, _ptr(x), x.stride(0), m,
+    l_arr = (ctypes.c_size_t * count)(*[_ld(o) for o in outs])
+    _check(_lib.load().rocknpu_hip_gemv_q_f32(kind, count, w_arr, b_arr, n_arr, k, _ptr(x), _ld(x), m,
                                               o_arr, l_arr, _stream()), "gemv_q_f32")
     return outs
