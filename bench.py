@@ -13,7 +13,8 @@ at 128 tokens and on larger shapes, rotating >1 GiB of weights), TinyLlama
 prefill MUL_MAT tokens/s, the dominant kernel's roofline, and the CPU oracle
 timed on the host cores as a baseline.
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--quick]
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--quick] [--no-cpu]
+       python bench.py --profile {gemv-q4k,gemm,copy}   (workload only, for rocprofv3 counter runs)
 """
 from __future__ import annotations
 
@@ -41,7 +42,23 @@ def parse():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--quick", action="store_true", help="skip the extra W8A8 shapes and the CPU baseline")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--profile", choices=["gemv-q4k", "gemm", "copy"],
+                    help="run one workload eagerly a few times and exit (for rocprofv3 --pmc passes)")
     return ap.parse_args()
+
+
+TRAFFIC_FILE = ROOT / "profiles" / "traffic.json"
+
+
+def measured_traffic(kernel: str):
+    """HBM bytes per launch of `kernel` from the counter runs recorded in
+    profiles/traffic.json (FETCH_SIZE + WRITE_SIZE, each scaled by what the
+    counter reads for a plain copy of known size), or None."""
+    try:
+        rec = json.loads(TRAFFIC_FILE.read_text())[kernel]
+        return int(rec["traffic_bytes_per_launch"])
+    except (OSError, KeyError, ValueError):
+        return None
 
 
 # ----------------------------------------------------------------------------- decode GEMV set
@@ -190,6 +207,58 @@ def prefill_tok_s(torch, hip, synth, m: int, layers: int) -> dict:
     return {"m": m, "ms_per_22_layers": round(per_model_ms, 4), "tok_s": round(m / (per_model_ms * 1e-3), 1)}
 
 
+def decode_large(torch, hip, synth) -> dict:
+    """Llama-3-8B decode projections at M=1 (gate+up 2 x [14336 x 4096] Q4_K in
+    one launch, down [4096 x 14336] Q6_K), rotating distinct weight copies:
+    the GEMV on matrices large enough for the launch cost not to dominate."""
+    dev = "cuda"
+    res = {}
+    for name, kind, ns, k in (("gate_up_q4k", 4, (14336, 14336), 4096), ("down_q6k", 6, (4096,), 14336)):
+        wbytes = sum(n * k // 256 * synth.BLOCK_BYTES[kind] for n in ns)
+        copies = max(2, min(24, int(1.2e9 // wbytes)))
+        W = [[torch.from_numpy(synth.kquant(kind, n, k, index=50_000 + 8 * c + j)).to(dev)
+              for j, n in enumerate(ns)] for c in range(copies)]
+        x = torch.from_numpy(synth.activations(1, k, index=51_000 + k)).to(dev)
+        outs = [torch.empty((1, n), dtype=torch.float32, device=dev) for n in ns]
+
+        def run():
+            for ws in W:
+                hip.gemv_q_f32(kind, ws, k, list(ns), x, outs=outs)
+
+        ms, _ = time_graph(torch, run, 5, 2)
+        us = ms * 1e3 / copies
+        byts = wbytes + k * 4 + sum(ns) * 4
+        gbs = byts / (us * 1e-6) / 1e9
+        res[name] = {"kind": kind, "n": list(ns), "k": k, "us": round(us, 3), "gb_s": round(gbs, 1),
+                     "frac_hbm_peak": round(gbs / HBM_PEAK_GBS, 4), "weight_copies": copies}
+        del W
+        torch.cuda.empty_cache()
+    return res
+
+
+def profile_workload(torch, hip, synth, which: str) -> None:
+    """Run one workload eagerly (3 times) for rocprofv3 counter passes."""
+    if which == "gemv-q4k":
+        ds = DecodeSet(torch, hip, synth, synth.TINYLLAMA_LAYERS)
+        for _ in range(3):
+            ds.step(only_kind=4)
+    elif which == "gemm":
+        m, n, k = 4096, 14336, 4096
+        w = torch.randint(-127, 128, (n, k), dtype=torch.int8, device="cuda")
+        wsc = torch.rand(n, device="cuda") / 127 + 1e-3
+        a8, asc = hip.quantize_a8(torch.from_numpy(synth.activations(m, k, index=5)).to("cuda"), k)
+        out = torch.empty((m, n), dtype=torch.float32, device="cuda")
+        for _ in range(3):
+            hip.gemm_w8a8(a8, asc, w, wsc, out=out)
+    else:  # a plain copy of known size: 256 MiB read, 256 MiB written
+        src = torch.ones(64 << 20, dtype=torch.float32, device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+    torch.cuda.synchronize()
+    print(f"profiled {which}", flush=True)
+
+
 # ----------------------------------------------------------------------------- CPU baseline
 def cpu_baseline(synth, budget_s: float = 12.0) -> dict:
     """The C oracle's decode GEMV (ggml generic arithmetic) on the host cores,
@@ -213,7 +282,37 @@ def cpu_baseline(synth, budget_s: float = 12.0) -> dict:
     dt = time.perf_counter() - t0
     return {"value": round(total_bytes / dt / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port",
             "sample": f"oracle decode GEMV (ggml generic dot, OpenMP) over TinyLlama layer 0's 7 projections "
-                      f"at M=1 and M=4, {reps} passes in {dt:.1f} s"}
+                      f"at M=1 and M=4, {reps} passes in {dt:.1f} s on {host_cpu()} ({os.cpu_count()} logical CPUs)"}
+
+
+def host_cpu() -> str:
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown CPU"
+
+
+def cpu_baseline_w8a8(synth, budget_s: float = 8.0) -> dict:
+    """The C oracle's W8A8 prefill route (repack + A8 quant + exact i32 GEMM +
+    rescale) on the config-0 workload (Q4_K [5632 x 2048], 128 tokens)."""
+    from oracle import oracle as orc
+
+    threads = min(os.cpu_count() or 1, 16)
+    blocks = synth.kquant(4, 5632, 2048, index=1)
+    a = synth.activations(128, 2048, index=2)
+    reps = 0
+    t0 = time.perf_counter()
+    while time.perf_counter() - t0 < budget_s:
+        orc.matmul_q_w8a8(4, blocks, a, 5632, threads=threads)
+        reps += 1
+    dt = time.perf_counter() - t0
+    ops = 2.0 * 128 * 5632 * 2048 * reps
+    return {"value": round(ops / dt / 1e12, 4), "unit": "int8 TOPS (repack included)", "cores": threads,
+            "kind": "port", "sample": f"oracle W8A8 route, Q4_K 5632x2048 weight x 128 tokens, {reps} runs "
+                                      f"in {dt:.1f} s on {host_cpu()}"}
 
 
 # ----------------------------------------------------------------------------- main
@@ -229,6 +328,9 @@ def main():
 
     assert torch.cuda.is_available(), "bench.py needs a GPU"
     torch.cuda.set_device(0)
+    if args.profile:
+        profile_workload(torch, hip, synth, args.profile)
+        return
 
     ds = DecodeSet(torch, hip, synth, synth.TINYLLAMA_LAYERS)
     torch.cuda.synchronize()
@@ -268,9 +370,9 @@ def main():
                                "shared input (qkv, o, gate+up, down), HIP graph",
                    "layers": synth.TINYLLAMA_LAYERS, "m": [1, 4], "launches_per_step": n_gemv,
                    "bytes_per_step": step_bytes},
-        "roofline": {"bound": "hbm", "kernel": "gemv_kernel<4,*,true> (Q4_K x Q8_K, fused Q8_K quant)",
+        "roofline": {"bound": "hbm", "kernel": "gemv_kernel<4,L,MT,true,D,false,W> (Q4_K x Q8_K, fused Q8_K quant)",
                      "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": measured_traffic("gemv_q4k"),
                      "avg_launch_us": round(q4_us, 3), "bytes_per_launch": q4_bytes // q4_launches},
     }
     if not args.quick:
@@ -282,8 +384,10 @@ def main():
             "prefill_tinyllama_m128": prefill_tok_s(torch, hip, synth, 128, 22),
             "prefill_tinyllama_m512": prefill_tok_s(torch, hip, synth, 512, 22),
         }
+        result["decode_gemv_large_m1"] = decode_large(torch, hip, synth)
     if not (args.quick or args.no_cpu):
         result["cpu_baseline"] = cpu_baseline(synth)
+        result["cpu_baseline_w8a8"] = cpu_baseline_w8a8(synth)
     print(json.dumps(result))
 
 

@@ -149,8 +149,15 @@ template <int BM, int BN, int WM, int WN>
 struct DmaTile {
     static constexpr int T = WM * WN * 64;
     static constexpr int W = WM * WN;
-    static constexpr int A_SEG = BM / 16 / W, B_SEG = BN / 16 / W;  // 1 KiB segments per wave and stage
-    static_assert(A_SEG * W * 16 == BM && B_SEG * W * 16 == BN, "tile rows must split into 16-row segments per wave");
+    // 1 KiB segments (16 rows) per wave and stage. When a tile has fewer
+    // segments than waves, waves load segments twice (the same bytes to the
+    // same LDS place), so every wave issues the same number of loads.
+    static constexpr int A_ROWSEG = BM / 16, B_ROWSEG = BN / 16;
+    static constexpr int A_SEG = A_ROWSEG >= W ? A_ROWSEG / W : 1, B_SEG = B_ROWSEG >= W ? B_ROWSEG / W : 1;
+    static_assert(BM % 16 == 0 && BN % 16 == 0, "tile rows must split into 16-row segments");
+    static_assert((B_ROWSEG >= W ? B_SEG * W == B_ROWSEG : W % B_ROWSEG == 0) &&
+                      (A_ROWSEG >= W ? A_SEG * W == A_ROWSEG : W % A_ROWSEG == 0),
+                  "segments split evenly over the waves");
 };
 
 // s_waitcnt with only vmcnt constrained (gfx9 encoding: vmcnt[3:0] | expcnt[6:4]
@@ -216,13 +223,13 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_w8a8_dma_kernel(
     const int8_t* bsrc[Cfg::B_SEG];
 #pragma unroll
     for (int q = 0; q < Cfg::A_SEG; ++q) {
-        const int r = (wave * Cfg::A_SEG + q) * 16 + (lane >> 2);
+        const int r = ((wave * Cfg::A_SEG + q) % Cfg::A_ROWSEG) * 16 + (lane >> 2);
         const int c = (lane & 3) ^ ((r >> 1) & 3);
         asrc[q] = a8 + static_cast<int64_t>(min(m0 + r, m - 1)) * lda + c * 16;
     }
 #pragma unroll
     for (int q = 0; q < Cfg::B_SEG; ++q) {
-        const int r = (wave * Cfg::B_SEG + q) * 16 + (lane >> 2);
+        const int r = ((wave * Cfg::B_SEG + q) % Cfg::B_ROWSEG) * 16 + (lane >> 2);
         const int c = (lane & 3) ^ ((r >> 1) & 3);
         bsrc[q] = w8 + static_cast<int64_t>(min(n0 + r, n - 1)) * ldw + c * 16;
     }
@@ -230,9 +237,11 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_w8a8_dma_kernel(
         int8_t* la = stage_a(st);
         int8_t* lb = stage_b(st);
 #pragma unroll
-        for (int q = 0; q < Cfg::A_SEG; ++q) dma16(asrc[q] + kt * kBK, la + (wave * Cfg::A_SEG + q) * 1024);
+        for (int q = 0; q < Cfg::A_SEG; ++q)
+            dma16(asrc[q] + kt * kBK, la + ((wave * Cfg::A_SEG + q) % Cfg::A_ROWSEG) * 1024);
 #pragma unroll
-        for (int q = 0; q < Cfg::B_SEG; ++q) dma16(bsrc[q] + kt * kBK, lb + (wave * Cfg::B_SEG + q) * 1024);
+        for (int q = 0; q < Cfg::B_SEG; ++q)
+            dma16(bsrc[q] + kt * kBK, lb + ((wave * Cfg::B_SEG + q) % Cfg::B_ROWSEG) * 1024);
     };
 
     v16i acc[FM][FN];
@@ -308,12 +317,13 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_w8a8_dma_kernel(
         mfma_half(set, H0{});
         mfma_half(set, H1{});
         constexpr int READS = 2 * (FM + FN), MFMAS = 2 * FM * FN;
-        static_assert(READS % PER_STAGE == 0 && MFMAS % PER_STAGE == 0, "schedule groups split evenly");
+        if constexpr (READS % PER_STAGE == 0 && MFMAS % PER_STAGE == 0) {
 #pragma unroll
-        for (int q = 0; q < PER_STAGE; ++q) {
-            __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);                  // VMEM read (direct load)
-            __builtin_amdgcn_sched_group_barrier(0x100, READS / PER_STAGE, 0);  // DS read
-            __builtin_amdgcn_sched_group_barrier(0x008, MFMAS / PER_STAGE, 0);  // MFMA
+            for (int q = 0; q < PER_STAGE; ++q) {
+                __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);                  // VMEM read (direct load)
+                __builtin_amdgcn_sched_group_barrier(0x100, READS / PER_STAGE, 0);  // DS read
+                __builtin_amdgcn_sched_group_barrier(0x008, MFMAS / PER_STAGE, 0);  // MFMA
+            }
         }
     };
     const int KT4 = KT & ~(kStages - 1);
@@ -333,12 +343,15 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_w8a8_dma_kernel(
     __builtin_amdgcn_s_barrier();
 
     // Epilogue. lane l holds column l%32 of each 32x32 fragment, rows
-    // (e%4) + 4*(l/32) + 8*(e/4). Each fragment is scaled, written to a 32x40
-    // f32 tile of the wave's own stage buffer, and read back as 4 rows x 32
-    // columns per pass, so every lane stores 16 contiguous bytes and eight
+    // (e%4) + 4*(l/32) + 8*(e/4). Each fragment is scaled, written to an
+    // HR x 40 f32 tile of the wave's own stage buffer (HR = 32 rows, or 16 in
+    // two passes when the buffer is smaller), and read back 8 rows x 32
+    // columns at a time, so every lane stores 16 contiguous bytes and eight
     // lanes fill a 128-byte row segment.
     constexpr int TS = 40;  // tile row stride in floats: 16-byte aligned rows, rows 4 apart 32 banks apart
-    static_assert(32 * TS * 4 <= BM * kBK, "epilogue tile fits a stage buffer");
+    constexpr int HR = 32 * TS * 4 <= BM * kBK ? 32 : 16;
+    static_assert(HR * TS * 4 <= BM * kBK, "epilogue tile fits a stage buffer");
+    static_assert(WM * WN <= 4, "one stage buffer per wave");
     float* tile = reinterpret_cast<float*>(wave == 0 ? la0 : wave == 1 ? la1 : wave == 2 ? la2 : la3);
     typedef float f4u __attribute__((ext_vector_type(4), aligned(4)));  // scales and outputs: 4-byte alignment
 #pragma unroll
@@ -361,24 +374,29 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_w8a8_dma_kernel(
             const int c0 = n0 + wn * TN + j * 32;
             const float ws = w_scales[min(c0 + (lane & 31), n - 1)];
 #pragma unroll
-            for (int e = 0; e < 16; ++e) {
-                const int lr = (e & 3) + 4 * (lane >> 5) + 8 * (e >> 2);
-                tile[lr * TS + (lane & 31)] = (static_cast<float>(acc[i][j][e]) * rs[e]) * ws;
-            }
-            // same wave: its LDS writes land before its reads
+            for (int h = 0; h < 32 / HR; ++h) {
+                // elements e of rows [h*HR, (h+1)*HR) are e in [h*HR/2, (h+1)*HR/2)
 #pragma unroll
-            for (int t = 0; t < 4; ++t) {
-                const int lr = (lane >> 3) + 8 * t, lc = 4 * (lane & 7);
-                const f4u v = *reinterpret_cast<const f4u*>(tile + lr * TS + lc);
-                const int row = m0 + wm * TM + i * 32 + lr, col = c0 + lc;
-                if (row < m) {
-                    float* dst = out + static_cast<int64_t>(row) * ldo + col;
-                    if (col + 3 < n) {
-                        *reinterpret_cast<f4u*>(dst) = v;
-                    } else {
-                        if (col < n) dst[0] = v.x;
-                        if (col + 1 < n) dst[1] = v.y;
-                        if (col + 2 < n) dst[2] = v.z;
+                for (int e = h * HR / 2; e < (h + 1) * HR / 2; ++e) {
+                    const int lr = (e & 3) + 4 * (lane >> 5) + 8 * (e >> 2) - h * HR;
+                    tile[lr * TS + (lane & 31)] = (static_cast<float>(acc[i][j][e]) * rs[e]) * ws;
+                }
+                // same wave: its LDS writes land before its reads, and its
+                // reads before the next pass's writes
+#pragma unroll
+                for (int t = 0; t < HR / 8; ++t) {
+                    const int lr = (lane >> 3) + 8 * t, lc = 4 * (lane & 7);
+                    const f4u v = *reinterpret_cast<const f4u*>(tile + lr * TS + lc);
+                    const int row = m0 + wm * TM + i * 32 + h * HR + lr, col = c0 + lc;
+                    if (row < m) {
+                        float* dst = out + static_cast<int64_t>(row) * ldo + col;
+                        if (col + 3 < n) {
+                            *reinterpret_cast<f4u*>(dst) = v;
+                        } else {
+                            if (col < n) dst[0] = v.x;
+                            if (col + 1 < n) dst[1] = v.y;
+                            if (col + 2 < n) dst[2] = v.z;
+                        }
                     }
                 }
             }
@@ -386,7 +404,7 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_w8a8_dma_kernel(
 #pragma unroll
                 for (int e = 0; e < 16; ++e) {
                     const int row = rbase + (e & 3) + 8 * (e >> 2), col = c0 + (lane & 31);
-                    if (row < m && col < n) out_i32[row * ldo_i32 + col] = acc[i][j][e];
+                    if (row < m && col < n) out_i32[static_cast<int64_t>(row) * ldo_i32 + col] = acc[i][j][e];
                 }
             }
         }
@@ -415,12 +433,19 @@ int launch_cfg(const int8_t* a8, int64_t lda, const int8_t* w8, int64_t ldw, con
 
 }  // namespace
 
+// Tile choice by M. Up to 32 rows the register-staged kernel (16/32 x 64
+// tiles); up to 256 rows small direct-load tiles, which for M = 128,
+// N = 5632, K = 2048 take 10.3 us against 20.3 us for the register-staged
+// 64x64 tile (the K loop's load latency, not the matrix cores, bounds these);
+// beyond that 256x256 tiles when they make at least one per CU, else 128x128.
 int launch_gemm_w8a8(const int8_t* a8, int64_t lda, const int8_t* w8, int64_t ldw, const float* as,
                      const float* ws, int m, int n, int k, float* out, int64_t ldo, int32_t* oi,
                      int64_t ldoi, hipStream_t stream) {
     if (m <= 16) return launch_cfg<16, 64, 1, 4>(a8, lda, w8, ldw, as, ws, m, n, k, out, ldo, oi, ldoi, stream);
     if (m <= 32) return launch_cfg<32, 64, 1, 4>(a8, lda, w8, ldw, as, ws, m, n, k, out, ldo, oi, ldoi, stream);
-    if (m <= 256) return launch_cfg<64, 64, 2, 2>(a8, lda, w8, ldw, as, ws, m, n, k, out, ldo, oi, ldoi, stream);
+    if (m <= 64) return launch_dma<64, 32, 2, 1>(a8, lda, w8, ldw, as, ws, m, n, k, out, ldo, oi, ldoi, stream);
+    if (m <= 128) return launch_dma<64, 64, 2, 2>(a8, lda, w8, ldw, as, ws, m, n, k, out, ldo, oi, ldoi, stream);
+    if (m <= 256) return launch_dma<128, 64, 4, 1>(a8, lda, w8, ldw, as, ws, m, n, k, out, ldo, oi, ldoi, stream);
     const int64_t big_tiles = static_cast<int64_t>((m + 255) / 256) * ((n + 255) / 256);
     if (big_tiles >= 256) return launch_dma<256, 256, 2, 2>(a8, lda, w8, ldw, as, ws, m, n, k, out, ldo, oi, ldoi, stream);
     return launch_dma<128, 128, 2, 2>(a8, lda, w8, ldw, as, ws, m, n, k, out, ldo, oi, ldoi, stream);

@@ -120,7 +120,10 @@ def _gemm_dev(a8, as_, w8, ws):
                                    (600, 520, 5632), (1, 5632, 2048), (257, 64, 128),
                                    (300, 300, 64),        # one K step: pipeline prologue only
                                    (4096, 4096, 256),     # 256x256 tiles
-                                   (4100, 4000, 192)])    # 256x256 tiles, ragged edges, 3 K steps
+                                   (4100, 4000, 192),     # 256x256 tiles, ragged edges, 3 K steps
+                                   (64, 48, 192),         # 64x32 tiles, half a tile of N past the edge
+                                   (250, 70, 4160),       # 128x32 tiles, K steps not a multiple of 4
+                                   (40, 33, 64)])         # 64x32 tiles, one K step
 def test_gemm_w8a8_bit_exact(m, n, k):
     print(f"gemm m={m} n={n} k={k}", flush=True)
     g = np.random.default_rng(m * 1000 + n + k)
