@@ -80,8 +80,7 @@ __device__ __forceinline__ int wave_or(int v) {
 
 
 // Decode GEMV launch description (kernel (d)): up to four projections that
-// share K and the activation rows. Each workgroup serves one projection:
-// workgroups [wg_end[i-1], wg_end[i]) belong to member i.
+// share K and the activation rows; the launch gives each its own workgroups.
 constexpr int kGemvMaxMembers = 4;
 // LDS bytes per activation row and super-block: quants with a 272-byte block
 // stride, bsums with a 48-byte stride, one f32 scale.
@@ -93,7 +92,6 @@ struct GemvParams {
     float* out[kGemvMaxMembers];
     int64_t ldo[kGemvMaxMembers];
     int64_t rows[kGemvMaxMembers];     // rows (output columns) of each member
-    int64_t wg_end[kGemvMaxMembers];   // cumulative workgroup counts
     int count;
     const float* x;      // f32 activations [m, ldx] (quantised in-kernel), or
     const uint8_t* q8k;  // Q8_K rows, ldx bytes apart

@@ -33,10 +33,6 @@
 namespace rk {
 namespace {
 
-// Waves per workgroup: 16, or 8 where 8 waves per CU cover the launch and one
-// 8-wave pass quantises the activations.
-constexpr int kGemvMaxWaves = 16;
-
 template <int CTRL>
 __device__ __forceinline__ int dpp(int v) {
     return __builtin_amdgcn_mov_dpp(v, CTRL, 0xF, 0xF, false);
@@ -216,21 +212,36 @@ struct Piece<4, L> {
     }
 };
 
-// Q6_K (210 bytes, so only 2-byte aligned; the hardware takes unaligned
-// loads): ql[128], qh[64], 16 int8 scales, f16 d. Unit u (16 ql bytes at 16u,
-// half h = u/4, quarter a = u/2 % 2, c = u % 2) with qh bytes 32h + 16c .. holds
-// values 128h + 32a + 16c + t (low nibbles) and that + 64 (high nibbles), of
-// sub-blocks 8h + 2a + c and 8h + 2a + c + 4. The scale comes with a 32-bit
-// load of bytes 206..209, so that no extension of a 16-bit load result sits
-// between the loads and their use.
+// Q6_K (210 bytes): ql[128], qh[64], 16 int8 scales, f16 d. Unit u (16 ql
+// bytes at 16u, half h = u/4, quarter a = u/2 % 2, c = u % 2) with qh bytes
+// 32h + 16c .. holds values 128h + 32a + 16c + t (low nibbles) and that + 64
+// (high nibbles), of sub-blocks 8h + 2a + c and 8h + 2a + c + 4.
+// Blocks are only 2-byte aligned. The pieces are loaded as 4-byte aligned
+// words from the word boundary at or below the block (sh = 0 or 2 bytes
+// lower), each run of 16-byte pieces with the word that follows it, and
+// shifted into place when used; the last word (bytes 206..209: scales 14-15
+// and d) serves the scales' shift and d. Every load stays inside the block.
+typedef v4u v4u_a4 __attribute__((aligned(4)));
+typedef const __attribute__((address_space(1))) v4u_a4* gv4u_a4;
+typedef uint32_t u32_a2 __attribute__((aligned(2)));
+
+// Bytes sh.. of the 16-byte run v followed by word nx (sh = 0 or 2).
+__device__ __forceinline__ v4u shift_run(const v4u& v, uint32_t nx, uint32_t sh) {
+    return v4u{__builtin_amdgcn_alignbyte(v.y, v.x, sh), __builtin_amdgcn_alignbyte(v.z, v.y, sh),
+               __builtin_amdgcn_alignbyte(v.w, v.z, sh), __builtin_amdgcn_alignbyte(nx, v.w, sh)};
+}
+
 template <int L>
 struct Piece<6, L> {
     static constexpr int NU = 8 / L;
     static constexpr int NH = L == 1 ? 4 : (L == 8 ? 1 : 2);  // qh pieces of the lane's units
     v4u ql[NU];
+    uint32_t ql_next;
     v4u qh[NH];
+    uint32_t qh_next;
     v4u sc;
-    uint32_t d;
+    uint32_t tail;  // bytes 206..209
+    uint32_t sh;
     // first qh piece (index 2h + c) of lane p
     __device__ __forceinline__ static int qh_first(int p) {
         if constexpr (L == 1) return 0;
@@ -239,14 +250,21 @@ struct Piece<6, L> {
         else return 2 * (p >> 2) + (p & 1);
     }
     __device__ __forceinline__ void load(gbytes blk, int p) {
-        typedef uint32_t u32_a2 __attribute__((aligned(2)));
+        sh = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(blk)) & 2u;
+        const gbytes b4 = blk - sh;
+        typedef const __attribute__((address_space(1))) uint32_t* gu32;
 #pragma unroll
-        for (int u = 0; u < NU; ++u) ql[u] = reinterpret_cast<gv4u_a2>(blk)[NU * p + u];
+        for (int u = 0; u < NU; ++u) ql[u] = reinterpret_cast<gv4u_a4>(b4)[NU * p + u];
+        ql_next = reinterpret_cast<gu32>(b4 + 16 * (NU * p + NU))[0];
 #pragma unroll
-        for (int i = 0; i < NH; ++i) qh[i] = reinterpret_cast<gv4u_a2>(blk + 128)[qh_first(p) + i];
-        sc = reinterpret_cast<gv4u_a2>(blk + 192)[0];
-        d = *reinterpret_cast<const __attribute__((address_space(1))) u32_a2*>(blk + 206);
+        for (int i = 0; i < NH; ++i) qh[i] = reinterpret_cast<gv4u_a4>(b4 + 128)[qh_first(p) + i];
+        qh_next = reinterpret_cast<gu32>(b4 + 128 + 16 * (qh_first(p) + NH))[0];
+        sc = reinterpret_cast<gv4u_a4>(b4 + 192)[0];
+        tail = *reinterpret_cast<const __attribute__((address_space(1))) u32_a2*>(blk + 206);
     }
+    __device__ __forceinline__ v4u get_ql(int u) const { return shift_run(ql[u], u + 1 < NU ? ql[u + 1].x : ql_next, sh); }
+    __device__ __forceinline__ v4u get_qh(int i) const { return shift_run(qh[i], i + 1 < NH ? qh[i + 1].x : qh_next, sh); }
+    __device__ __forceinline__ v4u get_sc() const { return shift_run(sc, tail, sh); }
 };
 
 // Sub-block scale/min pairs (2j, 2j+1) of a Q4_K block (ggml get_scale_min_k4).
@@ -315,6 +333,7 @@ template <int L, int MT>
 __device__ __forceinline__ void lane_sums(const Piece<6, L>& k, int p, const Q8Lds& a, int nb, int b, int m,
                                           int (&is)[MT], int (&ms)[MT]) {
     constexpr int NU = Piece<6, L>::NU;
+    const v4u scv = k.get_sc();
 #pragma unroll
     for (int mi = 0; mi < MT; ++mi) { is[mi] = 0; ms[mi] = 0; }
 #pragma unroll
@@ -323,9 +342,10 @@ __device__ __forceinline__ void lane_sums(const Piece<6, L>& k, int p, const Q8L
         const int h = gu >> 2, qa = (gu >> 1) & 1, c = gu & 1;
         const int hq = L == 1 ? 2 * h + c : (L == 8 ? 0 : c);
         const int s0 = 8 * h + 2 * qa + c;
-        const int sc0 = sbyte(k.sc, s0), sc1 = sbyte(k.sc, s0 + 4);
-        const uint32_t ql[4] = {k.ql[u].x, k.ql[u].y, k.ql[u].z, k.ql[u].w};
-        const v4u qhv = k.qh[hq];
+        const int sc0 = sbyte(scv, s0), sc1 = sbyte(scv, s0 + 4);
+        const v4u qlv = k.get_ql(u);
+        const uint32_t ql[4] = {qlv.x, qlv.y, qlv.z, qlv.w};
+        const v4u qhv = k.get_qh(hq);
         const uint32_t qh[4] = {qhv.x, qhv.y, qhv.z, qhv.w};
         const int sh = 2 * qa;
         uint32_t u0[4], u1[4];
@@ -362,19 +382,43 @@ __device__ __forceinline__ void block_scales(const Piece<4, L>& k, float& d, flo
 }
 template <int L>
 __device__ __forceinline__ void block_scales(const Piece<6, L>& k, float& d, float& dmin) {
-    d = f16_bits_to_f32(static_cast<uint16_t>(k.d >> 16));
+    d = f16_bits_to_f32(static_cast<uint16_t>(k.tail >> 16));
     dmin = 0.0f;
 }
 
 // A slot's block: row group `gi`, iteration `it` inside the group.
 struct Pos {
-    int64_t gi;
+    int gi;
     int it;
+};
+
+// Kernel arguments, derived on the host from GemvParams: 32-bit counts and
+// per-member row-group totals, so the kernel's set-up is one round of scalar
+// loads and a few selects, with no 64-bit division.
+struct GemvMember {
+    const uint8_t* w;
+    float* out;
+    int ldo;
+    int rows;
+    int groups;  // row groups of this member
+    int wg_end;  // cumulative workgroup count
+};
+struct GemvArgs {
+    GemvMember mb[kGemvMaxMembers];
+    const float* x;      // fused: f32 activations, ldx floats apart
+    const uint8_t* q8k;  // else: Q8_K rows, ldx bytes apart
+    int32_t* isum;
+    int32_t* msum;
+    int ldx;
+    int m;
+    int nb;
+    int log2g;
+    int iters;
 };
 
 // SUMS: also write every block's exact integer sums (p.isum / p.msum).
 template <int KIND, int L, int MT, bool FUSED, int D, bool SUMS, int W>
-__global__ __launch_bounds__(W * 64) void gemv_kernel(const GemvParams p) {
+__global__ __launch_bounds__(W * 64) void gemv_kernel(const GemvArgs p) {
     constexpr int BB = block_bytes(KIND);
     constexpr int SW = 64 / L;  // block slots per wave
     constexpr int LOG2L = L == 1 ? 0 : L == 2 ? 1 : L == 4 ? 2 : 3;
@@ -385,14 +429,19 @@ __global__ __launch_bounds__(W * 64) void gemv_kernel(const GemvParams p) {
     const int nb = p.nb, m = p.m, iters = p.iters, log2g = p.log2g;
     const Q8Lds a = q8_lds(smem, MT, nb);
 
-    // the projection this workgroup serves (wave-uniform)
-    const int64_t wg = blockIdx.x;
-    const uint8_t* w = p.w[0];
-    float* out = p.out[0];
-    int64_t ldo = p.ldo[0], rows = p.rows[0], wg0 = 0, wg1 = p.wg_end[0];
-    if (p.count > 1 && wg >= p.wg_end[0]) { w = p.w[1]; out = p.out[1]; ldo = p.ldo[1]; rows = p.rows[1]; wg0 = p.wg_end[0]; wg1 = p.wg_end[1]; }
-    if (p.count > 2 && wg >= p.wg_end[1]) { w = p.w[2]; out = p.out[2]; ldo = p.ldo[2]; rows = p.rows[2]; wg0 = p.wg_end[1]; wg1 = p.wg_end[2]; }
-    if (p.count > 3 && wg >= p.wg_end[2]) { w = p.w[3]; out = p.out[3]; ldo = p.ldo[3]; rows = p.rows[3]; wg0 = p.wg_end[2]; wg1 = p.wg_end[3]; }
+    // The projection this workgroup serves (wave-uniform). Every member's
+    // fields are read unconditionally and selected, so the arguments arrive
+    // in one round of scalar loads; unused members repeat the last one.
+    const int wg = blockIdx.x;
+    const bool c1 = wg >= p.mb[0].wg_end, c2 = wg >= p.mb[1].wg_end, c3 = wg >= p.mb[2].wg_end;
+    auto pick = [&](auto v0, auto v1, auto v2, auto v3) { return c3 ? v3 : c2 ? v2 : c1 ? v1 : v0; };
+    const uint8_t* w = pick(p.mb[0].w, p.mb[1].w, p.mb[2].w, p.mb[3].w);
+    float* out = pick(p.mb[0].out, p.mb[1].out, p.mb[2].out, p.mb[3].out);
+    const int ldo = pick(p.mb[0].ldo, p.mb[1].ldo, p.mb[2].ldo, p.mb[3].ldo);
+    const int rows = pick(p.mb[0].rows, p.mb[1].rows, p.mb[2].rows, p.mb[3].rows);
+    const int groups = pick(p.mb[0].groups, p.mb[1].groups, p.mb[2].groups, p.mb[3].groups);
+    const int wg0 = pick(0, p.mb[0].wg_end, p.mb[1].wg_end, p.mb[2].wg_end);
+    const int wg1 = pick(p.mb[0].wg_end, p.mb[1].wg_end, p.mb[2].wg_end, p.mb[3].wg_end);
     const gbytes wg_w = reinterpret_cast<gbytes>(reinterpret_cast<uint64_t>(w));
     const gfloats wg_out = reinterpret_cast<gfloats>(reinterpret_cast<uint64_t>(out));
 
@@ -402,12 +451,9 @@ __global__ __launch_bounds__(W * 64) void gemv_kernel(const GemvParams p) {
     const int rs = sl >> log2g;                          // row inside the row group
     const int rows_per_group = SW >> log2g;
     const int64_t row_bytes = static_cast<int64_t>(nb) * BB;
-    const int64_t groups = (rows + rows_per_group - 1) / rows_per_group;
-    const int64_t wave_gid = (wg - wg0) * W + wave;
-    const int64_t wave_stride = (wg1 - wg0) * W;
-    // this wave's blocks: row groups wave_gid + i*wave_stride, `iters` per slot each
-    const int64_t my_groups = wave_gid < groups ? (groups - 1 - wave_gid) / wave_stride + 1 : 0;
-    const int64_t S = my_groups * iters;
+    // this wave's row groups: wave_gid, wave_gid + wave_stride, ... below `groups`
+    const int wave_gid = (wg - wg0) * W + wave;
+    const int wave_stride = (wg1 - wg0) * W;
 
     auto advance = [=](Pos& q) {
         if (++q.it == iters) { q.it = 0; q.gi += wave_stride; }
@@ -416,34 +462,43 @@ __global__ __launch_bounds__(W * 64) void gemv_kernel(const GemvParams p) {
     // block of the wave's first row group (in bounds, cache-resident) and
     // ignores it. Branch-free load sequences let the wait-count pass wait for
     // exactly the loads a value depends on.
-    const int64_t home_row = min(wave_gid * rows_per_group + rs, rows - 1);
+    const int home_row = min(wave_gid * rows_per_group + rs, rows - 1);
     const int home_b = min(gl, nb - 1);
-    auto load_block = [=](const Pos& q, bool in_range, Piece<KIND, L>& k) {
-        int64_t row = q.gi * rows_per_group + rs;
+    auto load_block = [=](const Pos& q, Piece<KIND, L>& k) {
+        int row = q.gi * rows_per_group + rs;
         int b = gl + q.it * G;
-        if (!(in_range && row < rows && b < nb)) {
+        if (!(q.gi < groups && row < rows && b < nb)) {
             row = home_row;
             b = home_b;
         }
-        k.load(wg_w + row * row_bytes + static_cast<int64_t>(b) * BB, pc);
+        k.load(wg_w + row * row_bytes + b * BB, pc);
     };
 
-    // Fused activations: the waves that own quantisation blocks issue their
-    // activation loads, then one barrier (which also publishes the cleared
-    // q8_ready) puts those loads ahead of every weight load of the workgroup.
-    // The owners quantise and count themselves in q8_ready; every wave issues
-    // its weight loads and waits for that count. Only the owners' progress
-    // gates the rest, so no wave waits for another wave's weight loads to be
-    // issued (a barrier after them would, and under a saturated memory pipe
-    // that costs microseconds).
+    // Issue order: the owners of quantisation blocks load their activations
+    // first, then every wave loads its first D weight blocks, so the weights
+    // are in flight during the set-up below, and an owner's wait for its
+    // activations (an in-order count) does not include its weight loads.
+    // One barrier then publishes the cleared q8_ready; the owners quantise
+    // and count themselves in it; every wave waits for that count. Only the
+    // owners' progress gates the rest, so no wave waits for another wave's
+    // weight loads.
     const int quant_waves = FUSED ? min(W, (m * nb + 3) / 4) : 0;
     const bool quant_wave = wave < quant_waves;
+    float4 xfirst[4];
     if constexpr (FUSED) {
-        float4 xfirst[4];
         if (quant_wave) {
             const int qslot = threadIdx.x >> 4;
             load_x16(p.x, p.ldx, nb, qslot < m * nb ? qslot : 0, xfirst);
         }
+    }
+    Piece<KIND, L> buf[D];
+    Pos lq{wave_gid, 0};  // next block to load
+#pragma unroll
+    for (int j = 0; j < D; ++j) {
+        load_block(lq, buf[j]);
+        advance(lq);
+    }
+    if constexpr (FUSED) {
         if (threadIdx.x == 0) q8_ready = 0;
         __syncthreads();
         if (quant_wave) {
@@ -451,15 +506,6 @@ __global__ __launch_bounds__(W * 64) void gemv_kernel(const GemvParams p) {
             __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
             if (lane == 0) __hip_atomic_fetch_add(&q8_ready, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
         }
-    }
-    Piece<KIND, L> buf[D];
-    Pos lq{wave_gid, 0};  // next block to load
-#pragma unroll
-    for (int j = 0; j < D; ++j) {
-        load_block(lq, j < S, buf[j]);
-        advance(lq);
-    }
-    if constexpr (FUSED) {
         // Every wave (owners too: each reads all blocks) waits for the count.
         // Bounded for safety only: the owners depend on nothing but their own
         // activation loads, so the count arrives.
@@ -478,12 +524,11 @@ __global__ __launch_bounds__(W * 64) void gemv_kernel(const GemvParams p) {
     for (int mi = 0; mi < MT; ++mi) acc[mi] = 0.0f;
 
     Pos cq{wave_gid, 0};  // block being multiplied
-    for (int64_t base = 0; base < S; base += D) {
+    while (cq.gi < groups) {
 #pragma unroll
         for (int j = 0; j < D; ++j) {
-            const int64_t s = base + j;
-            const bool live = s < S;  // uniform across the wave
-            const int64_t row = cq.gi * rows_per_group + rs;
+            const bool live = cq.gi < groups;  // uniform across the wave
+            const int row = cq.gi * rows_per_group + rs;
             const int b = gl + cq.it * G;
             const bool have = row < rows && b < nb;  // uniform inside each block's L lanes
             if (live) {
@@ -511,7 +556,7 @@ __global__ __launch_bounds__(W * 64) void gemv_kernel(const GemvParams p) {
                 }
             }
             // refill this slot with the block D ahead
-            load_block(lq, s + D < S, buf[j]);
+            load_block(lq, buf[j]);
             advance(lq);
             if (live && cq.it == iters - 1) {
                 // row group done: add each row's G slot sums and store
@@ -537,17 +582,21 @@ constexpr int max_depth() {
 }
 
 template <int KIND, int L, int MT, bool FUSED, bool SUMS, int W>
-void launch_mt(const GemvParams& p, int d, dim3 grid, size_t lds, hipStream_t stream) {
-    constexpr int DM = SUMS ? 1 : (MT == 8 ? (max_depth<KIND, L>() > 1 ? max_depth<KIND, L>() / 2 : 1)
-                                           : max_depth<KIND, L>());
+void launch_mt(const GemvArgs& p, int d, dim3 grid, size_t lds, hipStream_t stream) {
+    // eight activation rows, and Q6_K at four rows and L = 2 within 128
+    // VGPRs, hold half the blocks in flight
+    constexpr bool HALF = MT == 8 || (MT == 4 && KIND == 6 && L == 2 && W == 16);
+    constexpr int DM = SUMS ? 1 : (HALF ? (max_depth<KIND, L>() > 1 ? max_depth<KIND, L>() / 2 : 1)
+                                        : max_depth<KIND, L>());
     const dim3 block(W * 64);
-    if (DM >= 4 && d >= 3) gemv_kernel<KIND, L, MT, FUSED, (DM >= 4 ? 4 : 1), SUMS, W><<<grid, block, lds, stream>>>(p);
+    if (DM >= 4 && d >= 4) gemv_kernel<KIND, L, MT, FUSED, (DM >= 4 ? 4 : 1), SUMS, W><<<grid, block, lds, stream>>>(p);
+    else if (DM >= 4 && d == 3) gemv_kernel<KIND, L, MT, FUSED, (DM >= 4 ? 3 : 1), SUMS, W><<<grid, block, lds, stream>>>(p);
     else if (DM >= 2 && d >= 2) gemv_kernel<KIND, L, MT, FUSED, (DM >= 2 ? 2 : 1), SUMS, W><<<grid, block, lds, stream>>>(p);
     else gemv_kernel<KIND, L, MT, FUSED, 1, SUMS, W><<<grid, block, lds, stream>>>(p);
 }
 
 template <int KIND, int L, bool FUSED, bool SUMS, int W>
-void launch_w(const GemvParams& p, int mt, int d, dim3 grid, size_t lds, hipStream_t stream) {
+void launch_w(const GemvArgs& p, int mt, int d, dim3 grid, size_t lds, hipStream_t stream) {
     switch (mt) {
     case 1: launch_mt<KIND, L, 1, FUSED, SUMS, W>(p, d, grid, lds, stream); break;
     case 2: launch_mt<KIND, L, 2, FUSED, SUMS, W>(p, d, grid, lds, stream); break;
@@ -561,7 +610,7 @@ void launch_w(const GemvParams& p, int mt, int d, dim3 grid, size_t lds, hipStre
 
 // 8-wave workgroups serve fused launches only.
 template <int KIND, int L, bool FUSED, bool SUMS>
-void launch_l(const GemvParams& p, int w, int mt, int d, dim3 grid, size_t lds, hipStream_t stream) {
+void launch_l(const GemvArgs& p, int w, int mt, int d, dim3 grid, size_t lds, hipStream_t stream) {
     if constexpr (FUSED && !SUMS) {
         if (w == 8) return launch_w<KIND, L, FUSED, SUMS, 8>(p, mt, d, grid, lds, stream);
     }
@@ -610,14 +659,22 @@ int launch_kind(GemvParams& p, hipStream_t stream) {
         for (int i = 0; i < p.count; ++i) n += (p.rows[i] + rpg - 1) / rpg;
         return n;
     };
-    // Lanes per block: the fewest that still give half of the device's waves
-    // a row group (eight activation rows: at most 2, more would spill).
+    // Lanes per block L and waves per workgroup W. Where some L >= 2 gives
+    // every row group a wave of its own (one round trip per wave), take the
+    // largest such L (the most contiguous loads), with 8-wave workgroups if
+    // they suffice, else 16. Otherwise (several row groups per wave) L = 4
+    // and 8 waves. Eight activation rows allow L <= 2 (more would spill);
+    // the exact-sums path runs L = 1 and 16 waves; 8-wave workgroups serve
+    // fused launches only.
     const int max_l = sums ? 1 : mt == 8 ? 2 : 8;
-    int L = 1;
-    while (L < max_l && row_groups(L) * 2 < static_cast<int64_t>(cus) * kGemvMaxWaves) L <<= 1;
-    // One workgroup per CU: 8 waves where that covers the row groups and one
-    // 8-wave pass quantises the activations, else 16.
-    const int W = FUSED && !sums && p.m * p.nb <= 32 && row_groups(L) <= static_cast<int64_t>(cus) * 8 ? 8 : 16;
+    const bool w8_ok = FUSED && !sums;
+    const int64_t slots8 = static_cast<int64_t>(cus) * 8, slots16 = static_cast<int64_t>(cus) * 16;
+    int L = 0, W = 16;
+    for (int l = max_l; l >= 2 && L == 0; l >>= 1)
+        if (w8_ok && row_groups(l) <= slots8) { L = l; W = 8; }
+    for (int l = max_l; l >= 2 && L == 0; l >>= 1)
+        if (row_groups(l) <= slots16) { L = l; W = 16; }
+    if (L == 0) { L = std::min(4, max_l); W = w8_ok ? 8 : 16; }
     const int64_t max_wgs = cus;
     const int64_t rows_per_group = 64 / L / G;
     // Workgroups: at most one per CU and one per W row groups, split between
@@ -626,28 +683,44 @@ int launch_kind(GemvParams& p, hipStream_t stream) {
     int64_t total_groups = 0;
     for (int i = 0; i < p.count; ++i) total_groups += (p.rows[i] + rows_per_group - 1) / rows_per_group;
     const int64_t budget = std::max<int64_t>(p.count, std::min<int64_t>(max_wgs, (total_groups + W - 1) / W));
+    GemvArgs ka{};
     int64_t wgs = 0, per_wave = 1;
     for (int i = 0; i < p.count; ++i) {
         const int64_t groups = (p.rows[i] + rows_per_group - 1) / rows_per_group;
         int64_t n = (budget * groups + total_groups / 2) / total_groups;
         n = std::max<int64_t>(1, std::min(n, (groups + W - 1) / W));
         wgs += n;
-        p.wg_end[i] = wgs;
         per_wave = std::max(per_wave, (groups + n * W - 1) / (n * W) * p.iters);
+        // the kernel's row, output and group arithmetic is 32-bit
+        if (p.rows[i] > INT32_MAX / 2 || p.ldo[i] > INT32_MAX || p.ldo[i] * (p.m - 1) + p.rows[i] > INT32_MAX)
+            return kStatusInvalid;
+        ka.mb[i] = GemvMember{p.w[i], p.out[i], static_cast<int>(p.ldo[i]), static_cast<int>(p.rows[i]),
+                              static_cast<int>(groups), static_cast<int>(wgs)};
     }
+    if (p.ldx > INT32_MAX / 8 || wgs * W > INT32_MAX / 2) return kStatusInvalid;
+    for (int i = p.count; i < kGemvMaxMembers; ++i) ka.mb[i] = ka.mb[p.count - 1];
+    ka.x = p.x;
+    ka.q8k = p.q8k;
+    ka.isum = p.isum;
+    ka.msum = p.msum;
+    ka.ldx = static_cast<int>(p.ldx);
+    ka.m = p.m;
+    ka.nb = p.nb;
+    ka.log2g = p.log2g;
+    ka.iters = p.iters;
     const int d = static_cast<int>(std::min<int64_t>(per_wave, 4));
     const size_t lds = static_cast<size_t>(mt) * p.nb * kGemvLdsPerBlock;
     const dim3 grid(static_cast<unsigned>(wgs));
     if (sums) {
-        if constexpr (!FUSED) launch_l<KIND, 1, FUSED, true>(p, W, mt, d, grid, lds, stream);
+        if constexpr (!FUSED) launch_l<KIND, 1, FUSED, true>(ka, W, mt, d, grid, lds, stream);
     } else if (L == 1) {
-        launch_l<KIND, 1, FUSED, false>(p, W, mt, d, grid, lds, stream);
+        launch_l<KIND, 1, FUSED, false>(ka, W, mt, d, grid, lds, stream);
     } else if (L == 2) {
-        launch_l<KIND, 2, FUSED, false>(p, W, mt, d, grid, lds, stream);
+        launch_l<KIND, 2, FUSED, false>(ka, W, mt, d, grid, lds, stream);
     } else if (L == 4) {
-        launch_l<KIND, 4, FUSED, false>(p, W, mt, d, grid, lds, stream);
+        launch_l<KIND, 4, FUSED, false>(ka, W, mt, d, grid, lds, stream);
     } else {
-        launch_l<KIND, 8, FUSED, false>(p, W, mt, d, grid, lds, stream);
+        launch_l<KIND, 8, FUSED, false>(ka, W, mt, d, grid, lds, stream);
     }
     return hipGetLastError() == hipSuccess ? kStatusOk : kStatusExec;
 }
