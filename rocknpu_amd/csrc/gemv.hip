@@ -118,64 +118,95 @@ __device__ __forceinline__ void load_x16(const float* __restrict__ x, int64_t ld
     for (int t = 0; t < 4; ++t) f[t] = src[t];
 }
 
-// Q8_K quantisation of rows [0, m) of x into LDS (ggml quantize_row_q8_K_ref
-// semantics, see quant.hip): 16 lanes per block, 16 values per lane, run by
-// the first waves of the workgroup. `first` holds this lane's values of its
-// first block.
-template <int THREADS>
-__device__ __forceinline__ void quantize_to_lds(const float* __restrict__ x, int64_t ldx, int m, int nb,
-                                                const float4 (&first)[4], const Q8Lds& a) {
+// Q8_K quantisation of one 256-value block (ggml quantize_row_q8_K_ref
+// semantics, see quant.hip) by 16 lanes, 16 values per lane, into LDS.
+//   max = the first value of largest magnitude; iscale = -127/max;
+//   q = min(127, nearest(iscale * x)); d = 1/iscale; bsums = sums of 16 q.
+// The block's largest and smallest values give the magnitude and, unless a
+// value and its negation both reach it (then the first one is searched
+// for), the sign of max. |iscale * x| <= 127 (1 + 2^-24)^2 < 127.5, so q is
+// in [-127, 127] and the min(127, .) never binds; q + 128 in [1, 255] is
+// packed to bytes by v_cvt_pk_u8_f32 and flipped back to two's complement.
+__device__ __forceinline__ void quantize_block_to_lds(const float4 (&f)[4], int qb, const Q8Lds& a) {
     const int sub = threadIdx.x & 15;
-    const int slot = threadIdx.x >> 4;
-    for (int qb = slot; qb < m * nb; qb += THREADS / 16) {
-        float4 f[4];
-        if (qb == slot) {
+    float v[16];
 #pragma unroll
-            for (int t = 0; t < 4; ++t) f[t] = first[t];
-        } else {
-            load_x16(x, ldx, nb, qb, f);
-        }
-        float v[16];
+    for (int t = 0; t < 4; ++t) {
+        v[4 * t] = f[t].x; v[4 * t + 1] = f[t].y; v[4 * t + 2] = f[t].z; v[4 * t + 3] = f[t].w;
+    }
+    float vmax = v[0], vmin = v[0];
 #pragma unroll
-        for (int t = 0; t < 4; ++t) {
-            v[4 * t] = f[t].x; v[4 * t + 1] = f[t].y; v[4 * t + 2] = f[t].z; v[4 * t + 3] = f[t].w;
-        }
-        float amax = 0.0f;
-        int first_i = 0;
-        bool neg = false;
+    for (int i = 1; i < 16; ++i) {
+        vmax = fmaxf(vmax, v[i]);
+        vmin = fminf(vmin, v[i]);
+    }
+    // both reductions interleaved, so the DPP moves do not wait on each other
+    vmax = fmaxf(vmax, __int_as_float(dpp<kDppXor1>(__float_as_int(vmax))));
+    vmin = fminf(vmin, __int_as_float(dpp<kDppXor1>(__float_as_int(vmin))));
+    vmax = fmaxf(vmax, __int_as_float(dpp<kDppXor2>(__float_as_int(vmax))));
+    vmin = fminf(vmin, __int_as_float(dpp<kDppXor2>(__float_as_int(vmin))));
+    vmax = fmaxf(vmax, __int_as_float(dpp<kDppMirror8>(__float_as_int(vmax))));
+    vmin = fminf(vmin, __int_as_float(dpp<kDppMirror8>(__float_as_int(vmin))));
+    vmax = fmaxf(vmax, __int_as_float(dpp<kDppMirror16>(__float_as_int(vmax))));
+    vmin = fminf(vmin, __int_as_float(dpp<kDppMirror16>(__float_as_int(vmin))));
+    const float gmax = fmaxf(fmaxf(vmax, -vmin), 0.0f);
+    const bool both = vmax == gmax && vmin == -gmax && gmax > 0.0f;
+    float mx = vmin == -gmax ? -gmax : gmax;
+    if (__any(both)) {  // a value and its negation both reach the magnitude: the first one wins
+        int first = 0x7fffffff;
+#pragma unroll
+        for (int i = 15; i >= 0; --i)
+            if (fabsf(v[i]) == gmax) first = (16 * sub + i) * 2 + (v[i] < 0.0f ? 1 : 0);
+        first = min16(first);
+        if (both) mx = (first & 1) ? -gmax : gmax;
+    }
+    uint32_t wq[4] = {0, 0, 0, 0};
+    float qs = 0.0f;
+    float d = 0.0f;
+    if (gmax > 0.0f) {
+        const float iscale = -127.0f / mx;
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
-            const float ax = fabsf(v[i]);
-            if (ax > amax) { amax = ax; first_i = i; neg = v[i] < 0.0f; }
+            const float q = __builtin_rintf(iscale * v[i]);
+            qs += q;
+            wq[i >> 2] = __builtin_amdgcn_cvt_pk_u8_f32(q + 128.0f, i & 3, wq[i >> 2]);
         }
-        const float gmax = max16(amax);
-        int key = (amax == gmax && gmax > 0.0f) ? ((16 * sub + first_i) * 2 + (neg ? 1 : 0)) : 0x7fffffff;
-        key = min16(key);
-        int q[16];
-        float d = 0.0f;
-        if (gmax > 0.0f) {
-            const float mx = (key & 1) ? -gmax : gmax;  // the first value of largest magnitude
-            const float iscale = -127.0f / mx;
 #pragma unroll
-            for (int i = 0; i < 16; ++i) q[i] = min(127, static_cast<int>(__builtin_rintf(iscale * v[i])));
-            d = 1.0f / iscale;
-        } else {
-#pragma unroll
-            for (int i = 0; i < 16; ++i) q[i] = 0;
-        }
-        int s = 0;
-        uint32_t wq[4];
-#pragma unroll
-        for (int t = 0; t < 4; ++t) {
-            s += q[4 * t] + q[4 * t + 1] + q[4 * t + 2] + q[4 * t + 3];
-            wq[t] = (q[4 * t] & 0xFF) | (q[4 * t + 1] & 0xFF) << 8 | (q[4 * t + 2] & 0xFF) << 16 |
-                    static_cast<uint32_t>(q[4 * t + 3] & 0xFF) << 24;
-        }
-        *reinterpret_cast<uint4*>(a.qs + qb * kGemvLdsQsStride + 16 * sub) = make_uint4(wq[0], wq[1], wq[2], wq[3]);
-        reinterpret_cast<int16_t*>(a.bs + qb * kGemvLdsBsStride)[sub] = static_cast<int16_t>(s);
-        if (sub == 0) a.d[qb] = d;
+        for (int t = 0; t < 4; ++t) wq[t] ^= 0x80808080u;
+        d = 1.0f / iscale;
     }
+    *reinterpret_cast<uint4*>(a.qs + qb * kGemvLdsQsStride + 16 * sub) = make_uint4(wq[0], wq[1], wq[2], wq[3]);
+    reinterpret_cast<int16_t*>(a.bs + qb * kGemvLdsBsStride)[sub] = static_cast<int16_t>(static_cast<int>(qs));
+    if (sub == 0) a.d[qb] = d;
 }
+
+// Q8_K quantisation of rows [0, m) of x into LDS by the first waves of the
+// workgroup: THREADS/16 blocks per pass. The activations of the first P
+// passes are loaded up front (XPre::issue, before the weight loads), so their
+// latencies overlap; later passes, if any, load as they go.
+template <int THREADS, int P>
+struct XPre {
+    float4 f[P][4];
+    __device__ __forceinline__ void issue(const float* __restrict__ x, int64_t ldx, int m, int nb) {
+        const int slot = threadIdx.x >> 4, last = m * nb - 1;
+#pragma unroll
+        for (int i = 0; i < P; ++i) load_x16(x, ldx, nb, min(slot + i * (THREADS / 16), last), f[i]);
+    }
+    __device__ __forceinline__ void quantize(const float* __restrict__ x, int64_t ldx, int m, int nb,
+                                             const Q8Lds& a) const {
+        const int slot = threadIdx.x >> 4;
+#pragma unroll
+        for (int i = 0; i < P; ++i) {
+            const int qb = slot + i * (THREADS / 16);
+            if (qb < m * nb) quantize_block_to_lds(f[i], qb, a);
+        }
+        for (int qb = slot + P * (THREADS / 16); qb < m * nb; qb += THREADS / 16) {
+            float4 g[4];
+            load_x16(x, ldx, nb, qb, g);
+            quantize_block_to_lds(g, qb, a);
+        }
+    }
+};
 
 // Copy Q8_K rows (292-byte blocks: f32 d, 256 quants, 16 int16 bsums) into
 // the LDS layout, one 32-bit word per thread and step.
@@ -417,7 +448,8 @@ struct GemvArgs {
 };
 
 // SUMS: also write every block's exact integer sums (p.isum / p.msum).
-template <int KIND, int L, int MT, bool FUSED, int D, bool SUMS, int W>
+// QP: activation quantisation passes whose loads are issued up front.
+template <int KIND, int L, int MT, bool FUSED, int D, bool SUMS, int W, int QP>
 __global__ __launch_bounds__(W * 64) void gemv_kernel(const GemvArgs p) {
     constexpr int BB = block_bytes(KIND);
     constexpr int SW = 64 / L;  // block slots per wave
@@ -484,12 +516,9 @@ __global__ __launch_bounds__(W * 64) void gemv_kernel(const GemvArgs p) {
     // weight loads.
     const int quant_waves = FUSED ? min(W, (m * nb + 3) / 4) : 0;
     const bool quant_wave = wave < quant_waves;
-    float4 xfirst[4];
+    XPre<W * 64, QP> xpre;
     if constexpr (FUSED) {
-        if (quant_wave) {
-            const int qslot = threadIdx.x >> 4;
-            load_x16(p.x, p.ldx, nb, qslot < m * nb ? qslot : 0, xfirst);
-        }
+        if (quant_wave) xpre.issue(p.x, p.ldx, m, nb);
     }
     Piece<KIND, L> buf[D];
     Pos lq{wave_gid, 0};  // next block to load
@@ -502,7 +531,7 @@ __global__ __launch_bounds__(W * 64) void gemv_kernel(const GemvArgs p) {
         if (threadIdx.x == 0) q8_ready = 0;
         __syncthreads();
         if (quant_wave) {
-            quantize_to_lds<W * 64>(p.x, p.ldx, m, nb, xfirst, a);
+            xpre.quantize(p.x, p.ldx, m, nb, a);
             __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
             if (lane == 0) __hip_atomic_fetch_add(&q8_ready, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
         }
@@ -581,40 +610,51 @@ constexpr int max_depth() {
     else return L == 1 ? 1 : L == 8 ? 4 : 2;
 }
 
-template <int KIND, int L, int MT, bool FUSED, bool SUMS, int W>
-void launch_mt(const GemvArgs& p, int d, dim3 grid, size_t lds, hipStream_t stream) {
+template <int KIND, int L, int MT, bool FUSED, bool SUMS, int W, int QP>
+void launch_d(const GemvArgs& p, int d, dim3 grid, size_t lds, hipStream_t stream) {
     // eight activation rows, and Q6_K at four rows and L = 2 within 128
     // VGPRs, hold half the blocks in flight
     constexpr bool HALF = MT == 8 || (MT == 4 && KIND == 6 && L == 2 && W == 16);
     constexpr int DM = SUMS ? 1 : (HALF ? (max_depth<KIND, L>() > 1 ? max_depth<KIND, L>() / 2 : 1)
                                         : max_depth<KIND, L>());
     const dim3 block(W * 64);
-    if (DM >= 4 && d >= 4) gemv_kernel<KIND, L, MT, FUSED, (DM >= 4 ? 4 : 1), SUMS, W><<<grid, block, lds, stream>>>(p);
-    else if (DM >= 4 && d == 3) gemv_kernel<KIND, L, MT, FUSED, (DM >= 4 ? 3 : 1), SUMS, W><<<grid, block, lds, stream>>>(p);
-    else if (DM >= 2 && d >= 2) gemv_kernel<KIND, L, MT, FUSED, (DM >= 2 ? 2 : 1), SUMS, W><<<grid, block, lds, stream>>>(p);
-    else gemv_kernel<KIND, L, MT, FUSED, 1, SUMS, W><<<grid, block, lds, stream>>>(p);
+    if (DM >= 4 && d >= 4) gemv_kernel<KIND, L, MT, FUSED, (DM >= 4 ? 4 : 1), SUMS, W, QP><<<grid, block, lds, stream>>>(p);
+    else if (DM >= 4 && d == 3) gemv_kernel<KIND, L, MT, FUSED, (DM >= 4 ? 3 : 1), SUMS, W, QP><<<grid, block, lds, stream>>>(p);
+    else if (DM >= 2 && d >= 2) gemv_kernel<KIND, L, MT, FUSED, (DM >= 2 ? 2 : 1), SUMS, W, QP><<<grid, block, lds, stream>>>(p);
+    else gemv_kernel<KIND, L, MT, FUSED, 1, SUMS, W, QP><<<grid, block, lds, stream>>>(p);
+}
+
+// Activation passes loaded up front: all of them (up to 4) in 8-wave
+// workgroups that quantise more than one pass (their VGPR budget holds
+// them), else the first.
+template <int KIND, int L, int MT, bool FUSED, bool SUMS, int W>
+void launch_mt(const GemvArgs& p, int d, int passes, dim3 grid, size_t lds, hipStream_t stream) {
+    if constexpr (FUSED && W == 8) {
+        if (passes > 1) return launch_d<KIND, L, MT, FUSED, SUMS, W, 4>(p, d, grid, lds, stream);
+    }
+    launch_d<KIND, L, MT, FUSED, SUMS, W, 1>(p, d, grid, lds, stream);
 }
 
 template <int KIND, int L, bool FUSED, bool SUMS, int W>
-void launch_w(const GemvArgs& p, int mt, int d, dim3 grid, size_t lds, hipStream_t stream) {
+void launch_w(const GemvArgs& p, int mt, int d, int passes, dim3 grid, size_t lds, hipStream_t stream) {
     switch (mt) {
-    case 1: launch_mt<KIND, L, 1, FUSED, SUMS, W>(p, d, grid, lds, stream); break;
-    case 2: launch_mt<KIND, L, 2, FUSED, SUMS, W>(p, d, grid, lds, stream); break;
-    case 4: launch_mt<KIND, L, 4, FUSED, SUMS, W>(p, d, grid, lds, stream); break;
+    case 1: launch_mt<KIND, L, 1, FUSED, SUMS, W>(p, d, passes, grid, lds, stream); break;
+    case 2: launch_mt<KIND, L, 2, FUSED, SUMS, W>(p, d, passes, grid, lds, stream); break;
+    case 4: launch_mt<KIND, L, 4, FUSED, SUMS, W>(p, d, passes, grid, lds, stream); break;
     default:
         // eight rows run with L <= 2 only (more lanes per block would spill)
-        if constexpr (L <= 2) launch_mt<KIND, L, 8, FUSED, SUMS, W>(p, d, grid, lds, stream);
+        if constexpr (L <= 2) launch_mt<KIND, L, 8, FUSED, SUMS, W>(p, d, passes, grid, lds, stream);
         break;
     }
 }
 
 // 8-wave workgroups serve fused launches only.
 template <int KIND, int L, bool FUSED, bool SUMS>
-void launch_l(const GemvArgs& p, int w, int mt, int d, dim3 grid, size_t lds, hipStream_t stream) {
+void launch_l(const GemvArgs& p, int w, int mt, int d, int passes, dim3 grid, size_t lds, hipStream_t stream) {
     if constexpr (FUSED && !SUMS) {
-        if (w == 8) return launch_w<KIND, L, FUSED, SUMS, 8>(p, mt, d, grid, lds, stream);
+        if (w == 8) return launch_w<KIND, L, FUSED, SUMS, 8>(p, mt, d, passes, grid, lds, stream);
     }
-    launch_w<KIND, L, FUSED, SUMS, 16>(p, mt, d, grid, lds, stream);
+    launch_w<KIND, L, FUSED, SUMS, 16>(p, mt, d, passes, grid, lds, stream);
 }
 
 // Compute units of the current device (cached per device).
@@ -709,18 +749,19 @@ int launch_kind(GemvParams& p, hipStream_t stream) {
     ka.log2g = p.log2g;
     ka.iters = p.iters;
     const int d = static_cast<int>(std::min<int64_t>(per_wave, 4));
+    const int passes = (p.m * p.nb + W * 4 - 1) / (W * 4);  // 16 lanes per block
     const size_t lds = static_cast<size_t>(mt) * p.nb * kGemvLdsPerBlock;
     const dim3 grid(static_cast<unsigned>(wgs));
     if (sums) {
-        if constexpr (!FUSED) launch_l<KIND, 1, FUSED, true>(ka, W, mt, d, grid, lds, stream);
+        if constexpr (!FUSED) launch_l<KIND, 1, FUSED, true>(ka, W, mt, d, passes, grid, lds, stream);
     } else if (L == 1) {
-        launch_l<KIND, 1, FUSED, false>(ka, W, mt, d, grid, lds, stream);
+        launch_l<KIND, 1, FUSED, false>(ka, W, mt, d, passes, grid, lds, stream);
     } else if (L == 2) {
-        launch_l<KIND, 2, FUSED, false>(ka, W, mt, d, grid, lds, stream);
+        launch_l<KIND, 2, FUSED, false>(ka, W, mt, d, passes, grid, lds, stream);
     } else if (L == 4) {
-        launch_l<KIND, 4, FUSED, false>(ka, W, mt, d, grid, lds, stream);
+        launch_l<KIND, 4, FUSED, false>(ka, W, mt, d, passes, grid, lds, stream);
     } else {
-        launch_l<KIND, 8, FUSED, false>(ka, W, mt, d, grid, lds, stream);
+        launch_l<KIND, 8, FUSED, false>(ka, W, mt, d, passes, grid, lds, stream);
     }
     return hipGetLastError() == hipSuccess ? kStatusOk : kStatusExec;
 }
