@@ -16,8 +16,9 @@
 // per CU, so that quantisation is repeated at most once per CU.
 //
 // Work split: L lanes (1, 2, 4 or 8) share a super-block; lane p of the L
-// takes 16-byte "units" [8p/L, 8(p+1)/L) of the block's 128 quant bytes (plus
-// the scale bytes every lane of the block reads). A wave therefore holds 64/L
+// takes 8/L of the 16-byte "units" of the block's 128 quant bytes (Q4_K:
+// units p, p + L, ..; Q6_K: a contiguous run), plus the scale bytes every
+// lane of the block reads. A wave therefore holds 64/L
 // block slots; G slots share a weight row, and a row group of 64/(L*G) rows
 // takes `iters` = ceil(nb/G) blocks per slot. Waves walk their row groups
 // grid-stride with D blocks of loads in flight per lane. A block's integer
@@ -231,15 +232,18 @@ struct Piece;
 // Q4_K (144 bytes): d|dmin, 12 packed scale bytes, 128 quant bytes. Unit u
 // (16 quant bytes 32j + 16h ..) holds values 64j + 16h + t (low nibbles,
 // sub-block 2j) and 64j + 32 + 16h + t (high nibbles, sub-block 2j + 1).
+// Lane p of the L takes units p, p + L, ..., so each load instruction reads
+// 16 L contiguous bytes of every block.
 template <int L>
 struct Piece<4, L> {
     static constexpr int NU = 8 / L;
     v4u h;
     v4u q[NU];
+    __device__ __forceinline__ static int unit(int p, int u) { return p + L * u; }
     __device__ __forceinline__ void load(gbytes blk, int p) {
         h = reinterpret_cast<gv4u>(blk)[0];
 #pragma unroll
-        for (int u = 0; u < NU; ++u) q[u] = reinterpret_cast<gv4u>(blk)[1 + NU * p + u];
+        for (int u = 0; u < NU; ++u) q[u] = reinterpret_cast<gv4u>(blk)[1 + unit(p, u)];
     }
 };
 
@@ -325,7 +329,7 @@ __device__ __forceinline__ void lane_sums(const Piece<4, L>& k, int p, const Q8L
     for (int mi = 0; mi < MT; ++mi) { is[mi] = 0; ms[mi] = 0; }
 #pragma unroll
     for (int u = 0; u < NU; ++u) {
-        const int gu = NU * p + u;
+        const int gu = Piece<4, L>::unit(p, u);
         const int j = gu >> 1, hh = gu & 1;
         int sc0, sc1, mn0, mn1;
         q4_scales(k.h, j, sc0, sc1, mn0, mn1);
