@@ -1,0 +1,181 @@
+// Device helpers shared by the decode GEMV kernels (gemv.hip, gemv_mfma.hip):
+// DPP reductions over 16-lane rows, the LDS layout of Q8_K activation rows,
+// the in-kernel Q8_K quantisation of f32 activations into it, and the copy of
+// Q8_K rows into it.
+#pragma once
+
+#include "common.h"
+
+namespace rk {
+namespace {
+
+template <int CTRL>
+__device__ __forceinline__ int dpp(int v) {
+    return __builtin_amdgcn_mov_dpp(v, CTRL, 0xF, 0xF, false);
+}
+// DPP controls: quad_perm [1,0,3,2] and [2,3,0,1], row_half_mirror, row_mirror.
+// Applied in this order to a value that is uniform over the lower lane-index
+// bits, they exchange across lane-index bits 0, 1, 2 and 3.
+constexpr int kDppXor1 = 0xB1, kDppXor2 = 0x4E, kDppMirror8 = 0x141, kDppMirror16 = 0x140;
+
+__device__ __forceinline__ float max16(float v) {
+    v = fmaxf(v, __int_as_float(dpp<kDppXor1>(__float_as_int(v))));
+    v = fmaxf(v, __int_as_float(dpp<kDppXor2>(__float_as_int(v))));
+    v = fmaxf(v, __int_as_float(dpp<kDppMirror8>(__float_as_int(v))));
+    return fmaxf(v, __int_as_float(dpp<kDppMirror16>(__float_as_int(v))));
+}
+__device__ __forceinline__ int min16(int v) {
+    v = min(v, dpp<kDppXor1>(v));
+    v = min(v, dpp<kDppXor2>(v));
+    v = min(v, dpp<kDppMirror8>(v));
+    return min(v, dpp<kDppMirror16>(v));
+}
+// Global-memory (address space 1) views keep global loads and stores even for
+// addresses the compiler cannot trace back to a kernel argument.
+typedef const __attribute__((address_space(1))) uint8_t* gbytes;
+typedef __attribute__((address_space(1))) float* gfloats;
+typedef unsigned v4u __attribute__((ext_vector_type(4)));
+typedef v4u v4u_a2 __attribute__((aligned(2)));
+typedef const __attribute__((address_space(1))) v4u* gv4u;
+typedef const __attribute__((address_space(1))) v4u_a2* gv4u_a2;
+
+// Activation rows in LDS (regions sized for MT rows; blk = mi*nb + b):
+//   quants of block blk: 256 bytes at qs + blk * 272
+//   its bsums:           16 x int16 at bs + blk * 48
+//   its scale:           d[blk]
+// The 272- and 48-byte strides put consecutive blocks in different LDS banks.
+struct Q8Lds {
+    uint8_t* qs;
+    uint8_t* bs;
+    float* d;
+    __device__ __forceinline__ const uint8_t* quants(int blk) const { return qs + blk * kGemvLdsQsStride; }
+    __device__ __forceinline__ const int16_t* bsums(int blk) const {
+        return reinterpret_cast<const int16_t*>(bs + blk * kGemvLdsBsStride);
+    }
+};
+
+__device__ __forceinline__ Q8Lds q8_lds(uint8_t* smem, int mt, int nb) {
+    Q8Lds a;
+    a.qs = smem;
+    a.bs = smem + mt * nb * kGemvLdsQsStride;
+    a.d = reinterpret_cast<float*>(a.bs + mt * nb * kGemvLdsBsStride);
+    return a;
+}
+
+// The 16 values of this lane for quantisation block qb.
+__device__ __forceinline__ void load_x16(const float* __restrict__ x, int64_t ldx, int nb, int qb, float4 (&f)[4]) {
+    const int sub = threadIdx.x & 15;
+    const int r = qb / nb, b = qb % nb;
+    const float4* src = reinterpret_cast<const float4*>(x + r * ldx + b * kQK + 16 * sub);
+#pragma unroll
+    for (int t = 0; t < 4; ++t) f[t] = src[t];
+}
+
+// Q8_K quantisation of one 256-value block (ggml quantize_row_q8_K_ref
+// semantics, see quant.hip) by 16 lanes, 16 values per lane, into LDS.
+//   max = the first value of largest magnitude; iscale = -127/max;
+//   q = min(127, nearest(iscale * x)); d = 1/iscale; bsums = sums of 16 q.
+// The block's largest and smallest values give the magnitude and, unless a
+// value and its negation both reach it (then the first one is searched
+// for), the sign of max. |iscale * x| <= 127 (1 + 2^-24)^2 < 127.5, so q is
+// in [-127, 127] and the min(127, .) never binds; q + 128 in [1, 255] is
+// packed to bytes by v_cvt_pk_u8_f32 and flipped back to two's complement.
+__device__ __forceinline__ void quantize_block_to_lds(const float4 (&f)[4], int qb, const Q8Lds& a) {
+    const int sub = threadIdx.x & 15;
+    float v[16];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+        v[4 * t] = f[t].x; v[4 * t + 1] = f[t].y; v[4 * t + 2] = f[t].z; v[4 * t + 3] = f[t].w;
+    }
+    float vmax = v[0], vmin = v[0];
+#pragma unroll
+    for (int i = 1; i < 16; ++i) {
+        vmax = fmaxf(vmax, v[i]);
+        vmin = fminf(vmin, v[i]);
+    }
+    // both reductions interleaved, so the DPP moves do not wait on each other
+    vmax = fmaxf(vmax, __int_as_float(dpp<kDppXor1>(__float_as_int(vmax))));
+    vmin = fminf(vmin, __int_as_float(dpp<kDppXor1>(__float_as_int(vmin))));
+    vmax = fmaxf(vmax, __int_as_float(dpp<kDppXor2>(__float_as_int(vmax))));
+    vmin = fminf(vmin, __int_as_float(dpp<kDppXor2>(__float_as_int(vmin))));
+    vmax = fmaxf(vmax, __int_as_float(dpp<kDppMirror8>(__float_as_int(vmax))));
+    vmin = fminf(vmin, __int_as_float(dpp<kDppMirror8>(__float_as_int(vmin))));
+    vmax = fmaxf(vmax, __int_as_float(dpp<kDppMirror16>(__float_as_int(vmax))));
+    vmin = fminf(vmin, __int_as_float(dpp<kDppMirror16>(__float_as_int(vmin))));
+    const float gmax = fmaxf(fmaxf(vmax, -vmin), 0.0f);
+    const bool both = vmax == gmax && vmin == -gmax && gmax > 0.0f;
+    float mx = vmin == -gmax ? -gmax : gmax;
+    if (__any(both)) {  // a value and its negation both reach the magnitude: the first one wins
+        int first = 0x7fffffff;
+#pragma unroll
+        for (int i = 15; i >= 0; --i)
+            if (fabsf(v[i]) == gmax) first = (16 * sub + i) * 2 + (v[i] < 0.0f ? 1 : 0);
+        first = min16(first);
+        if (both) mx = (first & 1) ? -gmax : gmax;
+    }
+    uint32_t wq[4] = {0, 0, 0, 0};
+    float qs = 0.0f;
+    float d = 0.0f;
+    if (gmax > 0.0f) {
+        const float iscale = -127.0f / mx;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            const float q = __builtin_rintf(iscale * v[i]);
+            qs += q;
+            wq[i >> 2] = __builtin_amdgcn_cvt_pk_u8_f32(q + 128.0f, i & 3, wq[i >> 2]);
+        }
+#pragma unroll
+        for (int t = 0; t < 4; ++t) wq[t] ^= 0x80808080u;
+        d = 1.0f / iscale;
+    }
+    *reinterpret_cast<uint4*>(a.qs + qb * kGemvLdsQsStride + 16 * sub) = make_uint4(wq[0], wq[1], wq[2], wq[3]);
+    reinterpret_cast<int16_t*>(a.bs + qb * kGemvLdsBsStride)[sub] = static_cast<int16_t>(static_cast<int>(qs));
+    if (sub == 0) a.d[qb] = d;
+}
+
+// Q8_K quantisation of rows [0, m) of x into LDS by the first waves of the
+// workgroup: THREADS/16 blocks per pass. The activations of the first P
+// passes are loaded up front (XPre::issue, before the weight loads), so their
+// latencies overlap; later passes, if any, load as they go.
+template <int THREADS, int P>
+struct XPre {
+    float4 f[P][4];
+    __device__ __forceinline__ void issue(const float* __restrict__ x, int64_t ldx, int m, int nb) {
+        const int slot = threadIdx.x >> 4, last = m * nb - 1;
+#pragma unroll
+        for (int i = 0; i < P; ++i) load_x16(x, ldx, nb, min(slot + i * (THREADS / 16), last), f[i]);
+    }
+    __device__ __forceinline__ void quantize(const float* __restrict__ x, int64_t ldx, int m, int nb,
+                                             const Q8Lds& a) const {
+        const int slot = threadIdx.x >> 4;
+#pragma unroll
+        for (int i = 0; i < P; ++i) {
+            const int qb = slot + i * (THREADS / 16);
+            if (qb < m * nb) quantize_block_to_lds(f[i], qb, a);
+        }
+        for (int qb = slot + P * (THREADS / 16); qb < m * nb; qb += THREADS / 16) {
+            float4 g[4];
+            load_x16(x, ldx, nb, qb, g);
+            quantize_block_to_lds(g, qb, a);
+        }
+    }
+};
+
+// Copy Q8_K rows (292-byte blocks: f32 d, 256 quants, 16 int16 bsums) into
+// the LDS layout, one 32-bit word per thread and step.
+template <int THREADS>
+__device__ __forceinline__ void stage_q8k(const uint8_t* __restrict__ q8k, int64_t ldq, int m, int nb,
+                                          const Q8Lds& a) {
+    const int words = m * nb * (kQ8KBytes / 4);
+    for (int i = threadIdx.x; i < words; i += THREADS) {
+        const int blk = i / (kQ8KBytes / 4), wi = i % (kQ8KBytes / 4);
+        const int mi = blk / nb, bi = blk % nb;
+        const uint32_t v = *reinterpret_cast<const uint32_t*>(q8k + mi * ldq + bi * kQ8KBytes + 4 * wi);
+        if (wi == 0) a.d[blk] = __uint_as_float(v);
+        else if (wi <= 64) reinterpret_cast<uint32_t*>(a.qs + blk * kGemvLdsQsStride)[wi - 1] = v;
+        else reinterpret_cast<uint32_t*>(a.bs + blk * kGemvLdsBsStride)[wi - 65] = v;
+    }
+}
+
+}  // namespace
+}  // namespace rk

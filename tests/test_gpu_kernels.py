@@ -226,6 +226,26 @@ def test_gemv_q8_k(kind, n, k, m):
     _gemv_check(kind, n, k, m, index=400 + kind + n + m)
 
 
+@pytest.mark.parametrize("n,k,m", [(16, 256, 2), (40, 1024, 3), (2048, 2048, 4), (130, 5632, 5), (300, 2048, 8),
+                                   (17, 14336, 3), (1000, 4096, 7), (33, 256, 6)])
+def test_gemv_q4k_multi_row(n, k, m):
+    """Q4_K at 2..8 activation rows without the exact-sums outputs (3..8 rows run on the
+    matrix-core kernel) against the oracle: ragged tiles of 16 weight rows, blocks per row
+    not a multiple of 8, padded activation rows."""
+    print(f"gemv multi-row n={n} k={k} m={m}", flush=True)
+    w = synth.kquant(4, n, k, index=800 + n + m)
+    x = synth.activations(m, k, index=801 + k)
+    q8 = orc.quantize_q8_k(x)
+    out = hip.gemv_q8_k(4, _dev(w), k, n, _dev(q8))
+    torch.cuda.synchronize()
+    got = out.cpu().numpy()
+    ref = orc.gemv_q8_k(4, w, k, n, q8, threads=8)
+    for mi in range(m):
+        _, _, mag = orc.gemv_block_sums(4, w, k, n, q8[mi])
+        err = np.abs(got[mi].astype(np.float64) - ref[mi])
+        assert np.all(err <= 1e-5 * mag), f"row {mi}: max err/mag {np.max(err / mag)}"
+
+
 def test_gemv_m_chunking():
     """m above one launch's 8 rows is split into launches; results unchanged."""
     _gemv_check(4, 96, 2048, 13, index=500)
