@@ -15,6 +15,8 @@
 // on the 16-byte chunk index so fragment reads are bank-conflict free.
 #include "common.h"
 
+#include <utility>
+
 #include <type_traits>
 
 namespace rk {
@@ -129,22 +131,17 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_w8a8_kernel(
         }
 }
 
-// Large tiles: the same product with a four-stage pipeline of LDS buffers
-// filled by direct global->LDS loads (global_load_lds_dwordx4, no register
-// staging). Each wave issues its share of a stage as 1 KiB segments (16 rows
-// x 64 bytes; lane i's 16 bytes land at segment + 16*i, so the lane loads the
-// global chunk that the swizzled layout puts there). Stage s+3 is issued while
-// stage s is multiplied; one barrier per K step both publishes stage s (after
-// each wave's own wait for its loads) and frees stage s-1 for reuse. The
-// barrier is a bare s_barrier: a fenced one would wait for every load in
-// flight, stages ahead included.
-constexpr int kStages = 4;
-
-template <int ROWS>
-struct StageBuf {
-    int8_t a[ROWS * kBK];
-};
-
+// Direct-load tiles: the same product with a pipeline of ST (4 or 8) LDS
+// stage buffers filled by direct global->LDS loads (global_load_lds_dwordx4,
+// no register staging). Each wave issues its share of a stage as 1 KiB
+// segments (16 rows x 64 bytes; lane i's 16 bytes land at segment + 16*i, so
+// the lane loads the global chunk that the swizzled layout puts there).
+// Stage s+ST-1 is issued while stage s is multiplied; one barrier per K step
+// both publishes stage s (after each wave's own wait for its loads) and frees
+// stage s-1 for reuse. The barrier is a bare s_barrier: a fenced one would
+// wait for every load in flight, stages ahead included. Small tiles run 8
+// stages: their K steps hold few MFMAs, so more of the load latency must be
+// in flight.
 template <int BM, int BN, int WM, int WN>
 struct DmaTile {
     static constexpr int T = WM * WN * 64;
@@ -174,7 +171,13 @@ __device__ __forceinline__ void dma16(const int8_t* src, int8_t* lds) {
     __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void*)(lds), 16, 0, 0);
 }
 
-template <int BM, int BN, int WM, int WN>
+// Calls f(integral_constant<int, I>) for I in the sequence, in order.
+template <typename F, int... I>
+__device__ __forceinline__ void unroll_seq(F&& f, std::integer_sequence<int, I...>) {
+    (f(std::integral_constant<int, I>{}), ...);
+}
+
+template <int BM, int BN, int WM, int WN, int ST>
 __global__ __launch_bounds__(WM* WN * 64) void gemm_w8a8_dma_kernel(
     const int8_t* __restrict__ a8, int64_t lda, const int8_t* __restrict__ w8, int64_t ldw,
     const float* __restrict__ a_scales, const float* __restrict__ w_scales, int m, int n, int k,
@@ -185,18 +188,29 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_w8a8_dma_kernel(
     // One array per stage, always indexed by a compile-time stage: the
     // wait-count pass then sees which LDS buffer a direct load writes and does
     // not wait for every load in flight before each LDS read.
+    // ST = 4..8 stages; arrays of stages >= ST are unused placeholders.
+    static_assert(ST >= 4 && ST <= 8, "four to eight stage buffers");
+    constexpr int A4 = ST > 4 ? BM * kBK : 16, A5 = ST > 5 ? BM * kBK : 16, A6 = ST > 6 ? BM * kBK : 16,
+                  A7 = ST > 7 ? BM * kBK : 16;
+    constexpr int B4 = ST > 4 ? BN * kBK : 16, B5 = ST > 5 ? BN * kBK : 16, B6 = ST > 6 ? BN * kBK : 16,
+                  B7 = ST > 7 ? BN * kBK : 16;
     __shared__ __align__(16) int8_t la0[BM * kBK], la1[BM * kBK], la2[BM * kBK], la3[BM * kBK];
     __shared__ __align__(16) int8_t lb0[BN * kBK], lb1[BN * kBK], lb2[BN * kBK], lb3[BN * kBK];
-    static_assert(kStages == 4, "four stage buffers");
+    __shared__ __align__(16) int8_t la4[A4], la5[A5], la6[A6], la7[A7];
+    __shared__ __align__(16) int8_t lb4[B4], lb5[B5], lb6[B6], lb7[B7];
     auto stage_a = [&](auto st) -> int8_t* {
         constexpr int S = decltype(st)::value;
         if constexpr (S == 0) return la0; else if constexpr (S == 1) return la1;
-        else if constexpr (S == 2) return la2; else return la3;
+        else if constexpr (S == 2) return la2; else if constexpr (S == 3) return la3;
+        else if constexpr (S == 4) return la4; else if constexpr (S == 5) return la5;
+        else if constexpr (S == 6) return la6; else return la7;
     };
     auto stage_b = [&](auto st) -> int8_t* {
         constexpr int S = decltype(st)::value;
         if constexpr (S == 0) return lb0; else if constexpr (S == 1) return lb1;
-        else if constexpr (S == 2) return lb2; else return lb3;
+        else if constexpr (S == 2) return lb2; else if constexpr (S == 3) return lb3;
+        else if constexpr (S == 4) return lb4; else if constexpr (S == 5) return lb5;
+        else if constexpr (S == 6) return lb6; else return lb7;
     };
 
     // XCD-aware tile order: workgroup b runs on XCD b % 8, so each XCD takes a
@@ -293,16 +307,16 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_w8a8_dma_kernel(
     };
     using R0 = std::integral_constant<int, 0>;
     using R1 = std::integral_constant<int, 1>;
-    issue(S0{}, 0);
-    issue(S1{}, min(1, KT - 1));
-    issue(S2{}, min(2, KT - 1));
-    wait_vm<2 * PER_STAGE>();
+    // prologue: stages 0 .. ST-2 in flight, wait for stage 0, then stage ST-1
+    unroll_seq([&](auto i) { issue(i, min(static_cast<int>(decltype(i)::value), KT - 1)); },
+               std::make_integer_sequence<int, ST - 1>{});
+    wait_vm<(ST - 2) * PER_STAGE>();
     __builtin_amdgcn_s_barrier();
-    issue(S3{}, min(3, KT - 1));
+    issue(std::integral_constant<int, ST - 1>{}, min(ST - 1, KT - 1));
     read_frags(S0{}, R0{});
     // step s: stage s in register set s%2; S1N = stage of s+1
     // Each step is one basic block: the barrier, the direct loads of stage
-    // s+4 and the fragment reads of stage s+1 are spread between the MFMAs of
+    // s+ST and the fragment reads of stage s+1 are spread between the MFMAs of
     // stage s (scheduling groups of one load, its share of the reads and of
     // the MFMAs), so the LDS and memory traffic overlaps the matrix cores
     // instead of stalling them. After the last K step the barrier, loads and reads
@@ -310,9 +324,9 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_w8a8_dma_kernel(
     auto step = [&](auto set, auto next_st, auto refill_st, int kt) {
         using NSET = std::integral_constant<int, 1 - decltype(set)::value>;
         wait_lgkm0();
-        wait_vm<2 * PER_STAGE>();  // stage s+1 done (s+2 and s+3 may be in flight)
+        wait_vm<(ST - 2) * PER_STAGE>();  // stage s+1 done (s+2 .. s+ST-1 may be in flight)
         __builtin_amdgcn_s_barrier();
-        issue(refill_st, min(kt + 4, KT - 1));
+        issue(refill_st, min(kt + ST, KT - 1));
         read_frags(next_st, NSET{});
         mfma_half(set, H0{});
         mfma_half(set, H1{});
@@ -326,16 +340,17 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_w8a8_dma_kernel(
             }
         }
     };
-    const int KT4 = KT & ~(kStages - 1);
-    for (int kt = 0; kt < KT4; kt += kStages) {
-        step(R0{}, S1{}, S0{}, kt);
-        step(R1{}, S2{}, S1{}, kt + 1);
-        step(R0{}, S3{}, S2{}, kt + 2);
-        step(R1{}, S0{}, S3{}, kt + 3);
-    }
-    if (KT4 < KT) step(R0{}, S1{}, S0{}, KT4);
-    if (KT4 + 1 < KT) step(R1{}, S2{}, S1{}, KT4 + 1);
-    if (KT4 + 2 < KT) step(R0{}, S3{}, S2{}, KT4 + 2);
+    // step kt + I: register set I % 2, next stage (I + 1) % ST, refill stage I
+    // (U = ST steps per loop pass, 2 ST when ST is odd, so the register sets alternate)
+    auto step_i = [&](auto i, int kt) {
+        constexpr int I = decltype(i)::value;
+        step(std::integral_constant<int, I % 2>{}, std::integral_constant<int, (I + 1) % ST>{},
+             std::integral_constant<int, I % ST>{}, kt + I);
+    };
+    constexpr int U = ST % 2 == 0 ? ST : 2 * ST;
+    const int KTA = KT - KT % U;
+    for (int kt = 0; kt < KTA; kt += U) unroll_seq([&](auto i) { step_i(i, kt); }, std::make_integer_sequence<int, U>{});
+    unroll_seq([&](auto i) { if (KTA + decltype(i)::value < KT) step_i(i, KTA); }, std::make_integer_sequence<int, U - 1>{});
     // Every wave's direct loads and fragment reads are done before any wave
     // reuses the stage buffers below.
     wait_vm<0>();
@@ -349,10 +364,13 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_w8a8_dma_kernel(
     // columns at a time, so every lane stores 16 contiguous bytes and eight
     // lanes fill a 128-byte row segment.
     constexpr int TS = 40;  // tile row stride in floats: 16-byte aligned rows, rows 4 apart 32 banks apart
-    constexpr int HR = 32 * TS * 4 <= BM * kBK ? 32 : 16;
-    static_assert(HR * TS * 4 <= BM * kBK, "epilogue tile fits a stage buffer");
-    static_assert(WM * WN <= 4, "one stage buffer per wave");
-    float* tile = reinterpret_cast<float*>(wave == 0 ? la0 : wave == 1 ? la1 : wave == 2 ? la2 : la3);
+    // waves 0-3 use stage buffers la0..la3, waves 4-7 lb0..lb3
+    constexpr int BUF = WM * WN > 4 ? (BM < BN ? BM : BN) * kBK : BM * kBK;
+    constexpr int HR = 32 * TS * 4 <= BUF ? 32 : 16;
+    static_assert(HR * TS * 4 <= BUF, "epilogue tile fits a stage buffer");
+    static_assert(WM * WN <= 8, "one stage buffer per wave");
+    float* tile = reinterpret_cast<float*>(wave == 0 ? la0 : wave == 1 ? la1 : wave == 2 ? la2 : wave == 3 ? la3
+                                           : wave == 4 ? lb0 : wave == 5 ? lb1 : wave == 6 ? lb2 : lb3);
     typedef float f4u __attribute__((ext_vector_type(4), aligned(4)));  // scales and outputs: 4-byte alignment
 #pragma unroll
     for (int i = 0; i < FM; ++i) {
@@ -411,12 +429,12 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_w8a8_dma_kernel(
     }
 }
 
-template <int BM, int BN, int WM, int WN>
+template <int BM, int BN, int WM, int WN, int ST>
 int launch_dma(const int8_t* a8, int64_t lda, const int8_t* w8, int64_t ldw, const float* as,
                const float* ws, int m, int n, int k, float* out, int64_t ldo, int32_t* oi,
                int64_t ldoi, hipStream_t stream) {
     const int64_t tiles = static_cast<int64_t>((m + BM - 1) / BM) * ((n + BN - 1) / BN);
-    gemm_w8a8_dma_kernel<BM, BN, WM, WN><<<dim3(static_cast<unsigned>(tiles)), dim3(WM * WN * 64), 0, stream>>>(
+    gemm_w8a8_dma_kernel<BM, BN, WM, WN, ST><<<dim3(static_cast<unsigned>(tiles)), dim3(WM * WN * 64), 0, stream>>>(
         a8, lda, w8, ldw, as, ws, m, n, k, out, ldo, oi, ldoi);
     return hipGetLastError() == hipSuccess ? kStatusOk : kStatusExec;
 }
@@ -443,12 +461,12 @@ int launch_gemm_w8a8(const int8_t* a8, int64_t lda, const int8_t* w8, int64_t ld
                      int64_t ldoi, hipStream_t stream) {
     if (m <= 16) return launch_cfg<16, 64, 1, 4>(a8, lda, w8, ldw, as, ws, m, n, k, out, ldo, oi, ldoi, stream);
     if (m <= 32) return launch_cfg<32, 64, 1, 4>(a8, lda, w8, ldw, as, ws, m, n, k, out, ldo, oi, ldoi, stream);
-    if (m <= 64) return launch_dma<64, 32, 2, 1>(a8, lda, w8, ldw, as, ws, m, n, k, out, ldo, oi, ldoi, stream);
-    if (m <= 128) return launch_dma<64, 64, 2, 2>(a8, lda, w8, ldw, as, ws, m, n, k, out, ldo, oi, ldoi, stream);
-    if (m <= 256) return launch_dma<128, 64, 4, 1>(a8, lda, w8, ldw, as, ws, m, n, k, out, ldo, oi, ldoi, stream);
+    if (m <= 64) return launch_dma<64, 32, 2, 1, 8>(a8, lda, w8, ldw, as, ws, m, n, k, out, ldo, oi, ldoi, stream);
+    if (m <= 128) return launch_dma<64, 64, 2, 2, 8>(a8, lda, w8, ldw, as, ws, m, n, k, out, ldo, oi, ldoi, stream);
+    if (m <= 256) return launch_dma<128, 64, 4, 1, 4>(a8, lda, w8, ldw, as, ws, m, n, k, out, ldo, oi, ldoi, stream);
     const int64_t big_tiles = static_cast<int64_t>((m + 255) / 256) * ((n + 255) / 256);
-    if (big_tiles >= 256) return launch_dma<256, 256, 2, 2>(a8, lda, w8, ldw, as, ws, m, n, k, out, ldo, oi, ldoi, stream);
-    return launch_dma<128, 128, 2, 2>(a8, lda, w8, ldw, as, ws, m, n, k, out, ldo, oi, ldoi, stream);
+    if (big_tiles >= 256) return launch_dma<256, 256, 2, 2, 4>(a8, lda, w8, ldw, as, ws, m, n, k, out, ldo, oi, ldoi, stream);
+    return launch_dma<128, 128, 2, 2, 4>(a8, lda, w8, ldw, as, ws, m, n, k, out, ldo, oi, ldoi, stream);
 }
 
 }  // namespace rk
