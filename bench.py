@@ -370,7 +370,8 @@ def main():
                                "shared input (qkv, o, gate+up, down), HIP graph",
                    "layers": synth.TINYLLAMA_LAYERS, "m": [1, 4], "launches_per_step": n_gemv,
                    "bytes_per_step": step_bytes},
-        "roofline": {"bound": "hbm", "kernel": "gemv_kernel<4,L,MT,true,D,false,W> (Q4_K x Q8_K, fused Q8_K quant)",
+        "roofline": {"bound": "hbm", "kernel": "Q4_K x Q8_K decode GEMV with fused Q8_K quant: gemv_kernel<4,...> "
+                                               "at M=1, gemv_mfma_kernel at M=4",
                      "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": measured_traffic("gemv_q4k"),
                      "avg_launch_us": round(q4_us, 3), "bytes_per_launch": q4_bytes // q4_launches},
