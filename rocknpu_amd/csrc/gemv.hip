@@ -604,14 +604,16 @@ int launch_kind(GemvParams& p, hipStream_t stream) {
 
 }  // namespace
 
-int launch_gemv_mfma(bool fused, GemvParams& p, hipStream_t stream);  // gemv_mfma.hip
+int launch_gemv_mfma(int kind, bool fused, GemvParams& p, hipStream_t stream);  // gemv_mfma.hip
 
 // p.m <= 8 activation rows; LDS holds m * nb * kGemvLdsPerBlock bytes (callers
-// keep it <= 64 KiB). Q4_K with 3..8 rows runs on the matrix cores (faster
-// from 3 rows on: 8.96 against 9.23 us for TinyLlama gate+up at 4 rows, 11.6
-// against 14.3 us at 8), except where the exact per-block sums are asked for.
+// keep it <= 112 KiB). Q4_K with 3..8 rows and Q6_K with 5..8 rows run on the
+// matrix cores, where they are faster (TinyLlama gate+up Q4_K: 8.96 against
+// 9.23 us at 4 rows, 11.6 against 14.3 us at 8; down Q6_K: 13.6 against 20.0
+// us at 6 rows, while at 4 rows the lane-per-block kernel's 11.4 us beats
+// 12.4), except where the exact per-block sums are asked for.
 int launch_gemv(int kind, bool fused, GemvParams& p, hipStream_t stream) {
-    if (kind == 4 && p.m >= 3 && p.isum == nullptr) return launch_gemv_mfma(fused, p, stream);
+    if (p.m >= (kind == 4 ? 3 : 5) && p.isum == nullptr) return launch_gemv_mfma(kind, fused, p, stream);
     if (kind == 4) return fused ? launch_kind<4, true>(p, stream) : launch_kind<4, false>(p, stream);
     if (kind == 6) return fused ? launch_kind<6, true>(p, stream) : launch_kind<6, false>(p, stream);
     return kStatusInvalid;

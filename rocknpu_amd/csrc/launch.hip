@@ -25,7 +25,10 @@ namespace {
 bool aligned(const void* p, uintptr_t a) { return reinterpret_cast<uintptr_t>(p) % a == 0; }
 
 constexpr size_t kMaxGrid = 0x7fffffff;
-constexpr size_t kGemvLdsBytes = 64 * 1024;
+// LDS a decode GEMV workgroup may give the Q8_K activation rows: of the 160
+// KiB of a gfx950 CU, 112 KiB, leaving room for the matrix-core kernel's
+// 16 KiB of partial sums; one workgroup runs per CU either way.
+constexpr size_t kGemvLdsBytes = 112 * 1024;
 
 }  // namespace
 
@@ -78,7 +81,7 @@ extern "C" int rocknpu_hip_quantize_q8_k(const float* x, size_t m, size_t k, siz
 }
 
 // rows per launch: a power of two (the kernel's register tile) whose Q8_K
-// blocks fit the 64 KiB of LDS a workgroup stages them in
+// blocks fit the LDS a workgroup stages them in
 size_t gemv_rows_per_launch(size_t nb) {
     size_t chunk = 8;
     while (chunk > 1 && chunk * nb * rk::kGemvLdsPerBlock > kGemvLdsBytes) chunk >>= 1;

@@ -246,6 +246,27 @@ def test_gemv_q4k_multi_row(n, k, m):
         assert np.all(err <= 1e-5 * mag), f"row {mi}: max err/mag {np.max(err / mag)}"
 
 
+@pytest.mark.parametrize("n,k,m", [(16, 256, 5), (40, 1024, 4), (2048, 5632, 6), (130, 5632, 5), (300, 2048, 8),
+                                   (17, 14336, 7), (1000, 4096, 7), (64, 28672, 8)])
+def test_gemv_q6k_multi_row(n, k, m):
+    """Q6_K at 4..8 activation rows without the exact-sums outputs (5..8 rows run on the
+    matrix-core kernel) against the oracle: ragged tiles, blocks per row not a multiple
+    of 8, odd row lengths (2-byte aligned blocks), padded activation rows, and a K whose
+    activation rows need two launches (112 KiB of LDS)."""
+    print(f"gemv q6k multi-row n={n} k={k} m={m}", flush=True)
+    w = synth.kquant(6, n, k, index=820 + n + m)
+    x = synth.activations(m, k, index=821 + k)
+    q8 = orc.quantize_q8_k(x)
+    out = hip.gemv_q8_k(6, _dev(w), k, n, _dev(q8))
+    torch.cuda.synchronize()
+    got = out.cpu().numpy()
+    ref = orc.gemv_q8_k(6, w, k, n, q8, threads=8)
+    for mi in range(m):
+        _, _, mag = orc.gemv_block_sums(6, w, k, n, q8[mi])
+        err = np.abs(got[mi].astype(np.float64) - ref[mi])
+        assert np.all(err <= 1e-5 * mag), f"row {mi}: max err/mag {np.max(err / mag)}"
+
+
 def test_gemv_m_chunking():
     """m above one launch's 8 rows is split into launches; results unchanged."""
     _gemv_check(4, 96, 2048, 13, index=500)
