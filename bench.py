@@ -236,6 +236,44 @@ def decode_large(torch, hip, synth) -> dict:
     return res
 
 
+def decode_crossover(torch, hip, synth) -> dict:
+    """Llama-3-8B gate+up (2 x [14336 x 4096] Q4_K) at batched decode sizes:
+    the GEMV route (f32 activations quantised to Q8_K in-kernel, Q4_K weights
+    read as they are) against the W8A8 route (per-token A8 quant + int8 GEMM
+    on weights repacked once to W8), to locate the batch where the GEMM takes
+    over. Weight copies rotate through > 256 MB for both routes."""
+    dev = "cuda"
+    n, k = 14336, 4096
+    res = {}
+    wq = [[torch.from_numpy(synth.kquant(4, n, k, index=52_000 + 2 * c + j)).to(dev) for j in range(2)]
+          for c in range(4)]
+    w8 = []
+    for pair in wq[:3]:
+        parts = [hip.repack_w8(4, blk, k, n) for blk in pair]
+        w8.append((torch.cat([p[0] for p in parts]), torch.cat([p[1] for p in parts])))
+    for m in (1, 4, 8, 16, 32, 64):
+        x = torch.from_numpy(synth.activations(m, k, index=53_000 + m)).to(dev)
+        outs = [torch.empty((m, n), dtype=torch.float32, device=dev) for _ in range(2)]
+        a8 = torch.empty((m, k), dtype=torch.int8, device=dev)
+        asc = torch.empty(m, dtype=torch.float32, device=dev)
+        out = torch.empty((m, 2 * n), dtype=torch.float32, device=dev)
+
+        def gemv():
+            for pair in wq:
+                hip.gemv_q_f32(4, pair, k, [n, n], x, outs=outs)
+
+        def gemm():
+            for w, wsc in w8:
+                hip.quantize_a8(x, k, a8, asc)
+                hip.gemm_w8a8(a8, asc, w, wsc, out=out)
+
+        gv_ms, _ = time_graph(torch, gemv, 5, 2)
+        gm_ms, _ = time_graph(torch, gemm, 5, 2)
+        gv, gm = gv_ms * 1e3 / len(wq), gm_ms * 1e3 / len(w8)
+        res[f"m{m}"] = {"gemv_us": round(gv, 2), "w8a8_us": round(gm, 2), "faster": "gemv" if gv < gm else "w8a8"}
+    return res
+
+
 def profile_workload(torch, hip, synth, which: str) -> None:
     """Run one workload eagerly (3 times) for rocprofv3 counter passes."""
     if which == "gemv-q4k":
@@ -386,6 +424,7 @@ def main():
             "prefill_tinyllama_m512": prefill_tok_s(torch, hip, synth, 512, 22),
         }
         result["decode_gemv_large_m1"] = decode_large(torch, hip, synth)
+        result["decode_crossover_llama3_8b_gate_up"] = decode_crossover(torch, hip, synth)
     if not (args.quick or args.no_cpu):
         result["cpu_baseline"] = cpu_baseline(synth)
         result["cpu_baseline_w8a8"] = cpu_baseline_w8a8(synth)
