@@ -451,15 +451,24 @@ int launch_cfg(const int8_t* a8, int64_t lda, const int8_t* w8, int64_t ldw, con
 
 }  // namespace
 
-// Tile choice by M. Up to 32 rows the register-staged kernel (16/32 x 64
-// tiles); up to 256 rows small direct-load tiles, which for M = 128,
+int launch_gemm_w8a8_skinny(const int8_t* a8, int64_t lda, const int8_t* w8, int64_t ldw, const float* as,
+                            const float* ws, int m, int n, int k, float* out, int64_t ldo, int32_t* oi,
+                            int64_t ldoi, hipStream_t stream);  // gemm_skinny.hip
+
+// Tile choice by M. Up to 16 rows the weight-streaming kernel of
+// gemm_skinny.hip (when the A8 rows fit its LDS), else the register-staged
+// kernel (16/32 x 64 tiles) up to 32 rows; up to 256 rows small direct-load tiles, which for M = 128,
 // N = 5632, K = 2048 take 10.3 us against 20.3 us for the register-staged
 // 64x64 tile (the K loop's load latency, not the matrix cores, bounds these);
 // beyond that 256x256 tiles when they make at least one per CU, else 128x128.
 int launch_gemm_w8a8(const int8_t* a8, int64_t lda, const int8_t* w8, int64_t ldw, const float* as,
                      const float* ws, int m, int n, int k, float* out, int64_t ldo, int32_t* oi,
                      int64_t ldoi, hipStream_t stream) {
-    if (m <= 16) return launch_cfg<16, 64, 1, 4>(a8, lda, w8, ldw, as, ws, m, n, k, out, ldo, oi, ldoi, stream);
+    if (m <= 16) {
+        const int st = launch_gemm_w8a8_skinny(a8, lda, w8, ldw, as, ws, m, n, k, out, ldo, oi, ldoi, stream);
+        if (st != kStatusInvalid) return st;
+        return launch_cfg<16, 64, 1, 4>(a8, lda, w8, ldw, as, ws, m, n, k, out, ldo, oi, ldoi, stream);
+    }
     if (m <= 32) return launch_cfg<32, 64, 1, 4>(a8, lda, w8, ldw, as, ws, m, n, k, out, ldo, oi, ldoi, stream);
     if (m <= 64) return launch_dma<64, 32, 2, 1, 8>(a8, lda, w8, ldw, as, ws, m, n, k, out, ldo, oi, ldoi, stream);
     if (m <= 128) return launch_dma<64, 64, 2, 2, 8>(a8, lda, w8, ldw, as, ws, m, n, k, out, ldo, oi, ldoi, stream);

@@ -123,7 +123,11 @@ def _gemm_dev(a8, as_, w8, ws):
                                    (4100, 4000, 192),     # 256x256 tiles, ragged edges, 3 K steps
                                    (64, 48, 192),         # 64x32 tiles, half a tile of N past the edge
                                    (250, 70, 4160),       # 128x32 tiles, K steps not a multiple of 4
-                                   (40, 33, 64)])         # 64x32 tiles, one K step
+                                   (40, 33, 64),          # 64x32 tiles, one K step
+                                   (3, 28672, 4096),      # weight-streaming kernel, many tiles per workgroup
+                                   (16, 17, 7168),        # weight-streaming kernel at its LDS limit, ragged tile
+                                   (9, 100, 64),          # weight-streaming kernel, fewer K chunks than waves
+                                   (12, 40, 7232)])       # A8 rows beyond the weight-streaming LDS: tiled kernel
 def test_gemm_w8a8_bit_exact(m, n, k):
     print(f"gemm m={m} n={n} k={k}", flush=True)
     g = np.random.default_rng(m * 1000 + n + k)
