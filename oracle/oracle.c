@@ -196,6 +196,34 @@ int or_quantize_a8(const float *a, size_t m, size_t k, size_t k_pad, int8_t *a8,
     return OR_OK;
 }
 
+/* lib.rs:2045-2071 (hilo_stack): the rows, then per row the residual
+ * `x - f32::from(q) * scale` of its symmetric quantisation, evaluated as a
+ * product rounded to f32 and then a difference (no contraction). */
+int or_hilo_stack(const float *a, size_t m, size_t k, float *stacked) {
+    int8_t *q = (int8_t *)malloc(k ? k : 1);
+    if (!q) return OR_INVALID;
+    int status = OR_OK;
+    memcpy(stacked, a, m * k * sizeof(float));
+    for (size_t r = 0; r < m && status == OR_OK; ++r) {
+        float scale;
+        if (or_quantize_symmetric_row(a + r * k, k, q, &scale) != OR_OK) {
+            status = OR_INVALID;
+            break;
+        }
+        for (size_t t = 0; t < k; ++t) {
+            const float deq = (float)q[t] * scale;
+            stacked[(m + r) * k + t] = a[r * k + t] - deq;
+        }
+    }
+    free(q);
+    return status;
+}
+
+/* lib.rs:2073-2082 (hilo_sum). */
+void or_hilo_sum(float *out, const float *stacked, size_t len) {
+    for (size_t i = 0; i < len; ++i) out[i] = stacked[i] + stacked[len + i];
+}
+
 void or_gemm_i32(const int8_t *a8, const int8_t *w8, size_t m, size_t n, size_t k, int32_t *c,
                  int threads) {
     const long long total = (long long)(m * n);

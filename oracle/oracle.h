@@ -80,6 +80,14 @@ void or_rescale(const int32_t *c, const float *a_scales, const float *w_scales, 
 int or_matmul_q_w8a8(uint32_t kind, const uint8_t *blocks, size_t bytes, const float *a, size_t m,
                      size_t k, size_t n, float *out, int threads);
 
+/* Two-part activation encoding (lib.rs:2045-2071): stacked[0, m) = a and
+ * stacked[m, 2m) = a - f32(q) * scale per row, q/scale from the symmetric
+ * row quantisation. Returns -1 on a non-finite row. */
+int or_hilo_stack(const float *a, size_t m, size_t k, float *stacked);
+
+/* lib.rs:2073-2082: out[i] = stacked[i] + stacked[len + i]. */
+void or_hilo_sum(float *out, const float *stacked, size_t len);
+
 /* ggml quantize_row_q8_K_ref: k/256 blocks of 292 bytes. */
 void or_quantize_row_q8_k(const float *x, size_t k, uint8_t *q8k);
 

@@ -55,6 +55,9 @@ def lib() -> ctypes.CDLL:
         L.or_rescale.argtypes = [_i32p, _f32p, _f32p, _sz, _sz, _f32p]
         L.or_rescale.restype = None
         L.or_matmul_q_w8a8.argtypes = [ctypes.c_uint32, _u8p, _sz, _f32p, _sz, _sz, _sz, _f32p, ctypes.c_int]
+        L.or_hilo_stack.argtypes = [_f32p, _sz, _sz, _f32p]
+        L.or_hilo_sum.argtypes = [_f32p, _f32p, _sz]
+        L.or_hilo_sum.restype = None
         L.or_quantize_row_q8_k.argtypes = [_f32p, _sz, _u8p]
         L.or_quantize_row_q8_k.restype = None
         L.or_vec_dot_q4_k_q8_k.argtypes = [_sz, _u8p, _u8p]
@@ -138,6 +141,30 @@ def matmul_q_w8a8(kind: int, blocks: np.ndarray, a: np.ndarray, n: int, threads:
                               threads) != 0:
         raise OracleError("matmul_q_w8a8")
     return out
+
+
+def hilo_stack(a: np.ndarray) -> np.ndarray:
+    """[a; residual(a)] as 2m rows (lib.rs:2045-2071)."""
+    a = np.ascontiguousarray(a, np.float32)
+    m, k = a.shape
+    st = np.empty((2 * m, k), np.float32)
+    if lib().or_hilo_stack(_p(a, _f32p), m, k, _p(st, _f32p)) != 0:
+        raise OracleError("hilo_stack")
+    return st
+
+
+def hilo_sum(stacked_out: np.ndarray) -> np.ndarray:
+    """Sum of the two output halves of a [2m, n] result (lib.rs:2073-2082)."""
+    st = np.ascontiguousarray(stacked_out, np.float32)
+    m = st.shape[0] // 2
+    out = np.empty((m,) + st.shape[1:], np.float32)
+    lib().or_hilo_sum(_p(out, _f32p), _p(st, _f32p), out.size)
+    return out
+
+
+def matmul_q_hilo(kind: int, blocks: np.ndarray, a: np.ndarray, n: int, threads: int = 1) -> np.ndarray:
+    """The prompt-path W8A8 route with the two-part activation encoding."""
+    return hilo_sum(matmul_q_w8a8(kind, blocks, hilo_stack(a), n, threads=threads))
 
 
 def quantize_q8_k(x: np.ndarray) -> np.ndarray:

@@ -154,6 +154,7 @@ struct RockNpuContext {
     uint64_t hit_ns = 0, miss_ns = 0;
     Profile mtile_profile, m1_profile;
     bool profile_mtile = false, profile_m1 = false, trace = false;
+    int hilo = 0;  // ROCKNPU_PREFILL_HILO: 0 off, 1 wide-K projections only, 2 every prompt projection
     rocknpu_overlap_fn overlap = nullptr;
     void* overlap_user = nullptr;
 };
@@ -262,35 +263,91 @@ int build_w8(RockNpuContext* ctx, const std::vector<Source>& srcs, size_t k, W8P
     return kOk;
 }
 
+// Two-part activation encoding of prompt projections (lib.rs:2005-2083):
+// each activation row x is quantised as usual, its residual
+// r = x - f32(q) * scale (f32, no contraction) is stacked as an extra row,
+// both run through the same W8A8 GEMM, and the two output halves are added.
+// ROCKNPU_PREFILL_HILO "1"/"all": every prompt projection (M >= 2); "down":
+// only wide-K ones (K > 4096 or K not a multiple of 512).
+int hilo_mode_from_env() {
+    const char* v = std::getenv("ROCKNPU_PREFILL_HILO");
+    if (!v) return 0;
+    if (std::strcmp(v, "1") == 0 || std::strcmp(v, "all") == 0) return 2;
+    if (std::strcmp(v, "down") == 0) return 1;
+    return 0;
+}
+
+bool hilo_applies(const RockNpuContext* ctx, size_t m, size_t k) {
+    if (ctx->hilo == 0 || m < 2 || k == 0) return false;
+    return !(ctx->hilo == 1 && k <= 4096 && k % 512 == 0);
+}
+
+// Rows m..2m-1 of act = x - f32(a8) * scale of rows 0..m-1.
+__global__ void hilo_residual_kernel(float* __restrict__ act, const int8_t* __restrict__ a8,
+                                     const float* __restrict__ scales, int64_t m, int64_t k, int64_t k_pad) {
+    const int64_t idx = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (idx >= m * k) return;
+    const int64_t r = idx / k, c = idx % k;
+    const float deq = static_cast<float>(a8[r * k_pad + c]) * scales[r];
+    act[(m + r) * k + c] = act[idx] - deq;
+}
+
+// out[r, :] += out[m + r, :] for rows r < m of an [2m, n] output.
+__global__ void hilo_sum_kernel(float* __restrict__ out, int64_t m, int64_t n) {
+    const int64_t idx = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (idx >= m * n) return;
+    out[idx] = out[idx] + out[m * n + idx];
+}
+
 // Quantise host activations [m, k], run the GEMM against `w`, download and
 // scatter the columns into outs[i] ([m, ns[i]] each, ns summing to w->n).
+// `hilo_ok`: the entry point is one the two-part encoding serves.
 int run_w8a8(RockNpuContext* ctx, const DeviceW8& w, const float* act, size_t m, size_t k,
-             const std::vector<float*>& outs, const std::vector<size_t>& ns, bool decode) {
-    size_t a_bytes, o_elems;
-    if (!mul_ok(m, k, &a_bytes) || !mul_ok(a_bytes, sizeof(float), &a_bytes) || !mul_ok(m, w.n, &o_elems))
+             const std::vector<float*>& outs, const std::vector<size_t>& ns, bool decode, bool hilo_ok = false) {
+    const bool hilo = hilo_ok && hilo_applies(ctx, m, k);
+    const size_t rows = hilo ? 2 * m : m;  // GEMM rows
+    size_t a_bytes, o_elems, a_rows_bytes, o_rows;
+    if (!mul_ok(m, k, &a_bytes) || !mul_ok(a_bytes, sizeof(float), &a_bytes) || !mul_ok(m, w.n, &o_elems) ||
+        !mul_ok(rows, k * sizeof(float), &a_rows_bytes) || !mul_ok(rows, w.n, &o_rows))
         return kInvalid;
-    if (!ctx->d_act.ensure(a_bytes) || !ctx->d_a8.ensure(m * w.k_pad) || !ctx->d_as.ensure(m * sizeof(float)) ||
-        !ctx->d_out.ensure(o_elems * sizeof(float)) || !ctx->h_out.ensure(o_elems * sizeof(float)) ||
-        !ctx->h_as.ensure(m * sizeof(float)))
+    if (!ctx->d_act.ensure(a_rows_bytes) || !ctx->d_a8.ensure(rows * w.k_pad) ||
+        !ctx->d_as.ensure(rows * sizeof(float)) || !ctx->d_out.ensure(o_rows * sizeof(float)) ||
+        !ctx->h_out.ensure(o_elems * sizeof(float)) || !ctx->h_as.ensure(rows * sizeof(float)))
         return kExec;
     if (!hip_ok(hipMemcpyAsync(ctx->d_act.p, act, a_bytes, hipMemcpyHostToDevice, ctx->stream), ctx, "act"))
         return kExec;
     int st = rocknpu_hip_quantize_a8(ctx->d_act.as<float>(), m, k, k, w.k_pad, ctx->d_a8.as<int8_t>(),
                                      ctx->d_as.as<float>(), ctx->stream);
     if (st != kOk) return st;
-    st = rocknpu_hip_gemm_w8a8(ctx->d_a8.as<int8_t>(), ctx->d_as.as<float>(), w.w8, w.scales, m, w.n, w.k_pad,
+    if (hilo) {
+        const int64_t total = static_cast<int64_t>(m * k);
+        hilo_residual_kernel<<<static_cast<unsigned>((total + 255) / 256), 256, 0, ctx->stream>>>(
+            ctx->d_act.as<float>(), ctx->d_a8.as<int8_t>(), ctx->d_as.as<float>(), static_cast<int64_t>(m),
+            static_cast<int64_t>(k), static_cast<int64_t>(w.k_pad));
+        if (!hip_ok(hipGetLastError(), ctx, "hilo residual")) return kExec;
+        st = rocknpu_hip_quantize_a8(ctx->d_act.as<float>() + m * k, m, k, k, w.k_pad, ctx->d_a8.as<int8_t>() + m * w.k_pad,
+                                     ctx->d_as.as<float>() + m, ctx->stream);
+        if (st != kOk) return st;
+    }
+    st = rocknpu_hip_gemm_w8a8(ctx->d_a8.as<int8_t>(), ctx->d_as.as<float>(), w.w8, w.scales, rows, w.n, w.k_pad,
                                ctx->d_out.as<float>(), w.n, nullptr, ctx->stream);
     if (st != kOk) return st;
+    if (hilo) {
+        const int64_t total = static_cast<int64_t>(o_elems);
+        hilo_sum_kernel<<<static_cast<unsigned>((total + 255) / 256), 256, 0, ctx->stream>>>(
+            ctx->d_out.as<float>(), static_cast<int64_t>(m), static_cast<int64_t>(w.n));
+        if (!hip_ok(hipGetLastError(), ctx, "hilo sum")) return kExec;
+    }
     if (!hip_ok(hipMemcpyAsync(ctx->h_out.p, ctx->d_out.p, o_elems * sizeof(float), hipMemcpyDeviceToHost,
                                ctx->stream),
                 ctx, "download") ||
-        !hip_ok(hipMemcpyAsync(ctx->h_as.p, ctx->d_as.p, m * sizeof(float), hipMemcpyDeviceToHost, ctx->stream),
+        !hip_ok(hipMemcpyAsync(ctx->h_as.p, ctx->d_as.p, rows * sizeof(float), hipMemcpyDeviceToHost, ctx->stream),
                 ctx, "download"))
         return kExec;
     if (decode) run_overlap(ctx);
     if (!hip_ok(hipStreamSynchronize(ctx->stream), ctx, "execute")) return kExec;
     const float* as = ctx->h_as.as<float>();
-    for (size_t r = 0; r < m; ++r)
+    for (size_t r = 0; r < rows; ++r)
         if (!std::isfinite(as[r])) return kInvalid;  // non-finite activation row
     const float* h = ctx->h_out.as<float>();
     size_t col = 0;
@@ -302,7 +359,8 @@ int run_w8a8(RockNpuContext* ctx, const DeviceW8& w, const float* act, size_t m,
 }
 
 // Cached single-projection W8A8 (M > 1 -> prompt cache, M = 1 -> decode cache).
-int exec_single(RockNpuContext* ctx, const Source& src, const float* act, float* out, size_t m) {
+int exec_single(RockNpuContext* ctx, const Source& src, const float* act, float* out, size_t m,
+                bool hilo_ok = false) {
     const bool decode = m == 1;
     const uint64_t t0 = now_ns();
     auto& primary = decode ? ctx->m1 : ctx->mtile;
@@ -315,7 +373,7 @@ int exec_single(RockNpuContext* ctx, const Source& src, const float* act, float*
         primary.emplace(src.key, w);
     }
     const uint64_t t1 = now_ns();
-    const int st = run_w8a8(ctx, *w, act, m, src.key.k, {out}, {src.key.n}, decode);
+    const int st = run_w8a8(ctx, *w, act, m, src.key.k, {out}, {src.key.n}, decode, hilo_ok);
     const uint64_t t2 = now_ns();
     Profile& p = decode ? ctx->m1_profile : ctx->mtile_profile;
     p.calls++;
@@ -337,7 +395,7 @@ int exec_single(RockNpuContext* ctx, const Source& src, const float* act, float*
 
 // Cached concatenated-N group: one GEMM, activations quantised once.
 int exec_group(RockNpuContext* ctx, const std::vector<Source>& srcs, const float* act, size_t m,
-               const std::vector<float*>& outs) {
+               const std::vector<float*>& outs, bool hilo_ok = false) {
     const bool decode = m == 1;
     std::vector<WeightKey> keys;
     std::vector<size_t> ns;
@@ -357,7 +415,7 @@ int exec_group(RockNpuContext* ctx, const std::vector<Source>& srcs, const float
         if (st != kOk) return st;
         cache.emplace(keys, w);
     }
-    const int st = run_w8a8(ctx, *w, act, m, srcs[0].key.k, outs, ns, decode);
+    const int st = run_w8a8(ctx, *w, act, m, srcs[0].key.k, outs, ns, decode, hilo_ok);
     const uint64_t t1 = now_ns();
     if (decode) {
         ctx->m1_calls++;
@@ -403,7 +461,8 @@ int matmul_kquant(rocknpu_context* ctx, uint32_t kind, const uint8_t* w, size_t 
     if (!mul_ok(m, k, &tmp) || !mul_ok(n, k, &tmp) || !mul_ok(m, n, &tmp)) return kInvalid;
     if (!kquant_shape_ok(kind, bytes, k, n)) return kInvalid;
     if (kind == 5 && m == 1) return kInvalid;  // Q5_K is a prompt-path format (lib.rs:5300)
-    return exec_single(ctx, kquant_source(w, bytes, kind, k, n), act, out, m);
+    // the two-part encoding serves the Q4_K and Q6_K entries (lib.rs:4981, 5428)
+    return exec_single(ctx, kquant_source(w, bytes, kind, k, n), act, out, m, kind != 5);
 }
 
 // Minimal FP16 bridge kernel: activations rounded to f16 (RNE), f16 weights,
@@ -442,6 +501,7 @@ rocknpu_context* rocknpu_context_create(void) {
     ctx->profile_mtile = env_enabled("ROCKNPU_MTILE_PROFILE");
     ctx->profile_m1 = env_enabled("ROCKNPU_M1_PROFILE");
     ctx->trace = env_enabled("ROCKNPU_MTILE_TRACE");
+    ctx->hilo = hilo_mode_from_env();
     return ctx;
 }
 
@@ -503,7 +563,7 @@ int rocknpu_matmul_q_concat_f32_f32_mtile(rocknpu_context* ctx, size_t count, co
         srcs.push_back(kquant_source(weights[i], bytes[i], kinds[i], k, ns[i]));
         outs.push_back(outputs[i]);
     }
-    return exec_group(ctx, srcs, act, m, outs);
+    return exec_group(ctx, srcs, act, m, outs, true);  // two-part encoding: lib.rs:2484
 }
 
 int rocknpu_mtile_release(rocknpu_context* ctx, size_t count, const uint8_t* const* weights) {

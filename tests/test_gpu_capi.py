@@ -203,3 +203,41 @@ def test_f16_bridge(ctx):
     assert ctx.matmul_f16(w.view(np.uint16), a, out, k, n) == STATUS_OK
     ref = a.astype(np.float16).astype(np.float64) @ w.astype(np.float64).T
     np.testing.assert_allclose(out, ref, rtol=1e-4, atol=1e-4)
+
+
+@pytest.mark.parametrize("mode,k", [("1", 2048), ("all", 512), ("down", 5632), ("down", 2048)])
+def test_prefill_hilo_matches_oracle(monkeypatch, mode, k):
+    """ROCKNPU_PREFILL_HILO (lib.rs:2005-2083): the prompt-path W8A8 with the two-part
+    activation encoding, bit for bit against the oracle's stack / W8A8 / sum. "down"
+    applies only where K > 4096 or K is not a multiple of 512; elsewhere the plain route
+    runs. M=1 never uses it."""
+    monkeypatch.setenv("ROCKNPU_PREFILL_HILO", mode)
+    c = Context()
+    keep = []  # weights stay alive (and at their addresses) for the context's lifetime, as the ABI requires
+    try:
+        m, n = 12, 96
+        for kind in (4, 6):
+            blocks = synth.kquant(kind, n, k, index=1300 + kind + k)
+            keep.append(blocks)
+            a = synth.activations(m, k, index=1310 + k)
+            out = np.empty((m, n), np.float32)
+            assert c.matmul_q(kind, blocks, a, out, k, n) == STATUS_OK
+            applies = mode != "down" or k > 4096 or k % 512 != 0
+            ref = orc.matmul_q_hilo(kind, blocks, a, n, threads=8) if applies else _w8a8_ref(kind, blocks, a, n)
+            assert np.array_equal(_bits(out), _bits(ref)), (kind, mode, k)
+        # concat-N entry uses it too
+        ws = [synth.q4_k(nn, k, index=1320 + nn) for nn in (64, 32)]
+        keep.extend(ws)
+        outs = [np.empty((m, nn), np.float32) for nn in (64, 32)]
+        assert c.matmul_q_concat(ws, [4, 4], [64, 32], a, outs, k) == STATUS_OK
+        for w, nn, o in zip(ws, (64, 32), outs):
+            ref = orc.matmul_q_hilo(4, w, a, nn, threads=8) if applies else _w8a8_ref(4, w, a, nn)
+            assert np.array_equal(_bits(o), _bits(ref))
+        # one row: the decode route, no two-part encoding
+        out1 = np.empty((1, n), np.float32)
+        blocks = synth.q4_k(n, k, index=1330)
+        keep.append(blocks)
+        assert c.matmul_q(4, blocks, a[:1].copy(), out1, k, n) == STATUS_OK
+        assert np.array_equal(_bits(out1), _bits(_w8a8_ref(4, blocks, a[:1], n)))
+    finally:
+        c.close()

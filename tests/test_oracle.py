@@ -205,6 +205,45 @@ def test_matmul_w8a8_route_composition():
         orc.matmul_q_w8a8(6, blocks, bad, n)
 
 
+def test_hilo_stack_and_sum():
+    """Two-part encoding (lib.rs:2045-2082) against numpy: rows kept, residual
+    x - f32(q) * scale per row; rows on the int8 grid leave a zero residual; the
+    reconstruction q*scale + residual is x wherever the subtraction is exact
+    (Sterbenz: residual and dequantised value within a factor 2)."""
+    m, k = 5, 700
+    a = synth.activations(m, k, index=40)
+    grid = (np.arange(k) % 255 - 127).astype(np.float32) * np.float32(0.03125)  # exact multiples of max/127
+    grid[0] = np.float32(127 * 0.03125)
+    a[3] = grid
+    st = orc.hilo_stack(a)
+    assert st.shape == (2 * m, k)
+    assert np.array_equal(_bits(st[:m]), _bits(a))
+    q, s = np_ref.quantize_symmetric(a)
+    resid = a - (q.astype(np.float32) * s[:, None]).astype(np.float32)
+    assert np.array_equal(_bits(st[m:]), _bits(resid.astype(np.float32)))
+    assert not st[m + 3].any()
+    # sum of halves
+    halves = synth.activations(2 * m, 33, index=41)
+    assert np.array_equal(_bits(orc.hilo_sum(halves)), _bits(halves[:m] + halves[m:]))
+    bad = a.copy()
+    bad[1, 2] = np.inf
+    with pytest.raises(orc.OracleError):
+        orc.hilo_stack(bad)
+
+
+def test_hilo_reduces_w8a8_error():
+    """The point of the encoding: against the exact f64 product of the dequantised
+    weights and the f32 activations, the two-part result is closer than plain W8A8."""
+    m, k, n = 8, 1024, 64
+    blocks = synth.q4_k(n, k, index=42)
+    a = synth.activations(m, k, index=43)
+    wq, ws = np_ref.quantize_symmetric(np_ref.dequant(4, blocks, n, k))
+    exact = a.astype(np.float64) @ (wq.astype(np.float64) * ws[:, None].astype(np.float64)).T
+    plain = orc.matmul_q_w8a8(4, blocks, a, n)
+    hilo = orc.matmul_q_hilo(4, blocks, a, n)
+    assert np.abs(hilo - exact).max() < 0.1 * np.abs(plain - exact).max()
+
+
 # ------------------------------------------------------------------ Q8_K and the decode dots
 def test_quantize_q8_k_matches_numpy():
     x = synth.activations(1, 2048, index=40)[0]
