@@ -224,6 +224,26 @@ void or_hilo_sum(float *out, const float *stacked, size_t len) {
     for (size_t i = 0; i < len; ++i) out[i] = stacked[i] + stacked[len + i];
 }
 
+uint64_t or_fnv1a64(uint64_t h, const uint8_t *data, size_t n) {
+    for (size_t i = 0; i < n; ++i) {
+        h ^= data[i];
+        h *= 1099511628211ULL;
+    }
+    return h;
+}
+
+/* ggml-rocknpu.cpp:123-146 */
+uint64_t or_source_fingerprint(const uint8_t *data, size_t bytes) {
+    uint8_t count[8];
+    for (int i = 0; i < 8; ++i) count[i] = (uint8_t)((uint64_t)bytes >> (8 * i));
+    uint64_t h = or_fnv1a64(14695981039346656037ULL, count, 8);
+    const size_t sample = 4096;
+    if (bytes <= 3 * sample) return or_fnv1a64(h, data, bytes);
+    h = or_fnv1a64(h, data, sample);
+    h = or_fnv1a64(h, data + (bytes - sample) / 2, sample);
+    return or_fnv1a64(h, data + bytes - sample, sample);
+}
+
 void or_gemm_i32(const int8_t *a8, const int8_t *w8, size_t m, size_t n, size_t k, int32_t *c,
                  int threads) {
     const long long total = (long long)(m * n);

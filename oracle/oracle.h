@@ -88,6 +88,17 @@ int or_hilo_stack(const float *a, size_t m, size_t k, float *stacked);
 /* lib.rs:2073-2082: out[i] = stacked[i] + stacked[len + i]. */
 void or_hilo_sum(float *out, const float *stacked, size_t len);
 
+/* FNV-1a 64 over n bytes continuing from hash h (offset basis
+ * 14695981039346656037, prime 1099511628211). */
+uint64_t or_fnv1a64(uint64_t h, const uint8_t *data, size_t n);
+
+/* W8 sidecar source fingerprint (adapters/ggml-rocknpu/src/ggml-rocknpu.cpp:
+ * 123-146; scripts/make_tinyllama_w8_sidecar_gguf.py:23-45): FNV-1a 64 over
+ * the 8 bytes of the byte count (least significant first), then over all
+ * bytes when bytes <= 3*4096, else over the first 4096, the 4096 at
+ * (bytes - 4096) / 2 and the last 4096. */
+uint64_t or_source_fingerprint(const uint8_t *data, size_t bytes);
+
 /* ggml quantize_row_q8_K_ref: k/256 blocks of 292 bytes. */
 void or_quantize_row_q8_k(const float *x, size_t k, uint8_t *q8k);
 

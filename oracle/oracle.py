@@ -55,6 +55,10 @@ def lib() -> ctypes.CDLL:
         L.or_rescale.argtypes = [_i32p, _f32p, _f32p, _sz, _sz, _f32p]
         L.or_rescale.restype = None
         L.or_matmul_q_w8a8.argtypes = [ctypes.c_uint32, _u8p, _sz, _f32p, _sz, _sz, _sz, _f32p, ctypes.c_int]
+        L.or_fnv1a64.argtypes = [ctypes.c_uint64, _u8p, _sz]
+        L.or_fnv1a64.restype = ctypes.c_uint64
+        L.or_source_fingerprint.argtypes = [_u8p, _sz]
+        L.or_source_fingerprint.restype = ctypes.c_uint64
         L.or_hilo_stack.argtypes = [_f32p, _sz, _sz, _f32p]
         L.or_hilo_sum.argtypes = [_f32p, _f32p, _sz]
         L.or_hilo_sum.restype = None
@@ -141,6 +145,21 @@ def matmul_q_w8a8(kind: int, blocks: np.ndarray, a: np.ndarray, n: int, threads:
                               threads) != 0:
         raise OracleError("matmul_q_w8a8")
     return out
+
+
+FNV_OFFSET = 14695981039346656037
+
+
+def fnv1a64(data: bytes, h: int = FNV_OFFSET) -> int:
+    buf = np.frombuffer(bytes(data), np.uint8).copy() if len(data) else np.zeros(1, np.uint8)
+    return int(lib().or_fnv1a64(h, _p(buf, _u8p), len(data)))
+
+
+def source_fingerprint(source: np.ndarray) -> int:
+    """W8 sidecar provenance fingerprint (ggml-rocknpu.cpp:123-146)."""
+    src = np.ascontiguousarray(source).view(np.uint8).reshape(-1)
+    buf = src if src.size else np.zeros(1, np.uint8)
+    return int(lib().or_source_fingerprint(_p(buf, _u8p), src.size))
 
 
 def hilo_stack(a: np.ndarray) -> np.ndarray:

@@ -482,6 +482,29 @@ __global__ void f16_matmul_kernel(const _Float16* __restrict__ w, const float* _
 
 }  // namespace
 
+namespace rk {
+
+// K-quant blocks (kind 4/5/6) of an [n, k] weight -> host W8 [n, k] + scales,
+// repacked on the context's GPU (the conversion half of the W8 sidecar).
+int context_repack_to_host(rocknpu_context* ctx, uint32_t kind, const uint8_t* source, size_t bytes, size_t k,
+                           size_t n, int8_t* w8, float* scales) {
+    if (!ctx || !source || !w8 || !scales || (kind != 4 && kind != 5 && kind != 6) ||
+        !kquant_shape_ok(kind, bytes, k, n))
+        return kInvalid;
+    W8Ptr w = alloc_w8(n, k);
+    if (!w) return kExec;
+    int st = repack_into(ctx, kind, source, bytes, k, n, *w, 0);
+    if (st != kOk) return st;
+    if (!hip_ok(hipMemcpy2DAsync(w8, k, w->w8, w->k_pad, k, n, hipMemcpyDeviceToHost, ctx->stream), ctx, "w8") ||
+        !hip_ok(hipMemcpyAsync(scales, w->scales, n * sizeof(float), hipMemcpyDeviceToHost, ctx->stream), ctx,
+                "scales") ||
+        !hip_ok(hipStreamSynchronize(ctx->stream), ctx, "download"))
+        return kExec;
+    return kOk;
+}
+
+}  // namespace rk
+
 extern "C" {
 
 size_t rocknpu_device_count(void) {

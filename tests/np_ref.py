@@ -153,3 +153,24 @@ def block_sums(kind, w: np.ndarray, n: int, k: int, x: np.ndarray):
         msum = np.zeros_like(isum)
         y = (d.reshape(n, nb).astype(np.float64) * dq[None] * isum).sum(axis=1)
     return isum.astype(np.int32), msum.astype(np.int32), y
+
+
+def source_sample_fnv1a64(raw: bytes) -> int:
+    """W8 sidecar fingerprint, restated from the generator
+    (scripts/make_tinyllama_w8_sidecar_gguf.py:23-45) in plain Python."""
+    mask = (1 << 64) - 1
+    h = 14695981039346656037
+    count = len(raw)
+    for shift in range(0, 64, 8):
+        h ^= (count >> shift) & 0xFF
+        h = (h * 1099511628211) & mask
+    sample = 4096
+    if count <= sample * 3:
+        ranges = ((0, count),)
+    else:
+        ranges = ((0, sample), ((count - sample) // 2, sample), (count - sample, sample))
+    for start, n in ranges:
+        for v in raw[start:start + n]:
+            h ^= v
+            h = (h * 1099511628211) & mask
+    return h

@@ -241,3 +241,40 @@ def test_prefill_hilo_matches_oracle(monkeypatch, mode, k):
         assert np.array_equal(_bits(out1), _bits(_w8a8_ref(4, blocks, a[:1], n)))
     finally:
         c.close()
+
+
+def test_w8_sidecar_get_converts_writes_and_reloads(tmp_path):
+    """rocknpu_w8_sidecar_get: a miss converts on the GPU (the oracle's repack, bit for
+    bit) and writes the sidecar; the next call is served from the files; a changed
+    source is converted again, not served stale; manifest of a directory of tensors."""
+    from rocknpu_amd import sidecar
+
+    c = Context()
+    try:
+        for kind, n, k in ((4, 40, 1024), (6, 33, 512), (5, 16, 256)):
+            blocks = synth.kquant(kind, n, k, index=1400 + kind)
+            w_ref, s_ref = orc.repack_w8(kind, blocks, k, n)
+            name = f"blk.0.q{kind}.weight"
+            st, w8, sc, hit = sidecar.get(c, tmp_path, name, kind, blocks, k, n, write_back=True)
+            assert st == STATUS_OK and not hit
+            assert np.array_equal(w8, w_ref) and np.array_equal(_bits(sc), _bits(s_ref))
+            st, w8b, scb, hit = sidecar.get(c, tmp_path, name, kind, blocks, k, n)
+            assert st == STATUS_OK and hit
+            assert np.array_equal(w8b, w_ref) and np.array_equal(_bits(scb), _bits(s_ref))
+            changed = blocks.copy()
+            changed.reshape(n, -1)[0, -1] ^= 0x11
+            st, w8c, _, hit = sidecar.get(c, tmp_path, name, kind, changed, k, n)
+            assert st == STATUS_OK and not hit
+            assert np.array_equal(w8c, orc.repack_w8(kind, changed, k, n)[0])
+        # no directory: conversion only
+        blocks = synth.q4_k(8, 256, index=1410)
+        st, w8, _, hit = sidecar.get(c, None, "x", 4, blocks, 256, 8)
+        assert st == STATUS_OK and not hit and np.array_equal(w8, orc.repack_w8(4, blocks, 256, 8)[0])
+        tensors = {f"blk.{i}.ffn_gate.weight": (4, synth.q4_k(16, 512, index=1420 + i), 512, 16) for i in range(3)}
+        man = sidecar.make_directory(c, tmp_path / "dir", tensors, "synthetic")
+        assert man["format"] == "rocknpu-w8-sidecar-v2" and len(man["tensors"]) == 3
+        for name, (kind, blocks, k, n) in tensors.items():
+            assert man["tensors"][name]["source_sample_fnv1a64"] == f"{orc.source_fingerprint(blocks):016x}"
+            assert sidecar.read(tmp_path / "dir", name, blocks, k, n) is not None
+    finally:
+        c.close()
