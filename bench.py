@@ -14,7 +14,7 @@ prefill MUL_MAT tokens/s, the dominant kernel's roofline, and the CPU oracle
 timed on the host cores as a baseline.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--quick] [--no-cpu]
-       python bench.py --profile {gemv-q4k,gemm,copy}   (workload only, for rocprofv3 counter runs)
+       python bench.py --profile {gemv-q4k,gemv-q4k-m4,gemm,copy}   (workload only, for rocprofv3 counter runs)
 """
 from __future__ import annotations
 
@@ -42,7 +42,7 @@ def parse():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--quick", action="store_true", help="skip the extra W8A8 shapes and the CPU baseline")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
-    ap.add_argument("--profile", choices=["gemv-q4k", "gemm", "copy"],
+    ap.add_argument("--profile", choices=["gemv-q4k", "gemv-q4k-m4", "gemm", "copy"],
                     help="run one workload eagerly a few times and exit (for rocprofv3 --pmc passes)")
     return ap.parse_args()
 
@@ -87,8 +87,10 @@ class DecodeSet:
                     self.outs[(m, li, name)] = torch.empty((m, n), dtype=torch.float32, device=dev)
         self.groups = (("attn", ("q", "k", "v")), ("o", ("o",)), ("ffn", ("gate", "up")), ("down", ("down",)))
 
-    def _launches(self, only_kind):
+    def _launches(self, only_kind, only_m=None):
         for m in (1, 4):
+            if only_m is not None and m != only_m:
+                continue
             for li, lw in enumerate(self.layers):
                 for tag, names in self.groups:
                     kind = lw[names[0]][3]
@@ -96,22 +98,22 @@ class DecodeSet:
                         continue
                     yield m, li, tag, names, kind
 
-    def step(self, only_kind: int | None = None):
+    def step(self, only_kind: int | None = None, only_m: int | None = None):
         """One pass: per layer and M, one fused launch per shared input
         (q/k/v, o, gate/up, down), each quantising its f32 input to Q8_K."""
         hip = self.hip
-        for m, li, tag, names, kind in self._launches(only_kind):
+        for m, li, tag, names, kind in self._launches(only_kind, only_m):
             lw = self.layers[li]
             k = lw[names[0]][1]
             hip.gemv_q_f32(kind, [lw[nm][0] for nm in names], k, [lw[nm][2] for nm in names],
                            self.inputs[(m, tag)], outs=[self.outs[(m, li, nm)] for nm in names])
 
-    def bytes_per_step(self, only_kind: int | None = None) -> tuple[int, int]:
+    def bytes_per_step(self, only_kind: int | None = None, only_m: int | None = None) -> tuple[int, int]:
         """(algorithmic HBM bytes, launches) per step: each launch reads its
         weights and the f32 activation rows once and writes the f32 outputs."""
         total = 0
         launches = 0
-        for m, li, tag, names, kind in self._launches(only_kind):
+        for m, li, tag, names, kind in self._launches(only_kind, only_m):
             lw = self.layers[li]
             k = lw[names[0]][1]
             total += m * k * 4
@@ -276,10 +278,10 @@ def decode_crossover(torch, hip, synth) -> dict:
 
 def profile_workload(torch, hip, synth, which: str) -> None:
     """Run one workload eagerly (3 times) for rocprofv3 counter passes."""
-    if which == "gemv-q4k":
+    if which in ("gemv-q4k", "gemv-q4k-m4"):
         ds = DecodeSet(torch, hip, synth, synth.TINYLLAMA_LAYERS)
         for _ in range(3):
-            ds.step(only_kind=4)
+            ds.step(only_kind=4, only_m=1 if which == "gemv-q4k" else 4)
     elif which == "gemm":
         m, n, k = 4096, 14336, 4096
         w = torch.randint(-127, 128, (n, k), dtype=torch.int8, device="cuda")
@@ -384,11 +386,17 @@ def main():
     torch.cuda.synchronize()
     assert all(torch.equal(ref[key], ds.outs[key]) for key in ref), "graph replay differs"
 
-    # dominant kernel: the Q4_K x Q8_K GEMV, timed alone in the same sequence
-    q4_bytes, q4_launches = ds.bytes_per_step(only_kind=4)
-    q4_ms, _ = time_graph(torch, lambda: ds.step(only_kind=4), args.steps, args.warmup)
-    q4_us = q4_ms * 1e3 / q4_launches
-    achieved = q4_bytes / q4_launches / (q4_us * 1e-6) / 1e9
+    # dominant kernel: the Q4_K x Q8_K GEMV at M=1 (the single-row kernel),
+    # its launches timed alone in the same sequence; the 4-row launches of the
+    # same weights run the matrix-core kernel and are timed beside it
+    def kernel_rate(only_m):
+        b, launches = ds.bytes_per_step(only_kind=4, only_m=only_m)
+        t_ms, _ = time_graph(torch, lambda: ds.step(only_kind=4, only_m=only_m), args.steps, args.warmup)
+        us = t_ms * 1e3 / launches
+        return b // launches, us, b / launches / (us * 1e-6) / 1e9
+
+    q4_bpl, q4_us, achieved = kernel_rate(1)
+    m4_bpl, m4_us, m4_achieved = kernel_rate(4)
 
     result = {
         "metric": METRIC,
@@ -408,11 +416,16 @@ def main():
                                "shared input (qkv, o, gate+up, down), HIP graph",
                    "layers": synth.TINYLLAMA_LAYERS, "m": [1, 4], "launches_per_step": n_gemv,
                    "bytes_per_step": step_bytes},
-        "roofline": {"bound": "hbm", "kernel": "Q4_K x Q8_K decode GEMV with fused Q8_K quant: gemv_kernel<4,...> "
-                                               "at M=1, gemv_mfma_kernel at M=4",
+        "roofline": {"bound": "hbm", "kernel": "Q4_K x Q8_K decode GEMV with fused Q8_K quant at M=1 "
+                                               "(gemv_kernel<4,...>), the 66 Q4_K launches of a step",
                      "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": measured_traffic("gemv_q4k"),
-                     "avg_launch_us": round(q4_us, 3), "bytes_per_launch": q4_bytes // q4_launches},
+                     "avg_launch_us": round(q4_us, 3), "bytes_per_launch": q4_bpl},
+        "roofline_m4": {"bound": "hbm", "kernel": "Q4_K x Q8_K decode GEMV at M=4 on the matrix cores "
+                                                  "(gemv_mfma_kernel<4,...>), the 66 Q4_K launches of a step",
+                        "achieved": round(m4_achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                        "frac": round(m4_achieved / HBM_PEAK_GBS, 4), "traffic": measured_traffic("gemv_q4k_m4"),
+                        "avg_launch_us": round(m4_us, 3), "bytes_per_launch": m4_bpl},
     }
     if not args.quick:
         rot = 1 << 30
