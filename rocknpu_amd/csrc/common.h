@@ -25,6 +25,10 @@ constexpr int kStatusInvalid = -1;
 constexpr int kStatusDevice = -2;
 constexpr int kStatusExec = -3;
 
+// Compute units of the current device (queried once per device; 256 when the
+// query fails). Defined in launch.hip.
+int device_cu_count();
+
 __host__ __device__ constexpr int block_bytes(int kind) {
     return kind == 4 ? kQ4KBytes : kind == 5 ? kQ5KBytes : kind == 6 ? kQ6KBytes : 0;
 }

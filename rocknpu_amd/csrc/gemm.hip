@@ -142,16 +142,18 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_w8a8_kernel(
 // wait for every load in flight, stages ahead included. Small tiles run 8
 // stages: their K steps hold few MFMAs, so more of the load latency must be
 // in flight.
-template <int BM, int BN, int WM, int WN>
+template <int BM, int BN, int WM, int WN, int KB>
 struct DmaTile {
     static constexpr int T = WM * WN * 64;
     static constexpr int W = WM * WN;
-    // 1 KiB segments (16 rows) per wave and stage. When a tile has fewer
-    // segments than waves, waves load segments twice (the same bytes to the
-    // same LDS place), so every wave issues the same number of loads.
-    static constexpr int A_ROWSEG = BM / 16, B_ROWSEG = BN / 16;
+    // 1 KiB segments (RPI rows of KB bytes) per wave and stage. When a tile
+    // has fewer segments than waves, waves load segments twice (the same
+    // bytes to the same LDS place), so every wave issues the same number of
+    // loads.
+    static constexpr int RPI = 1024 / KB;
+    static constexpr int A_ROWSEG = BM / RPI, B_ROWSEG = BN / RPI;
     static constexpr int A_SEG = A_ROWSEG >= W ? A_ROWSEG / W : 1, B_SEG = B_ROWSEG >= W ? B_ROWSEG / W : 1;
-    static_assert(BM % 16 == 0 && BN % 16 == 0, "tile rows must split into 16-row segments");
+    static_assert(BM % RPI == 0 && BN % RPI == 0, "tile rows must split into whole segments");
     static_assert((B_ROWSEG >= W ? B_SEG * W == B_ROWSEG : W % B_ROWSEG == 0) &&
                       (A_ROWSEG >= W ? A_SEG * W == A_ROWSEG : W % A_ROWSEG == 0),
                   "segments split evenly over the waves");
@@ -165,6 +167,12 @@ __device__ __forceinline__ void wait_vm() {
 }
 __device__ __forceinline__ void wait_lgkm0() { __builtin_amdgcn_s_waitcnt(0xF | (7 << 4) | ((0x3) << 14)); }
 
+// Stage layout of the direct-load tiles: rows of KB bytes (64 or 128), the
+// 16-byte chunks XOR-swizzled by row / 2, so the fragment reads (32 rows,
+// one chunk column per half wave) do not collide in the LDS banks.
+template <int KB>
+__device__ __forceinline__ int swz_kb(int r, int kc) { return r * KB + ((kc ^ ((r >> 1) & (KB / 16 - 1))) << 4); }
+
 // One 16-byte direct global->LDS load per lane; `lds` must be wave-uniform
 // (the 64 lanes fill lds .. lds + 1023).
 __device__ __forceinline__ void dma16(const int8_t* src, int8_t* lds) {
@@ -177,25 +185,32 @@ __device__ __forceinline__ void unroll_seq(F&& f, std::integer_sequence<int, I..
     (f(std::integral_constant<int, I>{}), ...);
 }
 
-template <int BM, int BN, int WM, int WN, int ST>
+template <int BM, int BN, int WM, int WN, int ST, int KB>
 __global__ __launch_bounds__(WM* WN * 64) void gemm_w8a8_dma_kernel(
     const int8_t* __restrict__ a8, int64_t lda, const int8_t* __restrict__ w8, int64_t ldw,
     const float* __restrict__ a_scales, const float* __restrict__ w_scales, int m, int n, int k,
     float* __restrict__ out, int64_t ldo, int32_t* __restrict__ out_i32, int64_t ldo_i32) {
-    using Cfg = DmaTile<BM, BN, WM, WN>;
+    using Cfg = DmaTile<BM, BN, WM, WN, KB>;
     constexpr int TM = BM / WM, TN = BN / WN;
     constexpr int FM = TM / 32, FN = TN / 32;  // 32x32 fragments
+    // A stage holds KB bytes of K (64, or 128: whole 128-byte lines per row,
+    // which the L2 serves at twice the rate of half lines) and is consumed
+    // in SUB sub-steps of 64.
+    static_assert(KB == 64 || KB == 128, "64- or 128-byte stages");
+    constexpr int SUB = KB / 64;
     // One array per stage, always indexed by a compile-time stage: the
     // wait-count pass then sees which LDS buffer a direct load writes and does
     // not wait for every load in flight before each LDS read.
-    // ST = 4..8 stages; arrays of stages >= ST are unused placeholders.
-    static_assert(ST >= 4 && ST <= 8, "four to eight stage buffers");
-    constexpr int A4 = ST > 4 ? BM * kBK : 16, A5 = ST > 5 ? BM * kBK : 16, A6 = ST > 6 ? BM * kBK : 16,
-                  A7 = ST > 7 ? BM * kBK : 16;
-    constexpr int B4 = ST > 4 ? BN * kBK : 16, B5 = ST > 5 ? BN * kBK : 16, B6 = ST > 6 ? BN * kBK : 16,
-                  B7 = ST > 7 ? BN * kBK : 16;
-    __shared__ __align__(16) int8_t la0[BM * kBK], la1[BM * kBK], la2[BM * kBK], la3[BM * kBK];
-    __shared__ __align__(16) int8_t lb0[BN * kBK], lb1[BN * kBK], lb2[BN * kBK], lb3[BN * kBK];
+    // ST = 2..8 stages; arrays of stages >= ST are unused placeholders.
+    static_assert(ST >= 2 && ST <= 8, "two to eight stage buffers");
+    constexpr int A2 = ST > 2 ? BM * KB : 16, A3 = ST > 3 ? BM * KB : 16;
+    constexpr int B2 = ST > 2 ? BN * KB : 16, B3 = ST > 3 ? BN * KB : 16;
+    constexpr int A4 = ST > 4 ? BM * KB : 16, A5 = ST > 5 ? BM * KB : 16, A6 = ST > 6 ? BM * KB : 16,
+                  A7 = ST > 7 ? BM * KB : 16;
+    constexpr int B4 = ST > 4 ? BN * KB : 16, B5 = ST > 5 ? BN * KB : 16, B6 = ST > 6 ? BN * KB : 16,
+                  B7 = ST > 7 ? BN * KB : 16;
+    __shared__ __align__(16) int8_t la0[BM * KB], la1[BM * KB], la2[A2], la3[A3];
+    __shared__ __align__(16) int8_t lb0[BN * KB], lb1[BN * KB], lb2[B2], lb3[B3];
     __shared__ __align__(16) int8_t la4[A4], la5[A5], la6[A6], la7[A7];
     __shared__ __align__(16) int8_t lb4[B4], lb5[B5], lb6[B6], lb7[B7];
     auto stage_a = [&](auto st) -> int8_t* {
@@ -235,27 +250,32 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_w8a8_dma_kernel(
     // are never stored).
     const int8_t* asrc[Cfg::A_SEG];
     const int8_t* bsrc[Cfg::B_SEG];
+    // lane l fills the 16 bytes at segment + 16 l: row l / CPR of the
+    // segment, swizzled chunk position l % CPR, so it loads the chunk whose
+    // swizzled place that is
+    constexpr int CPR = KB / 16;  // chunks per row
 #pragma unroll
     for (int q = 0; q < Cfg::A_SEG; ++q) {
-        const int r = ((wave * Cfg::A_SEG + q) % Cfg::A_ROWSEG) * 16 + (lane >> 2);
-        const int c = (lane & 3) ^ ((r >> 1) & 3);
+        const int r = ((wave * Cfg::A_SEG + q) % Cfg::A_ROWSEG) * Cfg::RPI + lane / CPR;
+        const int c = (lane % CPR) ^ ((r >> 1) & (CPR - 1));
         asrc[q] = a8 + static_cast<int64_t>(min(m0 + r, m - 1)) * lda + c * 16;
     }
 #pragma unroll
     for (int q = 0; q < Cfg::B_SEG; ++q) {
-        const int r = ((wave * Cfg::B_SEG + q) % Cfg::B_ROWSEG) * 16 + (lane >> 2);
-        const int c = (lane & 3) ^ ((r >> 1) & 3);
+        const int r = ((wave * Cfg::B_SEG + q) % Cfg::B_ROWSEG) * Cfg::RPI + lane / CPR;
+        const int c = (lane % CPR) ^ ((r >> 1) & (CPR - 1));
         bsrc[q] = w8 + static_cast<int64_t>(min(n0 + r, n - 1)) * ldw + c * 16;
     }
-    auto issue = [&](auto st, int kt) {
+    // stage number ks (K bytes ks*KB ..) into stage buffer st
+    auto issue = [&](auto st, int ks) {
         int8_t* la = stage_a(st);
         int8_t* lb = stage_b(st);
 #pragma unroll
         for (int q = 0; q < Cfg::A_SEG; ++q)
-            dma16(asrc[q] + kt * kBK, la + ((wave * Cfg::A_SEG + q) % Cfg::A_ROWSEG) * 1024);
+            dma16(asrc[q] + ks * KB, la + ((wave * Cfg::A_SEG + q) % Cfg::A_ROWSEG) * 1024);
 #pragma unroll
         for (int q = 0; q < Cfg::B_SEG; ++q)
-            dma16(bsrc[q] + kt * kBK, lb + ((wave * Cfg::B_SEG + q) % Cfg::B_ROWSEG) * 1024);
+            dma16(bsrc[q] + ks * KB, lb + ((wave * Cfg::B_SEG + q) % Cfg::B_ROWSEG) * 1024);
     };
 
     v16i acc[FM][FN];
@@ -264,38 +284,40 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_w8a8_dma_kernel(
 #pragma unroll
         for (int j = 0; j < FN; ++j) acc[i][j] = v16i{};
 
-    const int KT = k / kBK;
+    const int KS = k / KB;  // stages
+    const int KT = k / 64;  // 64-deep steps
     using S0 = std::integral_constant<int, 0>;
-    using S1 = std::integral_constant<int, 1>;
-    using S2 = std::integral_constant<int, 2>;
-    using S3 = std::integral_constant<int, 3>;
-    // Pipeline per K step s (stage s's fragments were read in step s-1):
-    //   wait for those reads and for this wave's loads of stage s+1; barrier
-    //   (every wave's stage s+1 is in, and every wave holds stage s in
-    //   registers, so its buffer is free); issue stage s+4 into that buffer;
-    //   read stage s+1's fragments into the other register set; then the
-    //   MFMAs of stage s, which run while those reads complete.
-    // Past the last K step the issue re-reads the last step into a buffer no
+    // Pipeline per 64-deep K step j (its fragments were read in step j-1):
+    //   wait for those reads. When j is the last step of its stage P: wait
+    //   for this wave's loads of stage P+1 and pass a barrier (every wave's
+    //   stage P+1 is in, and every wave holds all of stage P in registers, so
+    //   its buffer is free), then issue stage P+ST into that buffer.
+    //   Read step j+1's fragments into the other register set; then the MFMAs
+    //   of step j, which run while those reads complete.
+    // Past the last stage the issue re-reads the last stage into a buffer no
     // step reads, so the count of loads in flight stays fixed.
     constexpr int PER_STAGE = Cfg::A_SEG + Cfg::B_SEG;  // loads per wave and stage
     v4i fa[2][2][FM], fb[2][2][FN];  // [register set][32-deep half][fragment]
-    // lane l supplies row l%32 and the 16 bytes of chunk 2*h + l/32
-    auto read_half = [&](auto st, auto set, auto half) {
-        constexpr int R = decltype(set)::value, H = decltype(half)::value;
+    // step sub-step u of a stage: lane l supplies row l%32 and the 16 bytes of
+    // chunk 4u + 2h + l/32
+    auto read_half = [&](auto st, auto set, auto u, auto half) {
+        constexpr int R = decltype(set)::value, H = decltype(half)::value, SU = decltype(u)::value;
         const int8_t* la = stage_a(st);
         const int8_t* lb = stage_b(st);
 #pragma unroll
         for (int i = 0; i < FM; ++i)
-            fa[R][H][i] = *reinterpret_cast<const v4i*>(la + swz(wm * TM + i * 32 + (lane & 31), 2 * H + (lane >> 5)));
+            fa[R][H][i] = *reinterpret_cast<const v4i*>(
+                la + swz_kb<KB>(wm * TM + i * 32 + (lane & 31), 4 * SU + 2 * H + (lane >> 5)));
 #pragma unroll
         for (int j = 0; j < FN; ++j)
-            fb[R][H][j] = *reinterpret_cast<const v4i*>(lb + swz(wn * TN + j * 32 + (lane & 31), 2 * H + (lane >> 5)));
+            fb[R][H][j] = *reinterpret_cast<const v4i*>(
+                lb + swz_kb<KB>(wn * TN + j * 32 + (lane & 31), 4 * SU + 2 * H + (lane >> 5)));
     };
     using H0 = std::integral_constant<int, 0>;
     using H1 = std::integral_constant<int, 1>;
-    auto read_frags = [&](auto st, auto set) {
-        read_half(st, set, H0{});
-        read_half(st, set, H1{});
+    auto read_frags = [&](auto st, auto set, auto u) {
+        read_half(st, set, u, H0{});
+        read_half(st, set, u, H1{});
     };
     auto mfma_half = [&](auto set, auto half) {
         constexpr int R = decltype(set)::value, H = decltype(half)::value;
@@ -306,48 +328,59 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_w8a8_dma_kernel(
                 acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa[R][H][i], fb[R][H][j], acc[i][j], 0, 0, 0);
     };
     using R0 = std::integral_constant<int, 0>;
-    using R1 = std::integral_constant<int, 1>;
     // prologue: stages 0 .. ST-2 in flight, wait for stage 0, then stage ST-1
-    unroll_seq([&](auto i) { issue(i, min(static_cast<int>(decltype(i)::value), KT - 1)); },
+    unroll_seq([&](auto i) { issue(i, min(static_cast<int>(decltype(i)::value), KS - 1)); },
                std::make_integer_sequence<int, ST - 1>{});
     wait_vm<(ST - 2) * PER_STAGE>();
     __builtin_amdgcn_s_barrier();
-    issue(std::integral_constant<int, ST - 1>{}, min(ST - 1, KT - 1));
-    read_frags(S0{}, R0{});
-    // step s: stage s in register set s%2; S1N = stage of s+1
+    issue(std::integral_constant<int, ST - 1>{}, min(ST - 1, KS - 1));
+    read_frags(S0{}, R0{}, S0{});
     // Each step is one basic block: the barrier, the direct loads of stage
-    // s+ST and the fragment reads of stage s+1 are spread between the MFMAs of
-    // stage s (scheduling groups of one load, its share of the reads and of
+    // P+ST and the fragment reads of step j+1 are spread between the MFMAs of
+    // step j (scheduling groups of one load, its share of the reads and of
     // the MFMAs), so the LDS and memory traffic overlaps the matrix cores
-    // instead of stalling them. After the last K step the barrier, loads and reads
-    // still run (on buffers no step reads), which keeps the block branch-free.
-    auto step = [&](auto set, auto next_st, auto refill_st, int kt) {
+    // instead of stalling them. After the last step the barrier, loads and
+    // reads still run (on buffers no step reads), which keeps the block
+    // branch-free.
+    auto step = [&](auto set, auto next_st, auto next_u, auto refill_st, auto last_of_stage, int p) {
         using NSET = std::integral_constant<int, 1 - decltype(set)::value>;
+        constexpr bool LAST = decltype(last_of_stage)::value;
         wait_lgkm0();
-        wait_vm<(ST - 2) * PER_STAGE>();  // stage s+1 done (s+2 .. s+ST-1 may be in flight)
-        __builtin_amdgcn_s_barrier();
-        issue(refill_st, min(kt + ST, KT - 1));
-        read_frags(next_st, NSET{});
+        if constexpr (LAST) {
+            wait_vm<(ST - 2) * PER_STAGE>();  // stage P+1 done (P+2 .. P+ST-1 may be in flight)
+            __builtin_amdgcn_s_barrier();
+            issue(refill_st, min(p + ST, KS - 1));
+        }
+        read_frags(next_st, NSET{}, next_u);
         mfma_half(set, H0{});
         mfma_half(set, H1{});
         constexpr int READS = 2 * (FM + FN), MFMAS = 2 * FM * FN;
-        if constexpr (READS % PER_STAGE == 0 && MFMAS % PER_STAGE == 0) {
+        if constexpr (LAST && READS % PER_STAGE == 0 && MFMAS % PER_STAGE == 0) {
 #pragma unroll
             for (int q = 0; q < PER_STAGE; ++q) {
                 __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);                  // VMEM read (direct load)
                 __builtin_amdgcn_sched_group_barrier(0x100, READS / PER_STAGE, 0);  // DS read
                 __builtin_amdgcn_sched_group_barrier(0x008, MFMAS / PER_STAGE, 0);  // MFMA
             }
+        } else if constexpr (!LAST && MFMAS % READS == 0) {
+#pragma unroll
+            for (int q = 0; q < READS; ++q) {
+                __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);             // DS read
+                __builtin_amdgcn_sched_group_barrier(0x008, MFMAS / READS, 0);  // MFMA
+            }
         }
     };
-    // step kt + I: register set I % 2, next stage (I + 1) % ST, refill stage I
-    // (U = ST steps per loop pass, 2 ST when ST is odd, so the register sets alternate)
+    // step kt + I: register set I % 2; stage buffer (I / SUB) % ST, sub-step
+    // I % SUB; the next step's buffer and sub-step; the last step of a stage
+    // refills that stage's buffer. U steps per loop pass: a multiple of
+    // ST * SUB and of 2, so buffers and register sets repeat.
     auto step_i = [&](auto i, int kt) {
         constexpr int I = decltype(i)::value;
-        step(std::integral_constant<int, I % 2>{}, std::integral_constant<int, (I + 1) % ST>{},
-             std::integral_constant<int, I % ST>{}, kt + I);
+        step(std::integral_constant<int, I % 2>{}, std::integral_constant<int, ((I + 1) / SUB) % ST>{},
+             std::integral_constant<int, (I + 1) % SUB>{}, std::integral_constant<int, (I / SUB) % ST>{},
+             std::integral_constant<bool, (I + 1) % SUB == 0>{}, (kt + I) / SUB);
     };
-    constexpr int U = ST % 2 == 0 ? ST : 2 * ST;
+    constexpr int U = (ST * SUB) % 2 == 0 ? ST * SUB : 2 * ST * SUB;
     const int KTA = KT - KT % U;
     for (int kt = 0; kt < KTA; kt += U) unroll_seq([&](auto i) { step_i(i, kt); }, std::make_integer_sequence<int, U>{});
     unroll_seq([&](auto i) { if (KTA + decltype(i)::value < KT) step_i(i, KTA); }, std::make_integer_sequence<int, U - 1>{});
@@ -364,13 +397,20 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_w8a8_dma_kernel(
     // columns at a time, so every lane stores 16 contiguous bytes and eight
     // lanes fill a 128-byte row segment.
     constexpr int TS = 40;  // tile row stride in floats: 16-byte aligned rows, rows 4 apart 32 banks apart
-    // waves 0-3 use stage buffers la0..la3, waves 4-7 lb0..lb3
-    constexpr int BUF = WM * WN > 4 ? (BM < BN ? BM : BN) * kBK : BM * kBK;
+    // With four or more stages, waves 0-3 use stage buffers la0..la3 and
+    // waves 4-7 lb0..lb3; with fewer, the first half of the waves' tiles sit
+    // side by side in la0 and the rest in lb0.
+    constexpr int W = WM * WN, WH = (W + 1) / 2;
+    constexpr int BUF = ST >= 4 ? (W > 4 ? (BM < BN ? BM : BN) * KB : BM * KB) : (BM < BN ? BM : BN) * KB / WH;
     constexpr int HR = 32 * TS * 4 <= BUF ? 32 : 16;
-    static_assert(HR * TS * 4 <= BUF, "epilogue tile fits a stage buffer");
-    static_assert(WM * WN <= 8, "one stage buffer per wave");
-    float* tile = reinterpret_cast<float*>(wave == 0 ? la0 : wave == 1 ? la1 : wave == 2 ? la2 : wave == 3 ? la3
-                                           : wave == 4 ? lb0 : wave == 5 ? lb1 : wave == 6 ? lb2 : lb3);
+    static_assert(HR * TS * 4 <= BUF && BUF % 16 == 0, "epilogue tile fits its buffer");
+    static_assert(ST < 4 || W <= 8, "one stage buffer per wave");
+    float* tile;
+    if constexpr (ST >= 4)
+        tile = reinterpret_cast<float*>(wave == 0 ? la0 : wave == 1 ? la1 : wave == 2 ? la2 : wave == 3 ? la3
+                                        : wave == 4 ? lb0 : wave == 5 ? lb1 : wave == 6 ? lb2 : lb3);
+    else
+        tile = reinterpret_cast<float*>(wave < WH ? la0 + wave * BUF : lb0 + (wave - WH) * BUF);
     typedef float f4u __attribute__((ext_vector_type(4), aligned(4)));  // scales and outputs: 4-byte alignment
 #pragma unroll
     for (int i = 0; i < FM; ++i) {
@@ -429,12 +469,17 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_w8a8_dma_kernel(
     }
 }
 
-template <int BM, int BN, int WM, int WN, int ST>
+template <int BM, int BN, int WM, int WN, int ST, int KB = 64>
 int launch_dma(const int8_t* a8, int64_t lda, const int8_t* w8, int64_t ldw, const float* as,
                const float* ws, int m, int n, int k, float* out, int64_t ldo, int32_t* oi,
                int64_t ldoi, hipStream_t stream) {
+    // 128-byte stages need K % 128 == 0 (a stage never reads past a row)
+    if constexpr (KB != 64)
+        if (k % KB != 0)
+            return launch_dma<BM, BN, WM, WN, (ST < 4 ? 4 : ST), 64>(a8, lda, w8, ldw, as, ws, m, n, k, out, ldo, oi,
+                                                                     ldoi, stream);
     const int64_t tiles = static_cast<int64_t>((m + BM - 1) / BM) * ((n + BN - 1) / BN);
-    gemm_w8a8_dma_kernel<BM, BN, WM, WN, ST><<<dim3(static_cast<unsigned>(tiles)), dim3(WM * WN * 64), 0, stream>>>(
+    gemm_w8a8_dma_kernel<BM, BN, WM, WN, ST, KB><<<dim3(static_cast<unsigned>(tiles)), dim3(WM * WN * 64), 0, stream>>>(
         a8, lda, w8, ldw, as, ws, m, n, k, out, ldo, oi, ldoi);
     return hipGetLastError() == hipSuccess ? kStatusOk : kStatusExec;
 }
@@ -455,12 +500,30 @@ int launch_gemm_w8a8_skinny(const int8_t* a8, int64_t lda, const int8_t* w8, int
                             const float* ws, int m, int n, int k, float* out, int64_t ldo, int32_t* oi,
                             int64_t ldoi, hipStream_t stream);  // gemm_skinny.hip
 
+// Direct-load tiles with 128-byte stages: two stages when there are more
+// tiles than CUs (two workgroups share a CU, so the extra tiles do not wait
+// for a second round), else four (one workgroup per CU, a deeper pipeline).
+// For M = 256, N = 4096, K = 14336 (128 tiles) four stages take 49 us against
+// 86 us with two; for M = 256, N = 11264, K = 2048 (352 tiles) two stages
+// take 19.7 us against 21.8 us with four.
+template <int BM, int BN, int WM, int WN>
+int launch_dma_by_tiles(const int8_t* a8, int64_t lda, const int8_t* w8, int64_t ldw, const float* as,
+                        const float* ws, int m, int n, int k, float* out, int64_t ldo, int32_t* oi,
+                        int64_t ldoi, hipStream_t stream) {
+    const int64_t tiles = static_cast<int64_t>((m + BM - 1) / BM) * ((n + BN - 1) / BN);
+    if (tiles > device_cu_count())
+        return launch_dma<BM, BN, WM, WN, 2, 128>(a8, lda, w8, ldw, as, ws, m, n, k, out, ldo, oi, ldoi, stream);
+    return launch_dma<BM, BN, WM, WN, 4, 128>(a8, lda, w8, ldw, as, ws, m, n, k, out, ldo, oi, ldoi, stream);
+}
+
 // Tile choice by M. Up to 16 rows the weight-streaming kernel of
 // gemm_skinny.hip (when the A8 rows fit its LDS), else the register-staged
-// kernel (16/32 x 64 tiles) up to 32 rows; up to 256 rows small direct-load tiles, which for M = 128,
-// N = 5632, K = 2048 take 10.3 us against 20.3 us for the register-staged
-// 64x64 tile (the K loop's load latency, not the matrix cores, bounds these);
-// beyond that 256x256 tiles when they make at least one per CU, else 128x128.
+// kernel up to 32 rows; up to 256 rows direct-load tiles of 64 x 32, 64 x 64
+// and 128 x 64; beyond that 256 x 256 tiles when there is at least one per CU,
+// else 128 x 128 when there are more than CUs, else 128 x 64. The 128-byte
+// stages read whole 128-byte lines of each row, which the L2 serves at about
+// twice the rate of the 64-byte half lines (M x N x K = 4096 x 14336 x 4096:
+// 284 -> 272 us; 512 x 11264 x 2048: 31.5 -> 25.7 us).
 int launch_gemm_w8a8(const int8_t* a8, int64_t lda, const int8_t* w8, int64_t ldw, const float* as,
                      const float* ws, int m, int n, int k, float* out, int64_t ldo, int32_t* oi,
                      int64_t ldoi, hipStream_t stream) {
@@ -470,12 +533,17 @@ int launch_gemm_w8a8(const int8_t* a8, int64_t lda, const int8_t* w8, int64_t ld
         return launch_cfg<16, 64, 1, 4>(a8, lda, w8, ldw, as, ws, m, n, k, out, ldo, oi, ldoi, stream);
     }
     if (m <= 32) return launch_cfg<32, 64, 1, 4>(a8, lda, w8, ldw, as, ws, m, n, k, out, ldo, oi, ldoi, stream);
-    if (m <= 64) return launch_dma<64, 32, 2, 1, 8>(a8, lda, w8, ldw, as, ws, m, n, k, out, ldo, oi, ldoi, stream);
-    if (m <= 128) return launch_dma<64, 64, 2, 2, 8>(a8, lda, w8, ldw, as, ws, m, n, k, out, ldo, oi, ldoi, stream);
-    if (m <= 256) return launch_dma<128, 64, 4, 1, 4>(a8, lda, w8, ldw, as, ws, m, n, k, out, ldo, oi, ldoi, stream);
+    if (m <= 64) return launch_dma_by_tiles<64, 32, 2, 1>(a8, lda, w8, ldw, as, ws, m, n, k, out, ldo, oi, ldoi, stream);
+    if (m <= 128) return launch_dma_by_tiles<64, 64, 2, 2>(a8, lda, w8, ldw, as, ws, m, n, k, out, ldo, oi, ldoi, stream);
+    if (m <= 256) return launch_dma_by_tiles<128, 64, 4, 1>(a8, lda, w8, ldw, as, ws, m, n, k, out, ldo, oi, ldoi, stream);
+    const int cus = device_cu_count();
     const int64_t big_tiles = static_cast<int64_t>((m + 255) / 256) * ((n + 255) / 256);
-    if (big_tiles >= 256) return launch_dma<256, 256, 2, 2, 4>(a8, lda, w8, ldw, as, ws, m, n, k, out, ldo, oi, ldoi, stream);
-    return launch_dma<128, 128, 2, 2, 4>(a8, lda, w8, ldw, as, ws, m, n, k, out, ldo, oi, ldoi, stream);
+    if (big_tiles >= cus)
+        return launch_dma<256, 256, 2, 2, 2, 128>(a8, lda, w8, ldw, as, ws, m, n, k, out, ldo, oi, ldoi, stream);
+    const int64_t mid_tiles = static_cast<int64_t>((m + 127) / 128) * ((n + 127) / 128);
+    if (mid_tiles > cus)
+        return launch_dma<128, 128, 2, 2, 2, 128>(a8, lda, w8, ldw, as, ws, m, n, k, out, ldo, oi, ldoi, stream);
+    return launch_dma_by_tiles<128, 64, 4, 1>(a8, lda, w8, ldw, as, ws, m, n, k, out, ldo, oi, ldoi, stream);
 }
 
 }  // namespace rk

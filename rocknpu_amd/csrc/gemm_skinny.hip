@@ -140,18 +140,6 @@ __global__ __launch_bounds__(kSkinnyWaves * 64) void gemm_w8a8_skinny_kernel(
     }
 }
 
-int device_cus_skinny() {
-    static int cached[64] = {};
-    int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-    if (cached[dev] == 0) {
-        int v = 0;
-        if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || v <= 0) v = 256;
-        cached[dev] = v;
-    }
-    return cached[dev];
-}
-
 }  // namespace
 
 // m <= 16, k % 64 == 0, m * k <= 112 KiB; else kStatusInvalid (callers route
@@ -161,7 +149,7 @@ int launch_gemm_w8a8_skinny(const int8_t* a8, int64_t lda, const int8_t* w8, int
                             int64_t ldoi, hipStream_t stream) {
     if (m < 1 || m > 16 || k % 64 != 0 || static_cast<int64_t>(m) * k > kSkinnyLdsA) return kStatusInvalid;
     const int tiles = (n + 15) / 16;
-    const int wgs = std::min(tiles, device_cus_skinny());
+    const int wgs = std::min(tiles, device_cu_count());
     const int iters = (k / 64 + kSkinnyWaves - 1) / kSkinnyWaves;
     const int per_wave = (tiles + wgs - 1) / wgs * iters;
     const size_t lds = ((static_cast<size_t>(m) * k + 15) & ~size_t{15}) + 2 * kSkinnyWaves * 64 * 4 * sizeof(int);

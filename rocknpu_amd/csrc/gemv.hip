@@ -493,19 +493,6 @@ void launch_l(const GemvArgs& p, int w, int mt, int d, int passes, dim3 grid, si
     launch_w<KIND, L, FUSED, SUMS, 16>(p, mt, d, passes, grid, lds, stream);
 }
 
-// Compute units of the current device (cached per device).
-int device_cus() {
-    static int cached[64] = {};
-    int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-    if (cached[dev] == 0) {
-        int n = 0;
-        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
-        cached[dev] = n;
-    }
-    return cached[dev];
-}
-
 // Slots per row: the largest power of two <= min(slots, nb) whose last pass
 // over the row's blocks keeps at least 85% of the slots busy.
 int slots_per_row_log2(int nb, int slots) {
@@ -522,7 +509,7 @@ int slots_per_row_log2(int nb, int slots) {
 template <int KIND, bool FUSED>
 int launch_kind(GemvParams& p, hipStream_t stream) {
     const bool sums = !FUSED && p.isum != nullptr;
-    const int cus = device_cus();
+    const int cus = device_cu_count();
     const int mt = p.m <= 1 ? 1 : p.m <= 2 ? 2 : p.m <= 4 ? 4 : 8;
     // At most 8 slots per row whatever L is: a row's f32 sum then runs in the
     // same order for every L and every grouping of projections.

@@ -409,18 +409,6 @@ void launch_kind(bool fused, int mt, const MfmaArgs& ka, int d, int passes, dim3
     }
 }
 
-int device_cus_mfma() {
-    static int cached[64] = {};
-    int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-    if (cached[dev] == 0) {
-        int n = 0;
-        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
-        cached[dev] = n;
-    }
-    return cached[dev];
-}
-
 }  // namespace
 
 // Q4_K or Q6_K, 2 <= p.m <= 8.
@@ -444,7 +432,7 @@ int launch_gemv_mfma(int kind, bool fused, GemvParams& p, hipStream_t stream) {
     ka.nb = p.nb;
     ka.tiles = tiles;
     // one workgroup per CU at most; each walks its tiles with up to 4 blocks in flight per wave
-    const int cus = device_cus_mfma();
+    const int cus = device_cu_count();
     const int wgs = std::min(tiles, cus);
     const int iters = (p.nb + kMfmaWaves - 1) / kMfmaWaves;
     const int per_wave = (tiles + wgs - 1) / wgs * iters;

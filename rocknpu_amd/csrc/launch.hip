@@ -18,6 +18,18 @@ int launch_gemm_w8a8(const int8_t* a8, int64_t lda, const int8_t* w8, int64_t ld
                      const float* ws, int m, int n, int k, float* out, int64_t ldo, int32_t* oi,
                      int64_t ldoi, hipStream_t stream);
 int launch_gemv(int kind, bool fused, GemvParams& p, hipStream_t stream);
+
+int device_cu_count() {
+    static int cached[64] = {};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+    if (cached[dev] == 0) {
+        int n = 0;
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+        cached[dev] = n;
+    }
+    return cached[dev];
+}
 }  // namespace rk
 
 namespace {
