@@ -131,17 +131,16 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_w8a8_kernel(
         }
 }
 
-// Direct-load tiles: the same product with a pipeline of ST (4 or 8) LDS
+// Direct-load tiles: the same product with a pipeline of ST (2 to 8) LDS
 // stage buffers filled by direct global->LDS loads (global_load_lds_dwordx4,
-// no register staging). Each wave issues its share of a stage as 1 KiB
-// segments (16 rows x 64 bytes; lane i's 16 bytes land at segment + 16*i, so
-// the lane loads the global chunk that the swizzled layout puts there).
-// Stage s+ST-1 is issued while stage s is multiplied; one barrier per K step
-// both publishes stage s (after each wave's own wait for its loads) and frees
-// stage s-1 for reuse. The barrier is a bare s_barrier: a fenced one would
-// wait for every load in flight, stages ahead included. Small tiles run 8
-// stages: their K steps hold few MFMAs, so more of the load latency must be
-// in flight.
+// no register staging). A stage holds KB (64 or 128) bytes of K per row. Each
+// wave issues its share of a stage as 1 KiB segments (1024 / KB rows of KB
+// bytes; lane i's 16 bytes land at segment + 16*i, so the lane loads the
+// global chunk that the swizzled layout puts there). Stage s+ST-1 is issued
+// while stage s is multiplied; one barrier per stage both publishes stage s+1
+// (after each wave's own wait for its loads) and frees stage s for reuse. The
+// barrier is a bare s_barrier: a fenced one would wait for every load in
+// flight, stages ahead included.
 template <int BM, int BN, int WM, int WN, int KB>
 struct DmaTile {
     static constexpr int T = WM * WN * 64;
@@ -449,7 +448,10 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_w8a8_dma_kernel(
                     if (row < m) {
                         float* dst = out + static_cast<int64_t>(row) * ldo + col;
                         if (col + 3 < n) {
-                            *reinterpret_cast<f4u*>(dst) = v;
+                            // streamed once: non-temporal, so the output does not
+                            // evict operand lines from L2 (4096 x 14336 x 4096:
+                            // 275 -> 260 us)
+                            __builtin_nontemporal_store(v, reinterpret_cast<f4u*>(dst));
                         } else {
                             if (col < n) dst[0] = v.x;
                             if (col + 1 < n) dst[1] = v.y;

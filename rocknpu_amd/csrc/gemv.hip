@@ -454,9 +454,7 @@ void launch_d(const GemvArgs& p, int d, dim3 grid, size_t lds, hipStream_t strea
     constexpr int DM = SUMS ? 1 : (HALF ? (max_depth<KIND, L>() > 1 ? max_depth<KIND, L>() / 2 : 1)
                                         : max_depth<KIND, L>());
     const dim3 block(W * 64);
-    if (DM >= 4 && d >= 4) gemv_kernel<KIND, L, MT, FUSED, (DM >= 4 ? 4 : 1), SUMS, W, QP><<<grid, block, lds, stream>>>(p);
-    else if (DM >= 4 && d == 3) gemv_kernel<KIND, L, MT, FUSED, (DM >= 4 ? 3 : 1), SUMS, W, QP><<<grid, block, lds, stream>>>(p);
-    else if (DM >= 2 && d >= 2) gemv_kernel<KIND, L, MT, FUSED, (DM >= 2 ? 2 : 1), SUMS, W, QP><<<grid, block, lds, stream>>>(p);
+    if (DM >= 2 && d >= 2) gemv_kernel<KIND, L, MT, FUSED, (DM >= 2 ? 2 : 1), SUMS, W, QP><<<grid, block, lds, stream>>>(p);
     else gemv_kernel<KIND, L, MT, FUSED, 1, SUMS, W, QP><<<grid, block, lds, stream>>>(p);
 }
 
@@ -533,6 +531,13 @@ int launch_kind(GemvParams& p, hipStream_t stream) {
     const bool w8_ok = FUSED && !sums;
     const int64_t slots8 = static_cast<int64_t>(cus) * 8, slots16 = static_cast<int64_t>(cus) * 16;
     int L = 0, W = 16;
+    // Long rows (4 or more blocks per slot) first try 16 waves with the
+    // largest L that still gives every row group a wave: Llama-3-8B down
+    // (Q6_K, 4096 x 14336) then takes 14.5 us, against 15.8 us with L = 4 and
+    // 8 waves.
+    if (p.iters >= 4)
+        for (int l = max_l; l >= 2 && L == 0; l >>= 1)
+            if (row_groups(l) <= slots16) { L = l; W = 16; }
     for (int l = max_l; l >= 2 && L == 0; l >>= 1)
         if (w8_ok && row_groups(l) <= slots8) { L = l; W = 8; }
     for (int l = max_l; l >= 2 && L == 0; l >>= 1)
@@ -571,7 +576,11 @@ int launch_kind(GemvParams& p, hipStream_t stream) {
     ka.nb = p.nb;
     ka.log2g = p.log2g;
     ka.iters = p.iters;
-    const int d = static_cast<int>(std::min<int64_t>(per_wave, 4));
+    // Blocks in flight per lane: more than one Q6_K block, or more than two
+    // Q4_K blocks, measured slower in every shape (the memory pipeline of a
+    // CU is full with fewer): TinyLlama down (Q6_K, 2048 x 5632) 6.9 -> 6.2
+    // us, Llama-3-8B gate+up (Q4_K, 28672 x 4096) 15.9 -> 14.1 us.
+    const int d = static_cast<int>(std::min<int64_t>(per_wave, KIND == 6 ? 1 : 2));
     const int passes = (p.m * p.nb + W * 4 - 1) / (W * 4);  // 16 lanes per block
     const size_t lds = static_cast<size_t>(mt) * p.nb * kGemvLdsPerBlock;
     const dim3 grid(static_cast<unsigned>(wgs));
