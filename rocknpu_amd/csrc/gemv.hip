@@ -543,6 +543,14 @@ int launch_kind(GemvParams& p, hipStream_t stream) {
     for (int l = max_l; l >= 2 && L == 0; l >>= 1)
         if (row_groups(l) <= slots16) { L = l; W = 16; }
     if (L == 0) { L = std::min(4, max_l); W = w8_ok ? 8 : 16; }
+    // A shape that leaves CUs idle gives way to a wider L with 16 waves when
+    // that fills every CU within two row groups per wave: TinyLlama gate+up
+    // (2 x 5632 rows, K = 2048) runs L = 4 on 256 CUs in 5.45 us, against L = 2
+    // on 176 CUs in 5.95 us.
+    auto wgs_for = [&](int l, int w) { return std::min<int64_t>(cus, (row_groups(l) + w - 1) / w); };
+    if (wgs_for(L, W) < cus)
+        for (int l = max_l; l > L; l >>= 1)
+            if (wgs_for(l, 16) >= cus && row_groups(l) <= 2 * slots16) { L = l; W = 16; break; }
     const int64_t max_wgs = cus;
     const int64_t rows_per_group = 64 / L / G;
     // Workgroups: at most one per CU and one per W row groups, split between
@@ -576,11 +584,13 @@ int launch_kind(GemvParams& p, hipStream_t stream) {
     ka.nb = p.nb;
     ka.log2g = p.log2g;
     ka.iters = p.iters;
-    // Blocks in flight per lane: more than one Q6_K block, or more than two
-    // Q4_K blocks, measured slower in every shape (the memory pipeline of a
-    // CU is full with fewer): TinyLlama down (Q6_K, 2048 x 5632) 6.9 -> 6.2
-    // us, Llama-3-8B gate+up (Q4_K, 28672 x 4096) 15.9 -> 14.1 us.
-    const int d = static_cast<int>(std::min<int64_t>(per_wave, KIND == 6 ? 1 : 2));
+    // Blocks in flight per lane: one Q6_K block, and Q4_K blocks for 16 per
+    // CU and lane position (two with 8 waves, one with 16). More measured
+    // slower in every shape (the memory pipeline of a CU is full with fewer):
+    // TinyLlama down (Q6_K, 2048 x 5632) 6.9 -> 6.2 us, Llama-3-8B gate+up
+    // (Q4_K, 28672 x 4096) 15.9 -> 14.1 us; TinyLlama gate+up at L = 4 and 16
+    // waves takes 5.45 us with one Q4_K block in flight, 6.9 us with two.
+    const int d = static_cast<int>(std::min<int64_t>(per_wave, KIND == 6 ? 1 : 16 / W));
     const int passes = (p.m * p.nb + W * 4 - 1) / (W * 4);  // 16 lanes per block
     const size_t lds = static_cast<size_t>(mt) * p.nb * kGemvLdsPerBlock;
     const dim3 grid(static_cast<unsigned>(wgs));
