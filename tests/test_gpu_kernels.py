@@ -127,7 +127,14 @@ def _gemm_dev(a8, as_, w8, ws):
                                    (3, 28672, 4096),      # weight-streaming kernel, many tiles per workgroup
                                    (16, 17, 7168),        # weight-streaming kernel at its LDS limit, ragged tile
                                    (9, 100, 64),          # weight-streaming kernel, fewer K chunks than waves
-                                   (12, 40, 7232)])       # A8 rows beyond the weight-streaming LDS: tiled kernel
+                                   (12, 40, 7232),        # A8 rows beyond the weight-streaming LDS: tiled kernel
+                                   # 128-byte stages; two stages where tiles outnumber the 256 CUs
+                                   (64, 1000, 2048),      # 64x32 tiles, four stages
+                                   (64, 8224, 256),       # 64x32 tiles, two stages
+                                   (100, 8256, 384),      # 64x64 tiles, two stages, ragged M
+                                   (250, 8260, 256),      # 128x64 tiles, two stages, ragged N
+                                   (520, 8300, 384),      # 128x128 tiles, two stages, ragged edges
+                                   (4100, 4000, 256)])    # 256x256 tiles, two stages, ragged edges
 def test_gemm_w8a8_bit_exact(m, n, k):
     print(f"gemm m={m} n={n} k={k}", flush=True)
     g = np.random.default_rng(m * 1000 + n + k)
