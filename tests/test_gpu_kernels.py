@@ -122,12 +122,13 @@ def _gemm_dev(a8, as_, w8, ws):
                                    (4096, 4096, 256),     # 256x256 tiles
                                    (4100, 4000, 192),     # 256x256 tiles, ragged edges, 3 K steps
                                    (64, 48, 192),         # 64x32 tiles, half a tile of N past the edge
-                                   (250, 70, 4160),       # 128x32 tiles, K steps not a multiple of 4
+                                   (250, 70, 4160),       # 128x64 tiles, K not a multiple of 128: 64-byte stages
                                    (40, 33, 64),          # 64x32 tiles, one K step
                                    (3, 28672, 4096),      # weight-streaming kernel, many tiles per workgroup
                                    (16, 17, 7168),        # weight-streaming kernel at its LDS limit, ragged tile
                                    (9, 100, 64),          # weight-streaming kernel, fewer K chunks than waves
-                                   (12, 40, 7232),        # A8 rows beyond the weight-streaming LDS: tiled kernel
+                                   (16, 40, 7232),        # A8 rows beyond the weight-streaming LDS: direct-load tiles
+                                   (24, 5632, 2048),      # 17..32 rows: direct-load 64x32 tiles
                                    # 128-byte stages; two stages where tiles outnumber the 256 CUs
                                    (64, 1000, 2048),      # 64x32 tiles, four stages
                                    (64, 8224, 256),       # 64x32 tiles, two stages
