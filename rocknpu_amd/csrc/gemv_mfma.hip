@@ -28,7 +28,8 @@
 //
 // Work split: a tile is 16 weight rows. A workgroup holds 8 waves; wave g
 // takes blocks g, g + 8, .. of every tile its workgroup walks (tiles
-// blockIdx.x, + gridDim.x, ..), with D blocks of loads in flight. When a
+// blockIdx.x, + gridDim.x, ..), with D blocks of loads in flight (the
+// launcher runs D = 1). When a
 // tile's blocks are done, the waves leave their f32 partial sums in LDS and
 // wave 0 adds them in wave order and stores the rows. The f32 order of a
 // row's terms therefore depends only on nb: the same in fused launches, in
@@ -379,33 +380,33 @@ __global__ __launch_bounds__(kMfmaWaves * 64) void gemv_mfma_kernel(const MfmaAr
     }
 }
 
+// One block of loads in flight per wave: deeper rings measured slower in
+// every shape (TinyLlama gate+up at 4 rows 8.95 -> 8.40 us, Llama-3-8B
+// gate+up at 4 rows 28.0 -> 26.7 us, with one instead of up to four).
 template <int KIND, int MT, bool FUSED, int QP>
-void launch_d(const MfmaArgs& p, int d, dim3 grid, size_t lds, hipStream_t stream) {
-    const dim3 block(kMfmaWaves * 64);
-    if (d >= 4) gemv_mfma_kernel<KIND, MT, FUSED, 4, QP><<<grid, block, lds, stream>>>(p);
-    else if (d >= 2) gemv_mfma_kernel<KIND, MT, FUSED, 2, QP><<<grid, block, lds, stream>>>(p);
-    else gemv_mfma_kernel<KIND, MT, FUSED, 1, QP><<<grid, block, lds, stream>>>(p);
+void launch_d(const MfmaArgs& p, dim3 grid, size_t lds, hipStream_t stream) {
+    gemv_mfma_kernel<KIND, MT, FUSED, 1, QP><<<grid, dim3(kMfmaWaves * 64), lds, stream>>>(p);
 }
 
 template <int KIND, int MT, bool FUSED>
-void launch_mt(const MfmaArgs& p, int d, int passes, dim3 grid, size_t lds, hipStream_t stream) {
+void launch_mt(const MfmaArgs& p, int passes, dim3 grid, size_t lds, hipStream_t stream) {
     if constexpr (FUSED) {
-        if (passes > 1) return launch_d<KIND, MT, FUSED, 4>(p, d, grid, lds, stream);
+        if (passes > 1) return launch_d<KIND, MT, FUSED, 4>(p, grid, lds, stream);
     }
-    launch_d<KIND, MT, FUSED, 1>(p, d, grid, lds, stream);
+    launch_d<KIND, MT, FUSED, 1>(p, grid, lds, stream);
 }
 
 template <int KIND>
-void launch_kind(bool fused, int mt, const MfmaArgs& ka, int d, int passes, dim3 grid, size_t lds,
+void launch_kind(bool fused, int mt, const MfmaArgs& ka, int passes, dim3 grid, size_t lds,
                  hipStream_t stream) {
     if (fused) {
-        if (mt == 2) launch_mt<KIND, 2, true>(ka, d, passes, grid, lds, stream);
-        else if (mt == 4) launch_mt<KIND, 4, true>(ka, d, passes, grid, lds, stream);
-        else launch_mt<KIND, 8, true>(ka, d, passes, grid, lds, stream);
+        if (mt == 2) launch_mt<KIND, 2, true>(ka, passes, grid, lds, stream);
+        else if (mt == 4) launch_mt<KIND, 4, true>(ka, passes, grid, lds, stream);
+        else launch_mt<KIND, 8, true>(ka, passes, grid, lds, stream);
     } else {
-        if (mt == 2) launch_mt<KIND, 2, false>(ka, d, passes, grid, lds, stream);
-        else if (mt == 4) launch_mt<KIND, 4, false>(ka, d, passes, grid, lds, stream);
-        else launch_mt<KIND, 8, false>(ka, d, passes, grid, lds, stream);
+        if (mt == 2) launch_mt<KIND, 2, false>(ka, passes, grid, lds, stream);
+        else if (mt == 4) launch_mt<KIND, 4, false>(ka, passes, grid, lds, stream);
+        else launch_mt<KIND, 8, false>(ka, passes, grid, lds, stream);
     }
 }
 
@@ -431,18 +432,15 @@ int launch_gemv_mfma(int kind, bool fused, GemvParams& p, hipStream_t stream) {
     ka.m = p.m;
     ka.nb = p.nb;
     ka.tiles = tiles;
-    // one workgroup per CU at most; each walks its tiles with up to 4 blocks in flight per wave
+    // one workgroup per CU at most; each walks its tiles
     const int cus = device_cu_count();
     const int wgs = std::min(tiles, cus);
-    const int iters = (p.nb + kMfmaWaves - 1) / kMfmaWaves;
-    const int per_wave = (tiles + wgs - 1) / wgs * iters;
-    const int d = std::min(per_wave, 4);
     const int passes = (p.m * p.nb + kMfmaWaves * 4 - 1) / (kMfmaWaves * 4);
     const size_t lds = ((static_cast<size_t>(mt) * p.nb * kGemvLdsPerBlock + 15) & ~size_t{15}) +
                        2 * kMfmaWaves * 64 * 4 * sizeof(float);
     const dim3 grid(static_cast<unsigned>(wgs));
-    if (kind == 4) launch_kind<4>(fused, mt, ka, d, passes, grid, lds, stream);
-    else launch_kind<6>(fused, mt, ka, d, passes, grid, lds, stream);
+    if (kind == 4) launch_kind<4>(fused, mt, ka, passes, grid, lds, stream);
+    else launch_kind<6>(fused, mt, ka, passes, grid, lds, stream);
     return hipGetLastError() == hipSuccess ? kStatusOk : kStatusExec;
 }
 
