@@ -619,7 +619,14 @@ int launch_gemv_mfma(int kind, bool fused, GemvParams& p, hipStream_t stream);  
 // us at 6 rows, while at 4 rows the lane-per-block kernel's 11.4 us beats
 // 12.4), except where the exact per-block sums are asked for.
 int launch_gemv(int kind, bool fused, GemvParams& p, hipStream_t stream) {
-    if (p.m >= (kind == 4 ? 3 : 5) && p.isum == nullptr) return launch_gemv_mfma(kind, fused, p, stream);
+    // Matrix cores from 3 rows for Q4_K, from 5 rows for Q6_K, and for Q6_K
+    // at 3 or 4 rows when its 16-row tiles fill every CU (Llama-3-8B down,
+    // 4096 x 14336, at 4 rows: 25.8 -> 22.5 us; TinyLlama down, 2048 rows,
+    // stays on the lane-per-block kernel, 10.6 against 11.1 us).
+    int64_t rows = 0;
+    for (int i = 0; i < p.count; ++i) rows += p.rows[i];
+    const bool mfma = kind == 4 ? p.m >= 3 : p.m >= 5 || (p.m >= 3 && rows >= 16 * int64_t{device_cu_count()});
+    if (mfma && p.isum == nullptr) return launch_gemv_mfma(kind, fused, p, stream);
     if (kind == 4) return fused ? launch_kind<4, true>(p, stream) : launch_kind<4, false>(p, stream);
     if (kind == 6) return fused ? launch_kind<6, true>(p, stream) : launch_kind<6, false>(p, stream);
     return kStatusInvalid;

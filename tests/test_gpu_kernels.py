@@ -259,12 +259,14 @@ def test_gemv_q4k_multi_row(n, k, m):
 
 
 @pytest.mark.parametrize("n,k,m", [(16, 256, 5), (40, 1024, 4), (2048, 5632, 6), (130, 5632, 5), (300, 2048, 8),
-                                   (17, 14336, 7), (1000, 4096, 7), (64, 28672, 8)])
+                                   (17, 14336, 7), (1000, 4096, 7), (64, 28672, 8),
+                                   (4096, 2048, 3), (4200, 1024, 4)])
 def test_gemv_q6k_multi_row(n, k, m):
-    """Q6_K at 4..8 activation rows without the exact-sums outputs (5..8 rows run on the
-    matrix-core kernel) against the oracle: ragged tiles, blocks per row not a multiple
-    of 8, odd row lengths (2-byte aligned blocks), padded activation rows, and a K whose
-    activation rows need two launches (112 KiB of LDS)."""
+    """Q6_K at 3..8 activation rows without the exact-sums outputs against the oracle
+    (5..8 rows run on the matrix-core kernel, and 3..4 rows when the weight rows make
+    a 16-row tile per CU): ragged tiles, blocks per row not a multiple of 8, odd row
+    lengths (2-byte aligned blocks), padded activation rows, and a K whose activation
+    rows need two launches (112 KiB of LDS)."""
     print(f"gemv q6k multi-row n={n} k={k} m={m}", flush=True)
     w = synth.kquant(6, n, k, index=820 + n + m)
     x = synth.activations(m, k, index=821 + k)
