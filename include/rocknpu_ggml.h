@@ -29,6 +29,18 @@ int rocknpu_matmul_q_q8k_f32_f32(rocknpu_context * context, uint32_t kind, const
                                  size_t weights_bytes, const float * activations_mk_f32,
                                  float * output_mn_f32, size_t m, size_t k, size_t n);
 
+/* 1..4 projections that read the same activations (q/k/v, gate/up) in one
+ * call, each output bit-identical to rocknpu_matmul_q_q8k_f32_f32 on that
+ * projection. Arguments as rocknpu_matmul_q_concat_f32_f32_mtile (rocknpu.h;
+ * reference rocknpu.h:47-53, lib.rs:2457-2614): kinds[i] is 4 or 6 and may
+ * differ between members. The reference groups same-input projections this
+ * way only on its prompt path (ggml-rocknpu.cpp:856-976). */
+int rocknpu_matmul_q_q8k_group_f32_f32(rocknpu_context * context, size_t count,
+                                       const uint8_t * const * weights, const size_t * bytes,
+                                       const uint32_t * kinds, const size_t * ns,
+                                       const float * activations_mk_f32, float * const * outputs,
+                                       size_t m, size_t k);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,0 +1,96 @@
+/*
+ * rocknpu_route.h — MUL_MAT routing of a ggml backend over this C ABI,
+ * without ggml.
+ *
+ * The reference plugin decides per graph node whether the backend takes a
+ * MUL_MAT (supports_op, adapters/ggml-rocknpu/src/ggml-rocknpu.cpp:614-715),
+ * groups later projections that read the same activations into one call
+ * (rocknpu_mtile_group, :856-976), and dispatches each group or node to a
+ * rocknpu.h entry point (rocknpu_backend_graph_compute, :978-1650). These
+ * functions make the same three decisions from a plain description of each
+ * node, so a plugin fills one rocknpu_mul_mat_node per ggml MUL_MAT and calls
+ * them; the tests drive them the same way.
+ *
+ * GPU deviations from the NPU plugin: the NPU tile limits (K % 512,
+ * K <= 4096 or 12288, N % 32, N <= 8192 or 3 x 8192, M <= 128 without
+ * ROCKNPU_PREFILL_CACHE) and the scheduling experiments behind ROCKNPU_SCHED_*,
+ * ROCKNPU_M16_ONLY and ROCKNPU_RUNTIME_* are not applied: every entry point
+ * here takes any shape with K % 256 == 0. Groups hold up to 4 projections of
+ * any M (the NPU took M >= 32).
+ */
+#ifndef ROCKNPU_ROUTE_H
+#define ROCKNPU_ROUTE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#include "rocknpu.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ggml tensor type ids (ggml.h enum ggml_type) the routing reads. */
+#define ROCKNPU_TYPE_F32 0
+#define ROCKNPU_TYPE_F16 1
+#define ROCKNPU_TYPE_Q4_K 12
+#define ROCKNPU_TYPE_Q5_K 13
+#define ROCKNPU_TYPE_Q6_K 14
+
+/* What graph_compute reads of a MUL_MAT node dst = src0 x src1. */
+typedef struct rocknpu_mul_mat_node {
+    int32_t weight_type;      /* src0->type */
+    int32_t activation_type;  /* src1->type */
+    int32_t output_type;      /* dst->type */
+    int32_t contiguous;       /* ggml_is_contiguous of src0, src1 and dst */
+    int64_t weight_ne[4];     /* src0->ne: K, N, 1, 1 */
+    int64_t activation_ne[4]; /* src1->ne: K, M, 1, 1 */
+    const void * weights;     /* src0->data */
+    size_t weight_bytes;      /* ggml_nbytes(src0) */
+    const float * activations;/* src1->data: nodes with the same pointer share an input */
+    float * output;           /* dst->data, M x N f32 */
+} rocknpu_mul_mat_node;
+
+/* Where single-token (M = 1) MUL_MATs go (ROCKNPU_DECODE, ggml-rocknpu.cpp:305-322). */
+enum rocknpu_decode_route {
+    ROCKNPU_DECODE_CPU = 0,  /* left to ggml-cpu (the reference default) */
+    ROCKNPU_DECODE_GGML = 1, /* GPU, llama.cpp's Q8_K arithmetic (rocknpu_ggml.h) */
+    ROCKNPU_DECODE_W8A8 = 2, /* GPU, the reference's NPU route: W8A8 M=1 entries */
+};
+
+/* 1 when the backend takes the node, else 0 (supports_op,
+ * ggml-rocknpu.cpp:614-715): F16/Q4_K/Q5_K/Q6_K weights, f32 activations and
+ * output, all contiguous, 2-D, matching K, weight bytes that match the
+ * shape, K % 256 == 0 for K-quants; M = 1 only for Q4_K/Q6_K and
+ * a GPU decode route (Q5_K and F16 decode stay on the CPU, as in the
+ * reference). */
+int rocknpu_route_supported(const rocknpu_mul_mat_node * node, int32_t decode_route);
+
+/* Same-input groups in node order (rocknpu_mtile_group,
+ * ggml-rocknpu.cpp:856-887): a supported Q4_K/Q6_K node leads a group and
+ * takes up to 3 later supported Q4_K/Q6_K nodes with the same activations
+ * pointer, K and M, not already taken; every other node is a group of its
+ * own. group_of[i] = index of the lead node of node i's group (group_of has
+ * `count` entries; unsupported nodes get -1). Returns the number of groups. */
+size_t rocknpu_route_plan(const rocknpu_mul_mat_node * nodes, size_t count, int32_t decode_route,
+                          int32_t * group_of);
+
+/* Runs the nodes' groups in lead order through the entry points:
+ *   group of 2..4, M > 1:            rocknpu_matmul_q_concat_f32_f32_mtile
+ *   group of 2..4, M = 1, GGML:      rocknpu_matmul_q_q8k_group_f32_f32
+ *   group of 2 or 3, M = 1, W8A8:    rocknpu_matmul_q_pair_f32_f32_m1 / _triple_
+ *                                    (4: two pairs)
+ *   single Q4_K/Q6_K, M = 1, GGML:   rocknpu_matmul_q_q8k_f32_f32
+ *   single Q4_K/Q5_K/Q6_K:           rocknpu_matmul_q{4,5,6}_k_f32_f32
+ *   single F16:                      rocknpu_matmul_f16_f32_f32
+ * ROCKNPU_STATUS_INVALID_ARGUMENT for an unsupported node (the plugin's
+ * graph_compute fails the graph the same way, ggml-rocknpu.cpp:1099-1102);
+ * otherwise the first failing call's status, or ROCKNPU_STATUS_OK. */
+int rocknpu_route_run(rocknpu_context * context, const rocknpu_mul_mat_node * nodes, size_t count,
+                      int32_t decode_route);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif

@@ -1,5 +1,5 @@
 """ctypes binding of librocknpu_capi.so (include/rocknpu.h, rocknpu_ggml.h,
-rocknpu_hip.h, rocknpu_sidecar.h).
+rocknpu_hip.h, rocknpu_sidecar.h, rocknpu_route.h).
 
 The library is loaded from this package directory only. A missing library is
 an error, never a fallback: every compute path in this package goes through
@@ -47,6 +47,11 @@ SIGNATURES = {
     "rocknpu_matmul_q6_k_f32_f32": (_i, [_ctx, _vp, _sz, _vp, _vp, _sz, _sz, _sz]),
     # rocknpu_ggml.h — decode MUL_MAT with llama.cpp CPU numerics
     "rocknpu_matmul_q_q8k_f32_f32": (_i, [_ctx, _u32, _vp, _sz, _vp, _vp, _sz, _sz, _sz]),
+    "rocknpu_matmul_q_q8k_group_f32_f32": (_i, [_ctx, _sz, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _sz]),
+    # rocknpu_route.h — MUL_MAT routing over the C ABI
+    "rocknpu_route_supported": (_i, [_vp, ctypes.c_int32]),
+    "rocknpu_route_plan": (_sz, [_vp, _sz, ctypes.c_int32, _vp]),
+    "rocknpu_route_run": (_i, [_ctx, _vp, _sz, ctypes.c_int32]),
     # rocknpu_sidecar.h — the W8 sidecar
     "rocknpu_w8_source_fingerprint": (ctypes.c_uint64, [_vp, _sz]),
     "rocknpu_w8_sidecar_read": (_i, [ctypes.c_char_p, ctypes.c_char_p, _vp, _sz, _sz, _sz, _vp, _vp]),

@@ -87,6 +87,18 @@ class Context:
         return self.lib.rocknpu_matmul_q_q8k_f32_f32(self.handle, kind, _p(weights), weights.nbytes, _p(act),
                                                      _p(out), m, k, n)
 
+    def matmul_q_q8k_group(self, weights, kinds, ns, act: np.ndarray, outs, k: int) -> int:
+        """rocknpu_matmul_q_q8k_group_f32_f32 (include/rocknpu_ggml.h)."""
+        count = len(weights)
+        w_arr = _ptr_array(weights)
+        b_arr = (ctypes.c_size_t * count)(*[w.nbytes for w in weights])
+        k_arr = (ctypes.c_uint32 * count)(*kinds)
+        n_arr = (ctypes.c_size_t * count)(*ns)
+        o_arr = _ptr_array(outs)
+        m = act.shape[0] if act.ndim == 2 else 1
+        return self.lib.rocknpu_matmul_q_q8k_group_f32_f32(self.handle, count, w_arr, b_arr, k_arr, n_arr,
+                                                           _p(act), o_arr, m, k)
+
     def matmul_q_concat(self, weights, kinds, ns, act: np.ndarray, outs, k: int) -> int:
         count = len(weights)
         w_arr = _ptr_array(weights)

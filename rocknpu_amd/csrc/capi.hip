@@ -505,6 +505,22 @@ int context_repack_to_host(rocknpu_context* ctx, uint32_t kind, const uint8_t* s
 
 }  // namespace rk
 
+namespace {
+// The raw K-quant blocks of a weight, resident on the device under the
+// reference's cache key; uploaded on first use.
+std::shared_ptr<DevBuf> raw_weights(RockNpuContext* ctx, const uint8_t* w, size_t bytes, size_t k, size_t n,
+                                    uint32_t kind) {
+    const WeightKey key{reinterpret_cast<uintptr_t>(w), bytes, k, n, kind};
+    auto it = ctx->raw.find(key);
+    if (it != ctx->raw.end()) return it->second;
+    auto dw = std::make_shared<DevBuf>();
+    if (!dw->ensure(bytes) || !hip_ok(hipMemcpyAsync(dw->p, w, bytes, hipMemcpyHostToDevice, ctx->stream), ctx, "raw"))
+        return nullptr;
+    ctx->raw.emplace(key, dw);
+    return dw;
+}
+}  // namespace
+
 extern "C" {
 
 size_t rocknpu_device_count(void) {
@@ -778,18 +794,8 @@ int rocknpu_matmul_q_q8k_f32_f32(rocknpu_context* ctx, uint32_t kind, const uint
     if (!mul_ok(m, k, &a_elems) || !mul_ok(m, n, &o_elems)) return kInvalid;
     for (size_t i = 0; i < a_elems; ++i)
         if (!std::isfinite(act[i])) return kInvalid;
-    const WeightKey key{reinterpret_cast<uintptr_t>(w), bytes, k, n, kind};
-    auto it = ctx->raw.find(key);
-    std::shared_ptr<DevBuf> dw;
-    if (it != ctx->raw.end()) {
-        dw = it->second;
-    } else {
-        dw = std::make_shared<DevBuf>();
-        if (!dw->ensure(bytes) ||
-            !hip_ok(hipMemcpyAsync(dw->p, w, bytes, hipMemcpyHostToDevice, ctx->stream), ctx, "raw"))
-            return kExec;
-        ctx->raw.emplace(key, dw);
-    }
+    const std::shared_ptr<DevBuf> dw = raw_weights(ctx, w, bytes, k, n, kind);
+    if (!dw) return kExec;
     const size_t q8_bytes = m * (k / kQK) * 292;
     if (!ctx->d_act.ensure(a_elems * 4) || !ctx->d_q8k.ensure(q8_bytes) || !ctx->d_out.ensure(o_elems * 4))
         return kExec;
@@ -804,6 +810,61 @@ int rocknpu_matmul_q_q8k_f32_f32(rocknpu_context* ctx, uint32_t kind, const uint
         !hip_ok(hipStreamSynchronize(ctx->stream), ctx, "gemv"))
         return kExec;
     return kOk;
+}
+
+int rocknpu_matmul_q_q8k_group_f32_f32(rocknpu_context* ctx, size_t count, const uint8_t* const* weights,
+                                       const size_t* bytes, const uint32_t* kinds, const size_t* ns,
+                                       const float* act, float* const* outputs, size_t m, size_t k) {
+    if (!ctx || !weights || !bytes || !kinds || !ns || !act || !outputs || count == 0 || count > 4 || m == 0 ||
+        k == 0)
+        return kInvalid;
+    size_t a_elems, total_n = 0;
+    if (!mul_ok(m, k, &a_elems)) return kInvalid;
+    for (size_t i = 0; i < count; ++i) {
+        if (!weights[i] || !outputs[i] || ns[i] == 0 || !kquant_kind(kinds[i]) ||
+            !kquant_shape_ok(kinds[i], bytes[i], k, ns[i]))
+            return kInvalid;
+        total_n += ns[i];
+    }
+    size_t o_elems;
+    if (!mul_ok(m, total_n, &o_elems)) return kInvalid;
+    for (size_t i = 0; i < a_elems; ++i)
+        if (!std::isfinite(act[i])) return kInvalid;
+    std::shared_ptr<DevBuf> dw[4];
+    for (size_t i = 0; i < count; ++i)
+        if (!(dw[i] = raw_weights(ctx, weights[i], bytes[i], k, ns[i], kinds[i]))) return kExec;
+    if (!ctx->d_act.ensure(a_elems * 4) || !ctx->d_out.ensure(o_elems * 4)) return kExec;
+    if (!hip_ok(hipMemcpyAsync(ctx->d_act.p, act, a_elems * 4, hipMemcpyHostToDevice, ctx->stream), ctx, "act"))
+        return kExec;
+    // member i's rows at offset m * (n of the members before it); one fused
+    // launch per kind over that kind's members, in member order
+    size_t off[4];
+    for (size_t i = 0, o = 0; i < count; o += m * ns[i], ++i) off[i] = o;
+    for (uint32_t kind : {4u, 6u}) {
+        const uint8_t* w[4];
+        size_t wb[4], wn[4], ldo[4];
+        float* out[4];
+        size_t c = 0;
+        for (size_t i = 0; i < count; ++i) {
+            if (kinds[i] != kind) continue;
+            w[c] = dw[i]->as<uint8_t>();
+            wb[c] = bytes[i];
+            wn[c] = ns[i];
+            ldo[c] = ns[i];
+            out[c] = ctx->d_out.as<float>() + off[i];
+            ++c;
+        }
+        if (c == 0) continue;
+        const int st = rocknpu_hip_gemv_q_f32(kind, c, w, wb, wn, k, ctx->d_act.as<float>(), k, m, out, ldo,
+                                              ctx->stream);
+        if (st != kOk) return st;
+    }
+    for (size_t i = 0; i < count; ++i)
+        if (!hip_ok(hipMemcpyAsync(outputs[i], ctx->d_out.as<float>() + off[i], m * ns[i] * 4, hipMemcpyDeviceToHost,
+                                   ctx->stream),
+                    ctx, "out"))
+            return kExec;
+    return hip_ok(hipStreamSynchronize(ctx->stream), ctx, "gemv") ? kOk : kExec;
 }
 
 }  // extern "C"

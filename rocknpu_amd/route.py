@@ -1,0 +1,71 @@
+"""MUL_MAT routing over the C ABI (include/rocknpu_route.h), for numpy arrays.
+
+A node is what the reference plugin's graph_compute reads of a ggml MUL_MAT
+(adapters/ggml-rocknpu/src/ggml-rocknpu.cpp:614-715 supports_op, :856-976
+same-input grouping, :978-1650 dispatch): weight, activation and output types,
+ne[], contiguity and the data pointers. `supported`, `plan` and `run` call the
+library's routing functions; the arrays must outlive the call.
+"""
+from __future__ import annotations
+
+import ctypes
+
+import numpy as np
+
+from . import _lib
+
+F32, F16, Q4_K, Q5_K, Q6_K = 0, 1, 12, 13, 14
+DECODE_CPU, DECODE_GGML, DECODE_W8A8 = 0, 1, 2
+BLOCK_BYTES = {Q4_K: 144, Q5_K: 176, Q6_K: 210}
+
+
+class MulMatNode(ctypes.Structure):
+    """rocknpu_mul_mat_node (include/rocknpu_route.h)."""
+
+    _fields_ = [
+        ("weight_type", ctypes.c_int32), ("activation_type", ctypes.c_int32), ("output_type", ctypes.c_int32),
+        ("contiguous", ctypes.c_int32), ("weight_ne", ctypes.c_int64 * 4), ("activation_ne", ctypes.c_int64 * 4),
+        ("weights", ctypes.c_void_p), ("weight_bytes", ctypes.c_size_t), ("activations", ctypes.c_void_p),
+        ("output", ctypes.c_void_p),
+    ]
+
+
+def node(weight_type: int, weights: np.ndarray, k: int, n: int, activations: np.ndarray,
+         output: np.ndarray, contiguous: bool = True, activation_type: int = F32,
+         output_type: int = F32) -> MulMatNode:
+    """A node for dst[m, n] = activations[m, k] x weights (K-quant blocks or
+    f16 bits [n, k]); the pointers are the arrays' data."""
+    m = activations.shape[0] if activations.ndim == 2 else 1
+    nd = MulMatNode()
+    nd.weight_type, nd.activation_type, nd.output_type = weight_type, activation_type, output_type
+    nd.contiguous = 1 if contiguous else 0
+    nd.weight_ne[:] = (k, n, 1, 1)
+    nd.activation_ne[:] = (k, m, 1, 1)
+    nd.weights = weights.ctypes.data
+    nd.weight_bytes = weights.nbytes
+    nd.activations = activations.ctypes.data
+    nd.output = output.ctypes.data
+    return nd
+
+
+def _array(nodes):
+    arr = (MulMatNode * len(nodes))(*nodes)
+    return arr, ctypes.cast(arr, ctypes.c_void_p)
+
+
+def supported(nd: MulMatNode, decode: int = DECODE_CPU) -> bool:
+    return bool(_lib.load().rocknpu_route_supported(ctypes.byref(nd), decode))
+
+
+def plan(nodes, decode: int = DECODE_CPU) -> tuple[int, list[int]]:
+    """(number of groups, lead index of each node's group or -1)."""
+    arr, ptr = _array(nodes)
+    group_of = (ctypes.c_int32 * max(1, len(nodes)))()
+    groups = _lib.load().rocknpu_route_plan(ptr, len(nodes), decode, ctypes.cast(group_of, ctypes.c_void_p))
+    return groups, list(group_of)[:len(nodes)]
+
+
+def run(ctx, nodes, decode: int = DECODE_CPU) -> int:
+    """Status of rocknpu_route_run on an open context (rocknpu_amd.capi.Context)."""
+    arr, ptr = _array(nodes)
+    return _lib.load().rocknpu_route_run(ctx.handle if hasattr(ctx, "handle") else ctx, ptr, len(nodes), decode)
