@@ -409,6 +409,12 @@ int launch_dma_by_tiles(const int8_t* a8, int64_t lda, const int8_t* w8, int64_t
 // stages read whole 128-byte lines of each row, which the L2 serves at about
 // twice the rate of the 64-byte half lines (M x N x K = 4096 x 14336 x 4096:
 // 284 -> 272 us; 512 x 11264 x 2048: 31.5 -> 25.7 us).
+// Where the 128 x 64 (up to 256 rows) or 128 x 128 tiles outnumber the CUs
+// but tiles of twice the size fit on them in one round, the larger tiles run
+// one workgroup per CU with three stages instead: 128 x 128 tiles for up to
+// 256 rows (256 x 11264 x 2048: 19.1 -> 15.5 us; 256 x 14336 x 4096:
+// 35 -> 28.5 us), 256 x 128 tiles with eight waves above (512 x 11264 x 2048:
+// 27.2 -> 23.6 us; 768 x 8192 x 2048: 25.3 -> 23.5 us).
 int launch_gemm_w8a8(const int8_t* a8, int64_t lda, const int8_t* w8, int64_t ldw, const float* as,
                      const float* ws, int m, int n, int k, float* out, int64_t ldo, int32_t* oi,
                      int64_t ldoi, hipStream_t stream) {
@@ -418,14 +424,20 @@ int launch_gemm_w8a8(const int8_t* a8, int64_t lda, const int8_t* w8, int64_t ld
     }
     if (m <= 64) return launch_dma_by_tiles<64, 32, 2, 1>(a8, lda, w8, ldw, as, ws, m, n, k, out, ldo, oi, ldoi, stream);
     if (m <= 128) return launch_dma_by_tiles<64, 64, 2, 2>(a8, lda, w8, ldw, as, ws, m, n, k, out, ldo, oi, ldoi, stream);
-    if (m <= 256) return launch_dma_by_tiles<128, 64, 4, 1>(a8, lda, w8, ldw, as, ws, m, n, k, out, ldo, oi, ldoi, stream);
     const int cus = device_cu_count();
-    const int64_t big_tiles = static_cast<int64_t>((m + 255) / 256) * ((n + 255) / 256);
-    if (big_tiles >= cus)
+    auto tiles_of = [&](int bm, int bn) { return static_cast<int64_t>((m + bm - 1) / bm) * ((n + bn - 1) / bn); };
+    if (m <= 256) {
+        if (tiles_of(128, 64) > cus && tiles_of(128, 128) <= cus)
+            return launch_dma<128, 128, 2, 2, 3, 128>(a8, lda, w8, ldw, as, ws, m, n, k, out, ldo, oi, ldoi, stream);
+        return launch_dma_by_tiles<128, 64, 4, 1>(a8, lda, w8, ldw, as, ws, m, n, k, out, ldo, oi, ldoi, stream);
+    }
+    if (tiles_of(256, 256) >= cus)
         return launch_dma<256, 256, 2, 2, 2, 128>(a8, lda, w8, ldw, as, ws, m, n, k, out, ldo, oi, ldoi, stream);
-    const int64_t mid_tiles = static_cast<int64_t>((m + 127) / 128) * ((n + 127) / 128);
-    if (mid_tiles > cus)
+    if (tiles_of(128, 128) > cus) {
+        if (tiles_of(256, 128) <= cus)
+            return launch_dma<256, 128, 4, 2, 3, 128>(a8, lda, w8, ldw, as, ws, m, n, k, out, ldo, oi, ldoi, stream);
         return launch_dma<128, 128, 2, 2, 2, 128>(a8, lda, w8, ldw, as, ws, m, n, k, out, ldo, oi, ldoi, stream);
+    }
     return launch_dma_by_tiles<128, 64, 4, 1>(a8, lda, w8, ldw, as, ws, m, n, k, out, ldo, oi, ldoi, stream);
 }
 

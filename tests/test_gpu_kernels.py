@@ -133,8 +133,13 @@ def _gemm_dev(a8, as_, w8, ws):
                                    (64, 1000, 2048),      # 64x32 tiles, four stages
                                    (64, 8224, 256),       # 64x32 tiles, two stages
                                    (100, 8256, 384),      # 64x64 tiles, two stages, ragged M
-                                   (250, 8260, 256),      # 128x64 tiles, two stages, ragged N
-                                   (520, 8300, 384),      # 128x128 tiles, two stages, ragged edges
+                                   (250, 16500, 128),     # 128x64 tiles, two stages, ragged N
+                                   (520, 16500, 128),     # 128x128 tiles, two stages, ragged edges
+                                   # larger tiles that fit on the CUs in one round: three stages
+                                   (250, 8260, 256),      # 128x128 tiles, ragged N
+                                   (520, 8300, 384),      # 256x128 tiles, eight waves, ragged edges
+                                   (250, 8260, 320),      # 128x128 tiles, K % 128 != 0: 64-byte stages
+                                   (520, 8300, 320),      # 256x128 tiles, K % 128 != 0: 64-byte stages
                                    (4100, 4000, 256)])    # 256x256 tiles, two stages, ragged edges
 def test_gemm_w8a8_bit_exact(m, n, k):
     print(f"gemm m={m} n={n} k={k}", flush=True)
