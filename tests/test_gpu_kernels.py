@@ -140,6 +140,7 @@ def _gemm_dev(a8, as_, w8, ws):
                                    (520, 8300, 384),      # 256x128 tiles, eight waves, ragged edges
                                    (250, 8260, 320),      # 128x128 tiles, K % 128 != 0: 64-byte stages
                                    (520, 8300, 320),      # 256x128 tiles, K % 128 != 0: 64-byte stages
+                                   (2040, 11200, 128),    # 3 rounds of 256x128 tiles beat 2 of 256x256
                                    (4100, 4000, 256)])    # 256x256 tiles, two stages, ragged edges
 def test_gemm_w8a8_bit_exact(m, n, k):
     print(f"gemm m={m} n={n} k={k}", flush=True)
