@@ -360,8 +360,8 @@ def cpu_baseline_w8a8(synth, budget_s: float = 8.0) -> dict:
 def main():
     args = parse()
     if args.gpus != 1:
-        print(f"bench.py runs on one GPU only (got --gpus {args.gpus}); the multi-GPU split is a design "
-              "described in DESIGN.md, not a measured configuration.", file=sys.stderr)
+        print(f"bench.py runs on one GPU only (got --gpus {args.gpus}): the split of weight rows or K "
+              "over several GPUs is not built, so no multi-GPU figure exists.", file=sys.stderr)
         sys.exit(2)
     import torch
 
