@@ -89,6 +89,54 @@ __global__ __launch_bounds__(kA8Threads) void quantize_a8_kernel(const float* __
     if (t == 0) scales[row] = bad ? __builtin_nanf("") : scale;
 }
 
+// The same for rows of up to 16 * 1024 values with k, lda and k_pad multiples
+// of 4 and 16-byte aligned bases: each thread keeps its R float4 of the row in
+// registers, so the row is read once, not once per pass. The max is
+// order-independent and every value takes the same quant_sym, so the output
+// is bit-identical to quantize_a8_kernel's.
+template <int R>
+__global__ __launch_bounds__(kA8Threads) void quantize_a8_regs_kernel(const float* __restrict__ a,
+                                                                      int64_t k, int64_t lda,
+                                                                      int64_t k_pad,
+                                                                      int8_t* __restrict__ a8,
+                                                                      float* __restrict__ scales) {
+    __shared__ float red[kA8Threads / 64];
+    const int64_t row = blockIdx.x;
+    const float4* x = reinterpret_cast<const float4*>(a + row * lda);
+    uint32_t* q = reinterpret_cast<uint32_t*>(a8 + row * k_pad);
+    const int t = threadIdx.x;
+    const int k4 = static_cast<int>(k / 4);
+    float4 v[R];
+#pragma unroll
+    for (int j = 0; j < R; ++j) {
+        const int i = t + j * kA8Threads;
+        v[j] = i < k4 ? x[i] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    }
+    float vmax = 0.0f;
+#pragma unroll
+    for (int j = 0; j < R; ++j) {
+        const float e[4] = {v[j].x, v[j].y, v[j].z, v[j].w};
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            const float m = fabsf(e[c]);
+            vmax = fmaxf(vmax, (m <= 3.402823466e38f) ? m : __builtin_inff());
+        }
+    }
+    vmax = block_max(vmax, red);
+    const bool bad = !(vmax <= 3.402823466e38f);
+    const float scale = vmax == 0.0f ? 1.0f : vmax / 127.0f;
+#pragma unroll
+    for (int j = 0; j < R; ++j) {
+        const int i = t + j * kA8Threads;
+        if (i < k4)
+            q[i] = bad ? 0u
+                       : pack4(quant_sym(v[j].x, scale), quant_sym(v[j].y, scale), quant_sym(v[j].z, scale),
+                               quant_sym(v[j].w, scale));
+    }
+    for (int64_t i = k4 + t; i < k_pad / 4; i += kA8Threads) q[i] = 0;
+    if (t == 0) scales[row] = bad ? __builtin_nanf("") : scale;
+}
+
 // One wave per 256-value block, 4 blocks per workgroup. VEC: ldx % 4 == 0 and
 // x is 16-byte aligned.
 template <bool VEC>
@@ -150,7 +198,17 @@ int launch_quantize_a8(const float* a, int64_t m, int64_t k, int64_t lda, int64_
     const bool vec = k % 4 == 0 && lda % 4 == 0 && k_pad % 4 == 0 &&
                      reinterpret_cast<uintptr_t>(a) % 16 == 0 && reinterpret_cast<uintptr_t>(a8) % 16 == 0;
     const dim3 grid(static_cast<unsigned>(m)), block(kA8Threads);
-    if (vec) quantize_a8_kernel<true><<<grid, block, 0, stream>>>(a, k, lda, k_pad, a8, scales);
+    // float4 per thread that hold the row
+    const int64_t per = (k / 4 + kA8Threads - 1) / kA8Threads;
+    if (vec && per <= 16) {
+        if (per <= 1) quantize_a8_regs_kernel<1><<<grid, block, 0, stream>>>(a, k, lda, k_pad, a8, scales);
+        else if (per <= 2) quantize_a8_regs_kernel<2><<<grid, block, 0, stream>>>(a, k, lda, k_pad, a8, scales);
+        else if (per <= 4) quantize_a8_regs_kernel<4><<<grid, block, 0, stream>>>(a, k, lda, k_pad, a8, scales);
+        else if (per <= 6) quantize_a8_regs_kernel<6><<<grid, block, 0, stream>>>(a, k, lda, k_pad, a8, scales);
+        else if (per <= 8) quantize_a8_regs_kernel<8><<<grid, block, 0, stream>>>(a, k, lda, k_pad, a8, scales);
+        else if (per <= 12) quantize_a8_regs_kernel<12><<<grid, block, 0, stream>>>(a, k, lda, k_pad, a8, scales);
+        else quantize_a8_regs_kernel<16><<<grid, block, 0, stream>>>(a, k, lda, k_pad, a8, scales);
+    } else if (vec) quantize_a8_kernel<true><<<grid, block, 0, stream>>>(a, k, lda, k_pad, a8, scales);
     else quantize_a8_kernel<false><<<grid, block, 0, stream>>>(a, k, lda, k_pad, a8, scales);
     return hipGetLastError() == hipSuccess ? kStatusOk : kStatusExec;
 }

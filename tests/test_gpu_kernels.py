@@ -68,7 +68,10 @@ def _rounding_kat_row() -> np.ndarray:
 
 
 @pytest.mark.parametrize("m,k,k_pad", [(1, 2048, 2048), (128, 2048, 2048), (7, 5632, 5632), (3, 300, 320),
-                                       (5, 1001, 1024), (2, 2064, 2112)])
+                                       (5, 1001, 1024), (2, 2064, 2112),
+                                       (4, 14336, 14336),    # row in registers, 14 of 16 float4 per thread
+                                       (2, 16384, 16384),    # the longest row kept in registers
+                                       (3, 16388, 16448)])   # longer: two passes over the row
 def test_quantize_a8_bit_exact(m, k, k_pad):
     print(f"a8 m={m} k={k} k_pad={k_pad}", flush=True)
     a = synth.activations(m, k, index=200 + m + k)
@@ -79,9 +82,10 @@ def test_quantize_a8_bit_exact(m, k, k_pad):
     assert np.array_equal(_bits(sc.cpu().numpy()), _bits(sc_ref))
 
 
-def test_quantize_a8_edge_rows():
-    kat = _rounding_kat_row()
-    k = kat.size
+@pytest.mark.parametrize("k", [2051, 2048, 16388])  # scalar path; row in registers; two vector passes
+def test_quantize_a8_edge_rows(k):
+    print(f"a8 edge rows k={k}", flush=True)
+    kat = np.resize(_rounding_kat_row(), k)
     rows = np.zeros((6, k), np.float32)
     rows[0] = kat
     rows[1] = 0.0                                   # zero row: scale 1.0
