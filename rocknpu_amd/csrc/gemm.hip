@@ -405,7 +405,11 @@ int launch_dma_by_tiles(const int8_t* a8, int64_t lda, const int8_t* w8, int64_t
 // direct-load tiles of 64 x 32 (M <= 64: for M = 32, N = 5632, K = 2048 they
 // take 7.6 us against 18.5 us for register-staged 32 x 64 tiles), 64 x 64
 // and 128 x 64; beyond that 256 x 256 tiles when there is at least one per CU,
-// else 128 x 128 when there are more than CUs, else 128 x 64. The 128-byte
+// else 128 x 128 when there are more than CUs, else 128 x 64. Where the
+// 64 x 64 or 128 x 64 tiles would leave CUs idle, the smallest of 64 x 32,
+// 64 x 64 and 128 x 64 that fits on the CUs in one round runs instead
+// (512 x 2048 x 5632: 21.9 -> 16.5 us; 128 x 2048 x 5632: 16.2 -> 13.6 us;
+// 512 x 1024 x 4096: 15.9 -> 10.8 us). The 128-byte
 // stages read whole 128-byte lines of each row, which the L2 serves at about
 // twice the rate of the 64-byte half lines (M x N x K = 4096 x 14336 x 4096:
 // 284 -> 272 us; 512 x 11264 x 2048: 31.5 -> 25.7 us).
@@ -423,13 +427,21 @@ int launch_gemm_w8a8(const int8_t* a8, int64_t lda, const int8_t* w8, int64_t ld
         if (st != kStatusInvalid) return st;
     }
     if (m <= 64) return launch_dma_by_tiles<64, 32, 2, 1>(a8, lda, w8, ldw, as, ws, m, n, k, out, ldo, oi, ldoi, stream);
-    if (m <= 128) return launch_dma_by_tiles<64, 64, 2, 2>(a8, lda, w8, ldw, as, ws, m, n, k, out, ldo, oi, ldoi, stream);
     const int cus = device_cu_count();
     auto tiles_of = [&](int bm, int bn) { return static_cast<int64_t>((m + bm - 1) / bm) * ((n + bn - 1) / bn); };
+    // the smallest tiles that still fit on the CUs in one round
+    auto filling = [&](bool allow_128x64) {
+        if (tiles_of(64, 32) <= cus)
+            return launch_dma<64, 32, 2, 1, 4, 128>(a8, lda, w8, ldw, as, ws, m, n, k, out, ldo, oi, ldoi, stream);
+        if (!allow_128x64 || tiles_of(64, 64) <= cus)
+            return launch_dma_by_tiles<64, 64, 2, 2>(a8, lda, w8, ldw, as, ws, m, n, k, out, ldo, oi, ldoi, stream);
+        return launch_dma_by_tiles<128, 64, 4, 1>(a8, lda, w8, ldw, as, ws, m, n, k, out, ldo, oi, ldoi, stream);
+    };
+    if (m <= 128) return filling(false);
     if (m <= 256) {
         if (tiles_of(128, 64) > cus && tiles_of(128, 128) <= cus)
             return launch_dma<128, 128, 2, 2, 3, 128>(a8, lda, w8, ldw, as, ws, m, n, k, out, ldo, oi, ldoi, stream);
-        return launch_dma_by_tiles<128, 64, 4, 1>(a8, lda, w8, ldw, as, ws, m, n, k, out, ldo, oi, ldoi, stream);
+        return filling(true);
     }
     if (tiles_of(256, 256) >= cus) {
         // A round of 256 x 128 tiles (eight waves, three stages) takes about 0.61 of
@@ -446,7 +458,7 @@ int launch_gemm_w8a8(const int8_t* a8, int64_t lda, const int8_t* w8, int64_t ld
             return launch_dma<256, 128, 4, 2, 3, 128>(a8, lda, w8, ldw, as, ws, m, n, k, out, ldo, oi, ldoi, stream);
         return launch_dma<128, 128, 2, 2, 2, 128>(a8, lda, w8, ldw, as, ws, m, n, k, out, ldo, oi, ldoi, stream);
     }
-    return launch_dma_by_tiles<128, 64, 4, 1>(a8, lda, w8, ldw, as, ws, m, n, k, out, ldo, oi, ldoi, stream);
+    return filling(true);
 }
 
 }  // namespace rk

@@ -126,7 +126,7 @@ def _gemm_dev(a8, as_, w8, ws):
                                    (4096, 4096, 256),     # 256x256 tiles
                                    (4100, 4000, 192),     # 256x256 tiles, ragged edges, 3 K steps
                                    (64, 48, 192),         # 64x32 tiles, half a tile of N past the edge
-                                   (250, 70, 4160),       # 128x64 tiles, K not a multiple of 128: 64-byte stages
+                                   (250, 70, 4160),       # 64x32 tiles, K not a multiple of 128: 64-byte stages
                                    (40, 33, 64),          # 64x32 tiles, one K step
                                    (3, 28672, 4096),      # weight-streaming kernel, many tiles per workgroup
                                    (16, 17, 7168),        # weight-streaming kernel at its LDS limit, ragged tile
@@ -145,6 +145,11 @@ def _gemm_dev(a8, as_, w8, ws):
                                    (250, 8260, 320),      # 128x128 tiles, K % 128 != 0: 64-byte stages
                                    (520, 8300, 320),      # 256x128 tiles, K % 128 != 0: 64-byte stages
                                    (2040, 11200, 128),    # 3 rounds of 256x128 tiles beat 2 of 256x256
+                                   # the smallest of 64x32, 64x64 and 128x64 tiles that fits on the CUs in one round
+                                   (120, 1000, 2048),     # 65..128 rows: 64x32 tiles
+                                   (200, 2000, 320),      # 64x32 tiles, K % 128 != 0: 64-byte stages
+                                   (300, 2000, 384),      # 64x64 tiles
+                                   (520, 2050, 128),      # 128x64 tiles
                                    (4100, 4000, 256)])    # 256x256 tiles, two stages, ragged edges
 def test_gemm_w8a8_bit_exact(m, n, k):
     print(f"gemm m={m} n={n} k={k}", flush=True)
