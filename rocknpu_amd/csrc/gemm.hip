@@ -413,12 +413,14 @@ int launch_dma_by_tiles(const int8_t* a8, int64_t lda, const int8_t* w8, int64_t
 // stages read whole 128-byte lines of each row, which the L2 serves at about
 // twice the rate of the 64-byte half lines (M x N x K = 4096 x 14336 x 4096:
 // 284 -> 272 us; 512 x 11264 x 2048: 31.5 -> 25.7 us).
-// Where the 128 x 64 (up to 256 rows) or 128 x 128 tiles outnumber the CUs
-// but tiles of twice the size fit on them in one round, the larger tiles run
-// one workgroup per CU with three stages instead: 128 x 128 tiles for up to
-// 256 rows (256 x 11264 x 2048: 19.1 -> 15.5 us; 256 x 14336 x 4096:
-// 35 -> 28.5 us), 256 x 128 tiles with eight waves above (512 x 11264 x 2048:
-// 27.2 -> 23.6 us; 768 x 8192 x 2048: 25.3 -> 23.5 us).
+// Where the two-stage tiles outnumber the CUs but tiles of twice the size fit
+// on them in one round, the larger tiles run one workgroup per CU instead:
+// 64 x 64 up to 64 rows and 128 x 64 up to 128 rows with four stages
+// (128 x 11264 x 2048: 15.5 -> 11.8 us; 32 x 11264 x 2048: 13.8 -> 9.7 us),
+// 128 x 128 up to 256 rows with three (256 x 11264 x 2048: 19.1 -> 15.5 us;
+// 256 x 14336 x 4096: 35 -> 28.5 us), and 256 x 128 with eight waves and
+// three stages above (512 x 11264 x 2048: 27.2 -> 23.6 us; 768 x 8192 x 2048:
+// 25.3 -> 23.5 us).
 int launch_gemm_w8a8(const int8_t* a8, int64_t lda, const int8_t* w8, int64_t ldw, const float* as,
                      const float* ws, int m, int n, int k, float* out, int64_t ldo, int32_t* oi,
                      int64_t ldoi, hipStream_t stream) {
@@ -426,9 +428,13 @@ int launch_gemm_w8a8(const int8_t* a8, int64_t lda, const int8_t* w8, int64_t ld
         const int st = launch_gemm_w8a8_skinny(a8, lda, w8, ldw, as, ws, m, n, k, out, ldo, oi, ldoi, stream);
         if (st != kStatusInvalid) return st;
     }
-    if (m <= 64) return launch_dma_by_tiles<64, 32, 2, 1>(a8, lda, w8, ldw, as, ws, m, n, k, out, ldo, oi, ldoi, stream);
     const int cus = device_cu_count();
     auto tiles_of = [&](int bm, int bn) { return static_cast<int64_t>((m + bm - 1) / bm) * ((n + bn - 1) / bn); };
+    if (m <= 64) {
+        if (tiles_of(64, 32) > cus && tiles_of(64, 64) <= cus)
+            return launch_dma<64, 64, 2, 2, 4, 128>(a8, lda, w8, ldw, as, ws, m, n, k, out, ldo, oi, ldoi, stream);
+        return launch_dma_by_tiles<64, 32, 2, 1>(a8, lda, w8, ldw, as, ws, m, n, k, out, ldo, oi, ldoi, stream);
+    }
     // the smallest tiles that still fit on the CUs in one round
     auto filling = [&](bool allow_128x64) {
         if (tiles_of(64, 32) <= cus)
@@ -437,7 +443,11 @@ int launch_gemm_w8a8(const int8_t* a8, int64_t lda, const int8_t* w8, int64_t ld
             return launch_dma_by_tiles<64, 64, 2, 2>(a8, lda, w8, ldw, as, ws, m, n, k, out, ldo, oi, ldoi, stream);
         return launch_dma_by_tiles<128, 64, 4, 1>(a8, lda, w8, ldw, as, ws, m, n, k, out, ldo, oi, ldoi, stream);
     };
-    if (m <= 128) return filling(false);
+    if (m <= 128) {
+        if (tiles_of(64, 64) > cus && tiles_of(128, 64) <= cus)
+            return launch_dma<128, 64, 4, 1, 4, 128>(a8, lda, w8, ldw, as, ws, m, n, k, out, ldo, oi, ldoi, stream);
+        return filling(false);
+    }
     if (m <= 256) {
         if (tiles_of(128, 64) > cus && tiles_of(128, 128) <= cus)
             return launch_dma<128, 128, 2, 2, 3, 128>(a8, lda, w8, ldw, as, ws, m, n, k, out, ldo, oi, ldoi, stream);

@@ -135,13 +135,15 @@ def _gemm_dev(a8, as_, w8, ws):
                                    (24, 5632, 2048),      # 17..32 rows: direct-load 64x32 tiles
                                    # 128-byte stages; two stages where tiles outnumber the 256 CUs
                                    (64, 1000, 2048),      # 64x32 tiles, four stages
-                                   (64, 8224, 256),       # 64x32 tiles, two stages
-                                   (100, 8256, 384),      # 64x64 tiles, two stages, ragged M
+                                   (64, 16500, 128),      # 64x32 tiles, two stages
+                                   (100, 16500, 128),     # 64x64 tiles, two stages, ragged M
                                    (250, 16500, 128),     # 128x64 tiles, two stages, ragged N
                                    (520, 16500, 128),     # 128x128 tiles, two stages, ragged edges
-                                   # larger tiles that fit on the CUs in one round: three stages
-                                   (250, 8260, 256),      # 128x128 tiles, ragged N
-                                   (520, 8300, 384),      # 256x128 tiles, eight waves, ragged edges
+                                   # larger tiles that fit on the CUs in one round
+                                   (64, 8224, 256),       # 64x64 tiles, four stages
+                                   (100, 8256, 384),      # 128x64 tiles, four stages, ragged M
+                                   (250, 8260, 256),      # 128x128 tiles, three stages, ragged N
+                                   (520, 8300, 384),      # 256x128 tiles, eight waves, three stages, ragged edges
                                    (250, 8260, 320),      # 128x128 tiles, K % 128 != 0: 64-byte stages
                                    (520, 8300, 320),      # 256x128 tiles, K % 128 != 0: 64-byte stages
                                    (2040, 11200, 128),    # 3 rounds of 256x128 tiles beat 2 of 256x256
