@@ -138,7 +138,8 @@ def _gemm_dev(a8, as_, w8, ws):
                                    (64, 16500, 128),      # 64x32 tiles, two stages
                                    (100, 16500, 128),     # 64x64 tiles, two stages, ragged M
                                    (250, 16500, 128),     # 128x64 tiles, two stages, ragged N
-                                   (520, 16500, 128),     # 128x128 tiles, two stages, ragged edges
+                                   (600, 11000, 128),     # 128x128 tiles, two per CU, ragged edges
+                                   (520, 16500, 128),     # 256x256 tiles: one round instead of two of 128x128
                                    # larger tiles that fit on the CUs in one round
                                    (64, 8224, 256),       # 64x64 tiles, four stages
                                    (100, 8256, 384),      # 128x64 tiles, four stages, ragged M
