@@ -153,6 +153,7 @@ def _gemm_dev(a8, as_, w8, ws):
                                    (200, 2000, 320),      # 64x32 tiles, K % 128 != 0: 64-byte stages
                                    (300, 2000, 384),      # 64x64 tiles
                                    (520, 2050, 128),      # 128x64 tiles
+                                   (1000, 2600, 256),     # 128x128 tiles, three stages (128x64 would need two per CU)
                                    (4100, 4000, 256)])    # 256x256 tiles, two stages, ragged edges
 def test_gemm_w8a8_bit_exact(m, n, k):
     print(f"gemm m={m} n={n} k={k}", flush=True)
