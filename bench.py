@@ -15,6 +15,7 @@ timed on the host cores as a baseline.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--quick] [--no-cpu]
        python bench.py --profile {gemv-q4k,gemv-q4k-m4,gemm,gemm-512,gemm-128,copy}   (workload only, for rocprofv3 counter runs)
+       python bench.py --vs-hipblaslt   (W8A8 GEMM against torch._int_mm over 140 prefill shapes, one JSON line each)
 """
 from __future__ import annotations
 
@@ -44,6 +45,8 @@ def parse():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--profile", choices=["gemv-q4k", "gemv-q4k-m4", "gemm", "gemm-512", "gemm-128", "copy"],
                     help="run one workload eagerly a few times and exit (for rocprofv3 --pmc passes)")
+    ap.add_argument("--vs-hipblaslt", action="store_true",
+                    help="time the W8A8 GEMM against torch._int_mm over a grid of prefill shapes and exit")
     return ap.parse_args()
 
 
@@ -276,6 +279,31 @@ def decode_crossover(torch, hip, synth) -> dict:
     return res
 
 
+def vs_hipblaslt(torch, hip, synth) -> None:
+    """One line per shape: this GEMM (rescale fused, f32 out) against
+    hipBLASLt's int8 GEMM through torch._int_mm (i32 out, no rescale), both
+    on weight copies rotating through >= 512 MiB, M x N x K over prefill
+    sizes of the TinyLlama, Llama-3.2-1B and Llama-3-8B projections."""
+    rotate = 512 << 20
+    for m in (64, 128, 256, 384, 512, 768, 1024, 1536, 2048, 4096):
+        for n in (2048, 2560, 4096, 5632, 11264, 14336, 28672):
+            for k in (2048, 4096):
+                ours = w8a8_gemm(torch, hip, synth, m, n, k, reps=20, rotate_bytes=rotate)["us"]
+                copies = max(1, min(64, rotate // (n * k) + 1))
+                ws = [torch.randint(-127, 128, (n, k), dtype=torch.int8, device="cuda") for _ in range(copies)]
+                a = torch.randint(-127, 128, (max(m, 17), k), dtype=torch.int8, device="cuda")  # _int_mm needs m > 16
+
+                def run():
+                    for w in ws:
+                        torch._int_mm(a, w.t())
+
+                ms, _ = time_graph(torch, run, max(1, 20 // copies), 2)
+                theirs = ms * 1e3 / copies
+                print(json.dumps({"m": m, "n": n, "k": k, "us": ours, "int_mm_us": round(theirs, 3),
+                                  "speedup": round(theirs / ours, 3)}), flush=True)
+                del ws
+
+
 def profile_workload(torch, hip, synth, which: str) -> None:
     """Run one workload eagerly (3 times) for rocprofv3 counter passes."""
     if which in ("gemv-q4k", "gemv-q4k-m4"):
@@ -371,6 +399,9 @@ def main():
     torch.cuda.set_device(0)
     if args.profile:
         profile_workload(torch, hip, synth, args.profile)
+        return
+    if args.vs_hipblaslt:
+        vs_hipblaslt(torch, hip, synth)
         return
 
     ds = DecodeSet(torch, hip, synth, synth.TINYLLAMA_LAYERS)
