@@ -50,6 +50,14 @@ int rocknpu_hip_gemm_w8a8(const int8_t * a8, const float * a_scales, const int8_
                           const float * w_scales, size_t m, size_t n, size_t k_pad, float * out,
                           size_t ldo, int32_t * out_i32, void * stream);
 
+/* The tile rocknpu_hip_gemm_w8a8 runs an M x N x k_pad product with on a GPU
+ * of `cus` compute units (cus <= 0: the current device's): *bm x *bn tiles of
+ * *stages 128-byte K stages, or *bm = 0 for the weight-streaming kernel of up
+ * to 16 rows. Host code only; no GPU is needed when cus > 0. The choice has no
+ * effect on the results, which are exact. No counterpart in the reference: its
+ * NPU tiles are fixed by the register-command programs. */
+int rocknpu_hip_gemm_route(size_t m, size_t n, size_t k_pad, int cus, int * bm, int * bn, int * stages);
+
 /* Q8_K activation quantisation of x [m, ldx] f32 (k a multiple of 256) into
  * m rows of k/256 Q8_K blocks. Replaces ggml quantize_row_q8_K
  * (llama.cpp, ggml-quants.c quantize_row_q8_K_ref). q8k 4-byte aligned. */

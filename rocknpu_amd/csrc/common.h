@@ -29,6 +29,15 @@ constexpr int kStatusExec = -3;
 // query fails). Defined in launch.hip.
 int device_cu_count();
 
+// Rows of A8 (m * k_pad bytes) the weight-streaming GEMM stages in LDS at most.
+constexpr int kSkinnyMaxA8 = 112 * 1024;
+// A W8A8 GEMM launch: tile bm x bn with `stages` K stages of 128 bytes (bm = 0:
+// the weight-streaming kernel for up to 16 rows).
+struct GemmTile {
+    int bm, bn, stages;
+};
+GemmTile gemm_route(int m, int n, int k, int cus);  // gemm.hip
+
 __host__ __device__ constexpr int block_bytes(int kind) {
     return kind == 4 ? kQ4KBytes : kind == 5 ? kQ5KBytes : kind == 6 ? kQ6KBytes : 0;
 }

@@ -384,102 +384,92 @@ int launch_gemm_w8a8_skinny(const int8_t* a8, int64_t lda, const int8_t* w8, int
                             const float* ws, int m, int n, int k, float* out, int64_t ldo, int32_t* oi,
                             int64_t ldoi, hipStream_t stream);  // gemm_skinny.hip
 
-// Direct-load tiles with 128-byte stages: two stages when there are more
-// tiles than CUs (two workgroups share a CU, so the extra tiles do not wait
-// for a second round), else four (one workgroup per CU, a deeper pipeline).
-// For M = 256, N = 4096, K = 14336 (128 tiles) four stages take 49 us against
-// 86 us with two; for M = 256, N = 11264, K = 2048 (352 tiles) two stages
-// take 19.7 us against 21.8 us with four.
-template <int BM, int BN, int WM, int WN>
-int launch_dma_by_tiles(const int8_t* a8, int64_t lda, const int8_t* w8, int64_t ldw, const float* as,
-                        const float* ws, int m, int n, int k, float* out, int64_t ldo, int32_t* oi,
-                        int64_t ldoi, hipStream_t stream) {
-    const int64_t tiles = static_cast<int64_t>((m + BM - 1) / BM) * ((n + BN - 1) / BN);
-    if (tiles > device_cu_count())
-        return launch_dma<BM, BN, WM, WN, 2, 128>(a8, lda, w8, ldw, as, ws, m, n, k, out, ldo, oi, ldoi, stream);
-    return launch_dma<BM, BN, WM, WN, 4, 128>(a8, lda, w8, ldw, as, ws, m, n, k, out, ldo, oi, ldoi, stream);
-}
-
-// Tile choice by M. Up to 16 rows the weight-streaming kernel of
-// gemm_skinny.hip when the A8 rows fit its LDS; else, up to 256 rows,
-// direct-load tiles of 64 x 32 (M <= 64: for M = 32, N = 5632, K = 2048 they
-// take 7.6 us against 18.5 us for register-staged 32 x 64 tiles), 64 x 64
-// and 128 x 64; beyond that 256 x 256 tiles when there is at least one per CU,
-// else 128 x 128 when there are more than CUs, else 128 x 64. Where the
-// 64 x 64 or 128 x 64 tiles would leave CUs idle, the smallest of 64 x 32,
-// 64 x 64 and 128 x 64 that fits on the CUs in one round runs instead
-// (512 x 2048 x 5632: 21.9 -> 16.5 us; 128 x 2048 x 5632: 16.2 -> 13.6 us;
-// 512 x 1024 x 4096: 15.9 -> 10.8 us). The 128-byte
-// stages read whole 128-byte lines of each row, which the L2 serves at about
-// twice the rate of the 64-byte half lines (M x N x K = 4096 x 14336 x 4096:
+// Tile and stage count of the GEMM for an M x N x K product on `cus` CUs
+// (bm = 0: the weight-streaming kernel of gemm_skinny.hip). "Fits" below
+// means the tiles number at most the CUs: one round, one workgroup per CU.
+//
+// Stages: 2 where tiles outnumber the CUs (two workgroups share a CU, so the
+// extra tiles do not wait for a second round), else 4 (a deeper pipeline);
+// M = 256, N = 4096, K = 14336 (128 tiles) takes 49 us with four against 86
+// with two, M = 256, N = 11264, K = 2048 (352 tiles) 19.7 us with two against
+// 21.8 with four. 128-byte stages read whole 128-byte lines of each row, which
+// the L2 serves at about twice the rate of half lines (4096 x 14336 x 4096:
 // 284 -> 272 us; 512 x 11264 x 2048: 31.5 -> 25.7 us).
-// Where the two-stage tiles outnumber the CUs but tiles of twice the size fit
-// on them in one round, the larger tiles run one workgroup per CU instead:
-// 64 x 64 up to 64 rows and 128 x 64 up to 128 rows with four stages
-// (128 x 11264 x 2048: 15.5 -> 11.8 us; 32 x 11264 x 2048: 13.8 -> 9.7 us),
-// 128 x 128 up to 256 rows with three (256 x 11264 x 2048: 19.1 -> 15.5 us;
-// 256 x 14336 x 4096: 35 -> 28.5 us), and 256 x 128 with eight waves and
-// three stages above (512 x 11264 x 2048: 27.2 -> 23.6 us; 768 x 8192 x 2048:
-// 25.3 -> 23.5 us).
-int launch_gemm_w8a8(const int8_t* a8, int64_t lda, const int8_t* w8, int64_t ldw, const float* as,
-                     const float* ws, int m, int n, int k, float* out, int64_t ldo, int32_t* oi,
-                     int64_t ldoi, hipStream_t stream) {
-    if (m <= 16) {
-        const int st = launch_gemm_w8a8_skinny(a8, lda, w8, ldw, as, ws, m, n, k, out, ldo, oi, ldoi, stream);
-        if (st != kStatusInvalid) return st;
-    }
-    const int cus = device_cu_count();
-    auto tiles_of = [&](int bm, int bn) { return static_cast<int64_t>((m + bm - 1) / bm) * ((n + bn - 1) / bn); };
-    if (m <= 64) {
-        if (tiles_of(64, 32) > cus && tiles_of(64, 64) <= cus)
-            return launch_dma<64, 64, 2, 2, 4, 128>(a8, lda, w8, ldw, as, ws, m, n, k, out, ldo, oi, ldoi, stream);
-        return launch_dma_by_tiles<64, 32, 2, 1>(a8, lda, w8, ldw, as, ws, m, n, k, out, ldo, oi, ldoi, stream);
-    }
-    // the smallest tiles that still fit on the CUs in one round
-    auto filling = [&](bool allow_128x64) {
-        if (tiles_of(64, 32) <= cus)
-            return launch_dma<64, 32, 2, 1, 4, 128>(a8, lda, w8, ldw, as, ws, m, n, k, out, ldo, oi, ldoi, stream);
-        if (!allow_128x64 || tiles_of(64, 64) <= cus)
-            return launch_dma_by_tiles<64, 64, 2, 2>(a8, lda, w8, ldw, as, ws, m, n, k, out, ldo, oi, ldoi, stream);
-        // 128 x 128 tiles with three stages where 128 x 64 tiles need two per CU
-        // (1024 x 2560 x 4096: 29.9 -> 23.5 us; 512 x 5632 x 4096: 32.6 -> 26.6 us)
-        if (tiles_of(128, 64) > cus && tiles_of(128, 128) <= cus)
-            return launch_dma<128, 128, 2, 2, 3, 128>(a8, lda, w8, ldw, as, ws, m, n, k, out, ldo, oi, ldoi, stream);
-        return launch_dma_by_tiles<128, 64, 4, 1>(a8, lda, w8, ldw, as, ws, m, n, k, out, ldo, oi, ldoi, stream);
+//
+// By M (times on MI355X):
+// - <= 16: the weight-streaming kernel while its A8 rows fit its LDS.
+// - <= 64: 64 x 32 tiles (for M = 32, N = 5632, K = 2048 they take 7.6 us
+//   against 18.5 us for register-staged 32 x 64 tiles); 64 x 64 with four
+//   stages when 64 x 32 tiles do not fit but those do (32 x 11264 x 2048:
+//   13.8 -> 9.7 us).
+// - <= 128: 128 x 64 with four stages when 64 x 64 tiles do not fit but those
+//   do (128 x 11264 x 2048: 15.5 -> 11.8 us); else the filling choice without
+//   128-row tiles.
+// - <= 256: 128 x 128 with three stages when 128 x 64 tiles do not fit but
+//   those do (256 x 11264 x 2048: 19.1 -> 15.5 us); else the filling choice.
+// - above, with a 256 x 256 tile per CU: 256 x 256 tiles, or 256 x 128 tiles
+//   with eight waves and three stages when their rounds cost less (a round of
+//   them takes about 0.61 of a round of 256 x 256 tiles; 2048 x 11264 x 2048:
+//   76.6 -> 71.8 us).
+// - above, when 128 x 128 tiles do not fit: 256 x 128 tiles (eight waves,
+//   three stages) if they fit (512 x 11264 x 2048: 27.2 -> 23.6 us); else
+//   256 x 256 tiles when their rounds cost less than two-per-CU rounds of
+//   128 x 128 tiles (a round takes about 1.38 of one; 1024 x 14336 x 4096:
+//   93 -> 80 us); else 128 x 128 tiles, two per CU.
+// - else the filling choice: the first of 64 x 32, 64 x 64 and 128 x 64 that
+//   fits, then 128 x 128 with three stages, else 128 x 64 two per CU
+//   (512 x 2048 x 5632: 21.9 -> 16.5 us; 1024 x 2560 x 4096: 29.9 -> 23.5 us).
+// Tiles that need a second round where smaller or larger ones fit in one
+// measured slower, which is why each rule asks for one round.
+GemmTile gemm_route(int m, int n, int k, int cus) {
+    auto tiles = [&](int bm, int bn) { return static_cast<int64_t>((m + bm - 1) / bm) * ((n + bn - 1) / bn); };
+    auto by_tiles = [&](int bm, int bn) { return GemmTile{bm, bn, tiles(bm, bn) > cus ? 2 : 4}; };
+    auto rounds = [&](int64_t t, int per_cu) { return (t + per_cu * cus - 1) / (per_cu * cus); };
+    auto filling = [&](bool allow_128) {
+        if (tiles(64, 32) <= cus) return GemmTile{64, 32, 4};
+        if (!allow_128 || tiles(64, 64) <= cus) return by_tiles(64, 64);
+        if (tiles(128, 64) > cus && tiles(128, 128) <= cus) return GemmTile{128, 128, 3};
+        return by_tiles(128, 64);
     };
+    if (m <= 16 && k % 64 == 0 && static_cast<int64_t>(m) * k <= kSkinnyMaxA8) return GemmTile{0, 0, 0};
+    if (m <= 64) {
+        if (tiles(64, 32) > cus && tiles(64, 64) <= cus) return GemmTile{64, 64, 4};
+        return by_tiles(64, 32);
+    }
     if (m <= 128) {
-        if (tiles_of(64, 64) > cus && tiles_of(128, 64) <= cus)
-            return launch_dma<128, 64, 4, 1, 4, 128>(a8, lda, w8, ldw, as, ws, m, n, k, out, ldo, oi, ldoi, stream);
+        if (tiles(64, 64) > cus && tiles(128, 64) <= cus) return GemmTile{128, 64, 4};
         return filling(false);
     }
     if (m <= 256) {
-        if (tiles_of(128, 64) > cus && tiles_of(128, 128) <= cus)
-            return launch_dma<128, 128, 2, 2, 3, 128>(a8, lda, w8, ldw, as, ws, m, n, k, out, ldo, oi, ldoi, stream);
+        if (tiles(128, 64) > cus && tiles(128, 128) <= cus) return GemmTile{128, 128, 3};
         return filling(true);
     }
-    if (tiles_of(256, 256) >= cus) {
-        // A round of 256 x 128 tiles (eight waves, three stages) takes about 0.61 of
-        // a round of 256 x 256 tiles; they win where the big tiles leave more of
-        // their last round empty (2048 x 11264 x 2048: 76.6 -> 71.8 us).
-        const int64_t rounds_256 = (tiles_of(256, 256) + cus - 1) / cus;
-        const int64_t rounds_128 = (tiles_of(256, 128) + cus - 1) / cus;
-        if (rounds_128 * 61 < rounds_256 * 100)
-            return launch_dma<256, 128, 4, 2, 3, 128>(a8, lda, w8, ldw, as, ws, m, n, k, out, ldo, oi, ldoi, stream);
-        return launch_dma<256, 256, 2, 2, 2, 128>(a8, lda, w8, ldw, as, ws, m, n, k, out, ldo, oi, ldoi, stream);
+    if (tiles(256, 256) >= cus) {
+        if (rounds(tiles(256, 128), 1) * 61 < rounds(tiles(256, 256), 1) * 100) return GemmTile{256, 128, 3};
+        return GemmTile{256, 256, 2};
     }
-    if (tiles_of(128, 128) > cus) {
-        if (tiles_of(256, 128) <= cus)
-            return launch_dma<256, 128, 4, 2, 3, 128>(a8, lda, w8, ldw, as, ws, m, n, k, out, ldo, oi, ldoi, stream);
-        // A round of 256 x 256 tiles (one per CU) takes about 1.38 of a round of
-        // 128 x 128 tiles (two per CU); they win where they need fewer rounds
-        // (1024 x 14336 x 4096: 93 -> 80 us; 520 x 16500 x 2048: 52.7 -> 44.8 us).
-        const int64_t rounds_256 = (tiles_of(256, 256) + cus - 1) / cus;
-        const int64_t rounds_128 = (tiles_of(128, 128) + 2 * cus - 1) / (2 * cus);
-        if (rounds_256 * 138 < rounds_128 * 100)
-            return launch_dma<256, 256, 2, 2, 2, 128>(a8, lda, w8, ldw, as, ws, m, n, k, out, ldo, oi, ldoi, stream);
-        return launch_dma<128, 128, 2, 2, 2, 128>(a8, lda, w8, ldw, as, ws, m, n, k, out, ldo, oi, ldoi, stream);
+    if (tiles(128, 128) > cus) {
+        if (tiles(256, 128) <= cus) return GemmTile{256, 128, 3};
+        if (rounds(tiles(256, 256), 1) * 138 < rounds(tiles(128, 128), 2) * 100) return GemmTile{256, 256, 2};
+        return GemmTile{128, 128, 2};
     }
     return filling(true);
+}
+
+int launch_gemm_w8a8(const int8_t* a8, int64_t lda, const int8_t* w8, int64_t ldw, const float* as,
+                     const float* ws, int m, int n, int k, float* out, int64_t ldo, int32_t* oi,
+                     int64_t ldoi, hipStream_t stream) {
+    const GemmTile r = gemm_route(m, n, k, device_cu_count());
+#define RK_GEMM(BM, BN, WM, WN, ST) \
+    launch_dma<BM, BN, WM, WN, ST, 128>(a8, lda, w8, ldw, as, ws, m, n, k, out, ldo, oi, ldoi, stream)
+    if (r.bm == 0) return launch_gemm_w8a8_skinny(a8, lda, w8, ldw, as, ws, m, n, k, out, ldo, oi, ldoi, stream);
+    if (r.bm == 64 && r.bn == 32) return r.stages == 2 ? RK_GEMM(64, 32, 2, 1, 2) : RK_GEMM(64, 32, 2, 1, 4);
+    if (r.bm == 64) return r.stages == 2 ? RK_GEMM(64, 64, 2, 2, 2) : RK_GEMM(64, 64, 2, 2, 4);
+    if (r.bm == 128 && r.bn == 64) return r.stages == 2 ? RK_GEMM(128, 64, 4, 1, 2) : RK_GEMM(128, 64, 4, 1, 4);
+    if (r.bm == 128) return r.stages == 2 ? RK_GEMM(128, 128, 2, 2, 2) : RK_GEMM(128, 128, 2, 2, 3);
+    if (r.bn == 128) return RK_GEMM(256, 128, 4, 2, 3);
+    return RK_GEMM(256, 256, 2, 2, 2);
+#undef RK_GEMM
 }
 
 }  // namespace rk

@@ -28,7 +28,6 @@ namespace {
 typedef int v4i __attribute__((ext_vector_type(4)));
 
 constexpr int kSkinnyWaves = 8;
-constexpr int kSkinnyLdsA = 112 * 1024;  // A8 bytes a workgroup stages: m * k_pad
 
 template <int D>
 __global__ __launch_bounds__(kSkinnyWaves * 64) void gemm_w8a8_skinny_kernel(
@@ -147,7 +146,7 @@ __global__ __launch_bounds__(kSkinnyWaves * 64) void gemm_w8a8_skinny_kernel(
 int launch_gemm_w8a8_skinny(const int8_t* a8, int64_t lda, const int8_t* w8, int64_t ldw, const float* as,
                             const float* ws, int m, int n, int k, float* out, int64_t ldo, int32_t* oi,
                             int64_t ldoi, hipStream_t stream) {
-    if (m < 1 || m > 16 || k % 64 != 0 || static_cast<int64_t>(m) * k > kSkinnyLdsA) return kStatusInvalid;
+    if (m < 1 || m > 16 || k % 64 != 0 || static_cast<int64_t>(m) * k > kSkinnyMaxA8) return kStatusInvalid;
     const int tiles = (n + 15) / 16;
     const size_t lds = ((static_cast<size_t>(m) * k + 15) & ~size_t{15}) + 2 * kSkinnyWaves * 64 * 4 * sizeof(int);
     // two workgroups per CU where both fit its 160 KiB of LDS: more weight

@@ -83,6 +83,18 @@ extern "C" int rocknpu_hip_gemm_w8a8(const int8_t* a8, const float* a_scales, co
                                 static_cast<hipStream_t>(stream));
 }
 
+extern "C" int rocknpu_hip_gemm_route(size_t m, size_t n, size_t k_pad, int cus, int* bm, int* bn, int* stages) {
+    if (!bm || !bn || !stages || m == 0 || n == 0 || k_pad == 0 || k_pad % 64 != 0 || m > INT_MAX || n > INT_MAX ||
+        k_pad > INT_MAX)
+        return rk::kStatusInvalid;
+    if (cus <= 0) cus = rk::device_cu_count();
+    const rk::GemmTile r = rk::gemm_route(static_cast<int>(m), static_cast<int>(n), static_cast<int>(k_pad), cus);
+    *bm = r.bm;
+    *bn = r.bn;
+    *stages = r.stages;
+    return rk::kStatusOk;
+}
+
 extern "C" int rocknpu_hip_quantize_q8_k(const float* x, size_t m, size_t k, size_t ldx, uint8_t* q8k,
                                          void* stream) {
     if (!x || !q8k || m == 0 || k == 0 || k % rk::kQK != 0 || ldx < k || !aligned(q8k, 4))

@@ -1,0 +1,102 @@
+"""Tile choice of the W8A8 GEMM (rocknpu_hip_gemm_route, include/rocknpu_hip.h)
+on the CPU: the route of every shape whose measured times the rules rest on,
+and the invariants the rules keep over a grid of shapes. Host logic only; the
+choice never changes the (exact) results, which the GPU tests check per route."""
+import ctypes
+import itertools
+
+import pytest
+
+from rocknpu_amd import _lib
+
+CUS = 256  # MI355X
+
+
+def route(m, n, k, cus=CUS):
+    bm, bn, st = ctypes.c_int(), ctypes.c_int(), ctypes.c_int()
+    rc = _lib.load().rocknpu_hip_gemm_route(m, n, k, cus, ctypes.byref(bm), ctypes.byref(bn), ctypes.byref(st))
+    assert rc == 0
+    return bm.value, bn.value, st.value
+
+
+def tiles(m, n, bm, bn):
+    return -(-m // bm) * -(-n // bn)
+
+
+@pytest.mark.parametrize("m,n,k,expect", [
+    # weight-streaming kernel while m * k fits its 112 KiB of LDS
+    (1, 5632, 2048, (0, 0, 0)),
+    (16, 17, 7168, (0, 0, 0)),
+    (16, 40, 7232, (64, 32, 4)),
+    # up to 64 rows
+    (24, 5632, 2048, (64, 32, 4)),
+    (32, 11264, 2048, (64, 64, 4)),      # 64x32 tiles do not fit, 64x64 do
+    (64, 16500, 128, (64, 32, 2)),       # neither fits
+    # up to 128 rows
+    (128, 5632, 2048, (64, 64, 4)),      # the 5632 x 2048 Q4_K weight at 128 tokens
+    (128, 2048, 2048, (64, 32, 4)),
+    (128, 11264, 2048, (128, 64, 4)),    # 64x64 tiles do not fit, 128x64 do
+    (100, 16500, 128, (64, 64, 2)),
+    # up to 256 rows
+    (256, 11264, 2048, (128, 128, 3)),
+    (256, 14336, 4096, (128, 128, 3)),
+    (200, 2048, 2048, (64, 32, 4)),
+    (250, 16500, 128, (128, 64, 2)),
+    # above: one 256 x 256 tile per CU or more
+    (4096, 14336, 4096, (256, 256, 2)),  # 4 rounds against 7 x 0.61 of 256x128
+    (8192, 8192, 8192, (256, 256, 2)),
+    (2048, 11264, 2048, (256, 128, 3)),  # 3 x 0.61 rounds against 2
+    # above: 128 x 128 tiles that do not fit
+    (512, 11264, 2048, (256, 128, 3)),   # 256x128 tiles fit
+    (768, 8192, 2048, (256, 128, 3)),
+    (1024, 14336, 4096, (256, 256, 2)),  # 1 x 1.38 rounds against 2 of 128x128 two per CU
+    (520, 16500, 2048, (256, 256, 2)),
+    (640, 11264, 2048, (128, 128, 2)),   # 1 x 1.38 against 1
+    # above: the filling choice
+    (512, 2048, 5632, (64, 64, 4)),
+    (512, 1024, 4096, (64, 32, 4)),
+    (512, 2560, 2048, (128, 64, 4)),
+    (1024, 2560, 4096, (128, 128, 3)),   # 128x64 tiles would need two per CU
+    (2048, 2048, 4096, (128, 128, 3)),
+])
+def test_measured_routes(m, n, k, expect):
+    assert route(m, n, k) == expect
+
+
+def test_invariants_over_a_grid():
+    ms = (1, 8, 16, 17, 40, 64, 65, 100, 128, 129, 200, 256, 257, 384, 512, 640, 768, 1024, 1536, 2048, 4096)
+    ns = (16, 100, 1024, 2048, 2560, 4096, 5632, 8192, 11264, 14336, 16384, 28672, 32000)
+    ks = (64, 256, 2048, 5632, 7232, 14336)
+    for m, n, k in itertools.product(ms, ns, ks):
+        bm, bn, st = route(m, n, k)
+        if bm == 0:
+            assert m <= 16 and m * k <= 112 * 1024
+            continue
+        assert not (m <= 16 and m * k <= 112 * 1024)
+        assert (bm, bn) in {(64, 32), (64, 64), (128, 64), (128, 128), (256, 128), (256, 256)}
+        t = tiles(m, n, bm, bn)
+        # tile height follows M: 64 rows up to 64, at most 128 up to 256, more only above
+        assert bm == 64 or m > 64
+        assert bm <= 128 or m > 256
+        if bm <= 128 and (bm, bn) != (128, 128):
+            # two stages exactly when the tiles outnumber the CUs (two per CU)
+            assert (st == 2) == (t > CUS), (m, n, k, bm, bn, st)
+            assert st in (2, 4)
+        if (bm, bn) == (128, 128):
+            assert (st == 3 and t <= CUS) or (st == 2 and t > CUS), (m, n, k, st)
+        if (bm, bn) == (256, 128):
+            assert st == 3
+        if (bm, bn) == (256, 256):
+            assert st == 2
+
+
+def test_fewer_cus_and_bad_arguments():
+    # on a part with fewer CUs the one-round rules move accordingly
+    assert route(128, 11264, 2048, cus=256) == (128, 64, 4)
+    assert route(128, 11264, 2048, cus=128) == (64, 64, 2)
+    out = [ctypes.c_int() for _ in range(3)]
+    lib = _lib.load()
+    ptrs = [ctypes.byref(o) for o in out]
+    assert lib.rocknpu_hip_gemm_route(0, 64, 64, CUS, *ptrs) == -1
+    assert lib.rocknpu_hip_gemm_route(4, 64, 100, CUS, *ptrs) == -1  # k_pad % 64 != 0
+    assert lib.rocknpu_hip_gemm_route(4, 64, 64, CUS, None, ptrs[1], ptrs[2]) == -1
