@@ -58,6 +58,16 @@ int rocknpu_hip_gemm_w8a8(const int8_t * a8, const float * a_scales, const int8_
  * NPU tiles are fixed by the register-command programs. */
 int rocknpu_hip_gemm_route(size_t m, size_t n, size_t k_pad, int cus, int * bm, int * bn, int * stages);
 
+/* The launch shape rocknpu_hip_gemv_q_f32 (fused != 0) or rocknpu_hip_gemv_q8_k
+ * (fused == 0) takes for `count` projections of n[i] rows, K = k and m <= 8
+ * activation rows (larger m runs in launches of 8) on `cus` compute units
+ * (cus <= 0: the current device's): *mfma = 1 for the matrix-core kernel,
+ * else the lane-per-block kernel with *lanes lanes per super-block and *waves
+ * waves per workgroup. Host code only; no GPU is needed when cus > 0. No
+ * counterpart in the reference, whose decode GEMV runs on the CPU. */
+int rocknpu_hip_gemv_shape(uint32_t kind, size_t m, size_t k, const size_t * n, size_t count, int fused, int cus,
+                           int * mfma, int * lanes, int * waves);
+
 /* Q8_K activation quantisation of x [m, ldx] f32 (k a multiple of 256) into
  * m rows of k/256 Q8_K blocks. Replaces ggml quantize_row_q8_K
  * (llama.cpp, ggml-quants.c quantize_row_q8_K_ref). q8k 4-byte aligned. */

@@ -37,6 +37,13 @@ struct GemmTile {
     int bm, bn, stages;
 };
 GemmTile gemm_route(int m, int n, int k, int cus);  // gemm.hip
+// Decode GEMV launch shape: lanes per super-block and waves per workgroup of
+// the lane-per-block kernel, and whether the matrix-core kernel runs instead.
+struct GemvLanes {
+    int lanes, waves;
+};
+GemvLanes gemv_lanes(bool fused, bool sums, int m, int nb, const int64_t* rows, int count, int cus);  // gemv.hip
+bool gemv_uses_mfma(int kind, int m, int64_t rows, int cus);                                          // gemv.hip
 
 __host__ __device__ constexpr int block_bytes(int kind) {
     return kind == 4 ? kQ4KBytes : kind == 5 ? kQ5KBytes : kind == 6 ? kQ6KBytes : 0;

@@ -514,43 +514,8 @@ int launch_kind(GemvParams& p, hipStream_t stream) {
     p.log2g = slots_per_row_log2(p.nb, 8);
     const int G = 1 << p.log2g;
     p.iters = (p.nb + G - 1) / G;
-    auto row_groups = [&](int lanes_per_block) {
-        const int64_t rpg = 64 / lanes_per_block / G;
-        int64_t n = 0;
-        for (int i = 0; i < p.count; ++i) n += (p.rows[i] + rpg - 1) / rpg;
-        return n;
-    };
-    // Lanes per block L and waves per workgroup W. Where some L >= 2 gives
-    // every row group a wave of its own (one round trip per wave), take the
-    // largest such L (the most contiguous loads), with 8-wave workgroups if
-    // they suffice, else 16. Otherwise (several row groups per wave) L = 4
-    // and 8 waves. Eight activation rows allow L <= 2 (more would spill);
-    // the exact-sums path runs L = 1 and 16 waves; 8-wave workgroups serve
-    // fused launches only.
-    const int max_l = sums ? 1 : mt == 8 ? 2 : 8;
-    const bool w8_ok = FUSED && !sums;
-    const int64_t slots8 = static_cast<int64_t>(cus) * 8, slots16 = static_cast<int64_t>(cus) * 16;
-    int L = 0, W = 16;
-    // Long rows (4 or more blocks per slot) first try 16 waves with the
-    // largest L that still gives every row group a wave: Llama-3-8B down
-    // (Q6_K, 4096 x 14336) then takes 14.5 us, against 15.8 us with L = 4 and
-    // 8 waves.
-    if (p.iters >= 4)
-        for (int l = max_l; l >= 2 && L == 0; l >>= 1)
-            if (row_groups(l) <= slots16) { L = l; W = 16; }
-    for (int l = max_l; l >= 2 && L == 0; l >>= 1)
-        if (w8_ok && row_groups(l) <= slots8) { L = l; W = 8; }
-    for (int l = max_l; l >= 2 && L == 0; l >>= 1)
-        if (row_groups(l) <= slots16) { L = l; W = 16; }
-    if (L == 0) { L = std::min(4, max_l); W = w8_ok ? 8 : 16; }
-    // A shape that leaves CUs idle gives way to a wider L with 16 waves when
-    // that fills every CU within two row groups per wave: TinyLlama gate+up
-    // (2 x 5632 rows, K = 2048) runs L = 4 on 256 CUs in 5.45 us, against L = 2
-    // on 176 CUs in 5.95 us.
-    auto wgs_for = [&](int l, int w) { return std::min<int64_t>(cus, (row_groups(l) + w - 1) / w); };
-    if (wgs_for(L, W) < cus)
-        for (int l = max_l; l > L; l >>= 1)
-            if (wgs_for(l, 16) >= cus && row_groups(l) <= 2 * slots16) { L = l; W = 16; break; }
+    const GemvLanes shape = gemv_lanes(FUSED, sums, p.m, p.nb, p.rows, p.count, cus);
+    const int L = shape.lanes, W = shape.waves;
     const int64_t max_wgs = cus;
     const int64_t rows_per_group = 64 / L / G;
     // Workgroups: at most one per CU and one per W row groups, split between
@@ -618,15 +583,66 @@ int launch_gemv_mfma(int kind, bool fused, GemvParams& p, hipStream_t stream);  
 // 9.23 us at 4 rows, 11.6 against 14.3 us at 8; down Q6_K: 13.6 against 20.0
 // us at 6 rows, while at 4 rows the lane-per-block kernel's 11.4 us beats
 // 12.4), except where the exact per-block sums are asked for.
+// Lanes per block L and waves per workgroup W of the lane-per-block kernel for
+// m activation rows, rows of nb super-blocks, and `count` projections of the
+// given rows, on `cus` CUs.
+GemvLanes gemv_lanes(bool fused, bool sums, int m, int nb, const int64_t* rows, int count, int cus) {
+    const int mt = m <= 1 ? 1 : m <= 2 ? 2 : m <= 4 ? 4 : 8;
+    const int G = 1 << slots_per_row_log2(nb, 8);
+    const int iters = (nb + G - 1) / G;
+    auto row_groups = [&](int lanes_per_block) {
+        const int64_t rpg = 64 / lanes_per_block / G;
+        int64_t n = 0;
+        for (int i = 0; i < count; ++i) n += (rows[i] + rpg - 1) / rpg;
+        return n;
+    };
+    // Lanes per block L and waves per workgroup W. Where some L >= 2 gives
+    // every row group a wave of its own (one round trip per wave), take the
+    // largest such L (the most contiguous loads), with 8-wave workgroups if
+    // they suffice, else 16. Otherwise (several row groups per wave) L = 4
+    // and 8 waves. Eight activation rows allow L <= 2 (more would spill);
+    // the exact-sums path runs L = 1 and 16 waves; 8-wave workgroups serve
+    // fused launches only.
+    const int max_l = sums ? 1 : mt == 8 ? 2 : 8;
+    const bool w8_ok = fused && !sums;
+    const int64_t slots8 = static_cast<int64_t>(cus) * 8, slots16 = static_cast<int64_t>(cus) * 16;
+    int L = 0, W = 16;
+    // Long rows (4 or more blocks per slot) first try 16 waves with the
+    // largest L that still gives every row group a wave: Llama-3-8B down
+    // (Q6_K, 4096 x 14336) then takes 14.5 us, against 15.8 us with L = 4 and
+    // 8 waves.
+    if (iters >= 4)
+        for (int l = max_l; l >= 2 && L == 0; l >>= 1)
+            if (row_groups(l) <= slots16) { L = l; W = 16; }
+    for (int l = max_l; l >= 2 && L == 0; l >>= 1)
+        if (w8_ok && row_groups(l) <= slots8) { L = l; W = 8; }
+    for (int l = max_l; l >= 2 && L == 0; l >>= 1)
+        if (row_groups(l) <= slots16) { L = l; W = 16; }
+    if (L == 0) { L = std::min(4, max_l); W = w8_ok ? 8 : 16; }
+    // A shape that leaves CUs idle gives way to a wider L with 16 waves when
+    // that fills every CU within two row groups per wave: TinyLlama gate+up
+    // (2 x 5632 rows, K = 2048) runs L = 4 on 256 CUs in 5.45 us, against L = 2
+    // on 176 CUs in 5.95 us.
+    auto wgs_for = [&](int l, int w) { return std::min<int64_t>(cus, (row_groups(l) + w - 1) / w); };
+    if (wgs_for(L, W) < cus)
+        for (int l = max_l; l > L; l >>= 1)
+            if (wgs_for(l, 16) >= cus && row_groups(l) <= 2 * slots16) { L = l; W = 16; break; }
+    return GemvLanes{L, W};
+}
+
+// The matrix-core kernel from 3 rows for Q4_K, from 5 rows for Q6_K, and for
+// Q6_K at 3 or 4 rows when its 16-row tiles fill every CU (Llama-3-8B down,
+// 4096 x 14336, at 4 rows: 25.8 -> 22.5 us; TinyLlama down, 2048 rows, stays
+// on the lane-per-block kernel, 10.6 against 11.1 us).
+bool gemv_uses_mfma(int kind, int m, int64_t rows, int cus) {
+    return kind == 4 ? m >= 3 : m >= 5 || (m >= 3 && rows >= 16 * int64_t{cus});
+}
+
 int launch_gemv(int kind, bool fused, GemvParams& p, hipStream_t stream) {
-    // Matrix cores from 3 rows for Q4_K, from 5 rows for Q6_K, and for Q6_K
-    // at 3 or 4 rows when its 16-row tiles fill every CU (Llama-3-8B down,
-    // 4096 x 14336, at 4 rows: 25.8 -> 22.5 us; TinyLlama down, 2048 rows,
-    // stays on the lane-per-block kernel, 10.6 against 11.1 us).
     int64_t rows = 0;
     for (int i = 0; i < p.count; ++i) rows += p.rows[i];
-    const bool mfma = kind == 4 ? p.m >= 3 : p.m >= 5 || (p.m >= 3 && rows >= 16 * int64_t{device_cu_count()});
-    if (mfma && p.isum == nullptr) return launch_gemv_mfma(kind, fused, p, stream);
+    if (gemv_uses_mfma(kind, p.m, rows, device_cu_count()) && p.isum == nullptr)
+        return launch_gemv_mfma(kind, fused, p, stream);
     if (kind == 4) return fused ? launch_kind<4, true>(p, stream) : launch_kind<4, false>(p, stream);
     if (kind == 6) return fused ? launch_kind<6, true>(p, stream) : launch_kind<6, false>(p, stream);
     return kStatusInvalid;

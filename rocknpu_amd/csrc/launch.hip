@@ -95,6 +95,27 @@ extern "C" int rocknpu_hip_gemm_route(size_t m, size_t n, size_t k_pad, int cus,
     return rk::kStatusOk;
 }
 
+extern "C" int rocknpu_hip_gemv_shape(uint32_t kind, size_t m, size_t k, const size_t* n, size_t count, int fused,
+                                      int cus, int* mfma, int* lanes, int* waves) {
+    if ((kind != 4 && kind != 6) || !n || !mfma || !lanes || !waves || m == 0 || m > 8 || k == 0 ||
+        k % rk::kQK != 0 || count == 0 || count > rk::kGemvMaxMembers || k / rk::kQK > INT_MAX)
+        return rk::kStatusInvalid;
+    if (cus <= 0) cus = rk::device_cu_count();
+    int64_t rows[rk::kGemvMaxMembers] = {};
+    int64_t total = 0;
+    for (size_t i = 0; i < count; ++i) {
+        if (n[i] == 0 || n[i] > INT32_MAX / 2) return rk::kStatusInvalid;
+        rows[i] = static_cast<int64_t>(n[i]);
+        total += rows[i];
+    }
+    *mfma = rk::gemv_uses_mfma(static_cast<int>(kind), static_cast<int>(m), total, cus) ? 1 : 0;
+    const rk::GemvLanes l = rk::gemv_lanes(fused != 0, false, static_cast<int>(m), static_cast<int>(k / rk::kQK), rows,
+                                           static_cast<int>(count), cus);
+    *lanes = *mfma ? 0 : l.lanes;
+    *waves = *mfma ? 0 : l.waves;
+    return rk::kStatusOk;
+}
+
 extern "C" int rocknpu_hip_quantize_q8_k(const float* x, size_t m, size_t k, size_t ldx, uint8_t* q8k,
                                          void* stream) {
     if (!x || !q8k || m == 0 || k == 0 || k % rk::kQK != 0 || ldx < k || !aligned(q8k, 4))
