@@ -45,7 +45,8 @@ int rocknpu_hip_quantize_a8(const float * a, size_t m, size_t k, size_t lda, siz
  * there as [m, n]. Replaces Int8DecodePool::execute_prepared_mtile_direct
  * (crates/rocknpu-matmul/src/int8_decode_pool.rs:625-686) plus the
  * rescale_i32_row sink (crates/rocknpu-capi/src/lib.rs:692-709, :1868-1884).
- * a8 and w8 16-byte aligned, k_pad a multiple of 64. */
+ * a8 and w8 16-byte aligned, k_pad a multiple of 64 and at most 133120 (the
+ * largest K whose int32 sums are exact: 127 * 127 * K < 2^31). */
 int rocknpu_hip_gemm_w8a8(const int8_t * a8, const float * a_scales, const int8_t * w8,
                           const float * w_scales, size_t m, size_t n, size_t k_pad, float * out,
                           size_t ldo, int32_t * out_i32, void * stream);

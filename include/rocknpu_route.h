@@ -49,7 +49,25 @@ typedef struct rocknpu_mul_mat_node {
     size_t weight_bytes;      /* ggml_nbytes(src0) */
     const float * activations;/* src1->data: nodes with the same pointer share an input */
     float * output;           /* dst->data, M x N f32 */
+    const char * weight_name; /* src0->name ("blk.<layer>.attn_q.weight", ...), or NULL */
 } rocknpu_mul_mat_node;
+
+/* Dispatch counters of the routing over one context (the plugin's TRACE
+ * summary counters, ggml-rocknpu.cpp:721-736). Printed to stderr when the
+ * context is destroyed if ROCKNPU_GGML_TRACE or ROCKNPU_DISPATCH_SUMMARY is
+ * set. */
+typedef struct rocknpu_route_stats {
+    size_t graph_calls;        /* rocknpu_route_run calls */
+    size_t q4_k_mul_mat;       /* projections run, by weight type */
+    size_t q5_k_mul_mat;
+    size_t q6_k_mul_mat;
+    size_t f16_mul_mat;
+    size_t q8k_m1_mul_mat;     /* M = 1 projections on the ROCKNPU_DECODE_GGML route */
+    size_t w8a8_m1_mul_mat;    /* M = 1 projections on the ROCKNPU_DECODE_W8A8 route */
+    size_t mtile_group_calls;  /* same-input group calls (2..4 projections, M > 1) */
+    size_t qkv_triple_calls;   /* Q nodes run as Q+K+V with K/V stashed */
+    size_t qkv_stash_hits;     /* K/V nodes served from the stash */
+} rocknpu_route_stats;
 
 /* Where single-token (M = 1) MUL_MATs go (ROCKNPU_DECODE, ggml-rocknpu.cpp:305-322). */
 enum rocknpu_decode_route {
@@ -71,11 +89,29 @@ int rocknpu_route_supported(const rocknpu_mul_mat_node * node, int32_t decode_ro
  * takes up to 3 later supported Q4_K/Q6_K nodes with the same activations
  * pointer, K and M, not already taken; every other node is a group of its
  * own. group_of[i] = index of the lead node of node i's group (group_of has
- * `count` entries; unsupported nodes get -1). Returns the number of groups. */
+ * `count` entries; unsupported nodes get -1). Returns the number of groups.
+ *
+ * A group runs at its lead's position, so a later member j is taken only if
+ * that move is invisible: no node between the lead and j writes memory j
+ * reads or writes, or reads memory j writes, and j's output overlaps neither
+ * the shared activations nor another member's output. The plugin compares
+ * ggml tensors (src[1] identity); addresses are what this interface sees, and
+ * a buffer ggml-alloc reused for another tensor has the same address. `nodes`
+ * must therefore hold every computing node of the split, in graph order
+ * (the split's other ops are views). ROCKNPU_MTILE_GROUP=0 turns grouping off. */
 size_t rocknpu_route_plan(const rocknpu_mul_mat_node * nodes, size_t count, int32_t decode_route,
                           int32_t * group_of);
 
-/* Runs the nodes' groups in lead order through the entry points:
+/* Runs the nodes' groups in lead order through the entry points (below).
+ * With ROCKNPU_MTILE_QKV (default on; ggml-rocknpu.cpp:871-928) and M > 1, a
+ * Q projection ("blk.<L>.attn_q.weight") that runs alone while layer L's K and
+ * V weights are known from an earlier call runs as one Q+K+V group, its K/V
+ * outputs kept in the context; the K and V nodes of a later call (another
+ * split) that read the same activations with the same M are then filled from
+ * that stash instead of computed again, bit for bit the same values. After a
+ * layer's first such triple, the single and pair prompt caches of its three
+ * weights are released (rocknpu_mtile_release, :953-962).
+ * Entry points, by group:
  *   group of 2..4, M > 1:            rocknpu_matmul_q_concat_f32_f32_mtile
  *   group of 2..4, M = 1, GGML:      rocknpu_matmul_q_q8k_group_f32_f32
  *   group of 2 or 3, M = 1, W8A8:    rocknpu_matmul_q_pair_f32_f32_m1 / _triple_
@@ -88,6 +124,9 @@ size_t rocknpu_route_plan(const rocknpu_mul_mat_node * nodes, size_t count, int3
  * otherwise the first failing call's status, or ROCKNPU_STATUS_OK. */
 int rocknpu_route_run(rocknpu_context * context, const rocknpu_mul_mat_node * nodes, size_t count,
                       int32_t decode_route);
+
+/* Copies the context's dispatch counters to *out. */
+int rocknpu_route_stats_get(const rocknpu_context * context, rocknpu_route_stats * out);
 
 #ifdef __cplusplus
 }

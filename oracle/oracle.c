@@ -165,6 +165,33 @@ int or_quantize_symmetric_row(const float *x, size_t k, int8_t *q, float *scale)
     return OR_OK;
 }
 
+/* The aarch64 NEON form of the same quantisation, the reference's default on
+ * RK3588 (ROCKNPU_HOST_NEON defaults to the CPU's NEON support, lib.rs:
+ * 300-311): quantize_symmetric_neon_into (lib.rs:509-541) multiplies by the
+ * f32 reciprocal of the scale in chunks of 8 values, and divides only for the
+ * tail of fewer than 8; max_abs_finite_neon (:475-505) is order-free, so the
+ * scale is the scalar one. */
+int or_quantize_symmetric_row_neon(const float *x, size_t k, int8_t *q, float *scale) {
+    float max_abs = 0.0f;
+    for (size_t i = 0; i < k; ++i) {
+        if (!isfinite(x[i])) return OR_INVALID;
+        const float a = fabsf(x[i]);
+        if (a > max_abs) max_abs = a;
+    }
+    const float s = (max_abs == 0.0f) ? 1.0f : max_abs / 127.0f;
+    const float inv = 1.0f / s;
+    const size_t body = k - k % 8;
+    for (size_t i = 0; i < body; ++i) {
+        float r = roundf(x[i] * inv);
+        if (r < -127.0f) r = -127.0f;
+        if (r > 127.0f) r = 127.0f;
+        q[i] = (int8_t)r;
+    }
+    for (size_t i = body; i < k; ++i) q[i] = quant_one(x[i], s);
+    *scale = s;
+    return OR_OK;
+}
+
 /* crates/rocknpu-capi/src/lib.rs:711-757 (Q4_K), :759-806 (Q5_K),
  * :974-994 (Q6_K): dequantise a row, then quantise it symmetrically. */
 int or_repack_w8(uint32_t kind, const uint8_t *blocks, size_t bytes, size_t k, size_t n,
@@ -265,6 +292,24 @@ void or_rescale(const int32_t *c, const float *a_scales, const float *w_scales, 
             const float t = (float)c[i * n + j] * a_scales[i];
             out[i * n + j] = t * w_scales[j];
         }
+}
+
+/* rescale_i32_row_neon (lib.rs:664-690), the aarch64 default for prompt
+ * rows: (f32(c) * w_scale) * a_scale in chunks of 4 columns of the slice,
+ * the tail of fewer than 4 as the scalar (f32(c) * a_scale) * w_scale. */
+void or_rescale_neon(const int32_t *c, const float *a_scales, const float *w_scales, size_t m, size_t n,
+                     float *out) {
+    const size_t body = n - n % 4;
+    for (size_t i = 0; i < m; ++i) {
+        for (size_t j = 0; j < body; ++j) {
+            const float t = (float)c[i * n + j] * w_scales[j];
+            out[i * n + j] = t * a_scales[i];
+        }
+        for (size_t j = body; j < n; ++j) {
+            const float t = (float)c[i * n + j] * a_scales[i];
+            out[i * n + j] = t * w_scales[j];
+        }
+    }
 }
 
 int or_matmul_q_w8a8(uint32_t kind, const uint8_t *blocks, size_t bytes, const float *a, size_t m,

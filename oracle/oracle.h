@@ -60,6 +60,11 @@ int or_dequant_rows(uint32_t kind, const uint8_t *blocks, size_t k, size_t n, fl
  * Returns 0 and writes *scale, or -1 if the row holds a non-finite value. */
 int or_quantize_symmetric_row(const float *x, size_t k, int8_t *q, float *scale);
 
+/* The aarch64 NEON form (lib.rs:475-541), the reference's default on its
+ * RK3588 target: q = round(x * f32(1/scale)) in chunks of 8, the tail of
+ * k % 8 values by division. Same scale. */
+int or_quantize_symmetric_row_neon(const float *x, size_t k, int8_t *q, float *scale);
+
 /* Weight repack (lib.rs:711-757, 759-806, 974-994): W8 [n,k] + scales[n]. */
 int or_repack_w8(uint32_t kind, const uint8_t *blocks, size_t bytes, size_t k, size_t n,
                  int8_t *w8, float *scales);
@@ -75,6 +80,11 @@ void or_gemm_i32(const int8_t *a8, const int8_t *w8, size_t m, size_t n, size_t 
 /* out[m,n] = (f32(c) * a_scale[m]) * w_scale[n] (lib.rs:706-708). */
 void or_rescale(const int32_t *c, const float *a_scales, const float *w_scales, size_t m, size_t n,
                 float *out);
+
+/* The aarch64 NEON rescale (lib.rs:664-690): (f32(c) * w_scale[n]) * a_scale[m]
+ * in chunks of 4 columns, the n % 4 tail in the scalar order. */
+void or_rescale_neon(const int32_t *c, const float *a_scales, const float *w_scales, size_t m, size_t n,
+                     float *out);
 
 /* Whole W8A8 route of rocknpu_matmul_q{4,5,6}_k_f32_f32 for M > 1. */
 int or_matmul_q_w8a8(uint32_t kind, const uint8_t *blocks, size_t bytes, const float *a, size_t m,

@@ -48,6 +48,9 @@ def lib() -> ctypes.CDLL:
         L.or_fp16_to_f32.restype = ctypes.c_float
         L.or_dequant_rows.argtypes = [ctypes.c_uint32, _u8p, _sz, _sz, _f32p]
         L.or_quantize_symmetric_row.argtypes = [_f32p, _sz, _i8p, _f32p]
+        L.or_quantize_symmetric_row_neon.argtypes = [_f32p, _sz, _i8p, _f32p]
+        L.or_rescale_neon.argtypes = [_i32p, _f32p, _f32p, _sz, _sz, _f32p]
+        L.or_rescale_neon.restype = None
         L.or_repack_w8.argtypes = [ctypes.c_uint32, _u8p, _sz, _sz, _sz, _i8p, _f32p]
         L.or_quantize_a8.argtypes = [_f32p, _sz, _sz, _sz, _i8p, _f32p]
         L.or_gemm_i32.argtypes = [_i8p, _i8p, _sz, _sz, _sz, _i32p, ctypes.c_int]
@@ -90,11 +93,14 @@ def dequant_rows(kind: int, blocks: np.ndarray, k: int, n: int) -> np.ndarray:
     return out
 
 
-def quantize_symmetric_row(x: np.ndarray):
+def quantize_symmetric_row(x: np.ndarray, neon: bool = False):
+    """The reference's symmetric row quantisation; neon=True gives its aarch64
+    NEON form (multiply by the reciprocal scale in chunks of 8)."""
     x = np.ascontiguousarray(x, np.float32)
     q = np.empty(x.size, np.int8)
     s = ctypes.c_float()
-    if lib().or_quantize_symmetric_row(_p(x, _f32p), x.size, _p(q, _i8p), ctypes.byref(s)) != 0:
+    fn = lib().or_quantize_symmetric_row_neon if neon else lib().or_quantize_symmetric_row
+    if fn(_p(x, _f32p), x.size, _p(q, _i8p), ctypes.byref(s)) != 0:
         raise OracleError("non-finite row")
     return q, np.float32(s.value)
 
@@ -129,10 +135,11 @@ def gemm_i32(a8: np.ndarray, w8: np.ndarray, threads: int = 1) -> np.ndarray:
     return c
 
 
-def rescale(c: np.ndarray, a_scales: np.ndarray, w_scales: np.ndarray) -> np.ndarray:
+def rescale(c: np.ndarray, a_scales: np.ndarray, w_scales: np.ndarray, neon: bool = False) -> np.ndarray:
+    """(f32(c) * a) * w; neon=True gives the aarch64 prompt-path order (c * w) * a."""
     m, n = c.shape
     out = np.empty((m, n), np.float32)
-    lib().or_rescale(_p(np.ascontiguousarray(c), _i32p), _p(np.ascontiguousarray(a_scales, np.float32), _f32p),
+    (lib().or_rescale_neon if neon else lib().or_rescale)(_p(np.ascontiguousarray(c), _i32p), _p(np.ascontiguousarray(a_scales, np.float32), _f32p),
                      _p(np.ascontiguousarray(w_scales, np.float32), _f32p), m, n, _p(out, _f32p))
     return out
 

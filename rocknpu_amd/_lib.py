@@ -52,6 +52,7 @@ SIGNATURES = {
     "rocknpu_route_supported": (_i, [_vp, ctypes.c_int32]),
     "rocknpu_route_plan": (_sz, [_vp, _sz, ctypes.c_int32, _vp]),
     "rocknpu_route_run": (_i, [_ctx, _vp, _sz, ctypes.c_int32]),
+    "rocknpu_route_stats_get": (_i, [_ctx, _vp]),
     # rocknpu_sidecar.h — the W8 sidecar
     "rocknpu_w8_source_fingerprint": (ctypes.c_uint64, [_vp, _sz]),
     "rocknpu_w8_sidecar_read": (_i, [ctypes.c_char_p, ctypes.c_char_p, _vp, _sz, _sz, _sz, _vp, _vp]),

@@ -21,6 +21,7 @@
 #include <unordered_map>
 #include <vector>
 
+#include "context.h"
 #include "rocknpu.h"
 #include "rocknpu_ggml.h"
 #include "rocknpu_hip.h"
@@ -33,7 +34,7 @@ constexpr int kExec = ROCKNPU_STATUS_EXECUTION_ERROR;
 constexpr size_t kQK = 256;
 
 size_t block_bytes(uint32_t kind) { return kind == 4 ? 144 : kind == 5 ? 176 : kind == 6 ? 210 : 0; }
-size_t round_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
+using rk::round_up;
 
 bool env_enabled(const char* name) {
     const char* v = std::getenv(name);
@@ -48,116 +49,15 @@ uint64_t now_ns() {
                                      .count());
 }
 
-// (address, bytes, k, n, kind): lib.rs:33-39. Kind 8 marks caller-supplied
-// int8 weights (the reference files those under Q4K with bytes = k*n).
-struct WeightKey {
-    uintptr_t address;
-    size_t bytes, k, n;
-    uint32_t kind;
-    bool operator==(const WeightKey& o) const {
-        return address == o.address && bytes == o.bytes && k == o.k && n == o.n && kind == o.kind;
-    }
-    bool operator<(const WeightKey& o) const {
-        if (address != o.address) return address < o.address;
-        if (bytes != o.bytes) return bytes < o.bytes;
-        if (k != o.k) return k < o.k;
-        if (n != o.n) return n < o.n;
-        return kind < o.kind;
-    }
-};
-struct KeyHash {
-    size_t operator()(const WeightKey& w) const {
-        size_t h = w.address * 0x9E3779B97F4A7C15ull;
-        h ^= w.bytes + 0x632BE59BD9B4E019ull + (h << 6) + (h >> 2);
-        h ^= w.k + (w.n << 20) + (static_cast<size_t>(w.kind) << 56) + (h << 6) + (h >> 2);
-        return h;
-    }
-};
-
-// Device-resident W8 matrix [n, k_pad] + scales[n]; freed with the entry.
-struct DeviceW8 {
-    int8_t* w8 = nullptr;
-    float* scales = nullptr;
-    size_t n = 0, k = 0, k_pad = 0;
-    DeviceW8() = default;
-    DeviceW8(const DeviceW8&) = delete;
-    DeviceW8& operator=(const DeviceW8&) = delete;
-    ~DeviceW8() {
-        if (w8) (void)hipFree(w8);
-        if (scales) (void)hipFree(scales);
-    }
-    size_t resident_bytes() const { return n * k_pad + n * sizeof(float); }
-};
-using W8Ptr = std::shared_ptr<DeviceW8>;
-
-struct DevBuf {
-    void* p = nullptr;
-    size_t cap = 0;
-    ~DevBuf() {
-        if (p) (void)hipFree(p);
-    }
-    bool ensure(size_t bytes) {
-        if (bytes <= cap) return true;
-        if (p) (void)hipFree(p);
-        p = nullptr;
-        cap = 0;
-        const size_t want = round_up(bytes, size_t(1) << 20);
-        if (hipMalloc(&p, want) != hipSuccess) return false;
-        cap = want;
-        return true;
-    }
-    template <class T>
-    T* as() const { return static_cast<T*>(p); }
-};
-
-struct PinnedBuf {
-    void* p = nullptr;
-    size_t cap = 0;
-    ~PinnedBuf() {
-        if (p) (void)hipHostFree(p);
-    }
-    bool ensure(size_t bytes) {
-        if (bytes <= cap) return true;
-        if (p) (void)hipHostFree(p);
-        p = nullptr;
-        cap = 0;
-        const size_t want = round_up(bytes, size_t(1) << 20);
-        if (hipHostMalloc(&p, want, hipHostMallocDefault) != hipSuccess) return false;
-        cap = want;
-        return true;
-    }
-    template <class T>
-    T* as() const { return static_cast<T*>(p); }
-};
-
-struct Profile {
-    size_t calls = 0, cache_hits = 0, cache_misses = 0;
-    uint64_t prepare_ns = 0, execute_ns = 0;
-};
+using rk::DevBuf;
+using rk::DeviceW8;
+using rk::KeyHash;
+using rk::PinnedBuf;
+using rk::Profile;
+using rk::W8Ptr;
+using rk::WeightKey;
 
 }  // namespace
-
-struct RockNpuContext {
-    int device = 0;
-    hipStream_t stream = nullptr;
-    // prompt (M > 1) caches, dropped by rocknpu_mtile_release
-    std::unordered_map<WeightKey, W8Ptr, KeyHash> mtile;
-    std::map<std::vector<WeightKey>, W8Ptr> mtile_groups;
-    // decode (M = 1) caches, kept across releases
-    std::unordered_map<WeightKey, W8Ptr, KeyHash> m1;
-    std::map<std::vector<WeightKey>, W8Ptr> m1_groups;
-    // raw K-quant blocks resident for the Q8_K decode GEMV
-    std::unordered_map<WeightKey, std::shared_ptr<DevBuf>, KeyHash> raw;
-    DevBuf d_raw, d_act, d_a8, d_as, d_out, d_q8k;
-    PinnedBuf h_out, h_as;
-    size_t hits = 0, misses = 0, m1_calls = 0;
-    uint64_t hit_ns = 0, miss_ns = 0;
-    Profile mtile_profile, m1_profile;
-    bool profile_mtile = false, profile_m1 = false, trace = false;
-    int hilo = 0;  // ROCKNPU_PREFILL_HILO: 0 off, 1 wide-K projections only, 2 every prompt projection
-    rocknpu_overlap_fn overlap = nullptr;
-    void* overlap_user = nullptr;
-};
 
 namespace {
 
@@ -358,9 +258,14 @@ int run_w8a8(RockNpuContext* ctx, const DeviceW8& w, const float* act, size_t m,
     return kOk;
 }
 
+// The int8 GEMM's int32 sums are exact up to K = 133120 (127 * 127 * K < 2^31);
+// longer rows are rejected before any weight is uploaded or repacked.
+bool w8a8_k_ok(size_t k) { return round_up(k, 64) <= 133120; }
+
 // Cached single-projection W8A8 (M > 1 -> prompt cache, M = 1 -> decode cache).
 int exec_single(RockNpuContext* ctx, const Source& src, const float* act, float* out, size_t m,
                 bool hilo_ok = false) {
+    if (!w8a8_k_ok(src.key.k)) return kInvalid;
     const bool decode = m == 1;
     const uint64_t t0 = now_ns();
     auto& primary = decode ? ctx->m1 : ctx->mtile;
@@ -396,6 +301,7 @@ int exec_single(RockNpuContext* ctx, const Source& src, const float* act, float*
 // Cached concatenated-N group: one GEMM, activations quantised once.
 int exec_group(RockNpuContext* ctx, const std::vector<Source>& srcs, const float* act, size_t m,
                const std::vector<float*>& outs, bool hilo_ok = false) {
+    if (!w8a8_k_ok(srcs[0].key.k)) return kInvalid;
     const bool decode = m == 1;
     std::vector<WeightKey> keys;
     std::vector<size_t> ns;
@@ -484,6 +390,8 @@ __global__ void f16_matmul_kernel(const _Float16* __restrict__ w, const float* _
 
 namespace rk {
 
+void route_print_summary(const RockNpuContext* ctx);  // route.hip
+
 // K-quant blocks (kind 4/5/6) of an [n, k] weight -> host W8 [n, k] + scales,
 // repacked on the context's GPU (the conversion half of the W8 sidecar).
 int context_repack_to_host(rocknpu_context* ctx, uint32_t kind, const uint8_t* source, size_t bytes, size_t k,
@@ -509,15 +417,31 @@ namespace {
 // The raw K-quant blocks of a weight, resident on the device under the
 // reference's cache key; uploaded on first use.
 std::shared_ptr<DevBuf> raw_weights(RockNpuContext* ctx, const uint8_t* w, size_t bytes, size_t k, size_t n,
-                                    uint32_t kind) {
+                                    uint32_t kind, bool* hit) {
     const WeightKey key{reinterpret_cast<uintptr_t>(w), bytes, k, n, kind};
     auto it = ctx->raw.find(key);
     if (it != ctx->raw.end()) return it->second;
+    *hit = false;
     auto dw = std::make_shared<DevBuf>();
     if (!dw->ensure(bytes) || !hip_ok(hipMemcpyAsync(dw->p, w, bytes, hipMemcpyHostToDevice, ctx->stream), ctx, "raw"))
         return nullptr;
     ctx->raw.emplace(key, dw);
     return dw;
+}
+
+// Decode-cache accounting of one decode call (the reference's
+// decode_cache_hits / misses and their ns, lib.rs:3821-3826): a hit when every
+// weight was resident.
+void record_decode(RockNpuContext* ctx, bool hit, uint64_t t0) {
+    const uint64_t dt = now_ns() - t0;
+    ctx->m1_calls++;
+    if (hit) {
+        ctx->hits++;
+        ctx->hit_ns += dt;
+    } else {
+        ctx->misses++;
+        ctx->miss_ns += dt;
+    }
 }
 }  // namespace
 
@@ -546,13 +470,16 @@ rocknpu_context* rocknpu_context_create(void) {
 
 int rocknpu_context_decode_cache_stats(const rocknpu_context* ctx, rocknpu_decode_cache_stats* out) {
     if (!ctx || !out) return kInvalid;
+    // the decode caches: W8 of the W8A8 M=1 entries and the raw K-quant blocks
+    // the Q8_K decode GEMV reads (lib.rs:3785-3848 counts its decode caches)
     size_t resident = 0;
     for (const auto& e : ctx->m1) resident += e.second->resident_bytes();
     for (const auto& e : ctx->m1_groups) resident += e.second->resident_bytes();
+    for (const auto& e : ctx->raw) resident += e.first.bytes;
     rocknpu_decode_cache_stats s{};
     s.hits = ctx->hits;
     s.misses = ctx->misses;
-    s.entries = ctx->m1.size() + ctx->m1_groups.size();
+    s.entries = ctx->m1.size() + ctx->m1_groups.size() + ctx->raw.size();
     s.resident_bytes = resident;
     s.hit_ns = ctx->hit_ns;
     s.miss_ns = ctx->miss_ns;
@@ -568,6 +495,7 @@ int rocknpu_context_decode_cache_stats(const rocknpu_context* ctx, rocknpu_decod
 void rocknpu_context_destroy(rocknpu_context* ctx) {
     if (!ctx) return;
     if (ctx->stream) (void)hipStreamSynchronize(ctx->stream);
+    rk::route_print_summary(ctx);
     if (ctx->profile_mtile && ctx->mtile_profile.calls)
         std::fprintf(stderr, "ROCKNPU MTILE PROFILE calls=%zu hits=%zu misses=%zu prepare_ms=%.3f execute_ms=%.3f\n",
                      ctx->mtile_profile.calls, ctx->mtile_profile.cache_hits, ctx->mtile_profile.cache_misses,
@@ -794,7 +722,9 @@ int rocknpu_matmul_q_q8k_f32_f32(rocknpu_context* ctx, uint32_t kind, const uint
     if (!mul_ok(m, k, &a_elems) || !mul_ok(m, n, &o_elems)) return kInvalid;
     for (size_t i = 0; i < a_elems; ++i)
         if (!std::isfinite(act[i])) return kInvalid;
-    const std::shared_ptr<DevBuf> dw = raw_weights(ctx, w, bytes, k, n, kind);
+    const uint64_t t0 = now_ns();
+    bool hit = true;
+    const std::shared_ptr<DevBuf> dw = raw_weights(ctx, w, bytes, k, n, kind, &hit);
     if (!dw) return kExec;
     const size_t q8_bytes = m * (k / kQK) * 292;
     if (!ctx->d_act.ensure(a_elems * 4) || !ctx->d_q8k.ensure(q8_bytes) || !ctx->d_out.ensure(o_elems * 4))
@@ -809,6 +739,7 @@ int rocknpu_matmul_q_q8k_f32_f32(rocknpu_context* ctx, uint32_t kind, const uint
     if (!hip_ok(hipMemcpyAsync(out, ctx->d_out.p, o_elems * 4, hipMemcpyDeviceToHost, ctx->stream), ctx, "out") ||
         !hip_ok(hipStreamSynchronize(ctx->stream), ctx, "gemv"))
         return kExec;
+    record_decode(ctx, hit, t0);
     return kOk;
 }
 
@@ -830,9 +761,11 @@ int rocknpu_matmul_q_q8k_group_f32_f32(rocknpu_context* ctx, size_t count, const
     if (!mul_ok(m, total_n, &o_elems)) return kInvalid;
     for (size_t i = 0; i < a_elems; ++i)
         if (!std::isfinite(act[i])) return kInvalid;
+    const uint64_t t0 = now_ns();
+    bool hit = true;
     std::shared_ptr<DevBuf> dw[4];
     for (size_t i = 0; i < count; ++i)
-        if (!(dw[i] = raw_weights(ctx, weights[i], bytes[i], k, ns[i], kinds[i]))) return kExec;
+        if (!(dw[i] = raw_weights(ctx, weights[i], bytes[i], k, ns[i], kinds[i], &hit))) return kExec;
     if (!ctx->d_act.ensure(a_elems * 4) || !ctx->d_out.ensure(o_elems * 4)) return kExec;
     if (!hip_ok(hipMemcpyAsync(ctx->d_act.p, act, a_elems * 4, hipMemcpyHostToDevice, ctx->stream), ctx, "act"))
         return kExec;
@@ -864,7 +797,9 @@ int rocknpu_matmul_q_q8k_group_f32_f32(rocknpu_context* ctx, size_t count, const
                                    ctx->stream),
                     ctx, "out"))
             return kExec;
-    return hip_ok(hipStreamSynchronize(ctx->stream), ctx, "gemv") ? kOk : kExec;
+    if (!hip_ok(hipStreamSynchronize(ctx->stream), ctx, "gemv")) return kExec;
+    record_decode(ctx, hit, t0);
+    return kOk;
 }
 
 }  // extern "C"

@@ -29,6 +29,9 @@ constexpr int kStatusExec = -3;
 // query fails). Defined in launch.hip.
 int device_cu_count();
 
+// Largest K (a multiple of 64) whose int32 accumulation stays exact:
+// |sum| <= 127 * 127 * K < 2^31 for K <= 133143.
+constexpr int kMaxExactK = 133120;
 // Rows of A8 (m * k_pad bytes) the weight-streaming GEMM stages in LDS at most.
 constexpr int kSkinnyMaxA8 = 112 * 1024;
 // A W8A8 GEMM launch: tile bm x bn with `stages` K stages of 128 bytes (bm = 0:

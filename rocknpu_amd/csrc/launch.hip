@@ -72,7 +72,7 @@ extern "C" int rocknpu_hip_gemm_w8a8(const int8_t* a8, const float* a_scales, co
                                      const float* w_scales, size_t m, size_t n, size_t k_pad, float* out,
                                      size_t ldo, int32_t* out_i32, void* stream) {
     if (!a8 || !a_scales || !w8 || !w_scales || !out || m == 0 || n == 0 || k_pad == 0 || k_pad % 64 != 0 ||
-        ldo < n || m > INT_MAX || n > INT_MAX || k_pad > INT_MAX)
+        ldo < n || m > INT_MAX || n > INT_MAX || k_pad > rk::kMaxExactK)
         return rk::kStatusInvalid;
     if (!aligned(a8, 16) || !aligned(w8, 16)) return rk::kStatusInvalid;
     // worst-case tile count (16-row tiles, 64-column tiles) must fit one grid

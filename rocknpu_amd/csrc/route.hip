@@ -2,11 +2,16 @@
 // backend takes, which same-input projections run as one call, and which
 // entry point each group goes to — the decisions of the reference plugin's
 // supports_op (adapters/ggml-rocknpu/src/ggml-rocknpu.cpp:614-715),
-// rocknpu_mtile_group (:856-976) and graph_compute (:978-1650), made from
-// plain node descriptions instead of ggml tensors. Host code only.
+// rocknpu_mtile_group (:856-976, with the cross-partition Q/K/V stash of
+// :871-928) and graph_compute (:978-1650), made from plain node descriptions
+// instead of ggml tensors. Host code only.
 #include <cstdint>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
 #include <vector>
 
+#include "context.h"
 #include "rocknpu.h"
 #include "rocknpu_ggml.h"
 #include "rocknpu_route.h"
@@ -27,6 +32,17 @@ int64_t block_bytes(int32_t t) { return t == ROCKNPU_TYPE_Q4_K ? 144 : t == ROCK
 int64_t k_of(const rocknpu_mul_mat_node& nd) { return nd.weight_ne[0]; }
 int64_t n_of(const rocknpu_mul_mat_node& nd) { return nd.weight_ne[1]; }
 int64_t m_of(const rocknpu_mul_mat_node& nd) { return nd.activation_ne[1]; }
+
+// ROCKNPU_MTILE_GROUP / ROCKNPU_MTILE_QKV: on unless set to "0" (the plugin's
+// rocknpu_env_enabled_default(..., true)).
+bool env_default_on(const char* name) {
+    const char* v = std::getenv(name);
+    return v == nullptr || v[0] == '\0' || std::strcmp(v, "0") != 0;
+}
+bool env_on(const char* name) {
+    const char* v = std::getenv(name);
+    return v != nullptr && v[0] != '\0' && v[0] != '0';
+}
 
 bool supported(const rocknpu_mul_mat_node& nd, int32_t decode) {
     const int32_t wt = nd.weight_type;
@@ -56,7 +72,169 @@ bool supported(const rocknpu_mul_mat_node& nd, int32_t decode) {
     return true;
 }
 
+// Byte ranges a node reads (its activations) and writes (its output).
+struct Span {
+    uintptr_t lo, hi;
+};
+Span reads(const rocknpu_mul_mat_node& nd) {
+    const uintptr_t p = reinterpret_cast<uintptr_t>(nd.activations);
+    return Span{p, p + static_cast<uintptr_t>(m_of(nd) * k_of(nd)) * sizeof(float)};
+}
+Span writes(const rocknpu_mul_mat_node& nd) {
+    const uintptr_t p = reinterpret_cast<uintptr_t>(nd.output);
+    return Span{p, p + static_cast<uintptr_t>(m_of(nd) * n_of(nd)) * sizeof(float)};
+}
+bool overlap(Span a, Span b) { return a.lo < b.hi && b.lo < a.hi; }
+
+// Whether node j may run at lead i's position with the members already taken:
+// the move must not reorder j against any node between them that it depends
+// on (writes j's input, or reads or writes j's output), and j must not write
+// the shared input or another member's output.
+bool movable(const rocknpu_mul_mat_node* nodes, size_t i, size_t j, const size_t* members, size_t count) {
+    const Span rj = reads(nodes[j]), wj = writes(nodes[j]);
+    for (size_t t = i + 1; t < j; ++t) {
+        const Span rt = reads(nodes[t]), wt = writes(nodes[t]);
+        if (overlap(wt, rj) || overlap(rt, wj) || overlap(wt, wj)) return false;
+    }
+    if (overlap(wj, rj)) return false;
+    for (size_t g = 0; g < count; ++g)
+        if (overlap(wj, writes(nodes[members[g]]))) return false;
+    return true;
+}
+
+void plan_groups(const rocknpu_mul_mat_node* nodes, size_t count, int32_t decode, bool grouping,
+                 int32_t* group_of, size_t* groups_out) {
+    for (size_t i = 0; i < count; ++i) group_of[i] = -2;  // not yet placed
+    size_t groups = 0;
+    for (size_t i = 0; i < count; ++i) {
+        if (group_of[i] != -2) continue;
+        const rocknpu_mul_mat_node& lead = nodes[i];
+        if (!supported(lead, decode)) {
+            group_of[i] = -1;
+            continue;
+        }
+        group_of[i] = static_cast<int32_t>(i);
+        ++groups;
+        if (!grouping || !groupable(lead.weight_type) || overlap(writes(lead), reads(lead))) continue;
+        size_t members[kMaxGroup] = {i};
+        size_t taken = 1;
+        for (size_t j = i + 1; j < count && taken < kMaxGroup; ++j) {
+            const rocknpu_mul_mat_node& c = nodes[j];
+            if (group_of[j] != -2 || c.activations != lead.activations || !groupable(c.weight_type) ||
+                k_of(c) != k_of(lead) || m_of(c) != m_of(lead) || !supported(c, decode) ||
+                !movable(nodes, i, j, members, taken))
+                continue;
+            group_of[j] = static_cast<int32_t>(i);
+            members[taken++] = j;
+        }
+    }
+    *groups_out = groups;
+}
+
+// "blk.<layer>." prefix and the attention weight's suffix (the plugin's
+// rocknpu_attention_layer, ggml-rocknpu.cpp:505-516).
+bool attention_layer(const rocknpu_mul_mat_node& nd, const char* needle, size_t* layer) {
+    if (nd.weight_name == nullptr || std::strstr(nd.weight_name, needle) == nullptr) return false;
+    size_t parsed = 0;
+    if (std::sscanf(nd.weight_name, "blk.%zu.", &parsed) != 1 || parsed >= rk::kQkvMaxLayers) return false;
+    *layer = parsed;
+    return true;
+}
+
+void count_run(rocknpu_route_stats& st, const rocknpu_mul_mat_node& nd, int32_t decode) {
+    switch (nd.weight_type) {
+    case ROCKNPU_TYPE_Q4_K: st.q4_k_mul_mat++; break;
+    case ROCKNPU_TYPE_Q5_K: st.q5_k_mul_mat++; break;
+    case ROCKNPU_TYPE_Q6_K: st.q6_k_mul_mat++; break;
+    default: st.f16_mul_mat++; break;
+    }
+    if (m_of(nd) == 1) (decode == ROCKNPU_DECODE_GGML ? st.q8k_m1_mul_mat : st.w8a8_m1_mul_mat)++;
+}
+
+// The cross-partition Q/K/V stash for one prompt group (ggml-rocknpu.cpp:871-962).
+// Returns 1 when it handled the group (*status set), 0 when the group runs as usual.
+int qkv_stash(rocknpu_context* ctx, const rocknpu_mul_mat_node* const* g, size_t c, int* status) {
+    rk::RouteState& rs = ctx->route;
+    const rocknpu_mul_mat_node& lead = *g[0];
+    const size_t m = static_cast<size_t>(m_of(lead)), k = static_cast<size_t>(k_of(lead));
+    // remember each layer's K/V weights; count the members a pending stash holds
+    size_t stashed = 0, layer = 0;
+    for (size_t t = 0; t < c; ++t) {
+        const bool is_k = attention_layer(*g[t], ".attn_k.weight", &layer);
+        if (!is_k && !attention_layer(*g[t], ".attn_v.weight", &layer)) continue;
+        rk::QkvLayer& st = rs.qkv[layer];
+        rk::QkvWeight& w = is_k ? st.wk : st.wv;
+        w = rk::QkvWeight{g[t]->weights, g[t]->weight_bytes, static_cast<size_t>(n_of(*g[t])), k, g[t]->weight_type};
+        const bool pending = is_k ? st.k_pending : st.v_pending;
+        const std::vector<float>& out = is_k ? st.k_out : st.v_out;
+        stashed += pending && st.activation == lead.activations && st.rows == m &&
+                   out.size() == m * static_cast<size_t>(n_of(*g[t]));
+    }
+    if (stashed == c) {
+        for (size_t t = 0; t < c; ++t) {
+            const bool is_k = attention_layer(*g[t], ".attn_k.weight", &layer);
+            if (!is_k) attention_layer(*g[t], ".attn_v.weight", &layer);
+            rk::QkvLayer& st = rs.qkv[layer];
+            const std::vector<float>& out = is_k ? st.k_out : st.v_out;
+            std::memcpy(g[t]->output, out.data(), out.size() * sizeof(float));
+            (is_k ? st.k_pending : st.v_pending) = false;
+            rs.stats.qkv_stash_hits++;
+        }
+        *status = kOk;
+        return 1;
+    }
+    // a Q projection alone, with its layer's K/V weights known: run Q, K and V together
+    if (c != 1 || !attention_layer(lead, ".attn_q.weight", &layer)) return 0;
+    rk::QkvLayer& st = rs.qkv[layer];
+    st.k_pending = st.v_pending = false;
+    if (st.wk.data == nullptr || st.wv.data == nullptr || st.wk.k != k || st.wv.k != k || !groupable(st.wk.type) ||
+        !groupable(st.wv.type))
+        return 0;
+    st.k_out.resize(m * st.wk.n);
+    st.v_out.resize(m * st.wv.n);
+    const uint8_t* w[3] = {static_cast<const uint8_t*>(lead.weights), static_cast<const uint8_t*>(st.wk.data),
+                           static_cast<const uint8_t*>(st.wv.data)};
+    size_t bytes[3] = {lead.weight_bytes, st.wk.bytes, st.wv.bytes};
+    uint32_t kinds[3] = {kind_of(lead.weight_type), kind_of(st.wk.type), kind_of(st.wv.type)};
+    size_t ns[3] = {static_cast<size_t>(n_of(lead)), st.wk.n, st.wv.n};
+    float* outs[3] = {lead.output, st.k_out.data(), st.v_out.data()};
+    if (rocknpu_matmul_q_concat_f32_f32_mtile(ctx, 3, w, bytes, kinds, ns, lead.activations, outs, m, k) != kOk)
+        return 0;  // the plugin then runs Q on its own (:949-951)
+    st.activation = lead.activations;
+    st.rows = m;
+    st.k_pending = st.v_pending = true;
+    rs.stats.qkv_triple_calls++;
+    for (int32_t t : {lead.weight_type, st.wk.type, st.wv.type})
+        (t == ROCKNPU_TYPE_Q4_K ? rs.stats.q4_k_mul_mat : rs.stats.q6_k_mul_mat)++;
+    if (!st.released) {
+        // the single and pair prompt caches of these weights are now unused
+        rocknpu_mtile_release(ctx, 3, w);
+        st.released = true;
+    }
+    if (env_on("ROCKNPU_GGML_TRACE"))
+        std::fprintf(stderr, "ROCKNPU GGML TRACE qkv_triple layer=%zu M=%zu K=%zu N=%zu\n", layer, m, k,
+                     ns[0] + ns[1] + ns[2]);
+    *status = kOk;
+    return 1;
+}
+
 }  // namespace
+
+namespace rk {
+// Called from rocknpu_context_destroy: the plugin's TRACE summary line
+// (ggml-rocknpu.cpp:721-736).
+void route_print_summary(const RockNpuContext* ctx) {
+    if (!env_on("ROCKNPU_GGML_TRACE") && !env_on("ROCKNPU_DISPATCH_SUMMARY")) return;
+    const rocknpu_route_stats& s = ctx->route.stats;
+    if (s.graph_calls == 0) return;
+    std::fprintf(stderr,
+                 "ROCKNPU GGML TRACE summary graph_calls=%zu q4_K_mul_mat=%zu q5_K_mul_mat=%zu q6_K_mul_mat=%zu "
+                 "f16_mul_mat=%zu q8k_m1_mul_mat=%zu w8a8_m1_mul_mat=%zu mtile_group_calls=%zu "
+                 "qkv_triple_calls=%zu qkv_stash_hits=%zu\n",
+                 s.graph_calls, s.q4_k_mul_mat, s.q5_k_mul_mat, s.q6_k_mul_mat, s.f16_mul_mat, s.q8k_m1_mul_mat,
+                 s.w8a8_m1_mul_mat, s.mtile_group_calls, s.qkv_triple_calls, s.qkv_stash_hits);
+}
+}  // namespace rk
 
 extern "C" {
 
@@ -67,29 +245,15 @@ int rocknpu_route_supported(const rocknpu_mul_mat_node* node, int32_t decode_rou
 size_t rocknpu_route_plan(const rocknpu_mul_mat_node* nodes, size_t count, int32_t decode_route,
                           int32_t* group_of) {
     if (nodes == nullptr || group_of == nullptr) return 0;
-    for (size_t i = 0; i < count; ++i) group_of[i] = -2;  // not yet placed
     size_t groups = 0;
-    for (size_t i = 0; i < count; ++i) {
-        if (group_of[i] != -2) continue;
-        const rocknpu_mul_mat_node& lead = nodes[i];
-        if (!supported(lead, decode_route)) {
-            group_of[i] = -1;
-            continue;
-        }
-        group_of[i] = static_cast<int32_t>(i);
-        ++groups;
-        if (!groupable(lead.weight_type)) continue;
-        size_t members = 1;
-        for (size_t j = i + 1; j < count && members < kMaxGroup; ++j) {
-            const rocknpu_mul_mat_node& c = nodes[j];
-            if (group_of[j] != -2 || c.activations != lead.activations || !groupable(c.weight_type) ||
-                k_of(c) != k_of(lead) || m_of(c) != m_of(lead) || !supported(c, decode_route))
-                continue;
-            group_of[j] = static_cast<int32_t>(i);
-            ++members;
-        }
-    }
+    plan_groups(nodes, count, decode_route, env_default_on("ROCKNPU_MTILE_GROUP"), group_of, &groups);
     return groups;
+}
+
+int rocknpu_route_stats_get(const rocknpu_context* ctx, rocknpu_route_stats* out) {
+    if (ctx == nullptr || out == nullptr) return kInvalid;
+    *out = ctx->route.stats;
+    return kOk;
 }
 
 int rocknpu_route_run(rocknpu_context* ctx, const rocknpu_mul_mat_node* nodes, size_t count,
@@ -97,9 +261,14 @@ int rocknpu_route_run(rocknpu_context* ctx, const rocknpu_mul_mat_node* nodes, s
     if (ctx == nullptr || (nodes == nullptr && count > 0)) return kInvalid;
     for (size_t i = 0; i < count; ++i)
         if (!supported(nodes[i], decode_route)) return kInvalid;
+    rocknpu_route_stats& stats = ctx->route.stats;
+    stats.graph_calls++;
+    const bool trace = env_on("ROCKNPU_GGML_TRACE");
+    const bool qkv = env_default_on("ROCKNPU_MTILE_QKV");
     // the plan's groups, walked in lead order
     std::vector<int32_t> group_of(count);
-    rocknpu_route_plan(nodes, count, decode_route, group_of.data());
+    size_t groups = 0;
+    plan_groups(nodes, count, decode_route, env_default_on("ROCKNPU_MTILE_GROUP"), group_of.data(), &groups);
     for (size_t i = 0; i < count; ++i) {
         if (group_of[i] != static_cast<int32_t>(i)) continue;  // not a lead
         const rocknpu_mul_mat_node* g[kMaxGroup];
@@ -109,21 +278,31 @@ int rocknpu_route_run(rocknpu_context* ctx, const rocknpu_mul_mat_node* nodes, s
         const rocknpu_mul_mat_node& lead = *g[0];
         const size_t k = static_cast<size_t>(k_of(lead)), m = static_cast<size_t>(m_of(lead));
         int st = kOk;
+        if (qkv && m > 1 && groupable(lead.weight_type) && qkv_stash(ctx, g, c, &st)) {
+            if (st != kOk) return st;
+            continue;
+        }
         if (c > 1) {
             const uint8_t* w[kMaxGroup];
             size_t bytes[kMaxGroup], ns[kMaxGroup];
             uint32_t kinds[kMaxGroup];
             float* outs[kMaxGroup];
+            size_t total_n = 0;
             for (size_t t = 0; t < c; ++t) {
                 w[t] = static_cast<const uint8_t*>(g[t]->weights);
                 bytes[t] = g[t]->weight_bytes;
                 ns[t] = static_cast<size_t>(n_of(*g[t]));
                 kinds[t] = kind_of(g[t]->weight_type);
                 outs[t] = g[t]->output;
+                total_n += ns[t];
             }
             if (m > 1) {
                 st = rocknpu_matmul_q_concat_f32_f32_mtile(ctx, c, w, bytes, kinds, ns, lead.activations, outs,
                                                            m, k);
+                stats.mtile_group_calls++;
+                if (trace)
+                    std::fprintf(stderr, "ROCKNPU GGML TRACE mtile_group lead=%s count=%zu M=%zu K=%zu N=%zu\n",
+                                 lead.weight_name ? lead.weight_name : "?", c, m, k, total_n);
             } else if (decode_route == ROCKNPU_DECODE_GGML) {
                 st = rocknpu_matmul_q_q8k_group_f32_f32(ctx, c, w, bytes, kinds, ns, lead.activations, outs, m,
                                                         k);
@@ -138,6 +317,7 @@ int rocknpu_route_run(rocknpu_context* ctx, const rocknpu_mul_mat_node* nodes, s
                                                           bytes[t + 1], kinds[t + 1], ns[t + 1], lead.activations,
                                                           outs[t], outs[t + 1], k);
             }
+            for (size_t t = 0; t < c && st == kOk; ++t) count_run(stats, *g[t], decode_route);
         } else {
             const size_t n = static_cast<size_t>(n_of(lead));
             const uint8_t* w = static_cast<const uint8_t*>(lead.weights);
@@ -153,6 +333,7 @@ int rocknpu_route_run(rocknpu_context* ctx, const rocknpu_mul_mat_node* nodes, s
                 st = rocknpu_matmul_q5_k_f32_f32(ctx, w, lead.weight_bytes, lead.activations, lead.output, m, k, n);
             else
                 st = rocknpu_matmul_q6_k_f32_f32(ctx, w, lead.weight_bytes, lead.activations, lead.output, m, k, n);
+            if (st == kOk) count_run(stats, lead, decode_route);
         }
         if (st != kOk) return st;
     }

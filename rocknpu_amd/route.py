@@ -26,15 +26,27 @@ class MulMatNode(ctypes.Structure):
         ("weight_type", ctypes.c_int32), ("activation_type", ctypes.c_int32), ("output_type", ctypes.c_int32),
         ("contiguous", ctypes.c_int32), ("weight_ne", ctypes.c_int64 * 4), ("activation_ne", ctypes.c_int64 * 4),
         ("weights", ctypes.c_void_p), ("weight_bytes", ctypes.c_size_t), ("activations", ctypes.c_void_p),
-        ("output", ctypes.c_void_p),
+        ("output", ctypes.c_void_p), ("weight_name", ctypes.c_char_p),
     ]
+
+
+class RouteStats(ctypes.Structure):
+    """rocknpu_route_stats (include/rocknpu_route.h)."""
+
+    _fields_ = [(name, ctypes.c_size_t) for name in (
+        "graph_calls", "q4_k_mul_mat", "q5_k_mul_mat", "q6_k_mul_mat", "f16_mul_mat", "q8k_m1_mul_mat",
+        "w8a8_m1_mul_mat", "mtile_group_calls", "qkv_triple_calls", "qkv_stash_hits")]
+
+    def as_dict(self) -> dict:
+        return {name: getattr(self, name) for name, _ in self._fields_}
 
 
 def node(weight_type: int, weights: np.ndarray, k: int, n: int, activations: np.ndarray,
          output: np.ndarray, contiguous: bool = True, activation_type: int = F32,
-         output_type: int = F32) -> MulMatNode:
+         output_type: int = F32, name: str | None = None) -> MulMatNode:
     """A node for dst[m, n] = activations[m, k] x weights (K-quant blocks or
-    f16 bits [n, k]); the pointers are the arrays' data."""
+    f16 bits [n, k]); the pointers are the arrays' data, `name` the weight
+    tensor's ggml name ("blk.<layer>.attn_q.weight", ...)."""
     m = activations.shape[0] if activations.ndim == 2 else 1
     nd = MulMatNode()
     nd.weight_type, nd.activation_type, nd.output_type = weight_type, activation_type, output_type
@@ -45,6 +57,9 @@ def node(weight_type: int, weights: np.ndarray, k: int, n: int, activations: np.
     nd.weight_bytes = weights.nbytes
     nd.activations = activations.ctypes.data
     nd.output = output.ctypes.data
+    if name is not None:
+        nd._name = name.encode()  # kept alive with the node
+        nd.weight_name = nd._name
     return nd
 
 
@@ -63,6 +78,15 @@ def plan(nodes, decode: int = DECODE_CPU) -> tuple[int, list[int]]:
     group_of = (ctypes.c_int32 * max(1, len(nodes)))()
     groups = _lib.load().rocknpu_route_plan(ptr, len(nodes), decode, ctypes.cast(group_of, ctypes.c_void_p))
     return groups, list(group_of)[:len(nodes)]
+
+
+def stats(ctx) -> dict:
+    """The context's dispatch counters (rocknpu_route_stats_get)."""
+    st = RouteStats()
+    rc = _lib.load().rocknpu_route_stats_get(ctx.handle if hasattr(ctx, "handle") else ctx, ctypes.byref(st))
+    if rc != 0:
+        raise RuntimeError(f"rocknpu_route_stats_get returned {rc}")
+    return st.as_dict()
 
 
 def run(ctx, nodes, decode: int = DECODE_CPU) -> int:

@@ -64,6 +64,46 @@ def gemm_patterns():
     return out
 
 
+def q5_k_single_bit_blocks():
+    """Q5_K blocks with d = 1, dmin = 0, unit scales, every quant byte 0x5A
+    (low nibble 10, high nibble 5) and exactly one qh bit set: block (t, l) has
+    bit t of qh[l]. Per ggml dequantize_row_q5_K, value l of 64-chunk j takes
+    +16 from qh[l] bit 2j (its low-nibble half) and value 32 + l from bit 2j + 1
+    (its high-nibble half), so block (t, l) dequantises to the nibble values
+    with +16 at position 64 (t // 2) + 32 (t % 2) + l and nowhere else."""
+    blocks, expect = [], []
+    for t in range(8):
+        for l in range(32):
+            b = np.zeros(176, np.uint8)
+            b[0:2] = np.array([1.0], np.float16).view(np.uint8)
+            b[4:16] = synth.pack_scales_k4(np.ones((1, 8), int), np.zeros((1, 8), int))[0]
+            b[16 + l] = 1 << t
+            b[48:] = 0x5A
+            y = np.array([10.0 if (p % 64) < 32 else 5.0 for p in range(256)], np.float32)
+            y[64 * (t // 2) + 32 * (t % 2) + l] += 16.0
+            blocks.append(b)
+            expect.append(y)
+    return np.concatenate(blocks), np.stack(expect)
+
+
+def q8_k_tie_block():
+    """One 256-value block whose first largest magnitude is -127 (so iscale =
+    -127 / -127 = 1.0 exactly and d = 1.0), holding +-(j + 1/2) for j = 0..126
+    and a zero. ggml's nearest_int rounds half to even, so +-(j + 1/2) becomes
+    +-j for even j and +-(j + 1) for odd j."""
+    x = [-127.0]
+    q = [-127]
+    for j in range(127):
+        for sign in (1.0, -1.0):
+            x.append(sign * (j + 0.5))
+            q.append(int(sign) * (j if j % 2 == 0 else j + 1))
+    x.append(0.0)
+    q.append(0)
+    x, q = np.array(x, np.float32), np.array(q, np.int32)
+    assert x.size == 256 and np.abs(x[1:]).max() < 127
+    return x, q
+
+
 def main() -> None:
     g = np.random.default_rng(0x60_1D)
     # quantisation KATs (A4)
@@ -89,6 +129,16 @@ def main() -> None:
         blocks = synth.kquant(kind, n, k, index=900 + kind)
         w8, ws = np_ref.quantize_symmetric(np_ref.dequant(kind, blocks, n, k))
         np.savez_compressed(HERE / f"repack_q{kind}k.npz", blocks=blocks, k=k, n=n, w8=w8, scales=ws)
+    # Q5_K high bits (A3): single-bit blocks, expected values from the closed form
+    blocks, y = q5_k_single_bit_blocks()
+    w8, ws = np_ref.quantize_symmetric(y)
+    np.savez_compressed(HERE / "repack_q5k_bits.npz", blocks=blocks, k=256, n=y.shape[0], y=y, w8=w8, scales=ws)
+    # Q8_K half-to-even ties, in a row of two blocks (the second is N(0,1) data)
+    x, q = q8_k_tie_block()
+    row = np.concatenate([x, synth.activations(1, 256, index=915)[0]])
+    bs = q.reshape(16, 16).sum(axis=1)
+    tie_block = np_ref.pack_q8_k(np.array([1.0], np.float32), q[None], bs[None])
+    np.savez_compressed(HERE / "q8_k_ties.npz", x=row[None], q8k_block0=tie_block)
     # per-token A8 quantisation with K padded to a multiple of 64
     a = synth.activations(5, 1000, index=910)
     q, s = np_ref.quantize_symmetric(a)

@@ -77,6 +77,9 @@ def test_launch_layer_rejects_bad_shapes_before_launch():
     assert lib.rocknpu_hip_repack_w8(4, p, 144, 256, 1, 260, p, p, None) == -1
     assert lib.rocknpu_hip_repack_w8(7, p, 144, 256, 1, 256, p, p, None) == -1
     assert lib.rocknpu_hip_gemm_w8a8(p, p, p, p, 4, 4, 100, p, 4, None, None) == -1
+    # int32 sums are exact only while 127 * 127 * K < 2^31: K = 133120 is the largest multiple of 64
+    assert 127 * 127 * 133120 < 2**31 <= 127 * 127 * 133184
+    assert lib.rocknpu_hip_gemm_w8a8(p, p, p, p, 4, 4, 133184, p, 4, None, None) == -1
     assert lib.rocknpu_hip_quantize_q8_k(p, 1, 100, 100, p, None) == -1
     assert lib.rocknpu_hip_gemv_q8_k(5, p, 144, 256, 1, p, 1, p, 1, None, None, None) == -1
     assert lib.rocknpu_hip_gemv_q8_k(4, p, 144, 256, 1, p, 1, p, 1, p, None, None) == -1

@@ -278,3 +278,42 @@ def test_w8_sidecar_get_converts_writes_and_reloads(tmp_path):
             assert sidecar.read(tmp_path / "dir", name, blocks, k, n) is not None
     finally:
         c.close()
+
+
+def test_decode_cache_stats_count_the_q8k_route():
+    """The Q8_K decode route's resident raw blocks are decode-cache entries:
+    entries, resident bytes, hits and misses move with its calls."""
+    k, n = 2048, 96
+    w4 = synth.q4_k(n, k, index=1720)
+    w6 = synth.q6_k(n, k, index=1721)
+    x = synth.activations(1, k, index=1722)
+    out = np.empty((1, n), np.float32)
+    with Context() as c:
+        s0 = c.decode_cache_stats()
+        assert (s0.entries, s0.resident_bytes, s0.hits, s0.misses) == (0, 0, 0, 0)
+        assert c.matmul_q_q8k(4, w4, x, out, k, n) == STATUS_OK
+        s1 = c.decode_cache_stats()
+        assert (s1.entries, s1.resident_bytes, s1.misses, s1.hits) == (1, w4.nbytes, 1, 0)
+        assert c.matmul_q_q8k(4, w4, x, out, k, n) == STATUS_OK
+        s2 = c.decode_cache_stats()
+        assert (s2.entries, s2.resident_bytes, s2.misses, s2.hits) == (1, w4.nbytes, 1, 1)
+        outs = [np.empty((1, n), np.float32) for _ in range(2)]
+        assert c.matmul_q_q8k_group([w4, w6], [4, 6], [n, n], x, outs, k) == STATUS_OK
+        s3 = c.decode_cache_stats()
+        assert (s3.entries, s3.resident_bytes, s3.misses, s3.hits) == (2, w4.nbytes + w6.nbytes, 2, 1)
+        assert s3.miss_ns > 0 and s3.hit_ns > 0 and s3.worker1_calls == 3
+
+
+def test_w8a8_rejects_k_beyond_exact_int32():
+    """127 * 127 * K must stay below 2^31 for exact int32 sums: K = 133376 is refused
+    before any weight is uploaded, on every W8A8 entry."""
+    k, n = 133376, 2
+    w = synth.q4_k(n, k, index=1730)
+    a = synth.activations(2, k, index=1731)
+    out = np.zeros((2, n), np.float32)
+    with Context() as c:
+        assert c.matmul_q(4, w, a, out, k, n) == STATUS_INVALID_ARGUMENT
+        assert c.matmul_q(4, w, a[:1].copy(), out[:1], k, n) == STATUS_INVALID_ARGUMENT
+        s = c.decode_cache_stats()
+        assert s.entries == 0 and s.misses == 0
+    assert not out.any()

@@ -87,3 +87,38 @@ def test_gpu_golden_gemv(kind):
     assert np.array_equal(isum.cpu().numpy(), f["isum"]) and np.array_equal(msum.cpu().numpy(), f["msum"])
     for got in (out.cpu().numpy(), fused.cpu().numpy()):
         assert np.all(np.abs(got.astype(np.float64) - f["y"]) <= 1e-5 * f["mag"] + 1e-30)
+
+
+def test_gpu_golden_q5_k_high_bits():
+    """The Q5_K repack kernel on single-bit blocks: W8 and scales equal the
+    closed form's quantisation bit for bit."""
+    import torch
+    from rocknpu_amd import hip
+    f = _load("repack_q5k_bits")
+    w8, sc = hip.repack_w8(5, _dev(f["blocks"]), 256, int(f["n"]))
+    torch.cuda.synchronize()
+    assert np.array_equal(w8.cpu().numpy(), f["w8"]) and np.array_equal(_bits(sc.cpu().numpy()), _bits(f["scales"]))
+
+
+@pytest.mark.parametrize("kind", [4, 6])
+def test_gpu_golden_q8_k_half_even_ties(kind):
+    """Exact ties of iscale * x round half to even on the GPU: the Q8_K
+    quantiser reproduces the fixture, and the GEMV that quantises in-kernel
+    equals the GEMV on those Q8_K bytes bit for bit (so it rounds the same)."""
+    import torch
+    from rocknpu_amd import hip, synth
+    f = _load("q8_k_ties")
+    q = hip.quantize_q8_k(_dev(f["x"]))
+    torch.cuda.synchronize()
+    q = q.cpu().numpy()
+    assert np.array_equal(q[0, :292], f["q8k_block0"])
+    n, k = 48, 512
+    w = _dev(synth.kquant(kind, n, k, index=960 + kind))
+    for m in (1, 4):
+        x = np.repeat(f["x"], m, axis=0)
+        x[1:] *= np.float32(0.5)  # further rows: ties at the half-scale grid
+        q8 = hip.quantize_q8_k(_dev(x))
+        ref = hip.gemv_q8_k(kind, w, k, n, q8)
+        fused = hip.gemv_q_f32(kind, [w], k, [n], _dev(x))[0]
+        torch.cuda.synchronize()
+        assert np.array_equal(_bits(fused.cpu().numpy()), _bits(ref.cpu().numpy())), m

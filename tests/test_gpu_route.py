@@ -77,3 +77,74 @@ def test_q8k_group_entry_equals_single_entry(m):
         assert ctx.matmul_q_q8k_group([], [], [], x, [], k) == -1
         assert ctx.matmul_q_q8k_group(ws + ws[:1], kinds + [4], ns + [48], x, outs + outs[:1], k) == -1
         assert ctx.matmul_q_q8k_group([ws[0][:-1]], [4], [48], x, outs[:1], k) == -1
+
+
+def test_route_run_keeps_order_when_a_buffer_is_reused():
+    """[A reads X; C writes X; B reads X]: B must see C's output, as in graph
+    order, so the result equals direct calls made in node order."""
+    print("route alias", flush=True)
+    m, k = 5, 512
+    x = synth.activations(m, k, index=81)
+    y = synth.activations(m, k, index=82)
+    wa, wc, wb = (synth.kquant(4, n, k, index=810 + i) for i, n in enumerate((64, k, 48)))
+    oa, ob = np.zeros((m, 64), np.float32), np.zeros((m, 48), np.float32)
+    x_run = x.copy()
+    nodes = [R.node(R.Q4_K, wa, k, 64, x_run, oa), R.node(R.Q4_K, wc, k, k, y, x_run),
+             R.node(R.Q4_K, wb, k, 48, x_run, ob)]
+    assert R.plan(nodes)[1] == [0, 1, 2]
+    with Context() as ctx:
+        assert R.run(ctx, nodes) == 0
+        ra, rc, rb = np.zeros((m, 64), np.float32), np.zeros((m, k), np.float32), np.zeros((m, 48), np.float32)
+        assert ctx.matmul_q(4, wa, x, ra, k, 64) == 0
+        assert ctx.matmul_q(4, wc, y, rc, k, k) == 0
+        assert ctx.matmul_q(4, wb, rc, rb, k, 48) == 0   # B reads what C wrote
+    assert np.array_equal(_bits(oa), _bits(ra))
+    assert np.array_equal(_bits(x_run), _bits(rc))
+    assert np.array_equal(_bits(ob), _bits(rb))
+
+
+def test_qkv_stash_across_separate_calls():
+    """Layer 3's Q, then its K and V in a later call (another split): Q runs as
+    one Q+K+V concat call with K/V kept in the context, K and V are served from
+    that stash, and every output equals its direct call bit for bit
+    (ggml-rocknpu.cpp:871-928)."""
+    print("route qkv stash", flush=True)
+    m, k = 40, 1024
+    spec = (("q", 4, 128), ("k", 4, 32), ("v", 6, 32))
+    ws = {name: synth.kquant(kind, n, k, index=830 + i) for i, (name, kind, n) in enumerate(spec)}
+    x = synth.activations(m, k, index=84)
+
+    def nodes_for(names, outs, act):
+        return [R.node(TYPE[kind], ws[name], k, n, act, outs[name], name=f"blk.3.attn_{name}.weight")
+                for name, kind, n in spec if name in names]
+
+    with Context() as ctx:
+        ref = {}
+        for name, kind, n in spec:
+            ref[name] = np.zeros((m, n), np.float32)
+            assert ctx.matmul_q(kind, ws[name], x, ref[name], k, n) == 0
+        # first pass: Q, K and V in one call (one same-input group); K/V weights become known
+        outs = {name: np.zeros((m, n), np.float32) for name, _, n in spec}
+        assert R.run(ctx, nodes_for("qkv", outs, x)) == 0
+        st0 = R.stats(ctx)
+        assert st0["mtile_group_calls"] == 1 and st0["qkv_triple_calls"] == 0
+        # second pass: Q alone, then K and V in another call
+        outs = {name: np.zeros((m, n), np.float32) for name, _, n in spec}
+        assert R.run(ctx, nodes_for("q", outs, x)) == 0
+        st1 = R.stats(ctx)
+        assert st1["qkv_triple_calls"] == 1 and not outs["k"].any() and not outs["v"].any()
+        assert R.run(ctx, nodes_for("kv", outs, x)) == 0
+        st2 = R.stats(ctx)
+        assert st2["qkv_stash_hits"] == 2 and st2["mtile_group_calls"] == st1["mtile_group_calls"]
+        for name, _, _ in spec:
+            assert np.array_equal(_bits(outs[name]), _bits(ref[name])), name
+        # K/V of another input are computed, not served from the stash
+        x2 = synth.activations(m, k, index=85)
+        outs2 = {name: np.zeros((m, n), np.float32) for name, _, n in spec}
+        assert R.run(ctx, nodes_for("q", outs2, x)) == 0
+        assert R.run(ctx, nodes_for("kv", outs2, x2)) == 0
+        assert R.stats(ctx)["qkv_stash_hits"] == 2
+        for name, kind, n in spec[1:]:
+            r2 = np.zeros((m, n), np.float32)
+            assert ctx.matmul_q(kind, ws[name], x2, r2, k, n) == 0
+            assert np.array_equal(_bits(outs2[name]), _bits(r2)), name

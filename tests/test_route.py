@@ -138,3 +138,70 @@ def test_plan_of_synthetic_weights_matches_shapes():
         nd._keep = (w, out)
         nodes.append(nd)
     assert R.plan(nodes) == (1, [0, 0])
+
+
+def _out_node(wt, n, k, x, out, name=None):
+    """A node whose output array is given (so tests can make outputs alias inputs)."""
+    w = _blocks(wt, n, k)
+    nd = R.node(wt, w, k, n, x, out, name=name)
+    nd._keep = (w, x, out)
+    return nd
+
+
+def test_plan_does_not_move_a_member_past_a_writer_of_its_input():
+    # [A: reads X; C: writes X (a buffer ggml-alloc reused); B: reads X]: B reads
+    # C's output, so it must run after C and cannot join A's group
+    m, k = 4, 512
+    x, y = np.zeros((m, k), np.float32), np.zeros((m, k), np.float32)
+    a = _out_node(R.Q4_K, 64, k, x, np.zeros((m, 64), np.float32))
+    c = _out_node(R.Q4_K, k, k, y, x)          # N = K: its output is exactly X
+    b = _out_node(R.Q4_K, 64, k, x, np.zeros((m, 64), np.float32))
+    assert R.plan([a, c, b]) == (3, [0, 1, 2])
+    # a writer of only part of X is a conflict too
+    part = x.reshape(-1)[k:k + 32 * 2].reshape(2, 32)
+    c2 = _out_node(R.Q4_K, 32, k, np.zeros((2, k), np.float32), part)
+    assert R.plan([a, c2, b]) == (3, [0, 1, 2])
+
+
+def test_plan_does_not_move_a_member_past_a_reader_or_writer_of_its_output():
+    m, k = 4, 512
+    x, z = np.zeros((m, k), np.float32), np.zeros((m, k), np.float32)
+    a = _out_node(R.Q4_K, 64, k, x, np.zeros((m, 64), np.float32))
+    t_reads_z = _out_node(R.Q4_K, 64, k, z, np.zeros((m, 64), np.float32))
+    b_writes_z = _out_node(R.Q4_K, k, k, x, z)   # B's output is T's input
+    assert R.plan([a, t_reads_z, b_writes_z]) == (3, [0, 1, 2])
+    w = np.zeros((m, 64), np.float32)
+    t_writes_w = _out_node(R.Q4_K, 64, k, z, w)
+    b_writes_w = _out_node(R.Q4_K, 64, k, x, w)  # both write W: the later write must stay last
+    assert R.plan([a, t_writes_w, b_writes_w]) == (3, [0, 1, 2])
+
+
+def test_plan_groups_across_unrelated_nodes_and_rejects_self_aliasing_members():
+    m, k = 4, 512
+    x = np.zeros((m, k), np.float32)
+    a = _out_node(R.Q4_K, 64, k, x, np.zeros((m, 64), np.float32))
+    t = _out_node(R.Q4_K, 64, k, np.zeros((m, k), np.float32), np.zeros((m, 64), np.float32))
+    b = _out_node(R.Q4_K, 64, k, x, np.zeros((m, 64), np.float32))
+    assert R.plan([a, t, b]) == (2, [0, 1, 0])
+    # a member writing the shared input, or the output of an earlier member
+    b_in_place = _out_node(R.Q4_K, k, k, x, x)
+    assert R.plan([a, b_in_place]) == (2, [0, 1])
+    shared = np.zeros((m, 64), np.float32)
+    a2 = _out_node(R.Q4_K, 64, k, x, shared)
+    b2 = _out_node(R.Q4_K, 64, k, x, shared)
+    assert R.plan([a2, b2]) == (2, [0, 1])
+
+
+def test_plan_grouping_switch(monkeypatch):
+    monkeypatch.setenv("ROCKNPU_MTILE_GROUP", "0")
+    groups, lead = R.plan(_layer(8))
+    assert groups == 7 and lead == list(range(7))
+    monkeypatch.setenv("ROCKNPU_MTILE_GROUP", "1")
+    assert R.plan(_layer(8))[1] == [0, 0, 0, 3, 4, 4, 6]
+
+
+def test_route_stats_need_a_context():
+    import ctypes
+    from rocknpu_amd import _lib
+    st = R.RouteStats()
+    assert _lib.load().rocknpu_route_stats_get(None, ctypes.byref(st)) == -1
