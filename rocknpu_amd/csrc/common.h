@@ -46,7 +46,10 @@ struct GemvLanes {
     int lanes, waves;
 };
 GemvLanes gemv_lanes(bool fused, bool sums, int m, int nb, const int64_t* rows, int count, int cus);  // gemv.hip
-bool gemv_uses_mfma(int kind, int m, int64_t rows, int cus);                                          // gemv.hip
+bool gemv_uses_mfma(int kind, int m, int nb, int64_t rows, int cus);                                  // gemv.hip
+// Activation rows per launch the matrix-core GEMV holds for rows of nb blocks
+// (0: none). Defined in gemv_mfma.hip.
+int gemv_mfma_rows(int kind, int nb);
 
 __host__ __device__ constexpr int block_bytes(int kind) {
     return kind == 4 ? kQ4KBytes : kind == 5 ? kQ5KBytes : kind == 6 ? kQ6KBytes : 0;

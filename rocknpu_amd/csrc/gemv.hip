@@ -633,15 +633,17 @@ GemvLanes gemv_lanes(bool fused, bool sums, int m, int nb, const int64_t* rows, 
 // The matrix-core kernel from 3 rows for Q4_K, from 5 rows for Q6_K, and for
 // Q6_K at 3 or 4 rows when its 16-row tiles fill every CU (Llama-3-8B down,
 // 4096 x 14336, at 4 rows: 25.8 -> 22.5 us; TinyLlama down, 2048 rows, stays
-// on the lane-per-block kernel, 10.6 against 11.1 us).
-bool gemv_uses_mfma(int kind, int m, int64_t rows, int cus) {
+// on the lane-per-block kernel, 10.6 against 11.1 us), whenever its LDS holds
+// the launch's rows (gemv_mfma_rows).
+bool gemv_uses_mfma(int kind, int m, int nb, int64_t rows, int cus) {
+    if (m > gemv_mfma_rows(kind, nb)) return false;
     return kind == 4 ? m >= 3 : m >= 5 || (m >= 3 && rows >= 16 * int64_t{cus});
 }
 
 int launch_gemv(int kind, bool fused, GemvParams& p, hipStream_t stream) {
     int64_t rows = 0;
     for (int i = 0; i < p.count; ++i) rows += p.rows[i];
-    if (gemv_uses_mfma(kind, p.m, rows, device_cu_count()) && p.isum == nullptr)
+    if (gemv_uses_mfma(kind, p.m, p.nb, rows, device_cu_count()) && p.isum == nullptr)
         return launch_gemv_mfma(kind, fused, p, stream);
     if (kind == 4) return fused ? launch_kind<4, true>(p, stream) : launch_kind<4, false>(p, stream);
     if (kind == 6) return fused ? launch_kind<6, true>(p, stream) : launch_kind<6, false>(p, stream);

@@ -62,25 +62,28 @@ __device__ __forceinline__ Q8Lds q8_lds(uint8_t* smem, int mt, int nb) {
     return a;
 }
 
-// The 16 values of this lane for quantisation block qb.
+// The 16 values of this lane for quantisation block qb: lane sub of the 16
+// holds values 64 t + 4 sub + e (t, e = 0..3), so each of the four loads reads
+// 256 contiguous bytes per 16 lanes (whole cache lines).
 __device__ __forceinline__ void load_x16(const float* __restrict__ x, int64_t ldx, int nb, int qb, float4 (&f)[4]) {
     const int sub = threadIdx.x & 15;
     const int r = qb / nb, b = qb % nb;
-    const float4* src = reinterpret_cast<const float4*>(x + r * ldx + b * kQK + 16 * sub);
+    const float4* src = reinterpret_cast<const float4*>(x + r * ldx + b * kQK + 4 * sub);
 #pragma unroll
-    for (int t = 0; t < 4; ++t) f[t] = src[t];
+    for (int t = 0; t < 4; ++t) f[t] = src[16 * t];
 }
 
-// Q8_K quantisation of one 256-value block (ggml quantize_row_q8_K_ref
-// semantics, see quant.hip) by 16 lanes, 16 values per lane, into LDS.
+// Q8_K quantisation of one 256-value block (ggml quantize_row_q8_K_ref) by 16
+// lanes, lane sub holding values 64 t + 4 sub + e as loaded by load_x16:
 //   max = the first value of largest magnitude; iscale = -127/max;
-//   q = min(127, nearest(iscale * x)); d = 1/iscale; bsums = sums of 16 q.
-// The block's largest and smallest values give the magnitude and, unless a
-// value and its negation both reach it (then the first one is searched
-// for), the sign of max. |iscale * x| <= 127 (1 + 2^-24)^2 < 127.5, so q is
-// in [-127, 127] and the min(127, .) never binds; q + 128 in [1, 255] is
-// packed to bytes by v_cvt_pk_u8_f32 and flipped back to two's complement.
-__device__ __forceinline__ void quantize_block_to_lds(const float4 (&f)[4], int qb, const Q8Lds& a) {
+//   q = min(127, nearest_int(iscale * x)); d = 1/iscale; bsums = sums of 16 q.
+// nearest_int is ggml's own: add 1.5 * 2^23 and keep the low mantissa bits,
+// i.e. round half to even. |iscale * x| <= 127 (1 + 2^-24)^2 < 127.5, so q is
+// in [-127, 127] (the min never binds) and its low byte is q as int8. The
+// block's largest and smallest values give the magnitude and, unless a value
+// and its negation both reach it (then the first one is searched for), the
+// sign of max. Writes the 256 quants at qs, the 16 int16 bsums at bs and d.
+__device__ __forceinline__ void quantize_block(const float4 (&f)[4], uint8_t* qs, int16_t* bs, float* d_out) {
     const int sub = threadIdx.x & 15;
     float v[16];
 #pragma unroll
@@ -109,28 +112,44 @@ __device__ __forceinline__ void quantize_block_to_lds(const float4 (&f)[4], int 
         int first = 0x7fffffff;
 #pragma unroll
         for (int i = 15; i >= 0; --i)
-            if (fabsf(v[i]) == gmax) first = (16 * sub + i) * 2 + (v[i] < 0.0f ? 1 : 0);
+            if (fabsf(v[i]) == gmax) first = min(first, (64 * (i >> 2) + 4 * sub + (i & 3)) * 2 + (v[i] < 0.0f ? 1 : 0));
         first = min16(first);
         if (both) mx = (first & 1) ? -gmax : gmax;
     }
     uint32_t wq[4] = {0, 0, 0, 0};
-    float qs = 0.0f;
     float d = 0.0f;
     if (gmax > 0.0f) {
         const float iscale = -127.0f / mx;
+        uint32_t r[16];
 #pragma unroll
-        for (int i = 0; i < 16; ++i) {
-            const float q = __builtin_rintf(iscale * v[i]);
-            qs += q;
-            wq[i >> 2] = __builtin_amdgcn_cvt_pk_u8_f32(q + 128.0f, i & 3, wq[i >> 2]);
+        for (int i = 0; i < 16; ++i) r[i] = __float_as_uint(iscale * v[i] + 12582912.0f);
+        // the low bytes of four rounded values per word: bytes 0,1, then 2,3, by v_perm
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            const uint32_t lo = __builtin_amdgcn_perm(r[4 * t + 1], r[4 * t], 0x0C0C0400u);
+            const uint32_t hi = __builtin_amdgcn_perm(r[4 * t + 3], r[4 * t + 2], 0x0C0C0400u);
+            wq[t] = __builtin_amdgcn_perm(hi, lo, 0x05040100u);
         }
-#pragma unroll
-        for (int t = 0; t < 4; ++t) wq[t] ^= 0x80808080u;
         d = 1.0f / iscale;
     }
-    *reinterpret_cast<uint4*>(a.qs + qb * kGemvLdsQsStride + 16 * sub) = make_uint4(wq[0], wq[1], wq[2], wq[3]);
-    reinterpret_cast<int16_t*>(a.bs + qb * kGemvLdsBsStride)[sub] = static_cast<int16_t>(static_cast<int>(qs));
-    if (sub == 0) a.d[qb] = d;
+    // bsum of 16-value group 4 t + sub / 4: four lanes' word sums, added over the lane quad
+    int gs[4];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+        gs[t] = __builtin_amdgcn_sdot4(static_cast<int>(wq[t]), 0x01010101, 0, false);
+        gs[t] += dpp<kDppXor1>(gs[t]);
+        gs[t] += dpp<kDppXor2>(gs[t]);
+        *reinterpret_cast<uint32_t*>(qs + 64 * t + 4 * sub) = wq[t];
+    }
+    const int tq = sub & 3;  // lane tq of each quad writes group 4 tq + sub / 4
+    const int g = tq == 0 ? gs[0] : tq == 1 ? gs[1] : tq == 2 ? gs[2] : gs[3];
+    bs[4 * tq + (sub >> 2)] = static_cast<int16_t>(g);
+    if (sub == 0) *d_out = d;
+}
+
+__device__ __forceinline__ void quantize_block_to_lds(const float4 (&f)[4], int qb, const Q8Lds& a) {
+    quantize_block(f, a.qs + qb * kGemvLdsQsStride, reinterpret_cast<int16_t*>(a.bs + qb * kGemvLdsBsStride),
+                   a.d + qb);
 }
 
 // Q8_K quantisation of rows [0, m) of x into LDS by the first waves of the

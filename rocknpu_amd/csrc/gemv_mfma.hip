@@ -1,39 +1,35 @@
-// Kernel (d) for 2..8 activation rows, Q4_K and Q6_K weights (the launch
-// layer sends Q4_K at 3..8 rows and Q6_K at 5..8 here): the decode GEMV with
-// the per-sub-block integer dot products on the matrix cores.
+// Kernel (d) for up to 16 activation rows (Q4_K) or 8 (Q6_K): the decode
+// GEMV with the per-sub-block integer dot products on the matrix cores.
 //
 // Same arithmetic as gemv.hip (ggml_vec_dot_q{4,6}_K_q8_K, per block and row):
 //   isum = sum_s sc_s * sum_{k in sub-block s} q8[k] * q[k]
 //          (Q4_K: s = 0..7 of 32 values; Q6_K: s = 0..15 of 16, q = stored - 32)
 //   msum = sum_s mn_s * (sum of the activation quants of sub-block s)   (Q4_K)
 //   row += (d * d_a) * isum - (dmin * d_a) * msum                 (f32)
-// with exact integers up to the f32 scaling, so the results differ from the
-// VALU kernel's only in the f32 order of the per-block terms.
+// with exact integers up to the f32 scaling.
 //
 // v_mfma_i32_16x16x32_i8 on gfx950: lane l supplies row l%16 of A and column
 // l%16 of B, with K bytes 8*(l/16) .. +7, and holds D column l%16, rows
-// 4*(l/16) + e (e = 0..3). Here B's 16 columns are 16 weight rows and A's 16
-// rows are MT activation rows times SPLIT = 16/MT sub-blocks: A row r =
-// (sub-block r / MT of the instruction's group, activation row r % MT), and
-// instruction t of a group of SPLIT sub-blocks puts the activations of its
-// sub-block t in rows t*MT .. t*MT+MT-1 and zeros elsewhere. The SPLIT
-// instructions of a group then fill disjoint rows of one accumulator, so D
-// holds SPLIT sub-block products for all MT rows and 16 weight rows with no
-// padding. Q6_K's 16-value sub-blocks take half an instruction's 32 K slots
-// each: slot r / MT then holds its sub-block in K half (r / MT) & 1, so one
-// instruction serves two slots and a group of SPLIT slots takes SPLIT / 2.
-// Each lane scales its four D values by its weight row's sub-block scales
-// (integer multiply-add), and the lanes that hold the same activation row and
-// weight row add their sub-blocks' sums with lane exchanges.
+// 4*(l/16) + e (e = 0..3). B's 16 columns are 16 weight rows of a tile. A's 16
+// rows are MT activation rows times SPLIT = 16/MT sub-block slots, placed so
+// that A row r holds activation row r / SPLIT and slot r % SPLIT: the four D
+// values of lane l then belong to activation rows NR*(l/16) .. +NR-1 (NR =
+// MT/4) and slots e % SPLIT, so a lane adds its sub-blocks' scaled sums on its
+// own, with the sub-block of every D value known at compile time. Instruction
+// t of a group of SPLIT slots carries sub-block (group * SPLIT + t) in the A
+// rows of slot t and zeros in the others, so the group's instructions fill
+// disjoint rows of one accumulator. Q6_K's 16-value sub-blocks take half an
+// instruction's 32 K slots each: slot s sits in K half s & 1 of instruction
+// s >> 1 of its group.
 //
-// Work split: a tile is 16 weight rows. A workgroup holds 8 waves; wave g
-// takes blocks g, g + 8, .. of every tile its workgroup walks (tiles
-// blockIdx.x, + gridDim.x, ..), with D blocks of loads in flight (the
-// launcher runs D = 1). When a
-// tile's blocks are done, the waves leave their f32 partial sums in LDS and
-// wave 0 adds them in wave order and stores the rows. The f32 order of a
-// row's terms therefore depends only on nb: the same in fused launches, in
-// grouped launches and in Q8_K-input launches.
+// Work split: a tile is 16 weight rows. A workgroup holds W waves; wave g owns
+// super-blocks g, g + W, .. of every tile its workgroup walks (tiles
+// blockIdx.x, + gridDim.x, ..). Each wave quantises the activation blocks it
+// owns (f32 -> Q8_K, ggml quantize_row_q8_K_ref) into its own part of LDS, or
+// copies them from Q8_K rows, so no wave waits for another before computing.
+// When a tile's blocks are done, the waves leave their f32 partial sums in LDS
+// and one wave adds them in wave order and stores the rows: a row's f32 order
+// depends only on nb and W, the same in fused, grouped and Q8_K-input launches.
 #include "gemv_lds.h"
 
 #include <algorithm>
@@ -42,9 +38,16 @@ namespace rk {
 namespace {
 
 typedef int v4i __attribute__((ext_vector_type(4)));
+typedef short v2s __attribute__((ext_vector_type(2)));
 
-constexpr int kMfmaWaves = 8;  // waves per workgroup = block slots per tile
 constexpr int kTileRows = 16;
+// LDS of one (block, activation row): 256 quants (272-byte stride: consecutive
+// rows in different banks), 16 int16 bsums, one f32 scale.
+constexpr int kQsStride = 272;
+constexpr int kBsStride = 32;
+constexpr int kPerRowBlock = kQsStride + kBsStride + 4;
+// LDS a workgroup may use: gfx950's 160 KiB per CU.
+constexpr int kLdsMax = 160 * 1024;
 
 struct MfmaMember {
     const uint8_t* w;
@@ -62,17 +65,22 @@ struct MfmaArgs {
     int m;
     int nb;
     int tiles;
+    int iters;  // blocks per wave and tile: ceil(nb / W)
 };
 
-// Scale and min of Q4_K sub-block 4*hi + idx (idx = 0..3; ggml
-// get_scale_min_k4) from the three scale words s0 s1 s2 of the header.
-__device__ __forceinline__ void q4_scale_min(uint32_t s0, uint32_t s1, uint32_t s2, bool hi, int idx, int& sc,
-                                             int& mn) {
-    const int sh = 8 * idx;
-    const uint32_t a0 = s0 >> sh, a1 = s1 >> sh, a2 = s2 >> sh;
-    sc = hi ? static_cast<int>((a2 & 0xF) | ((a0 >> 2) & 0x30)) : static_cast<int>(a0 & 63);
-    mn = hi ? static_cast<int>(((a2 >> 4) & 0xF) | ((a1 >> 2) & 0x30)) : static_cast<int>(a1 & 63);
-}
+// The wave-owned activation blocks in LDS: block b, activation row mi.
+template <int MT>
+struct ActLds {
+    uint8_t* base;
+    int nb;
+    __device__ __forceinline__ uint8_t* quants(int b, int mi) const { return base + (b * MT + mi) * kQsStride; }
+    __device__ __forceinline__ uint32_t* bsums(int b, int mi) const {
+        return reinterpret_cast<uint32_t*>(base + nb * MT * kQsStride + (b * MT + mi) * kBsStride);
+    }
+    __device__ __forceinline__ float* d(int b, int mi) const {
+        return reinterpret_cast<float*>(base + nb * MT * (kQsStride + kBsStride)) + b * MT + mi;
+    }
+};
 
 typedef const __attribute__((address_space(1))) uint32_t* gu32;
 typedef const __attribute__((address_space(1))) uint64_t* gu64;
@@ -93,6 +101,18 @@ struct MPiece<4> {
         h = reinterpret_cast<gv4u>(blk)[0];
 #pragma unroll
         for (int j = 0; j < 4; ++j) qp[j] = reinterpret_cast<gu64>(blk + 16 + 32 * j + 8 * q)[0];
+    }
+    // this lane's 8 values of sub-block s (0..7), one per byte
+    __device__ __forceinline__ uint64_t values(int s) const {
+        return (qp[s >> 1] >> (4 * (s & 1))) & 0x0F0F0F0F0F0F0F0Full;
+    }
+    // 6-bit scales and mins of sub-blocks 0..3 and 4..7 as packed bytes
+    // (ggml get_scale_min_k4 on bytes 4..15 of the block, four at a time)
+    __device__ __forceinline__ void packed(uint32_t& sc_lo, uint32_t& sc_hi, uint32_t& mn_lo, uint32_t& mn_hi) const {
+        sc_lo = h.y & 0x3F3F3F3Fu;
+        mn_lo = h.z & 0x3F3F3F3Fu;
+        sc_hi = (h.w & 0x0F0F0F0Fu) | ((h.y >> 2) & 0x30303030u);
+        mn_hi = ((h.w >> 4) & 0x0F0F0F0Fu) | ((h.z >> 2) & 0x30303030u);
     }
     __device__ __forceinline__ void scales(float& d, float& dmin) const {
         d = f16_bits_to_f32(static_cast<uint16_t>(h.x & 0xFFFF));
@@ -139,7 +159,8 @@ struct MPiece<6> {
         const uint32_t lo = __builtin_amdgcn_alignbyte(w[1], w[0], sh), hi = __builtin_amdgcn_alignbyte(w[2], w[1], sh);
         return static_cast<uint64_t>(hi) << 32 | lo;
     }
-    // The 8 signed values of quarter t % 4 of half t / 4 in this lane's K slots.
+    // The 8 signed values of quarter t % 4 of half t / 4 in this lane's K slots
+    // (sub-block 2t for lane groups 0-1, 2t + 1 for 2-3).
     __device__ __forceinline__ uint64_t values(int t) const {
         const int h = t >> 2, g = t & 3;
         const uint64_t lo4 = (run8(ql[2 * h + (g & 1)]) >> (4 * (g >> 1))) & 0x0F0F0F0F0F0F0F0Full;
@@ -148,12 +169,10 @@ struct MPiece<6> {
         // v - 32 per byte without borrows between bytes
         return ((v | 0x8080808080808080ull) - 0x2020202020202020ull) ^ 0x8080808080808080ull;
     }
-    // int8 scale of 16-value sub-block s
-    __device__ __forceinline__ int scale(int s) const {
-        const v4u v = v4u{__builtin_amdgcn_alignbyte(sc.y, sc.x, sh), __builtin_amdgcn_alignbyte(sc.z, sc.y, sh),
-                          __builtin_amdgcn_alignbyte(sc.w, sc.z, sh), __builtin_amdgcn_alignbyte(tail, sc.w, sh)};
-        const uint32_t w = s < 4 ? v.x : s < 8 ? v.y : s < 12 ? v.z : v.w;
-        return static_cast<int8_t>((w >> (8 * (s & 3))) & 0xFF);
+    // the 16 int8 scales as four words
+    __device__ __forceinline__ v4u scale_words() const {
+        return v4u{__builtin_amdgcn_alignbyte(sc.y, sc.x, sh), __builtin_amdgcn_alignbyte(sc.z, sc.y, sh),
+                   __builtin_amdgcn_alignbyte(sc.w, sc.z, sh), __builtin_amdgcn_alignbyte(tail, sc.w, sh)};
     }
     __device__ __forceinline__ void scales(float& d, float& dmin) const {
         d = f16_bits_to_f32(static_cast<uint16_t>(tail >> 16));
@@ -161,35 +180,25 @@ struct MPiece<6> {
     }
 };
 
-// Sums of v over lanes l and l ^ 16, and over l and l ^ 32: gfx950's row swaps
-// (v_permlane16_swap / v_permlane32_swap exchange the odd 16-lane rows of one
-// operand with the even rows of the other; with both operands v, the two
-// results hold v of the lane and of its partner).
-__device__ __forceinline__ int sum_xor16(int v) {
-    const auto r = __builtin_amdgcn_permlane16_swap(v, v, false, false);
-    return static_cast<int>(r[0]) + static_cast<int>(r[1]);
-}
-__device__ __forceinline__ int sum_xor32(int v) {
-    const auto r = __builtin_amdgcn_permlane32_swap(v, v, false, false);
-    return static_cast<int>(r[0]) + static_cast<int>(r[1]);
-}
-
-template <int KIND, int MT, bool FUSED, int D, int QP>
-__global__ __launch_bounds__(kMfmaWaves * 64) void gemv_mfma_kernel(const MfmaArgs p) {
-    constexpr int W = kMfmaWaves;
+template <int KIND, int MT, bool FUSED, int W, bool AREG, int D>
+__global__ __launch_bounds__(W * 64) void gemv_mfma_kernel(const MfmaArgs p) {
     constexpr int BB = block_bytes(KIND);
     constexpr int SPLIT = 16 / MT;  // sub-block slots per accumulator
+    constexpr int NR = MT / 4;      // activation rows per lane
+    constexpr int NSUB = KIND == 4 ? 8 : 16;
+    constexpr int GROUPS = NSUB / SPLIT;
+    constexpr int PER_GROUP = KIND == 4 ? SPLIT : SPLIT / 2;  // instructions per group
+    static_assert(GROUPS * PER_GROUP == 8, "eight instructions per block");
     extern __shared__ __align__(16) uint8_t smem[];
-    __shared__ int q8_ready;
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int nb = p.nb, m = p.m;
-    const Q8Lds a = q8_lds(smem, MT, nb);
-    // f32 partial sums of a tile: [buffer][wave][lane][e], after the activations
-    float* part = reinterpret_cast<float*>(smem + ((MT * nb * kGemvLdsPerBlock + 15) & ~15));
+    const int nb = p.nb, m = p.m, iters = p.iters;
+    const ActLds<MT> act{smem, nb};
+    // f32 partial sums of a tile: [buffer][wave][lane][NR], after the activations
+    float* part = reinterpret_cast<float*>(smem + ((nb * MT * kPerRowBlock + 15) & ~15));
 
     const int n = lane & 15, q = lane >> 4;  // B column (weight row in the tile), K slot group
-    const int iters = (nb + W - 1) / W;       // blocks per wave and tile
+    const int ra = lane & 15, ma = ra / SPLIT, sa = ra % SPLIT;  // this lane's A row: activation row, slot
 
     // Items: (tile t = blockIdx.x + k * gridDim.x, iteration it < iters), walked
     // with counters. Loads past the last item re-read the last tile's first
@@ -214,40 +223,104 @@ __global__ __launch_bounds__(kMfmaWaves * 64) void gemv_mfma_kernel(const MfmaAr
         k.load(reinterpret_cast<gbytes>(reinterpret_cast<uint64_t>(w)) + static_cast<int64_t>(row) * (nb * BB) + b * BB, q);
     };
 
-    const int quant_waves = FUSED ? min(W, (m * nb + 3) / 4) : 0;
-    const bool quant_wave = wave < quant_waves;
-    XPre<W * 64, QP> xpre;
+    // The activation blocks this wave owns: block wave + W * it (it < iters)
+    // of rows mi < m, four (block, row) items per pass of 16 lanes each, so
+    // QP = MT / 4 passes per block index; lane group qslot takes row 4 i + qslot
+    // in pass i.
+    constexpr int QP = MT / 4;
+    const int qslot = lane >> 4;
+    float4 xf[FUSED ? QP : 1][4];
+    auto x_block = [&](int it, int i) { return min(4 * i + qslot, m - 1) * nb + min(wave + W * it, nb - 1); };
     if constexpr (FUSED) {
-        if (quant_wave) xpre.issue(p.x, p.ldx, m, nb);
+        // the first block index's activations first, so their waits never include the weight loads
+#pragma unroll
+        for (int i = 0; i < QP; ++i) load_x16(p.x, p.ldx, nb, x_block(0, i), xf[i]);
     }
+    // the first weight block before the quantisation, the rest of the ring after
+    // it: each load instruction issued ahead of the quantisation delays it
     MPiece<KIND> buf[D];
     Pos lq{static_cast<int>(blockIdx.x), 0};  // next item to load
+    load(lq, buf[0]);
+    advance(lq);
+    if constexpr (FUSED) {
+        for (int it = 0; it < iters; ++it) {
+            const int b = wave + W * it;
 #pragma unroll
-    for (int j = 0; j < D; ++j) {
+            for (int i = 0; i < QP; ++i) {
+                float4 cur[4] = {xf[i][0], xf[i][1], xf[i][2], xf[i][3]};
+                if (it + 1 < iters) load_x16(p.x, p.ldx, nb, x_block(it + 1, i), xf[i]);  // next block index
+                const int mi = 4 * i + qslot;
+                if (mi < m && b < nb)
+                    quantize_block(cur, act.quants(b, mi), reinterpret_cast<int16_t*>(act.bsums(b, mi)), act.d(b, mi));
+            }
+        }
+    } else {
+        // copy this wave's Q8_K blocks (292 bytes: f32 d, 256 quants, 16 int16 bsums)
+        for (int w = lane; w < iters * MT * (kQ8KBytes / 4); w += 64) {
+            const int j = w / (kQ8KBytes / 4), wi = w - j * (kQ8KBytes / 4);
+            const int mi = j % MT, b = wave + W * (j / MT);
+            if (b >= nb || mi >= m) continue;
+            const uint32_t v = *reinterpret_cast<const uint32_t*>(p.q8k + mi * p.ldx + b * kQ8KBytes + 4 * wi);
+            if (wi == 0) *act.d(b, mi) = __uint_as_float(v);
+            else if (wi <= 64) reinterpret_cast<uint32_t*>(act.quants(b, mi))[wi - 1] = v;
+            else act.bsums(b, mi)[wi - 65] = v;
+        }
+    }
+#pragma unroll
+    for (int j = 1; j < D; ++j) {
         load(lq, buf[j]);
         advance(lq);
     }
-    if constexpr (FUSED) {
-        if (threadIdx.x == 0) q8_ready = 0;
-        __syncthreads();
-        if (quant_wave) {
-            xpre.quantize(p.x, p.ldx, m, nb, a);
-            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
-            if (lane == 0) __hip_atomic_fetch_add(&q8_ready, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    // The wave's own LDS writes complete before its lanes read each other's
+    // bytes; a compiler barrier too, and no wait for the weight loads.
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+
+    // A operands of a block: instruction i of 8 (group i / PER_GROUP) gets this
+    // lane's 8 bytes of its activation row's sub-block for the lane's slot, or
+    // zeros when the lane's slot is not the one instruction i carries.
+    auto a_ops = [&](int b, uint64_t (&a)[8]) {
+        const uint8_t* qs = act.quants(b, ma);
+#pragma unroll
+        for (int gi = 0; gi < GROUPS; ++gi) {
+            if constexpr (KIND == 4) {
+                const uint64_t v = *reinterpret_cast<const uint64_t*>(qs + 32 * (gi * SPLIT + sa) + 8 * q);
+#pragma unroll
+                for (int t = 0; t < SPLIT; ++t) a[gi * SPLIT + t] = sa == t ? v : 0;
+            } else {
+                const uint64_t v = *reinterpret_cast<const uint64_t*>(qs + 16 * (gi * SPLIT + sa) + 8 * (q & 1));
+                const bool half = (q >> 1) == (sa & 1);
+#pragma unroll
+                for (int u = 0; u < PER_GROUP; ++u) a[gi * PER_GROUP + u] = half && (sa >> 1) == u ? v : 0;
+            }
         }
-        for (int spin = 0; spin < (1 << 24); ++spin) {
-            if (__hip_atomic_load(&q8_ready, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) >= quant_waves) break;
-            __builtin_amdgcn_s_sleep(1);
+    };
+    // bsums (as int16 pairs) and scales of the lane's activation rows
+    auto row_data = [&](int b, uint32_t (&bs)[NR][8], float (&da)[NR]) {
+#pragma unroll
+        for (int lr = 0; lr < NR; ++lr) {
+            const int mo = NR * q + lr;
+            if constexpr (KIND == 4) {
+                const uint4* src = reinterpret_cast<const uint4*>(act.bsums(b, mo));
+                const uint4 v0 = src[0], v1 = src[1];
+                bs[lr][0] = v0.x; bs[lr][1] = v0.y; bs[lr][2] = v0.z; bs[lr][3] = v0.w;
+                bs[lr][4] = v1.x; bs[lr][5] = v1.y; bs[lr][6] = v1.z; bs[lr][7] = v1.w;
+            }
+            da[lr] = *act.d(b, mo);
         }
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
-    } else {
-        stage_q8k<W * 64>(p.q8k, p.ldx, m, nb, a);
-        __syncthreads();
+    };
+
+    uint64_t areg[AREG ? 8 : 1];
+    uint32_t bsreg[AREG ? NR : 1][8];
+    float dareg[AREG ? NR : 1];
+    if constexpr (AREG) {  // one block per wave: its operands stay in registers
+        const int b = min(wave, nb - 1);
+        a_ops(b, areg);
+        row_data(b, bsreg, dareg);
     }
 
-    // A operand row of this lane: sub-block slot sa of a group, activation row ma
-    const int ra = lane & 15, sa = ra / MT, ma = ra % MT;
-    float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    float acc[NR];
+#pragma unroll
+    for (int lr = 0; lr < NR; ++lr) acc[lr] = 0.0f;
     int tile_iter = 0;
     Pos cq{static_cast<int>(blockIdx.x), 0};  // item being computed
     while (cq.t < p.tiles) {
@@ -259,99 +332,99 @@ __global__ __launch_bounds__(kMfmaWaves * 64) void gemv_mfma_kernel(const MfmaAr
                 const bool have = b < nb;  // uniform; a missing block is computed on block nb-1 and dropped
                 const int bk = min(b, nb - 1);
                 const MPiece<KIND>& k = buf[j];
-                int is[4] = {0, 0, 0, 0}, ms[4] = {0, 0, 0, 0};
-                if constexpr (KIND == 4) {
-                    // 8 sub-blocks of 32: SPLIT per accumulator, one per instruction
+                uint64_t alocal[AREG ? 1 : 8];
+                uint32_t bslocal[AREG ? 1 : NR][8];
+                float dalocal[AREG ? 1 : NR];
+                if constexpr (!AREG) {
+                    a_ops(bk, alocal);
+                    row_data(bk, bslocal, dalocal);
+                }
+                const uint64_t* a = AREG ? areg : alocal;
+                int is[NR];
 #pragma unroll
-                    for (int gi = 0; gi < 8 / SPLIT; ++gi) {
-                        // this lane's activation bytes for its A row (rows >= m of the LDS area are
-                        // not written: read, then replaced by zeros)
-                        uint64_t xa = *reinterpret_cast<const uint64_t*>(a.quants(ma * nb + bk) + 32 * (gi * SPLIT + sa) + 8 * q);
-                        xa = ma < m ? xa : 0;
+                for (int lr = 0; lr < NR; ++lr) is[lr] = 0;
+                if constexpr (KIND == 4) {
+                    uint32_t sc_lo, sc_hi, mn_lo, mn_hi;
+                    k.packed(sc_lo, sc_hi, mn_lo, mn_hi);
+#pragma unroll
+                    for (int gi = 0; gi < GROUPS; ++gi) {
                         v4i dacc = {0, 0, 0, 0};
 #pragma unroll
-                        for (int t = 0; t < SPLIT; ++t) {
-                            const int s = gi * SPLIT + t;  // sub-block
-                            const uint64_t wq = (k.qp[s >> 1] >> (4 * (s & 1))) & 0x0F0F0F0F0F0F0F0Full;
-                            const uint64_t av = sa == t ? xa : 0;
-                            dacc = __builtin_amdgcn_mfma_i32_16x16x32_i8(static_cast<long>(av), static_cast<long>(wq),
+                        for (int t = 0; t < SPLIT; ++t)
+                            dacc = __builtin_amdgcn_mfma_i32_16x16x32_i8(static_cast<long>(a[gi * SPLIT + t]),
+                                                                         static_cast<long>(k.values(gi * SPLIT + t)),
                                                                          dacc, 0, 0, 0);
-                        }
-                        // D row 4q + e = (sub-block slot so, activation row mo)
 #pragma unroll
                         for (int e = 0; e < 4; ++e) {
-                            const int r = 4 * q + e, so = r / MT, mo = r % MT;
-                            const int s = gi * SPLIT + so;
-                            int sc, mn;
-                            q4_scale_min(k.h.y, k.h.z, k.h.w, s >= 4, s & 3, sc, mn);
-                            is[e] += sc * dacc[e];
-                            const uint32_t bp = *reinterpret_cast<const uint32_t*>(a.bsums(mo * nb + bk) + 2 * s);
-                            const int bsum = static_cast<int16_t>(bp & 0xFFFF) + static_cast<int16_t>(bp >> 16);
-                            ms[e] += mn * (mo < m ? bsum : 0);
+                            const int s = gi * SPLIT + e % SPLIT;  // sub-block of D value e
+                            const int sc = static_cast<int>(((s < 4 ? sc_lo : sc_hi) >> (8 * (s & 3))) & 0xFF);
+                            is[e / SPLIT] += __mul24(sc, dacc[e]);
                         }
+                    }
+                    // mins: sum_s mn_s * (bsums 2s + 2s+1) by int16 dot products
+                    int ms[NR];
+#pragma unroll
+                    for (int lr = 0; lr < NR; ++lr) {
+                        const uint32_t(&bsl)[8] = AREG ? bsreg[lr] : bslocal[lr];
+                        int acc_ms = 0;
+#pragma unroll
+                        for (int s = 0; s < 8; ++s) {
+                            const uint32_t w = s < 4 ? mn_lo : mn_hi;
+                            const uint32_t sel = 0x0C000C00u | (0x00010001u * static_cast<uint32_t>(s & 3));
+                            const uint32_t mn2 = __builtin_amdgcn_perm(0u, w, sel);  // (mn_s, mn_s) as int16
+                            acc_ms = __builtin_amdgcn_sdot2(__builtin_bit_cast(v2s, bsl[s]), __builtin_bit_cast(v2s, mn2),
+                                                            acc_ms, false);
+                        }
+                        ms[lr] = acc_ms;
+                    }
+                    float dw, dmw;
+                    k.scales(dw, dmw);
+#pragma unroll
+                    for (int lr = 0; lr < NR; ++lr) {
+                        const float da = AREG ? dareg[lr] : dalocal[lr];
+                        const float term = (dw * da) * static_cast<float>(is[lr]) - (dmw * da) * static_cast<float>(ms[lr]);
+                        acc[lr] += have ? term : 0.0f;
                     }
                 } else {
-                    // 16 sub-blocks of 16: an instruction covers two (K slots 0-15 and 16-31,
-                    // lane groups q >> 1 = 0 and 1), so SPLIT / 2 instructions per accumulator;
-                    // slot sa of the A rows holds sub-block gi * SPLIT + sa in K half sa & 1
-                    const bool my_half = (q >> 1) == (sa & 1);
+                    const v4u scw = k.scale_words();
 #pragma unroll
-                    for (int gi = 0; gi < 16 / SPLIT; ++gi) {
-                        uint64_t xa = *reinterpret_cast<const uint64_t*>(a.quants(ma * nb + bk) + 16 * (gi * SPLIT + sa) + 8 * (q & 1));
-                        xa = ma < m && my_half ? xa : 0;
+                    for (int gi = 0; gi < GROUPS; ++gi) {
                         v4i dacc = {0, 0, 0, 0};
 #pragma unroll
-                        for (int u = 0; u < SPLIT / 2; ++u) {
-                            const uint64_t wq = k.values(gi * SPLIT / 2 + u);
-                            const uint64_t av = (sa >> 1) == u ? xa : 0;
-                            dacc = __builtin_amdgcn_mfma_i32_16x16x32_i8(static_cast<long>(av), static_cast<long>(wq),
+                        for (int u = 0; u < PER_GROUP; ++u)
+                            dacc = __builtin_amdgcn_mfma_i32_16x16x32_i8(static_cast<long>(a[gi * PER_GROUP + u]),
+                                                                         static_cast<long>(k.values(gi * PER_GROUP + u)),
                                                                          dacc, 0, 0, 0);
-                        }
 #pragma unroll
                         for (int e = 0; e < 4; ++e) {
-                            const int so = (4 * q + e) / MT;
-                            is[e] += k.scale(gi * SPLIT + so) * dacc[e];
+                            const int s = gi * SPLIT + e % SPLIT;
+                            const uint32_t w = s < 4 ? scw.x : s < 8 ? scw.y : s < 12 ? scw.z : scw.w;
+                            const int sc = static_cast<int8_t>((w >> (8 * (s & 3))) & 0xFF);
+                            is[e / SPLIT] += __mul24(sc, dacc[e]);
                         }
                     }
-                }
-                // add the sub-block slots holding the same activation row
-                if constexpr (MT == 2) {  // rows 4q + e: slot 2q + e/2, row e%2
+                    float dw, dmw;
+                    k.scales(dw, dmw);
 #pragma unroll
-                    for (int e = 0; e < 2; ++e) { is[e] += is[e + 2]; ms[e] += ms[e + 2]; }
-                }
-                constexpr int NE = MT == 2 ? 2 : 4;
-#pragma unroll
-                for (int e = 0; e < NE; ++e) {
-                    if constexpr (MT <= 4) {
-                        is[e] = sum_xor16(is[e]);
-                        if constexpr (KIND == 4) ms[e] = sum_xor16(ms[e]);
+                    for (int lr = 0; lr < NR; ++lr) {
+                        const float da = AREG ? dareg[lr] : dalocal[lr];
+                        acc[lr] += have ? (dw * da) * static_cast<float>(is[lr]) : 0.0f;
                     }
-                    if constexpr (MT <= 8) {
-                        is[e] = sum_xor32(is[e]);
-                        if constexpr (KIND == 4) ms[e] = sum_xor32(ms[e]);
-                    }
-                }
-                float dw, dmw;
-                k.scales(dw, dmw);
-#pragma unroll
-                for (int e = 0; e < NE; ++e) {
-                    const int mo = (4 * q + e) % MT;
-                    const float da = a.d[mo * nb + bk];
-                    float term = (dw * da) * static_cast<float>(is[e]);
-                    if constexpr (KIND == 4) term = term - (dmw * da) * static_cast<float>(ms[e]);
-                    acc[e] += have ? term : 0.0f;
                 }
                 load(lq, buf[j]);
                 advance(lq);
                 if (it == iters - 1) {
-                    // tile done: partial sums to LDS, then wave 0 adds them in wave order
-                    float* pb = part + (tile_iter & 1) * (W * 64 * 4);
-                    *reinterpret_cast<float4*>(pb + (wave * 64 + lane) * 4) = make_float4(acc[0], acc[1], acc[2], acc[3]);
-                    acc[0] = acc[1] = acc[2] = acc[3] = 0.0f;
+                    // tile done: partial sums to LDS, then one wave adds them in wave order
+                    float* pb = part + (tile_iter & 1) * (W * 64 * NR);
+                    if constexpr (NR == 1) pb[wave * 64 + lane] = acc[0];
+                    else if constexpr (NR == 2) *reinterpret_cast<float2*>(pb + (wave * 64 + lane) * 2) = make_float2(acc[0], acc[1]);
+                    else *reinterpret_cast<float4*>(pb + (wave * 64 + lane) * 4) = make_float4(acc[0], acc[1], acc[2], acc[3]);
+#pragma unroll
+                    for (int lr = 0; lr < NR; ++lr) acc[lr] = 0.0f;
                     // the LDS writes complete, then the barrier; a compiler memory
                     // barrier too, and no wait for the weight loads in flight
                     asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-                    if (wave == 0) {
+                    if (wave == (tile_iter & (W - 1))) {
                         const int t = cq.t;
                         const bool c1 = t >= p.mb[0].tile_end, c2 = t >= p.mb[1].tile_end, c3 = t >= p.mb[2].tile_end;
                         float* out = c3 ? p.mb[3].out : c2 ? p.mb[2].out : c1 ? p.mb[1].out : p.mb[0].out;
@@ -359,17 +432,14 @@ __global__ __launch_bounds__(kMfmaWaves * 64) void gemv_mfma_kernel(const MfmaAr
                         const int rows = c3 ? p.mb[3].rows : c2 ? p.mb[2].rows : c1 ? p.mb[1].rows : p.mb[0].rows;
                         const int t0 = c3 ? p.mb[2].tile_end : c2 ? p.mb[1].tile_end : c1 ? p.mb[0].tile_end : 0;
                         const int row = (t - t0) * kTileRows + n;
-                        // activation row mo is held by lane 16 (mo / 4) + n, element mo % 4
 #pragma unroll
-                        for (int k4 = 0; k4 < (MT + 3) / 4; ++k4) {
-                            const int mo = q + 4 * k4;
-                            if (mo < m && row < rows) {
-                                const int src = 16 * (mo >> 2) + n, e = mo & 3;
-                                float r = pb[src * 4 + e];
+                        for (int lr = 0; lr < NR; ++lr) {
+                            float r = pb[lane * NR + lr];
 #pragma unroll
-                                for (int g = 1; g < W; ++g) r += pb[(g * 64 + src) * 4 + e];
+                            for (int g = 1; g < W; ++g) r += pb[(g * 64 + lane) * NR + lr];
+                            const int mo = NR * q + lr;
+                            if (mo < m && row < rows)
                                 reinterpret_cast<gfloats>(reinterpret_cast<uint64_t>(out))[mo * ldo + row] = r;
-                            }
                         }
                     }
                     ++tile_iter;
@@ -380,42 +450,58 @@ __global__ __launch_bounds__(kMfmaWaves * 64) void gemv_mfma_kernel(const MfmaAr
     }
 }
 
-// One block of loads in flight per wave: deeper rings measured slower in
-// every shape (TinyLlama gate+up at 4 rows 8.95 -> 8.40 us, Llama-3-8B
-// gate+up at 4 rows 28.0 -> 26.7 us, with one instead of up to four).
-template <int KIND, int MT, bool FUSED, int QP>
-void launch_d(const MfmaArgs& p, dim3 grid, size_t lds, hipStream_t stream) {
-    gemv_mfma_kernel<KIND, MT, FUSED, 1, QP><<<grid, dim3(kMfmaWaves * 64), lds, stream>>>(p);
+template <int KIND, int MT, bool FUSED, int W, bool AREG>
+void launch_d(const MfmaArgs& p, int depth, dim3 grid, size_t lds, hipStream_t stream) {
+    if (depth >= 4) gemv_mfma_kernel<KIND, MT, FUSED, W, AREG, 4><<<grid, dim3(W * 64), lds, stream>>>(p);
+    else if (depth >= 2) gemv_mfma_kernel<KIND, MT, FUSED, W, AREG, 2><<<grid, dim3(W * 64), lds, stream>>>(p);
+    else gemv_mfma_kernel<KIND, MT, FUSED, W, AREG, 1><<<grid, dim3(W * 64), lds, stream>>>(p);
+}
+
+template <int KIND, int MT, bool FUSED, int W>
+void launch_w(const MfmaArgs& p, int depth, dim3 grid, size_t lds, hipStream_t stream) {
+    if (p.iters == 1) launch_d<KIND, MT, FUSED, W, true>(p, depth, grid, lds, stream);
+    else launch_d<KIND, MT, FUSED, W, false>(p, depth, grid, lds, stream);
 }
 
 template <int KIND, int MT, bool FUSED>
-void launch_mt(const MfmaArgs& p, int passes, dim3 grid, size_t lds, hipStream_t stream) {
-    if constexpr (FUSED) {
-        if (passes > 1) return launch_d<KIND, MT, FUSED, 4>(p, grid, lds, stream);
-    }
-    launch_d<KIND, MT, FUSED, 1>(p, grid, lds, stream);
+void launch_mt(const MfmaArgs& p, int w, int depth, dim3 grid, size_t lds, hipStream_t stream) {
+    if (w == 4) launch_w<KIND, MT, FUSED, 4>(p, depth, grid, lds, stream);
+    else if (MT == 4 && w == 16) launch_w<KIND, MT, FUSED, MT == 4 ? 16 : 8>(p, depth, grid, lds, stream);
+    else launch_w<KIND, MT, FUSED, 8>(p, depth, grid, lds, stream);
 }
 
-template <int KIND>
-void launch_kind(bool fused, int mt, const MfmaArgs& ka, int passes, dim3 grid, size_t lds,
-                 hipStream_t stream) {
-    if (fused) {
-        if (mt == 2) launch_mt<KIND, 2, true>(ka, passes, grid, lds, stream);
-        else if (mt == 4) launch_mt<KIND, 4, true>(ka, passes, grid, lds, stream);
-        else launch_mt<KIND, 8, true>(ka, passes, grid, lds, stream);
-    } else {
-        if (mt == 2) launch_mt<KIND, 2, false>(ka, passes, grid, lds, stream);
-        else if (mt == 4) launch_mt<KIND, 4, false>(ka, passes, grid, lds, stream);
-        else launch_mt<KIND, 8, false>(ka, passes, grid, lds, stream);
-    }
+template <int KIND, bool FUSED>
+void launch_kind(int mt, const MfmaArgs& p, int w, int depth, dim3 grid, size_t lds, hipStream_t stream) {
+    if (mt == 4) launch_mt<KIND, 4, FUSED>(p, w, depth, grid, lds, stream);
+    else if (mt == 8) launch_mt<KIND, 8, FUSED>(p, w, depth, grid, lds, stream);
+    else if constexpr (KIND == 4) launch_mt<KIND, 16, FUSED>(p, w, depth, grid, lds, stream);
 }
 
 }  // namespace
 
-// Q4_K or Q6_K, 2 <= p.m <= 8.
+// LDS bytes of a launch: the activation blocks of mt rows and the double-buffered
+// partial sums of w waves.
+size_t gemv_mfma_lds(int mt, int nb, int w) {
+    return ((static_cast<size_t>(nb) * mt * kPerRowBlock + 15) & ~size_t{15}) + 2 * static_cast<size_t>(w) * 64 * (mt / 4) * 4;
+}
+
+// Activation rows per launch of the matrix-core kernel for rows of nb blocks:
+// the largest register tile (16 for Q4_K, 8 for Q6_K, then 4) whose LDS fits,
+// or 0 when none does.
+int gemv_mfma_rows(int kind, int nb) {
+    for (int mt : {16, 8, 4}) {
+        if (kind == 6 && mt == 16) continue;
+        if (gemv_mfma_lds(mt, nb, 8) <= static_cast<size_t>(kLdsMax)) return mt;
+    }
+    return 0;
+}
+
+// Q4_K or Q6_K, 2 <= p.m <= gemv_mfma_rows(kind, p.nb).
 int launch_gemv_mfma(int kind, bool fused, GemvParams& p, hipStream_t stream) {
-    if (p.m < 2 || p.m > 8 || (kind != 4 && kind != 6)) return kStatusInvalid;
-    const int mt = p.m <= 2 ? 2 : p.m <= 4 ? 4 : 8;
+    if ((kind != 4 && kind != 6) || p.m < 2 || p.m > gemv_mfma_rows(kind, p.nb)) return kStatusInvalid;
+    const int mt = p.m <= 4 ? 4 : p.m <= 8 ? 8 : 16;
+    // eight waves (eight block slots per tile) unless the rows are shorter
+    const int w = p.nb < 8 ? 4 : 8;
     MfmaArgs ka{};
     int tiles = 0;
     for (int i = 0; i < p.count; ++i) {
@@ -432,15 +518,21 @@ int launch_gemv_mfma(int kind, bool fused, GemvParams& p, hipStream_t stream) {
     ka.m = p.m;
     ka.nb = p.nb;
     ka.tiles = tiles;
+    ka.iters = (p.nb + w - 1) / w;
     // one workgroup per CU at most; each walks its tiles
     const int cus = device_cu_count();
     const int wgs = std::min(tiles, cus);
-    const int passes = (p.m * p.nb + kMfmaWaves * 4 - 1) / (kMfmaWaves * 4);
-    const size_t lds = ((static_cast<size_t>(mt) * p.nb * kGemvLdsPerBlock + 15) & ~size_t{15}) +
-                       2 * kMfmaWaves * 64 * 4 * sizeof(float);
+    const int per_wg = (tiles + wgs - 1) / wgs;
+    const int depth = per_wg * ka.iters > 1 ? 2 : 1;
+    const size_t lds = gemv_mfma_lds(mt, p.nb, w);
     const dim3 grid(static_cast<unsigned>(wgs));
-    if (kind == 4) launch_kind<4>(fused, mt, ka, passes, grid, lds, stream);
-    else launch_kind<6>(fused, mt, ka, passes, grid, lds, stream);
+    if (kind == 4) {
+        if (fused) launch_kind<4, true>(mt, ka, w, depth, grid, lds, stream);
+        else launch_kind<4, false>(mt, ka, w, depth, grid, lds, stream);
+    } else {
+        if (fused) launch_kind<6, true>(mt, ka, w, depth, grid, lds, stream);
+        else launch_kind<6, false>(mt, ka, w, depth, grid, lds, stream);
+    }
     return hipGetLastError() == hipSuccess ? kStatusOk : kStatusExec;
 }
 
