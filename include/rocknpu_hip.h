@@ -60,9 +60,10 @@ int rocknpu_hip_gemm_w8a8(const int8_t * a8, const float * a_scales, const int8_
 int rocknpu_hip_gemm_route(size_t m, size_t n, size_t k_pad, int cus, int * bm, int * bn, int * stages);
 
 /* The launch shape rocknpu_hip_gemv_q_f32 (fused != 0) or rocknpu_hip_gemv_q8_k
- * (fused == 0) takes for `count` projections of n[i] rows, K = k and m <= 8
- * activation rows (larger m runs in launches of 8) on `cus` compute units
- * (cus <= 0: the current device's): *mfma = 1 for the matrix-core kernel,
+ * (fused == 0) takes for `count` projections of n[i] rows, K = k and m
+ * activation rows on `cus` compute units (cus <= 0: the current device's), for
+ * its first launch (m beyond one launch's rows, up to 16 on the matrix-core
+ * Q4_K kernel and 8 otherwise, runs in several): *mfma = 1 for the matrix-core kernel,
  * else the lane-per-block kernel with *lanes lanes per super-block and *waves
  * waves per workgroup. Host code only; no GPU is needed when cus > 0. No
  * counterpart in the reference, whose decode GEMV runs on the CPU. */
@@ -95,6 +96,25 @@ int rocknpu_hip_gemv_q_f32(uint32_t kind, size_t count, const uint8_t * const * 
                            const size_t * w_bytes, const size_t * n, size_t k, const float * x,
                            size_t ldx, size_t m, float * const * out, const size_t * ldo,
                            void * stream);
+
+/* Stall report of rocknpu_hip_gemv_q_f32. In the lane-per-block kernel
+ * (rocknpu_hip_gemv_shape: *mfma == 0) a workgroup's waves wait for the waves
+ * that quantise the activations with a bounded poll (about 2^24 sleeps). A
+ * wave whose poll runs out writes NaN for each of its outputs and sets a
+ * process-wide flag in pinned host memory. Call after synchronising the
+ * streams of the launches to check: returns 1 if a launch gave up since the
+ * last call, else 0, and clears the flag. The fused decode entry point of
+ * the C ABI (rocknpu_matmul_q_q8k_group_f32_f32) checks it after its own
+ * synchronisation and returns ROCKNPU_STATUS_EXECUTION_ERROR. The flag is
+ * shared by every stream and thread of the process. No counterpart in the
+ * reference, whose decode GEMV runs on the CPU. */
+int rocknpu_hip_gemv_take_stall(void);
+
+/* Test hook for the stall path: with spins > 0, later lane-per-block fused
+ * launches wait for one more quantising wave than exists and give up after
+ * `spins` polls (every wave then exits normally, outputs NaN, flag set);
+ * spins == 0 restores normal launches. Returns 0, or -1 for spins < 0. */
+int rocknpu_hip_gemv_test_stall(int spins);
 
 #ifdef __cplusplus
 }

@@ -798,6 +798,11 @@ int rocknpu_matmul_q_q8k_group_f32_f32(rocknpu_context* ctx, size_t count, const
                     ctx, "out"))
             return kExec;
     if (!hip_ok(hipStreamSynchronize(ctx->stream), ctx, "gemv")) return kExec;
+    // a fused launch whose wait for its quantising waves gave up wrote NaN
+    if (rocknpu_hip_gemv_take_stall()) {
+        if (ctx->trace) std::fprintf(stderr, "ROCKNPU DECODE ERROR gemv: activation quantisation wait gave up\n");
+        return kExec;
+    }
     record_decode(ctx, hit, t0);
     return kOk;
 }

@@ -28,8 +28,10 @@
 // busy); large launches use L = 1, which spends the fewest instructions per
 // block.
 #include "gemv_lds.h"
+#include "rocknpu_hip.h"
 
 #include <algorithm>
+#include <atomic>
 
 namespace rk {
 namespace {
@@ -281,6 +283,9 @@ struct GemvArgs {
     int nb;
     int log2g;
     int iters;
+    int* stall;       // fused: set to 1 (pinned host memory) by a wave whose wait gives up
+    int spin_limit;   // fused: polls of the wait for the quantising waves
+    int ready_extra;  // fused: arrivals waited for beyond the quantising waves (0; 1 tests the give-up)
 };
 
 // SUMS: also write every block's exact integer sums (p.isum / p.msum).
@@ -352,6 +357,7 @@ __global__ __launch_bounds__(W * 64) void gemv_kernel(const GemvArgs p) {
     // weight loads.
     const int quant_waves = FUSED ? min(W, (m * nb + 3) / 4) : 0;
     const bool quant_wave = wave < quant_waves;
+    bool stalled = false;  // the wait below gave up
     XPre<W * 64, QP> xpre;
     if constexpr (FUSED) {
         if (quant_wave) xpre.issue(p.x, p.ldx, m, nb);
@@ -373,12 +379,16 @@ __global__ __launch_bounds__(W * 64) void gemv_kernel(const GemvArgs p) {
         }
         // Every wave (owners too: each reads all blocks) waits for the count.
         // Bounded for safety only: the owners depend on nothing but their own
-        // activation loads, so the count arrives.
-        for (int spin = 0; spin < (1 << 24); ++spin) {
-            if (__hip_atomic_load(&q8_ready, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) >= quant_waves) break;
+        // activation loads, so the count arrives. A wave that gives up reports
+        // it (host-visible flag) and writes NaN for its outputs.
+        const int need = quant_waves + p.ready_extra;
+        for (int spin = 0; spin < p.spin_limit; ++spin) {
+            if (__hip_atomic_load(&q8_ready, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) >= need) break;
             __builtin_amdgcn_s_sleep(1);
         }
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+        stalled = __hip_atomic_load(&q8_ready, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) < need;
+        if (stalled && lane == 0) __hip_atomic_store(p.stall, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
     } else {
         stage_q8k<W * 64>(p.q8k, p.ldx, m, nb, a);
         __syncthreads();
@@ -428,7 +438,8 @@ __global__ __launch_bounds__(W * 64) void gemv_kernel(const GemvArgs p) {
 #pragma unroll
                 for (int mi = 0; mi < MT; ++mi) {
                     const float r = sum_bits(acc[mi], LOG2L, LOG2L + log2g);
-                    if (gl == 0 && pc == 0 && row < rows && mi < m) wg_out[mi * ldo + row] = r;
+                    if (gl == 0 && pc == 0 && row < rows && mi < m)
+                        wg_out[mi * ldo + row] = stalled ? __builtin_nanf("") : r;
                     acc[mi] = 0.0f;
                 }
             }
@@ -504,6 +515,23 @@ int slots_per_row_log2(int nb, int slots) {
     return lg;
 }
 
+// The stall flag of fused launches: one int of pinned host memory, allocated
+// by the first fused launch and kept until the process ends.
+std::atomic<int*> g_stall_flag{nullptr};
+std::atomic<int> g_test_stall_spins{0};
+
+int* stall_flag() {
+    static int* const flag = [] {
+        void* mem = nullptr;
+        if (hipHostMalloc(&mem, 64, hipHostMallocDefault) != hipSuccess) return static_cast<int*>(nullptr);
+        int* f = static_cast<int*>(mem);
+        __atomic_store_n(f, 0, __ATOMIC_SEQ_CST);
+        g_stall_flag.store(f);
+        return f;
+    }();
+    return flag;
+}
+
 template <int KIND, bool FUSED>
 int launch_kind(GemvParams& p, hipStream_t stream) {
     const bool sums = !FUSED && p.isum != nullptr;
@@ -549,6 +577,13 @@ int launch_kind(GemvParams& p, hipStream_t stream) {
     ka.nb = p.nb;
     ka.log2g = p.log2g;
     ka.iters = p.iters;
+    if constexpr (FUSED) {
+        ka.stall = stall_flag();
+        if (ka.stall == nullptr) return kStatusExec;
+        const int test_spins = g_test_stall_spins.load(std::memory_order_relaxed);
+        ka.spin_limit = test_spins > 0 ? test_spins : 1 << 24;
+        ka.ready_extra = test_spins > 0 ? 1 : 0;
+    }
     // Blocks in flight per lane: one Q6_K block, and Q4_K blocks for 16 per
     // CU and lane position (two with 8 waves, one with 16). More measured
     // slower in every shape (the memory pipeline of a CU is full with fewer):
@@ -651,3 +686,14 @@ int launch_gemv(int kind, bool fused, GemvParams& p, hipStream_t stream) {
 }
 
 }  // namespace rk
+
+extern "C" int rocknpu_hip_gemv_take_stall(void) {
+    int* f = rk::g_stall_flag.load();
+    return f != nullptr && __atomic_exchange_n(f, 0, __ATOMIC_SEQ_CST) != 0 ? 1 : 0;
+}
+
+extern "C" int rocknpu_hip_gemv_test_stall(int spins) {
+    if (spins < 0) return rk::kStatusInvalid;
+    rk::g_test_stall_spins.store(spins);
+    return rk::kStatusOk;
+}

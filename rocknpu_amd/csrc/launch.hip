@@ -42,6 +42,21 @@ constexpr size_t kMaxGrid = 0x7fffffff;
 // 16 KiB of partial sums; one workgroup runs per CU either way.
 constexpr size_t kGemvLdsBytes = 112 * 1024;
 
+// Rows of the next launch when `rem` activation rows are left: as many as the
+// matrix-core kernel holds when it takes them, else a power of two (the
+// lane-per-block kernel's register tile, at most 8) whose Q8_K blocks fit the
+// LDS that kernel stages them in.
+size_t gemv_rows_per_launch(uint32_t kind, size_t nb, size_t rem, int64_t rows, bool sums, int cus) {
+    const size_t mf = static_cast<size_t>(rk::gemv_mfma_rows(static_cast<int>(kind), static_cast<int>(nb)));
+    const size_t c = std::min(rem, mf);
+    if (!sums && c >= 3 &&
+        rk::gemv_uses_mfma(static_cast<int>(kind), static_cast<int>(c), static_cast<int>(nb), rows, cus))
+        return c;
+    size_t chunk = 8;
+    while (chunk > 1 && chunk * nb * rk::kGemvLdsPerBlock > kGemvLdsBytes) chunk >>= 1;
+    return std::min(rem, chunk);
+}
+
 }  // namespace
 
 extern "C" int rocknpu_hip_repack_w8(uint32_t kind, const uint8_t* blocks, size_t blocks_bytes, size_t k,
@@ -97,10 +112,12 @@ extern "C" int rocknpu_hip_gemm_route(size_t m, size_t n, size_t k_pad, int cus,
 
 extern "C" int rocknpu_hip_gemv_shape(uint32_t kind, size_t m, size_t k, const size_t* n, size_t count, int fused,
                                       int cus, int* mfma, int* lanes, int* waves) {
-    if ((kind != 4 && kind != 6) || !n || !mfma || !lanes || !waves || m == 0 || m > 16 || k == 0 ||
+    if ((kind != 4 && kind != 6) || !n || !mfma || !lanes || !waves || m == 0 || m > INT_MAX || k == 0 ||
         k % rk::kQK != 0 || count == 0 || count > rk::kGemvMaxMembers || k / rk::kQK > INT_MAX)
         return rk::kStatusInvalid;
     if (cus <= 0) cus = rk::device_cu_count();
+    const size_t nb = k / rk::kQK;
+    if (nb * rk::kGemvLdsPerBlock > kGemvLdsBytes) return rk::kStatusInvalid;
     int64_t rows[rk::kGemvMaxMembers] = {};
     int64_t total = 0;
     for (size_t i = 0; i < count; ++i) {
@@ -108,10 +125,10 @@ extern "C" int rocknpu_hip_gemv_shape(uint32_t kind, size_t m, size_t k, const s
         rows[i] = static_cast<int64_t>(n[i]);
         total += rows[i];
     }
-    *mfma = rk::gemv_uses_mfma(static_cast<int>(kind), static_cast<int>(m), static_cast<int>(k / rk::kQK), total, cus)
-                ? 1
-                : 0;
-    const rk::GemvLanes l = rk::gemv_lanes(fused != 0, false, static_cast<int>(m), static_cast<int>(k / rk::kQK), rows,
+    // the first launch's rows
+    const int rows0 = static_cast<int>(gemv_rows_per_launch(kind, nb, m, total, false, cus));
+    *mfma = rk::gemv_uses_mfma(static_cast<int>(kind), rows0, static_cast<int>(nb), total, cus) ? 1 : 0;
+    const rk::GemvLanes l = rk::gemv_lanes(fused != 0, false, rows0, static_cast<int>(nb), rows,
                                            static_cast<int>(count), cus);
     *lanes = *mfma ? 0 : l.lanes;
     *waves = *mfma ? 0 : l.waves;
@@ -127,21 +144,6 @@ extern "C" int rocknpu_hip_quantize_q8_k(const float* x, size_t m, size_t k, siz
                                     static_cast<int64_t>(ldx), q8k, static_cast<hipStream_t>(stream));
 }
 
-// Rows of the next launch when `rem` activation rows are left: as many as the
-// matrix-core kernel holds when it takes them, else a power of two (the
-// lane-per-block kernel's register tile, at most 8) whose Q8_K blocks fit the
-// LDS that kernel stages them in.
-size_t gemv_rows_per_launch(uint32_t kind, size_t nb, size_t rem, int64_t rows, bool sums) {
-    const int cus = rk::device_cu_count();
-    const size_t mf = static_cast<size_t>(rk::gemv_mfma_rows(static_cast<int>(kind), static_cast<int>(nb)));
-    const size_t c = std::min(rem, mf);
-    if (!sums && c >= 3 &&
-        rk::gemv_uses_mfma(static_cast<int>(kind), static_cast<int>(c), static_cast<int>(nb), rows, cus))
-        return c;
-    size_t chunk = 8;
-    while (chunk > 1 && chunk * nb * rk::kGemvLdsPerBlock > kGemvLdsBytes) chunk >>= 1;
-    return std::min(rem, chunk);
-}
 
 extern "C" int rocknpu_hip_gemv_q8_k(uint32_t kind, const uint8_t* w, size_t w_bytes, size_t k, size_t n,
                                      const uint8_t* q8k, size_t m, float* out, size_t ldo, int32_t* isum,
@@ -156,7 +158,7 @@ extern "C" int rocknpu_hip_gemv_q8_k(uint32_t kind, const uint8_t* w, size_t w_b
     if (nb * rk::kGemvLdsPerBlock > kGemvLdsBytes) return rk::kStatusInvalid;
     const hipStream_t s = static_cast<hipStream_t>(stream);
     for (size_t m0 = 0, chunk = 0; m0 < m; m0 += chunk) {
-        chunk = gemv_rows_per_launch(kind, nb, m - m0, static_cast<int64_t>(n), isum != nullptr);
+        chunk = gemv_rows_per_launch(kind, nb, m - m0, static_cast<int64_t>(n), isum != nullptr, rk::device_cu_count());
         rk::GemvParams p{};
         p.count = 1;
         p.w[0] = w;
@@ -194,7 +196,7 @@ extern "C" int rocknpu_hip_gemv_q_f32(uint32_t kind, size_t count, const uint8_t
     if (total > INT_MAX) return rk::kStatusInvalid;
     const hipStream_t s = static_cast<hipStream_t>(stream);
     for (size_t m0 = 0, chunk = 0; m0 < m; m0 += chunk) {
-        chunk = gemv_rows_per_launch(kind, nb, m - m0, static_cast<int64_t>(total), false);
+        chunk = gemv_rows_per_launch(kind, nb, m - m0, static_cast<int64_t>(total), false, rk::device_cu_count());
         rk::GemvParams p{};
         p.count = static_cast<int>(count);
         for (size_t i = 0; i < count; ++i) {

@@ -122,3 +122,16 @@ def gemv_q_f32(kind: int, weights, k: int, ns, x: torch.Tensor, outs=None):
     _check(_lib.load().rocknpu_hip_gemv_q_f32(kind, count, w_arr, b_arr, n_arr, k, _ptr(x), _ld(x), m,
                                               o_arr, l_arr, _stream()), "gemv_q_f32")
     return outs
+
+
+def gemv_take_stall() -> bool:
+    """Whether a fused lane-per-block GEMV launch gave up its wait for the
+    activation quantisation since the last call (call after synchronising);
+    clears the flag."""
+    return bool(_lib.load().rocknpu_hip_gemv_take_stall())
+
+
+def gemv_test_stall(spins: int) -> None:
+    """Test hook: spins > 0 makes later fused lane-per-block launches wait for
+    an arrival that never comes and give up after `spins` polls; 0 restores."""
+    _check(_lib.load().rocknpu_hip_gemv_test_stall(spins), "gemv_test_stall")

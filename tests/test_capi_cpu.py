@@ -92,3 +92,14 @@ def test_no_device_means_no_context():
     lib = _lib.load()
     assert lib.rocknpu_device_count() == 0
     assert not lib.rocknpu_context_create()
+
+
+def test_gemv_stall_report_host_side():
+    """The decode GEMV's stall report before any launch: the flag reads 0 (no
+    fused launch has allocated it), the test hook refuses a negative count and
+    accepts 0 (normal launches)."""
+    lib = _lib.load()
+    assert lib.rocknpu_hip_gemv_take_stall() == 0
+    assert lib.rocknpu_hip_gemv_test_stall(-1) == -1
+    assert lib.rocknpu_hip_gemv_test_stall(0) == 0
+    assert lib.rocknpu_hip_gemv_take_stall() == 0

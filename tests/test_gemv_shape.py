@@ -68,7 +68,7 @@ def test_bad_arguments():
     out = [ctypes.c_int() for _ in range(3)]
     ptrs = [ctypes.byref(o) for o in out]
     assert lib.rocknpu_hip_gemv_shape(5, 1, 2048, arr, 1, 1, CUS, *ptrs) == -1     # Q5_K has no GEMV
-    assert lib.rocknpu_hip_gemv_shape(4, 9, 2048, arr, 1, 1, CUS, *ptrs) == -1     # more than 8 rows
+    assert lib.rocknpu_hip_gemv_shape(4, 1, 256 * 1000, arr, 1, 1, CUS, *ptrs) == -1  # rows beyond the LDS
     assert lib.rocknpu_hip_gemv_shape(4, 1, 2000, arr, 1, 1, CUS, *ptrs) == -1     # K % 256 != 0
     assert lib.rocknpu_hip_gemv_shape(4, 1, 2048, arr, 5, 1, CUS, *ptrs) == -1     # more than 4 members
     assert lib.rocknpu_hip_gemv_shape(4, 1, 2048, None, 1, 1, CUS, *ptrs) == -1

@@ -317,3 +317,60 @@ def test_w8a8_rejects_k_beyond_exact_int32():
         s = c.decode_cache_stats()
         assert s.entries == 0 and s.misses == 0
     assert not out.any()
+
+
+def test_gemv_stall_gives_nan_and_execution_error():
+    """The fused lane-per-block decode GEMV waits for its workgroup's quantising
+    waves with a bounded poll. Forced from the host to give up (test hook: one
+    arrival more than the workgroup has, 8 polls; every wave still exits), each
+    output is NaN, the stall flag is set once, and the C ABI's fused decode entry
+    returns ROCKNPU_STATUS_EXECUTION_ERROR. With the hook off the same calls
+    match the oracle and leave the flag clear. A context of its own: the weight
+    caches are keyed by host address, which freed arrays of other tests reuse."""
+    import ctypes
+
+    import torch
+
+    from rocknpu_amd import _lib, hip
+    from rocknpu_amd.capi import STATUS_EXECUTION_ERROR
+
+    kind, ns, k, m = 4, (256, 512), 2048, 1
+    mf, lanes, waves = ctypes.c_int(), ctypes.c_int(), ctypes.c_int()
+    arr = (ctypes.c_size_t * 2)(*ns)
+    assert _lib.load().rocknpu_hip_gemv_shape(kind, m, k, arr, 2, 1, 0, ctypes.byref(mf), ctypes.byref(lanes),
+                                              ctypes.byref(waves)) == 0
+    assert mf.value == 0  # the lane-per-block kernel, the one with the wait
+    ws = [synth.kquant(kind, n, k, index=2300 + i) for i, n in enumerate(ns)]
+    x = synth.activations(m, k, index=2310)
+    dws = [torch.from_numpy(w).to("cuda") for w in ws]
+    dx = torch.from_numpy(x).to("cuda")
+    torch.cuda.synchronize()
+    assert not hip.gemv_take_stall()
+    ctx = Context()
+    print("stall hook on: launch layer", flush=True)
+    hip.gemv_test_stall(8)
+    try:
+        outs = hip.gemv_q_f32(kind, dws, k, ns, dx)
+        torch.cuda.synchronize()
+        assert all(np.isnan(o.cpu().numpy()).all() for o in outs)
+        assert hip.gemv_take_stall()
+        assert not hip.gemv_take_stall()  # taking clears it
+        print("stall hook on: C ABI", flush=True)
+        houts = [np.zeros((m, n), np.float32) for n in ns]
+        assert ctx.matmul_q_q8k_group(ws, [kind, kind], ns, x, houts, k) == STATUS_EXECUTION_ERROR
+        assert not hip.gemv_take_stall()
+    finally:
+        hip.gemv_test_stall(0)
+    print("stall hook off", flush=True)
+    houts = [np.zeros((m, n), np.float32) for n in ns]
+    assert ctx.matmul_q_q8k_group(ws, [kind, kind], ns, x, houts, k) == STATUS_OK
+    ctx.close()
+    outs = hip.gemv_q_f32(kind, dws, k, ns, dx)
+    torch.cuda.synchronize()
+    assert not hip.gemv_take_stall()
+    q8 = orc.quantize_q8_k(x)
+    for w, n, o, h in zip(ws, ns, outs, houts):
+        assert np.array_equal(_bits(o.cpu().numpy()), _bits(h))
+        ref = orc.gemv_q8_k(kind, w, k, n, q8, threads=8)
+        _, _, mag = orc.gemv_block_sums(kind, w, k, n, q8[0])
+        assert np.all(np.abs(h[0].astype(np.float64) - ref[0]) <= 1e-5 * mag)

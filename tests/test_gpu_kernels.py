@@ -310,6 +310,9 @@ def test_gemv_m_chunking():
     (4, (5632, 5632), 2048, 4), (6, (2048,), 5632, 1), (6, (2048,), 5632, 4), (4, (96, 160, 32, 64), 1024, 8),
     (6, (130, 70), 2048, 3), (4, (40,), 14336, 2), (4, (33,), 256, 11),
     (6, (300000,), 256, 1),  # grid capped: several prefetch rounds per wave
+    # Q4_K rows longer than one 8-block stage: LDS-staged weights at 4, 16 and 8 rows,
+    # then rows too long for the staged kernel's LDS (the unstaged matrix-core kernel)
+    (4, (1000, 3000), 4096, 4), (4, (700,), 3072, 13), (4, (256, 4100), 6144, 8), (4, (256, 4100), 14336, 8),
 ])
 def test_gemv_fused_grouped(kind, ns, k, m):
     """Fused Q8_K quant + grouped GEMV == separate quant + per-member GEMV, bit for bit,
