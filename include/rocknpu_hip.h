@@ -51,6 +51,19 @@ int rocknpu_hip_gemm_w8a8(const int8_t * a8, const float * a_scales, const int8_
                           const float * w_scales, size_t m, size_t n, size_t k_pad, float * out,
                           size_t ldo, int32_t * out_i32, void * stream);
 
+/* Kernels (b) + (c): the W8A8 prompt route on device buffers. A [m, lda] f32
+ * (first k columns) is quantised per token into an int8 workspace, then
+ * out[m, ldo] = (f32(A8 W8^T) * a_scale[m]) * w_scales[n] against the resident
+ * W8 [n, k_pad] (16-byte aligned, k_pad a multiple of 64, at most 133120).
+ * The library allocates the workspace (m * k_pad bytes + m scales) on
+ * `stream`, stream-ordered, and releases it behind the GEMM. Replaces the
+ * quantise / i32 GEMM / rescale sequence of execute_cached_w8a8_mtile_pool_padded
+ * (crates/rocknpu-capi/src/lib.rs:1776-1791, :1868-1884) without its weight
+ * cache. Results equal rocknpu_hip_quantize_a8 followed by rocknpu_hip_gemm_w8a8. */
+int rocknpu_hip_matmul_w8a8_f32(const float * a, size_t m, size_t k, size_t lda, const int8_t * w8,
+                                const float * w_scales, size_t n, size_t k_pad, float * out, size_t ldo,
+                                void * stream);
+
 /* The tile rocknpu_hip_gemm_w8a8 runs an M x N x k_pad product with on a GPU
  * of `cus` compute units (cus <= 0: the current device's): *bm x *bn tiles of
  * *stages 128-byte K stages, or *bm = 0 for the weight-streaming kernel of up

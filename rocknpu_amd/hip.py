@@ -86,6 +86,21 @@ def gemm_w8a8(a8: torch.Tensor, a_scales: torch.Tensor, w8: torch.Tensor, w_scal
     return out
 
 
+def matmul_w8a8_f32(a: torch.Tensor, w8: torch.Tensor, w_scales: torch.Tensor, k: int | None = None,
+                    out: torch.Tensor | None = None) -> torch.Tensor:
+    """Kernels (b) + (c) in one call: f32 activations a [m, >= k] quantised per
+    token into a library workspace, times the resident W8 [n, k_pad]."""
+    m = a.shape[0]
+    k = a.shape[1] if k is None else k
+    n, kp = w8.shape
+    assert w8.is_contiguous() and a.stride(1) == 1
+    if out is None:
+        out = torch.empty((m, n), dtype=torch.float32, device=a.device)
+    _check(_lib.load().rocknpu_hip_matmul_w8a8_f32(_ptr(a), m, k, _ld(a), _ptr(w8), _ptr(w_scales), n, kp,
+                                                   _ptr(out), _ld(out), _stream()), "matmul_w8a8_f32")
+    return out
+
+
 def quantize_q8_k(x: torch.Tensor, q8k: torch.Tensor | None = None) -> torch.Tensor:
     """f32 [m, k] -> Q8_K rows, uint8 [m, (k/256)*292]."""
     m, k = x.shape

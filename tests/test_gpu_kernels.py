@@ -216,6 +216,21 @@ def test_w8a8_pipeline_config0():
     assert np.array_equal(_bits(out.cpu().numpy()), _bits(ref))
 
 
+@pytest.mark.parametrize("kind,m,k,n,lda", [(4, 128, 2048, 5632, 2048), (6, 37, 5632, 300, 5640), (5, 1, 256, 64, 256)])
+def test_matmul_w8a8_f32_device_route(kind, m, k, n, lda):
+    """rocknpu_hip_matmul_w8a8_f32 (A8 quantisation into a library workspace + GEMM)
+    equals the reference W8A8 route bit for bit, including a strided activation
+    matrix and a padded K (5632 -> 5632, 256 -> 256 with 64-aligned k_pad)."""
+    print(f"matmul_w8a8_f32 kind={kind} m={m} k={k} n={n}", flush=True)
+    blocks = synth.kquant(kind, n, k, index=1200 + m)
+    a = synth.activations(m, lda, index=1201 + m)
+    w8, ws = hip.repack_w8(kind, _dev(blocks), k, n)
+    out = hip.matmul_w8a8_f32(_dev(a), w8, ws, k=k)
+    torch.cuda.synchronize()
+    ref = orc.matmul_q_w8a8(kind, blocks, np.ascontiguousarray(a[:, :k]), n, threads=8)
+    assert np.array_equal(_bits(out.cpu().numpy()), _bits(ref))
+
+
 # ---------------------------------------------------------------- kernel (d)
 @pytest.mark.parametrize("m,k", [(1, 256), (1, 2048), (4, 2048), (3, 5632), (8, 2048), (11, 1024)])
 def test_quantize_q8_k_bit_exact(m, k):
