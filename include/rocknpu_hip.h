@@ -64,6 +64,20 @@ int rocknpu_hip_matmul_w8a8_f32(const float * a, size_t m, size_t k, size_t lda,
                                 const float * w_scales, size_t n, size_t k_pad, float * out, size_t ldo,
                                 void * stream);
 
+/* rocknpu_hip_matmul_w8a8_f32 without allocating: no counterpart in the
+ * reference. For callers that cannot allocate device memory (code under HIP
+ * graph capture, tight serving loops, harnesses that forbid hipMalloc). The
+ * workspace is a fixed array in the library's device memory, one copy per GPU
+ * the library runs on, held until the process ends: at most 16384 rows and
+ * m * k_pad <= 32 MiB; beyond that the call returns
+ * ROCKNPU_STATUS_INVALID_ARGUMENT and prints the limit on stderr. Every call on
+ * one GPU uses that GPU's copy, so calls that overlap on one GPU (other
+ * streams, other threads) race. Same arguments and results as
+ * rocknpu_hip_matmul_w8a8_f32. */
+int rocknpu_hip_matmul_w8a8_f32_noalloc(const float * a, size_t m, size_t k, size_t lda, const int8_t * w8,
+                                        const float * w_scales, size_t n, size_t k_pad, float * out,
+                                        size_t ldo, void * stream);
+
 /* The tile rocknpu_hip_gemm_w8a8 runs an M x N x k_pad product with on a GPU
  * of `cus` compute units (cus <= 0: the current device's): *bm x *bn tiles of
  * *stages 128-byte K stages, or *bm = 0 for the weight-streaming kernel of up
