@@ -105,10 +105,27 @@ def quantize_symmetric_row(x: np.ndarray, neon: bool = False):
     return q, np.float32(s.value)
 
 
-def repack_w8(kind: int, blocks: np.ndarray, k: int, n: int):
+def repack_w8(kind: int, blocks: np.ndarray, k: int, n: int, threads: int = 1):
+    """W8 [n, k] + scales [n]. threads > 1 repacks row ranges concurrently
+    (rows are independent; the C call releases the GIL)."""
     w8 = np.empty((n, k), np.int8)
     sc = np.empty(n, np.float32)
-    if lib().or_repack_w8(kind, _p(blocks, _u8p), blocks.nbytes, k, n, _p(w8, _i8p), _p(sc, _f32p)) != 0:
+    flat = np.ascontiguousarray(blocks).view(np.uint8).reshape(-1)
+    row_bytes = (k // QK) * BLOCK_BYTES.get(kind, 0)
+
+    def one(r0, r1):
+        part = flat[r0 * row_bytes:r1 * row_bytes] if row_bytes else flat
+        return lib().or_repack_w8(kind, _p(part, _u8p), part.nbytes, k, r1 - r0, _p(w8[r0:r1], _i8p),
+                                  _p(sc[r0:r1], _f32p))
+
+    if threads <= 1 or n < 2 * threads or row_bytes == 0 or flat.nbytes != n * row_bytes:
+        rcs = [one(0, n)]
+    else:
+        from concurrent.futures import ThreadPoolExecutor
+        step = (n + threads - 1) // threads
+        with ThreadPoolExecutor(threads) as pool:
+            rcs = list(pool.map(lambda r0: one(r0, min(n, r0 + step)), range(0, n, step)))
+    if any(rc != 0 for rc in rcs):
         raise OracleError("repack_w8")
     return w8, sc
 
