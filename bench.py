@@ -8,10 +8,14 @@ is one such pass (22 distinct layers, 0.61 GB of weights, so the 256 MB
 last-level cache cannot hold it); the step is captured once in a HIP graph and
 replayed. value = algorithmic HBM bytes per step / step time.
 
-Extra fields: the W8A8 prefill GEMM (int8 TOPS on the 5632x2048 Q4_K weight
-at 128 tokens and on larger shapes, rotating >1 GiB of weights), TinyLlama
-prefill MUL_MAT tokens/s, the dominant kernel's roofline, and the CPU oracle
-timed on the host cores as a baseline.
+Extra fields: the dominant kernel's roofline (the 4-row Q4_K GEMV on the
+matrix cores) and the single-row kernel's beside it; the repack and A8
+quantisation rooflines; the W8A8 prefill GEMM (int8 TOPS on the 5632x2048 Q4_K
+weight at 128 tokens and on larger shapes, rotating >1 GiB of weights); the
+prefill MUL_MAT tokens/s of TinyLlama-1.1B (128, 512 tokens), Llama-3.2-1B
+(128, 512, 2048) and Llama-3-8B (4096), every layer and the output head on
+repacked Q4_K/Q6_K weights; large and batched decode GEMVs; and the CPU oracle
+timed on the host cores (all usable threads up to 16, and one) as a baseline.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--quick] [--no-cpu]
        python bench.py --profile {gemv-q4k,gemv-q4k-m4,gemm,gemm-512,gemm-128,copy}   (workload only, for rocprofv3 counter runs)
@@ -183,33 +187,152 @@ def w8a8_gemm(torch, hip, synth, m: int, n: int, k: int, reps: int, rotate_bytes
             "bound": "mfma" if bound_tops >= INT8_PEAK_TOPS else "hbm", "weight_copies": copies}
 
 
-def prefill_tok_s(torch, hip, synth, m: int, layers: int) -> dict:
-    """TinyLlama prefill MUL_MATs (QKV concat N=2560, O, gate+up N=11264, down
-    K=5632) over `layers` distinct layers of W8 weights, with the A8 quant of
-    each projection input, as tokens per second of the MUL_MAT work."""
+# layers, hidden, FFN, K/V rows (KV heads x head dim), vocab
+MODELS = {
+    "tinyllama_1.1b": (22, 2048, 5632, 256, 32000),
+    "llama3.2_1b": (16, 2048, 8192, 512, 128256),
+    "llama3_8b": (32, 4096, 14336, 1024, 128256),
+}
+
+
+class PrefillModel:
+    """Every prefill MUL_MAT of one model on device-resident W8, in the order and
+    grouping the routing runs them: per layer q/k/v as one GEMM over their
+    concatenated W8 (one A8 quantisation of the shared input), o, gate+up as
+    one GEMM, down; then the output head. Weights are seeded Q4_K (Q6_K for
+    ffn_down and the head) repacked on the GPU into distinct buffers per layer,
+    so a step streams every layer's weights from HBM."""
+
+    def __init__(self, torch, hip, synth, model: str, m_max: int):
+        self.torch, self.hip = torch, hip
+        layers, hidden, ffn, kv, vocab = MODELS[model]
+        dev = "cuda"
+        groups = (("qkv", hidden, ((4, hidden), (4, kv), (4, kv))), ("o", hidden, ((4, hidden),)),
+                  ("gateup", hidden, ((4, ffn), (4, ffn))), ("down", ffn, ((6, hidden),)))
+        # one set of seeded blocks per projection shape, repacked into every layer's buffers
+        blocks = {}
+        for gname, k, members in groups:
+            for j, (kind, n) in enumerate(members):
+                blocks[(gname, j)] = torch.from_numpy(synth.kquant(kind, n, k, index=60_000 + 8 * len(blocks))).to(dev)
+        head_rows = 8192  # seeded rows, tiled to the vocabulary
+        hb = synth.kquant(6, head_rows, hidden, index=61_000).reshape(head_rows, -1)
+        reps = (vocab + head_rows - 1) // head_rows
+        head_blocks = torch.from_numpy(np.ascontiguousarray(np.tile(hb, (reps, 1))[:vocab])).to(dev)
+        self.layers = []
+        self.weight_bytes = 0
+        for _ in range(layers):
+            lw = []
+            for gname, k, members in groups:
+                kp = hip.k_pad_of(k)
+                n_total = sum(n for _, n in members)
+                w8 = torch.empty((n_total, kp), dtype=torch.int8, device=dev)
+                sc = torch.empty(n_total, dtype=torch.float32, device=dev)
+                r0 = 0
+                for j, (kind, n) in enumerate(members):
+                    hip.repack_w8(kind, blocks[(gname, j)], k, n, w8=w8[r0:r0 + n], scales=sc[r0:r0 + n])
+                    r0 += n
+                lw.append((k, w8, sc))
+                self.weight_bytes += w8.numel() + 4 * n_total
+            self.layers.append(lw)
+        self.head = (hidden, *hip.repack_w8(6, head_blocks, hidden, vocab))
+        self.weight_bytes += self.head[1].numel() + 4 * vocab
+        del blocks, head_blocks
+        self.ops_per_token = 2.0 * sum(w8.shape[0] * k for lw in self.layers for k, w8, _ in lw)
+        self.ops_per_token += 2.0 * vocab * hidden
+        self.model, self.m_max = model, m_max
+        self.x = {k: torch.from_numpy(synth.activations(m_max, k, index=62_000 + k)).to(dev) for k in {hidden, ffn}}
+        self.a8 = {k: (torch.empty((m_max, hip.k_pad_of(k)), dtype=torch.int8, device=dev),
+                       torch.empty(m_max, dtype=torch.float32, device=dev)) for k in {hidden, ffn}}
+        n_max = max(max(w8.shape[0] for _, w8, _ in self.layers[0]), vocab)
+        self.out = torch.empty(m_max * n_max, dtype=torch.float32, device=dev)
+        torch.cuda.synchronize()
+
+    def step(self, m: int):
+        hip = self.hip
+        for k, w8, sc in [g for lw in self.layers for g in lw] + [self.head]:
+            a8, asc = self.a8[k]
+            hip.quantize_a8(self.x[k][:m], hip.k_pad_of(k), a8[:m], asc[:m])
+            hip.gemm_w8a8(a8[:m], asc[:m], w8, sc, out=self.out[:m * w8.shape[0]].view(m, w8.shape[0]))
+
+    def time(self, m: int, steps: int) -> dict:
+        ms, _ = time_graph(self.torch, lambda: self.step(m), steps, 2)
+        tops = self.ops_per_token * m / (ms * 1e-3) / 1e12
+        return {"m": m, "ms": round(ms, 4), "tok_s": round(m / (ms * 1e-3), 1), "int8_tops": round(tops, 1),
+                "frac_int8_peak": round(tops / INT8_PEAK_TOPS, 4)}
+
+
+def prefill_sequences(torch, hip, synth, steps: int) -> dict:
+    """Prefill MUL_MAT tokens/s of the three model shapes at their prompt sizes."""
+    res = {}
+    for model, ms in (("tinyllama_1.1b", (128, 512)), ("llama3.2_1b", (128, 512, 2048)), ("llama3_8b", (4096,))):
+        pm = PrefillModel(torch, hip, synth, model, max(ms))
+        layers, hidden, ffn, kv, vocab = MODELS[model]
+        res[model] = {"layers": layers, "hidden": hidden, "ffn": ffn, "kv": kv, "vocab": vocab,
+                      "w8_bytes": pm.weight_bytes, "launches_per_step": 2 * (4 * layers + 1),
+                      "runs": [pm.time(m, steps if m < 4096 else max(2, steps // 4)) for m in ms]}
+        del pm
+        torch.cuda.empty_cache()
+    return res
+
+
+def repack_roofline(torch, hip, synth) -> dict:
+    """Kernel (a) on the Llama-3-8B gate weight (Q4_K 14336 x 4096) and the
+    Llama-3.2-1B head (Q6_K 128256 x 2048), rotating distinct copies through
+    more than 1 GB: algorithmic bytes (blocks read, W8 and scales written) per
+    launch over the launch time."""
     dev = "cuda"
-    shapes = (("qkv", 2048, 2560), ("o", 2048, 2048), ("gateup", 2048, 11264), ("down", 5632, 2048))
-    g = torch.Generator(device=dev)
-    g.manual_seed(m)
-    W = [{name: (torch.randint(-127, 128, (n, k), dtype=torch.int8, device=dev, generator=g),
-                 torch.rand(n, device=dev, generator=g) / 127 + 1e-3) for name, k, n in shapes}
-         for _ in range(layers)]
-    X = {name: torch.from_numpy(synth.activations(m, k, index=31_000 + k)).to(dev) for name, k, n in shapes}
-    A8 = {name: (torch.empty((m, k), dtype=torch.int8, device=dev), torch.empty(m, device=dev))
-          for name, k, n in shapes}
-    O = {name: torch.empty((m, n), dtype=torch.float32, device=dev) for name, k, n in shapes}
+    res = {}
+    for name, kind, n, k in (("q4k_14336x4096", 4, 14336, 4096), ("q6k_128256x2048", 6, 128256, 2048)):
+        src = torch.from_numpy(synth.kquant(kind, n, k, index=63_000 + kind)).to(dev)
+        kp = hip.k_pad_of(k)
+        byts = src.numel() + n * kp + 4 * n
+        copies = max(2, min(16, int(1.2e9 // byts) + 1))
+        srcs = [src] + [src.clone() for _ in range(copies - 1)]
+        outs = [(torch.empty((n, kp), dtype=torch.int8, device=dev), torch.empty(n, dtype=torch.float32, device=dev))
+                for _ in range(copies)]
 
-    def run():
-        for lw in W:
-            for name, k, n in shapes:
-                a8, asc = A8[name]
-                hip.quantize_a8(X[name], k, a8, asc)
-                w, wsc = lw[name]
-                hip.gemm_w8a8(a8, asc, w, wsc, out=O[name])
+        def run():
+            for b, (w8, sc) in zip(srcs, outs):
+                hip.repack_w8(kind, b, k, n, w8=w8, scales=sc)
 
-    ms, _ = time_graph(torch, run, 5, 2)
-    per_model_ms = ms * 22 / layers
-    return {"m": m, "ms_per_22_layers": round(per_model_ms, 4), "tok_s": round(m / (per_model_ms * 1e-3), 1)}
+        ms, _ = time_graph(torch, run, 5, 2)
+        us = ms * 1e3 / copies
+        gbs = byts / (us * 1e-6) / 1e9
+        res[name] = {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": measured_traffic(f"repack_{name}"),
+                     "avg_launch_us": round(us, 3), "bytes_per_launch": byts}
+        del srcs, outs
+        torch.cuda.empty_cache()
+    return res
+
+
+def a8_roofline(torch, hip, synth) -> dict:
+    """Kernel (b) on 4096 tokens x 4096 and 512 tokens x 5632 f32 activations,
+    rotating distinct copies through more than 1 GB: f32 read, A8 and scales
+    written, per launch over the launch time."""
+    dev = "cuda"
+    res = {}
+    for m, k in ((4096, 4096), (512, 5632)):
+        kp = hip.k_pad_of(k)
+        byts = m * k * 4 + m * kp + 4 * m
+        copies = max(2, min(32, int(1.2e9 // byts) + 1))
+        xs = [torch.from_numpy(synth.activations(m, k, index=64_000 + i)).to(dev) for i in range(copies)]
+        outs = [(torch.empty((m, kp), dtype=torch.int8, device=dev), torch.empty(m, dtype=torch.float32, device=dev))
+                for _ in range(copies)]
+
+        def run():
+            for x, (a8, sc) in zip(xs, outs):
+                hip.quantize_a8(x, kp, a8, sc)
+
+        ms, _ = time_graph(torch, run, 5, 2)
+        us = ms * 1e3 / copies
+        gbs = byts / (us * 1e-6) / 1e9
+        res[f"m{m}_k{k}"] = {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                             "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": measured_traffic(f"a8_m{m}_k{k}"),
+                             "avg_launch_us": round(us, 3), "bytes_per_launch": byts}
+        del xs, outs
+        torch.cuda.empty_cache()
+    return res
 
 
 def decode_large(torch, hip, synth) -> dict:
@@ -329,59 +452,114 @@ def profile_workload(torch, hip, synth, which: str) -> None:
 
 
 # ----------------------------------------------------------------------------- CPU baseline
-def cpu_baseline(synth, budget_s: float = 12.0) -> dict:
+def cpu_threads() -> int:
+    """Threads for the CPU legs: the CPUs this process may run on, at most 16
+    (one GPU's share of the host)."""
+    try:
+        n = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        n = os.cpu_count() or 1
+    return max(1, min(n, 16))
+
+
+def cpu_topology() -> str:
+    """Host CPU model, sockets x cores x threads, and the CPUs this process may use."""
+    model, sockets, cores, siblings = "unknown CPU", set(), None, None
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            key, _, val = line.partition(":")
+            key, val = key.strip(), val.strip()
+            if key == "model name":
+                model = val
+            elif key == "physical id":
+                sockets.add(val)
+            elif key == "cpu cores" and cores is None:
+                cores = int(val)
+            elif key == "siblings" and siblings is None:
+                siblings = int(val)
+    except (OSError, ValueError):
+        pass
+    try:
+        allowed = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        allowed = os.cpu_count() or 1
+    shape = ""
+    if sockets and cores and siblings:
+        shape = f"{len(sockets)} socket(s) x {cores} cores x {siblings // cores} threads, "
+    return f"{model}: {shape}{os.cpu_count()} logical CPUs, {allowed} usable by this process"
+
+
+def _use_native_oracle(orc) -> str:
+    """Time a -march=native build of the oracle (same floating-point flags);
+    fall back to the shipped build when no compiler is found."""
+    import shutil
+    import tempfile
+
+    if shutil.which("gcc") is None:
+        return "shipped -march=x86-64-v3 build"
+    orc.use_native_build(tempfile.mkdtemp(prefix="oracle_native_"))
+    return "-O3 -march=native build"
+
+
+def cpu_baseline(synth, budget_s: float = 10.0, budget_1t_s: float = 5.0) -> dict:
     """The C oracle's decode GEMV (ggml generic arithmetic) on the host cores,
-    over layer 0 of the same set at M=1 and M=4, repeated until ~budget_s."""
+    over layer 0 of the same set at M=1 and M=4, repeated for ~budget_s on
+    cpu_threads() threads and ~budget_1t_s on one thread."""
     from oracle import oracle as orc
 
-    threads = min(os.cpu_count() or 1, 16)
+    build = _use_native_oracle(orc)
+    threads = cpu_threads()
     layer = [(synth.kquant(kind, n, k, index=10_000 + pi), k, n, kind)
              for pi, (name, k, n, kind) in enumerate(synth.TINYLLAMA_LAYER)]
     q8 = {(m, k): orc.quantize_q8_k(synth.activations(m, k, index=20_000 + m * 8 + k))
           for m in (1, 4) for k in (2048, 5632)}
-    total_bytes = 0
-    reps = 0
-    t0 = time.perf_counter()
-    while time.perf_counter() - t0 < budget_s:
-        for m in (1, 4):
-            for w, k, n, kind in layer:
-                orc.gemv_q8_k(kind, w, k, n, q8[(m, k)], threads=threads)
-                total_bytes += w.nbytes + q8[(m, k)].nbytes + m * n * 4
-        reps += 1
-    dt = time.perf_counter() - t0
-    return {"value": round(total_bytes / dt / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port",
-            "sample": f"oracle decode GEMV (ggml generic dot, OpenMP) over TinyLlama layer 0's 7 projections "
-                      f"at M=1 and M=4, {reps} passes in {dt:.1f} s on {host_cpu()} ({os.cpu_count()} logical CPUs)"}
+
+    def run(nthreads, budget):
+        total_bytes, reps = 0, 0
+        t0 = time.perf_counter()
+        while time.perf_counter() - t0 < budget:
+            for m in (1, 4):
+                for w, k, n, kind in layer:
+                    orc.gemv_q8_k(kind, w, k, n, q8[(m, k)], threads=nthreads)
+                    total_bytes += w.nbytes + q8[(m, k)].nbytes + m * n * 4
+            reps += 1
+        dt = time.perf_counter() - t0
+        return total_bytes / dt / 1e9, reps, dt
+
+    gbs, reps, dt = run(threads, budget_s)
+    gbs1, reps1, dt1 = run(1, budget_1t_s)
+    return {"value": round(gbs, 3), "unit": "GB/s", "cores": threads, "kind": "port",
+            "value_1thread": round(gbs1, 3),
+            "topology": cpu_topology(),
+            "sample": f"oracle decode GEMV (ggml generic dot, OpenMP, {build}) over TinyLlama layer 0's 7 "
+                      f"projections at M=1 and M=4: {reps} passes in {dt:.1f} s on {threads} threads, "
+                      f"{reps1} passes in {dt1:.1f} s on 1 thread"}
 
 
-def host_cpu() -> str:
-    try:
-        for line in Path("/proc/cpuinfo").read_text().splitlines():
-            if line.startswith("model name"):
-                return line.split(":", 1)[1].strip()
-    except OSError:
-        pass
-    return "unknown CPU"
-
-
-def cpu_baseline_w8a8(synth, budget_s: float = 8.0) -> dict:
+def cpu_baseline_w8a8(synth, budget_s: float = 8.0, budget_1t_s: float = 5.0) -> dict:
     """The C oracle's W8A8 prefill route (repack + A8 quant + exact i32 GEMM +
-    rescale) on the config-0 workload (Q4_K [5632 x 2048], 128 tokens)."""
+    rescale) on the 5632 x 2048 Q4_K weight at 128 tokens."""
     from oracle import oracle as orc
 
-    threads = min(os.cpu_count() or 1, 16)
+    threads = cpu_threads()
     blocks = synth.kquant(4, 5632, 2048, index=1)
     a = synth.activations(128, 2048, index=2)
-    reps = 0
-    t0 = time.perf_counter()
-    while time.perf_counter() - t0 < budget_s:
-        orc.matmul_q_w8a8(4, blocks, a, 5632, threads=threads)
-        reps += 1
-    dt = time.perf_counter() - t0
-    ops = 2.0 * 128 * 5632 * 2048 * reps
-    return {"value": round(ops / dt / 1e12, 4), "unit": "int8 TOPS (repack included)", "cores": threads,
-            "kind": "port", "sample": f"oracle W8A8 route, Q4_K 5632x2048 weight x 128 tokens, {reps} runs "
-                                      f"in {dt:.1f} s on {host_cpu()}"}
+
+    def run(nthreads, budget):
+        reps = 0
+        t0 = time.perf_counter()
+        while time.perf_counter() - t0 < budget:
+            orc.matmul_q_w8a8(4, blocks, a, 5632, threads=nthreads)
+            reps += 1
+        dt = time.perf_counter() - t0
+        return 2.0 * 128 * 5632 * 2048 * reps / dt / 1e12, reps, dt
+
+    tops, reps, dt = run(threads, budget_s)
+    tops1, reps1, dt1 = run(1, budget_1t_s)
+    return {"value": round(tops, 4), "unit": "int8 TOPS (repack included)", "cores": threads, "kind": "port",
+            "value_1thread": round(tops1, 4), "topology": cpu_topology(),
+            "sample": f"oracle W8A8 route, Q4_K 5632x2048 weight x 128 tokens: {reps} runs in {dt:.1f} s on "
+                      f"{threads} threads, {reps1} runs in {dt1:.1f} s on 1 thread"}
 
 
 # ----------------------------------------------------------------------------- main
@@ -418,9 +596,9 @@ def main():
     torch.cuda.synchronize()
     assert all(torch.equal(ref[key], ds.outs[key]) for key in ref), "graph replay differs"
 
-    # dominant kernel: the Q4_K x Q8_K GEMV at M=1 (the single-row kernel),
-    # its launches timed alone in the same sequence; the 4-row launches of the
-    # same weights run the matrix-core kernel and are timed beside it
+    # dominant kernel: the Q4_K x Q8_K GEMV at M=4 on the matrix cores (the
+    # largest share of a step), its launches timed alone in the same sequence;
+    # the single-row launches of the same weights are timed beside it
     def kernel_rate(only_m):
         b, launches = ds.bytes_per_step(only_kind=4, only_m=only_m)
         t_ms, _ = time_graph(torch, lambda: ds.step(only_kind=4, only_m=only_m), args.steps, args.warmup)
@@ -448,16 +626,17 @@ def main():
                                "shared input (qkv, o, gate+up, down), HIP graph",
                    "layers": synth.TINYLLAMA_LAYERS, "m": [1, 4], "launches_per_step": n_gemv,
                    "bytes_per_step": step_bytes},
-        "roofline": {"bound": "hbm", "kernel": "Q4_K x Q8_K decode GEMV with fused Q8_K quant at M=1 "
-                                               "(gemv_kernel<4,...>), the 66 Q4_K launches of a step",
-                     "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": measured_traffic("gemv_q4k"),
-                     "avg_launch_us": round(q4_us, 3), "bytes_per_launch": q4_bpl},
-        "roofline_m4": {"bound": "hbm", "kernel": "Q4_K x Q8_K decode GEMV at M=4 on the matrix cores "
-                                                  "(gemv_mfma_kernel<4,...>), the 66 Q4_K launches of a step",
-                        "achieved": round(m4_achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                        "frac": round(m4_achieved / HBM_PEAK_GBS, 4), "traffic": measured_traffic("gemv_q4k_m4"),
-                        "avg_launch_us": round(m4_us, 3), "bytes_per_launch": m4_bpl},
+        "roofline": {"bound": "hbm", "kernel": "Q4_K x Q8_K decode GEMV at M=4 on the matrix cores with fused "
+                                               "Q8_K quant (gemv_mfma_kernel<4,4,true,...>), the 66 Q4_K launches "
+                                               "of a step",
+                     "achieved": round(m4_achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(m4_achieved / HBM_PEAK_GBS, 4), "traffic": measured_traffic("gemv_q4k_m4"),
+                     "avg_launch_us": round(m4_us, 3), "bytes_per_launch": m4_bpl},
+        "roofline_m1": {"bound": "hbm", "kernel": "Q4_K x Q8_K decode GEMV with fused Q8_K quant at M=1 "
+                                                  "(gemv_kernel<4,...>), the 66 Q4_K launches of a step",
+                        "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                        "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": measured_traffic("gemv_q4k"),
+                        "avg_launch_us": round(q4_us, 3), "bytes_per_launch": q4_bpl},
     }
     if not args.quick:
         rot = 1 << 30
@@ -465,9 +644,10 @@ def main():
             "config0_m128": w8a8_gemm(torch, hip, synth, 128, 5632, 2048, 200, rot),
             "tinyllama_gateup_m512": w8a8_gemm(torch, hip, synth, 512, 11264, 2048, 100, rot),
             "llama3_8b_ffn_m4096": w8a8_gemm(torch, hip, synth, 4096, 14336, 4096, 8, rot),
-            "prefill_tinyllama_m128": prefill_tok_s(torch, hip, synth, 128, 22),
-            "prefill_tinyllama_m512": prefill_tok_s(torch, hip, synth, 512, 22),
         }
+        result["roofline_repack"] = repack_roofline(torch, hip, synth)
+        result["roofline_a8_quant"] = a8_roofline(torch, hip, synth)
+        result["prefill_mul_mat_tok_s"] = prefill_sequences(torch, hip, synth, 5)
         result["decode_gemv_large_m1"] = decode_large(torch, hip, synth)
         result["decode_crossover_llama3_8b_gate_up"] = decode_crossover(torch, hip, synth)
     if not (args.quick or args.no_cpu):

@@ -38,43 +38,58 @@ def build() -> Path:
     return LIB_PATH
 
 
+def use_native_build(out_dir: str) -> Path:
+    """Compile oracle.c for this host's CPU (-march=native, the same
+    floating-point flags) into out_dir and make it the library the functions
+    below call. For timing the CPU baseline on the machine it runs on."""
+    out = Path(out_dir) / "liboracle_native.so"
+    subprocess.run(["gcc", "-O3", "-march=native", "-std=gnu11", "-fPIC", "-fopenmp", "-ffp-contract=off",
+                    "-fno-fast-math", "-shared", "-o", str(out), str(HERE / "oracle.c"), "-lm"], check=True)
+    global _lib
+    _lib = _configure(ctypes.CDLL(str(out)))
+    return out
+
+
 def lib() -> ctypes.CDLL:
     global _lib
     if _lib is None:
         if not LIB_PATH.exists():
             build()
-        L = ctypes.CDLL(str(LIB_PATH))
-        L.or_fp16_to_f32.argtypes = [ctypes.c_uint16]
-        L.or_fp16_to_f32.restype = ctypes.c_float
-        L.or_dequant_rows.argtypes = [ctypes.c_uint32, _u8p, _sz, _sz, _f32p]
-        L.or_quantize_symmetric_row.argtypes = [_f32p, _sz, _i8p, _f32p]
-        L.or_quantize_symmetric_row_neon.argtypes = [_f32p, _sz, _i8p, _f32p]
-        L.or_rescale_neon.argtypes = [_i32p, _f32p, _f32p, _sz, _sz, _f32p]
-        L.or_rescale_neon.restype = None
-        L.or_repack_w8.argtypes = [ctypes.c_uint32, _u8p, _sz, _sz, _sz, _i8p, _f32p]
-        L.or_quantize_a8.argtypes = [_f32p, _sz, _sz, _sz, _i8p, _f32p]
-        L.or_gemm_i32.argtypes = [_i8p, _i8p, _sz, _sz, _sz, _i32p, ctypes.c_int]
-        L.or_gemm_i32.restype = None
-        L.or_rescale.argtypes = [_i32p, _f32p, _f32p, _sz, _sz, _f32p]
-        L.or_rescale.restype = None
-        L.or_matmul_q_w8a8.argtypes = [ctypes.c_uint32, _u8p, _sz, _f32p, _sz, _sz, _sz, _f32p, ctypes.c_int]
-        L.or_fnv1a64.argtypes = [ctypes.c_uint64, _u8p, _sz]
-        L.or_fnv1a64.restype = ctypes.c_uint64
-        L.or_source_fingerprint.argtypes = [_u8p, _sz]
-        L.or_source_fingerprint.restype = ctypes.c_uint64
-        L.or_hilo_stack.argtypes = [_f32p, _sz, _sz, _f32p]
-        L.or_hilo_sum.argtypes = [_f32p, _f32p, _sz]
-        L.or_hilo_sum.restype = None
-        L.or_quantize_row_q8_k.argtypes = [_f32p, _sz, _u8p]
-        L.or_quantize_row_q8_k.restype = None
-        L.or_vec_dot_q4_k_q8_k.argtypes = [_sz, _u8p, _u8p]
-        L.or_vec_dot_q4_k_q8_k.restype = ctypes.c_float
-        L.or_vec_dot_q6_k_q8_k.argtypes = [_sz, _u8p, _u8p]
-        L.or_vec_dot_q6_k_q8_k.restype = ctypes.c_float
-        L.or_gemv_q8_k.argtypes = [ctypes.c_uint32, _u8p, _sz, _sz, _u8p, _sz, _f32p, ctypes.c_int]
-        L.or_gemv_block_sums.argtypes = [ctypes.c_uint32, _u8p, _sz, _sz, _u8p, _i32p, _i32p, _f64p]
-        _lib = L
+        _lib = _configure(ctypes.CDLL(str(LIB_PATH)))
     return _lib
+
+
+def _configure(L: ctypes.CDLL) -> ctypes.CDLL:
+    L.or_fp16_to_f32.argtypes = [ctypes.c_uint16]
+    L.or_fp16_to_f32.restype = ctypes.c_float
+    L.or_dequant_rows.argtypes = [ctypes.c_uint32, _u8p, _sz, _sz, _f32p]
+    L.or_quantize_symmetric_row.argtypes = [_f32p, _sz, _i8p, _f32p]
+    L.or_quantize_symmetric_row_neon.argtypes = [_f32p, _sz, _i8p, _f32p]
+    L.or_rescale_neon.argtypes = [_i32p, _f32p, _f32p, _sz, _sz, _f32p]
+    L.or_rescale_neon.restype = None
+    L.or_repack_w8.argtypes = [ctypes.c_uint32, _u8p, _sz, _sz, _sz, _i8p, _f32p]
+    L.or_quantize_a8.argtypes = [_f32p, _sz, _sz, _sz, _i8p, _f32p]
+    L.or_gemm_i32.argtypes = [_i8p, _i8p, _sz, _sz, _sz, _i32p, ctypes.c_int]
+    L.or_gemm_i32.restype = None
+    L.or_rescale.argtypes = [_i32p, _f32p, _f32p, _sz, _sz, _f32p]
+    L.or_rescale.restype = None
+    L.or_matmul_q_w8a8.argtypes = [ctypes.c_uint32, _u8p, _sz, _f32p, _sz, _sz, _sz, _f32p, ctypes.c_int]
+    L.or_fnv1a64.argtypes = [ctypes.c_uint64, _u8p, _sz]
+    L.or_fnv1a64.restype = ctypes.c_uint64
+    L.or_source_fingerprint.argtypes = [_u8p, _sz]
+    L.or_source_fingerprint.restype = ctypes.c_uint64
+    L.or_hilo_stack.argtypes = [_f32p, _sz, _sz, _f32p]
+    L.or_hilo_sum.argtypes = [_f32p, _f32p, _sz]
+    L.or_hilo_sum.restype = None
+    L.or_quantize_row_q8_k.argtypes = [_f32p, _sz, _u8p]
+    L.or_quantize_row_q8_k.restype = None
+    L.or_vec_dot_q4_k_q8_k.argtypes = [_sz, _u8p, _u8p]
+    L.or_vec_dot_q4_k_q8_k.restype = ctypes.c_float
+    L.or_vec_dot_q6_k_q8_k.argtypes = [_sz, _u8p, _u8p]
+    L.or_vec_dot_q6_k_q8_k.restype = ctypes.c_float
+    L.or_gemv_q8_k.argtypes = [ctypes.c_uint32, _u8p, _sz, _sz, _u8p, _sz, _f32p, ctypes.c_int]
+    L.or_gemv_block_sums.argtypes = [ctypes.c_uint32, _u8p, _sz, _sz, _u8p, _i32p, _i32p, _f64p]
+    return L
 
 
 def _p(a: np.ndarray, t):
