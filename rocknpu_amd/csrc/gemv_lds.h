@@ -13,6 +13,13 @@ template <int CTRL>
 __device__ __forceinline__ int dpp(int v) {
     return __builtin_amdgcn_mov_dpp(v, CTRL, 0xF, 0xF, false);
 }
+// The same move with 0 for lanes that read nothing (none do with these
+// controls): 0 is the identity of an unsigned max and of an add, so the
+// compiler can fold the move into the DPP form of that operation.
+template <int CTRL>
+__device__ __forceinline__ unsigned dpp0(unsigned v) {
+    return static_cast<unsigned>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), CTRL, 0xF, 0xF, true));
+}
 // DPP controls: quad_perm [1,0,3,2] and [2,3,0,1], row_half_mirror, row_mirror.
 // Applied in this order to a value that is uniform over the lower lane-index
 // bits, they exchange across lane-index bits 0, 1, 2 and 3.
@@ -79,12 +86,15 @@ __device__ __forceinline__ void load_x16(const float* __restrict__ x, int64_t ld
 //   q = min(127, nearest_int(iscale * x)); d = 1/iscale; bsums = sums of 16 q.
 // nearest_int is ggml's own: add 1.5 * 2^23 and keep the low mantissa bits,
 // i.e. round half to even. |iscale * x| <= 127 (1 + 2^-24)^2 < 127.5, so q is
-// in [-127, 127] (the min never binds) and its low byte is q as int8. The
-// block's largest and smallest values give the magnitude and, unless a value
-// and its negation both reach it (then the first one is searched for), the
-// sign of max. Writes the 256 quants at qs, the 16 int16 bsums at bs and d.
+// in [-127, 127] (the min never binds) and its low byte is q as int8.
+// The magnitude and sign of max come from one reduction over the 16 lanes of
+// key = (bits of |lane extreme| << 1) | (that extreme is negative): for
+// non-negative floats the bit patterns order as the values. Where a value and
+// its negation both reach the magnitude (found with two ballots), the first
+// one in block order is searched for. Writes the 256 quants at qs, the 16 int16
+// bsums at bs and d.
 __device__ __forceinline__ void quantize_block(const float4 (&f)[4], uint8_t* qs, int16_t* bs, float* d_out) {
-    const int sub = threadIdx.x & 15;
+    const int lane = threadIdx.x & 63, sub = lane & 15;
     float v[16];
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
@@ -96,19 +106,22 @@ __device__ __forceinline__ void quantize_block(const float4 (&f)[4], uint8_t* qs
         vmax = fmaxf(vmax, v[i]);
         vmin = fminf(vmin, v[i]);
     }
-    // both reductions interleaved, so the DPP moves do not wait on each other
-    vmax = fmaxf(vmax, __int_as_float(dpp<kDppXor1>(__float_as_int(vmax))));
-    vmin = fminf(vmin, __int_as_float(dpp<kDppXor1>(__float_as_int(vmin))));
-    vmax = fmaxf(vmax, __int_as_float(dpp<kDppXor2>(__float_as_int(vmax))));
-    vmin = fminf(vmin, __int_as_float(dpp<kDppXor2>(__float_as_int(vmin))));
-    vmax = fmaxf(vmax, __int_as_float(dpp<kDppMirror8>(__float_as_int(vmax))));
-    vmin = fminf(vmin, __int_as_float(dpp<kDppMirror8>(__float_as_int(vmin))));
-    vmax = fmaxf(vmax, __int_as_float(dpp<kDppMirror16>(__float_as_int(vmax))));
-    vmin = fminf(vmin, __int_as_float(dpp<kDppMirror16>(__float_as_int(vmin))));
-    const float gmax = fmaxf(fmaxf(vmax, -vmin), 0.0f);
-    const bool both = vmax == gmax && vmin == -gmax && gmax > 0.0f;
-    float mx = vmin == -gmax ? -gmax : gmax;
-    if (__any(both)) {  // a value and its negation both reach the magnitude: the first one wins
+    const float amag = fmaxf(fabsf(vmax), fabsf(vmin));
+    unsigned key = (__float_as_uint(amag) << 1) | (vmax < amag ? 1u : 0u);
+    key = max(key, dpp0<kDppXor1>(key));
+    key = max(key, dpp0<kDppXor2>(key));
+    key = max(key, dpp0<kDppMirror8>(key));
+    key = max(key, dpp0<kDppMirror16>(key));
+    const float gmax = __uint_as_float(key >> 1);
+    float mx = (key & 1u) ? -gmax : gmax;
+    // +gmax and -gmax both in a group: its lanes search for the first. Bit
+    // 16 j of `both` is set for such a group j (ballots folded per 16 lanes).
+    uint64_t pos = __ballot(gmax > 0.0f && vmax == gmax), neg = __ballot(gmax > 0.0f && vmin == -gmax);
+    pos |= pos >> 8; pos |= pos >> 4; pos |= pos >> 2; pos |= pos >> 1;
+    neg |= neg >> 8; neg |= neg >> 4; neg |= neg >> 2; neg |= neg >> 1;
+    const uint64_t both_groups = pos & neg & 0x0001000100010001ull;
+    if (both_groups) {
+        const bool both = (both_groups >> (lane & 48)) & 1;
         int first = 0x7fffffff;
 #pragma unroll
         for (int i = 15; i >= 0; --i)
@@ -136,14 +149,16 @@ __device__ __forceinline__ void quantize_block(const float4 (&f)[4], uint8_t* qs
     int gs[4];
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
-        gs[t] = __builtin_amdgcn_sdot4(static_cast<int>(wq[t]), 0x01010101, 0, false);
-        gs[t] += dpp<kDppXor1>(gs[t]);
-        gs[t] += dpp<kDppXor2>(gs[t]);
+        unsigned g = static_cast<unsigned>(__builtin_amdgcn_sdot4(static_cast<int>(wq[t]), 0x01010101, 0, false));
+        g += dpp0<kDppXor1>(g);
+        g += dpp0<kDppXor2>(g);
+        gs[t] = static_cast<int>(g);
         *reinterpret_cast<uint32_t*>(qs + 64 * t + 4 * sub) = wq[t];
     }
-    const int tq = sub & 3;  // lane tq of each quad writes group 4 tq + sub / 4
-    const int g = tq == 0 ? gs[0] : tq == 1 ? gs[1] : tq == 2 ? gs[2] : gs[3];
-    bs[4 * tq + (sub >> 2)] = static_cast<int16_t>(g);
+    // lane tq of each quad writes group 4 tq + sub / 4 (selects on the bits of tq)
+    const int tq = sub & 3;
+    const int g01 = (tq & 1) ? gs[1] : gs[0], g23 = (tq & 1) ? gs[3] : gs[2];
+    bs[4 * tq + (sub >> 2)] = static_cast<int16_t>((tq & 2) ? g23 : g01);
     if (sub == 0) *d_out = d;
 }
 

@@ -329,9 +329,21 @@ struct OwnedActs {
                 load_x16(p.x, p.ldx, p.nb, min(4 * i + qslot, p.m - 1) * p.nb + min(wave, p.nb - 1), xf[i]);
         }
     }
+    // ONE: one block index per wave (iters == 1), quantised from the loaded
+    // registers as they are
+    template <bool ONE = false>
     __device__ __forceinline__ void stage(const MfmaArgs& p, int wave, const ActLds<MT>& act) {
         const int lane = threadIdx.x & 63, nb = p.nb, m = p.m, iters = p.iters;
-        if constexpr (FUSED) {
+        if constexpr (FUSED && ONE) {
+            const int qslot = lane >> 4;
+#pragma unroll
+            for (int i = 0; i < QP; ++i) {
+                const int mi = 4 * i + qslot;
+                if (mi < m && wave < nb)
+                    quantize_block(xf[i], act.quants(wave, mi), reinterpret_cast<int16_t*>(act.bsums(wave, mi)),
+                                   act.d(wave, mi));
+            }
+        } else if constexpr (FUSED) {
             const int qslot = lane >> 4;
             for (int it = 0; it < iters; ++it) {
                 const int b = wave + W * it;
@@ -415,13 +427,17 @@ __global__ __launch_bounds__(W * 64) void gemv_mfma_kernel(const MfmaArgs p) {
 
     OwnedActs<MT, W, FUSED> owned;
     owned.first(p, wave);
+    // Every wave's activation loads are issued before any weight load: the
+    // weight loads miss in the vector L1 and fill its queue, and an activation
+    // load issued behind them waits for them.
+    __builtin_amdgcn_s_barrier();
     // the first weight block before the quantisation, the rest of the ring after
     // it: each load instruction issued ahead of the quantisation delays it
     MPiece<KIND> buf[D];
     Pos lq{static_cast<int>(blockIdx.x), 0};  // next item to load
     load(lq, buf[0]);
     advance(lq);
-    owned.stage(p, wave, act);
+    owned.template stage<AREG>(p, wave, act);
 #pragma unroll
     for (int j = 1; j < D; ++j) {
         load(lq, buf[j]);
