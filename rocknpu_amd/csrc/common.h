@@ -92,15 +92,48 @@ __device__ __forceinline__ int quant_sym(float v, float s) {
     return static_cast<int>(r);
 }
 
+// quant_sym over N values with the reciprocal inv = f32(1 / s), dividing
+// only where it can matter. r = f32(v * inv) is within 1.5 * 2^-23 * |v / s|
+// (<= 2.3e-5 for |v / s| <= 128) of the correctly rounded quotient
+// f32(v / s), so both round to the same integer, half away from zero, unless
+// r lies within 2^-15 of a half-integer; away from half-integers rint (ties
+// to even) rounds the same way. r - rint(r) is exact. When any of this lane's
+// values is that close (about one in 16000), or |r| > 127.5 or NaN, the
+// lane's values all take quant_sym itself.
+template <int N>
+__device__ __forceinline__ void quant_sym_rcp(const float (&v)[N], float s, float inv, int (&q)[N]) {
+    bool exact = false;
+#pragma unroll
+    for (int i = 0; i < N; ++i) {
+        const float r = v[i] * inv;
+        const float rr = rintf(r);
+        exact |= !(fabsf(r - rr) < 0.5f - 0x1p-15f) || !(fabsf(r) <= 127.5f);
+        q[i] = static_cast<int>(rr);
+    }
+    if (exact) {
+#pragma unroll
+        for (int i = 0; i < N; ++i) q[i] = quant_sym(v[i], s);
+    }
+}
+
+// Max over the wave of non-negative floats (their bit patterns order as the
+// values): DPP steps across lane bits 0-3 (0 is the identity of an unsigned
+// max, so each move folds into v_max_u32_dpp), then the four 16-lane rows by
+// lane reads. Every lane gets the result.
+__device__ __forceinline__ float wave_max_nonneg(float v) {
+    unsigned u = __float_as_uint(v);
+    u = max(u, static_cast<unsigned>(__builtin_amdgcn_update_dpp(0, static_cast<int>(u), 0xB1, 0xF, 0xF, true)));
+    u = max(u, static_cast<unsigned>(__builtin_amdgcn_update_dpp(0, static_cast<int>(u), 0x4E, 0xF, 0xF, true)));
+    u = max(u, static_cast<unsigned>(__builtin_amdgcn_update_dpp(0, static_cast<int>(u), 0x141, 0xF, 0xF, true)));
+    u = max(u, static_cast<unsigned>(__builtin_amdgcn_update_dpp(0, static_cast<int>(u), 0x140, 0xF, 0xF, true)));
+    const unsigned r0 = __builtin_amdgcn_readlane(u, 0), r1 = __builtin_amdgcn_readlane(u, 16);
+    const unsigned r2 = __builtin_amdgcn_readlane(u, 32), r3 = __builtin_amdgcn_readlane(u, 48);
+    return __uint_as_float(max(max(r0, r1), max(r2, r3)));
+}
+
 __device__ __forceinline__ float wave_max(float v) {
 #pragma unroll
     for (int o = 32; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
-    return v;
-}
-
-__device__ __forceinline__ int wave_or(int v) {
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) v |= __shfl_xor(v, o, 64);
     return v;
 }
 

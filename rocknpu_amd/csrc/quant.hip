@@ -71,14 +71,19 @@ __global__ __launch_bounds__(kA8Threads) void quantize_a8_kernel(const float* __
     vmax = block_max(vmax, red);
     const bool bad = !(vmax <= 3.402823466e38f);
     const float scale = vmax == 0.0f ? 1.0f : vmax / 127.0f;
+    [[maybe_unused]] const float inv = 1.0f / scale;
 
     // Pass 2: quantise (the row is cache-resident now) and zero the padding.
     if constexpr (VEC) {
         for (int64_t i = t; i < k / 4; i += kA8Threads) {
             const float4 v = reinterpret_cast<const float4*>(x)[i];
             uint32_t w = 0;
-            if (!bad) w = pack4(quant_sym(v.x, scale), quant_sym(v.y, scale), quant_sym(v.z, scale),
-                                quant_sym(v.w, scale));
+            if (!bad) {
+                const float e[4] = {v.x, v.y, v.z, v.w};
+                int qq[4];
+                quant_sym_rcp(e, scale, inv, qq);
+                w = pack4(qq[0], qq[1], qq[2], qq[3]);
+            }
             reinterpret_cast<uint32_t*>(q)[i] = w;
         }
         for (int64_t i = k / 4 + t; i < k_pad / 4; i += kA8Threads) reinterpret_cast<uint32_t*>(q)[i] = 0;
@@ -92,7 +97,7 @@ __global__ __launch_bounds__(kA8Threads) void quantize_a8_kernel(const float* __
 // The same for rows of up to 16 * 1024 values with k, lda and k_pad multiples
 // of 4 and 16-byte aligned bases: each thread keeps its R float4 of the row in
 // registers, so the row is read once, not once per pass. The max is
-// order-independent and every value takes the same quant_sym, so the output
+// order-independent and every value takes the same quant_sym_rcp, so the output
 // is bit-identical to quantize_a8_kernel's.
 template <int R>
 __global__ __launch_bounds__(kA8Threads) void quantize_a8_regs_kernel(const float* __restrict__ a,
@@ -125,13 +130,16 @@ __global__ __launch_bounds__(kA8Threads) void quantize_a8_regs_kernel(const floa
     vmax = block_max(vmax, red);
     const bool bad = !(vmax <= 3.402823466e38f);
     const float scale = vmax == 0.0f ? 1.0f : vmax / 127.0f;
+    const float inv = 1.0f / scale;
 #pragma unroll
     for (int j = 0; j < R; ++j) {
         const int i = t + j * kA8Threads;
-        if (i < k4)
-            q[i] = bad ? 0u
-                       : pack4(quant_sym(v[j].x, scale), quant_sym(v[j].y, scale), quant_sym(v[j].z, scale),
-                               quant_sym(v[j].w, scale));
+        if (i < k4) {
+            const float e[4] = {v[j].x, v[j].y, v[j].z, v[j].w};
+            int qq[4];
+            quant_sym_rcp(e, scale, inv, qq);
+            q[i] = bad ? 0u : pack4(qq[0], qq[1], qq[2], qq[3]);
+        }
     }
     for (int64_t i = k4 + t; i < k_pad / 4; i += kA8Threads) q[i] = 0;
     if (t == 0) scales[row] = bad ? __builtin_nanf("") : scale;

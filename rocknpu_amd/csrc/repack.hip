@@ -11,11 +11,14 @@
 // rounds; Q6_K: d*sc*q has <= 24 bits and is exact), so they match every f32
 // implementation of the ggml formulas bit for bit.
 //
-// Mapping: one wave per output row, 4 waves per workgroup. A row is walked in
-// chunks of 8 super-blocks (2048 values): per chunk the wave first stages the
-// per-sub-block factors (d*sc, dmin*m) into LDS, one sub-block per lane, then
-// every lane decodes one 32-value unit. Pass 1 finds max|row|; pass 2 decodes
-// again (the row is L2-resident by then), quantises and stores.
+// Mapping: one wave per output row, 4 independent waves per workgroup. A row
+// is walked in chunks of 8 super-blocks (2048 values): per chunk the wave
+// stages the per-sub-block factors (d*sc, dmin*m) into its own LDS area, one
+// sub-block per lane, then every lane decodes one 32-value unit. Rows of up to
+// HOLD chunks keep their decoded values in registers between finding
+// max|row| and quantising; longer rows decode twice (the second time from
+// L2). Quantisation multiplies by the reciprocal scale and divides only where
+// the product is within 2^-15 of a rounding boundary (quant_sym_rcp).
 #include "common.h"
 
 namespace rk {
@@ -27,9 +30,13 @@ constexpr int kWaves = 4;
 // Stage the per-sub-block factors of `cnt` blocks starting at `chunk` into
 // st[16 * block + i]: Q4_K/Q5_K i<8 -> d*sc_i, i>=8 -> dmin*m_(i-8);
 // Q6_K i<16 -> d*sc_i.
+// Returns whether a staged factor is not finite. A dequantised value is then
+// not finite exactly when its factors are not: |d*sc| <= 65504 * 127 and the
+// quants are at most 6 bits, so finite factors give finite values.
 template <int KIND>
-__device__ __forceinline__ void stage_factors(const uint8_t* chunk, int cnt, int lane, float* st) {
+__device__ __forceinline__ bool stage_factors(const uint8_t* chunk, int cnt, int lane, float* st) {
     constexpr int BB = block_bytes(KIND);
+    bool bad = false;
     if constexpr (KIND == 4 || KIND == 5) {
         const int bi = lane >> 3, j = lane & 7;
         if (bi < cnt) {
@@ -39,8 +46,10 @@ __device__ __forceinline__ void stage_factors(const uint8_t* chunk, int cnt, int
             const float dmin = f16_bits_to_f32(static_cast<uint16_t>(w0 >> 16));
             int sc, mn;
             scale_min_k4(j, ld_u32(blk + 4), ld_u32(blk + 8), ld_u32(blk + 12), sc, mn);
-            st[bi * 16 + j] = d * static_cast<float>(sc);
-            st[bi * 16 + 8 + j] = dmin * static_cast<float>(mn);
+            const float f0 = d * static_cast<float>(sc), f1 = dmin * static_cast<float>(mn);
+            st[bi * 16 + j] = f0;
+            st[bi * 16 + 8 + j] = f1;
+            bad = !(fabsf(f0) <= 3.402823466e38f) || !(fabsf(f1) <= 3.402823466e38f);
         }
     } else {
 #pragma unroll
@@ -50,71 +59,79 @@ __device__ __forceinline__ void stage_factors(const uint8_t* chunk, int cnt, int
                 const uint8_t* blk = chunk + bi * BB;
                 const float d = f16_bits_to_f32(ld_u16(blk + 208));
                 const int sc = static_cast<int8_t>(blk[192 + idx]);
-                st[bi * 16 + idx] = d * static_cast<float>(sc);
+                const float f = d * static_cast<float>(sc);
+                st[bi * 16 + idx] = f;
+                bad |= !(fabsf(f) <= 3.402823466e38f);
             }
         }
     }
+    return bad;
 }
 
-__device__ __forceinline__ void bytes16(const uint8_t* p, uint8_t (&b)[16]) {
-    const uint4 v = *reinterpret_cast<const uint4*>(p);
-    __builtin_memcpy(b, &v, 16);
+// 32-bit word of the two 16-bit halves at p (2-byte aligned).
+__device__ __forceinline__ uint32_t ld_u16x2(const uint8_t* p) {
+    return static_cast<uint32_t>(ld_u16(p)) | static_cast<uint32_t>(ld_u16(p + 2)) << 16;
 }
 
-__device__ __forceinline__ void bytes8_u16(const uint8_t* p, uint8_t (&b)[8]) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const uint16_t h = ld_u16(p + 2 * i);
-        b[2 * i] = static_cast<uint8_t>(h & 0xFF);
-        b[2 * i + 1] = static_cast<uint8_t>(h >> 8);
-    }
+// Byte e of w as f32 (v_cvt_f32_ubyte<e>).
+template <int E>
+__device__ __forceinline__ float ubyte(uint32_t w) {
+    return static_cast<float>((w >> (8 * E)) & 0xFF);
 }
 
-// Decode unit v (0..7) of a block into vals[32].
+// Decode unit v (0..7) of a block into vals[32], four quants per 32-bit word.
 // Q4_K/Q5_K: j = v/2, h = v%2; vals[0..16) are positions 64j+16h+i (sub-block
-//   2j), vals[16..32) are positions 64j+32+16h+i (sub-block 2j+1).
-// Q6_K: half = v/4, g = v%4; vals[8q+i] is position 128*half + 32q + 8g + i.
+//   2j), vals[16..32) are positions 64j+32+16h+i (sub-block 2j+1);
+//   value = d_sub * q - m_sub. d_sub * q is exact (a half times a 6-bit scale
+//   times a 5-bit quant: at most 22 bits), so the fused multiply-add rounds
+//   once, as the product-then-difference does.
+// Q6_K: half = v/4, g = v%4; vals[8q+i] is position 128*half + 32q + 8g + i;
+//   value = d_sub * (u - 32) = fma(d_sub, u, -32 d_sub), exact either way
+//   (at most 24 bits).
 template <int KIND>
 __device__ __forceinline__ void decode_unit(const uint8_t* blk, int v, const float* st,
                                             float (&vals)[32]) {
+    auto put4 = [&](int at, uint32_t w, float d, float neg_m) {
+        vals[at] = __builtin_fmaf(d, ubyte<0>(w), neg_m);
+        vals[at + 1] = __builtin_fmaf(d, ubyte<1>(w), neg_m);
+        vals[at + 2] = __builtin_fmaf(d, ubyte<2>(w), neg_m);
+        vals[at + 3] = __builtin_fmaf(d, ubyte<3>(w), neg_m);
+    };
     if constexpr (KIND == 4 || KIND == 5) {
         const int j = v >> 1, h = v & 1;
-        uint8_t q[16];
-        bytes16(blk + (KIND == 4 ? 16 : 48) + 32 * j + 16 * h, q);
+        const uint4 qv = *reinterpret_cast<const uint4*>(blk + (KIND == 4 ? 16 : 48) + 32 * j + 16 * h);
+        const uint32_t q[4] = {qv.x, qv.y, qv.z, qv.w};
         const float d1 = st[2 * j], d2 = st[2 * j + 1];
-        const float m1 = st[8 + 2 * j], m2 = st[8 + 2 * j + 1];
-        if constexpr (KIND == 4) {
+        const float m1 = -st[8 + 2 * j], m2 = -st[8 + 2 * j + 1];
+        uint32_t hb[4] = {0, 0, 0, 0};
+        if constexpr (KIND == 5) {
+            const uint4 hv = *reinterpret_cast<const uint4*>(blk + 16 + 16 * h);
+            hb[0] = hv.x; hb[1] = hv.y; hb[2] = hv.z; hb[3] = hv.w;
+        }
 #pragma unroll
-            for (int i = 0; i < 16; ++i) {
-                vals[i] = d1 * static_cast<float>(q[i] & 0xF) - m1;
-                vals[16 + i] = d2 * static_cast<float>(q[i] >> 4) - m2;
+        for (int w = 0; w < 4; ++w) {
+            uint32_t lo = q[w] & 0x0F0F0F0Fu, hi = (q[w] >> 4) & 0x0F0F0F0Fu;
+            if constexpr (KIND == 5) {
+                lo |= ((hb[w] >> (2 * j)) & 0x01010101u) << 4;
+                hi |= ((hb[w] >> (2 * j + 1)) & 0x01010101u) << 4;
             }
-        } else {
-            uint8_t qh[16];
-            bytes16(blk + 16 + 16 * h, qh);
-#pragma unroll
-            for (int i = 0; i < 16; ++i) {
-                const int lo = (q[i] & 0xF) + (((qh[i] >> (2 * j)) & 1) << 4);
-                const int hi = (q[i] >> 4) + (((qh[i] >> (2 * j + 1)) & 1) << 4);
-                vals[i] = d1 * static_cast<float>(lo) - m1;
-                vals[16 + i] = d2 * static_cast<float>(hi) - m2;
-            }
+            put4(4 * w, lo, d1, m1);
+            put4(16 + 4 * w, hi, d2, m2);
         }
     } else {
         const int half = v >> 2, g = v & 3;
-        uint8_t ql0[8], ql1[8], qh[8];
-        bytes8_u16(blk + 64 * half + 8 * g, ql0);
-        bytes8_u16(blk + 64 * half + 32 + 8 * g, ql1);
-        bytes8_u16(blk + 128 + 32 * half + 8 * g, qh);
+        const uint8_t* lp = blk + 64 * half + 8 * g;
+        const uint8_t* hp = blk + 128 + 32 * half + 8 * g;
 #pragma unroll
-        for (int qd = 0; qd < 4; ++qd) {
-            const float ds = st[8 * half + (g >> 1) + 2 * qd];
+        for (int t = 0; t < 2; ++t) {
+            const uint32_t l0 = ld_u16x2(lp + 4 * t), l1 = ld_u16x2(lp + 32 + 4 * t), hq = ld_u16x2(hp + 4 * t);
 #pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                const uint8_t lb = (qd & 1) ? ql1[i] : ql0[i];
-                const int lo = (qd < 2) ? (lb & 0xF) : (lb >> 4);
-                const int hi = (qh[i] >> (2 * qd)) & 3;
-                vals[8 * qd + i] = ds * static_cast<float>((lo | (hi << 4)) - 32);
+            for (int qd = 0; qd < 4; ++qd) {
+                const float ds = st[8 * half + (g >> 1) + 2 * qd];
+                const uint32_t lb = (qd & 1) ? l1 : l0;
+                const uint32_t lo = qd < 2 ? (lb & 0x0F0F0F0Fu) : ((lb >> 4) & 0x0F0F0F0Fu);
+                const uint32_t u = lo | (((hq >> (2 * qd)) & 0x03030303u) << 4);
+                put4(8 * qd + 4 * t, u, ds, -32.0f * ds);
             }
         }
     }
@@ -152,70 +169,123 @@ __device__ __forceinline__ void store_unit(int8_t* out_blk, int v, const int (&q
     }
 }
 
-template <int KIND>
+// Copy `bytes` (even) from global src to the wave's LDS dst with the widest
+// loads the alignment allows: 16-byte pieces read whole cache lines per
+// instruction, where per-lane 1- and 2-byte reads of the block fields would
+// touch many lines each.
+__device__ __forceinline__ void copy_to_lds(const uint8_t* src, int bytes, uint8_t* dst, int lane) {
+    const uintptr_t a = reinterpret_cast<uintptr_t>(src);
+    if ((a & 15) == 0 && (bytes & 15) == 0) {
+        for (int i = lane; i < bytes / 16; i += 64)
+            reinterpret_cast<uint4*>(dst)[i] = reinterpret_cast<const uint4*>(src)[i];
+    } else if ((a & 3) == 0 && (bytes & 3) == 0) {
+        for (int i = lane; i < bytes / 4; i += 64)
+            reinterpret_cast<uint32_t*>(dst)[i] = reinterpret_cast<const uint32_t*>(src)[i];
+    } else {
+        for (int i = lane; i < bytes / 2; i += 64)
+            reinterpret_cast<uint16_t*>(dst)[i] = reinterpret_cast<const uint16_t*>(src)[i];
+    }
+}
+
+template <int KIND, int HOLD>
 __global__ __launch_bounds__(kWaves * 64) void repack_w8_kernel(const uint8_t* __restrict__ blocks,
                                                                 int64_t n, int nb, int64_t k_pad,
                                                                 int8_t* __restrict__ w8,
                                                                 float* __restrict__ scales) {
     constexpr int BB = block_bytes(KIND);
     __shared__ float lds[kWaves][kChunkBlocks * 16];
+    __shared__ __align__(16) uint8_t raw[kWaves][kChunkBlocks * BB];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int64_t row = static_cast<int64_t>(blockIdx.x) * kWaves + wave;
-    const bool active = row < n;
-    const uint8_t* rowp = blocks + (active ? row : 0) * static_cast<int64_t>(nb) * BB;
-    int8_t* outp = w8 + (active ? row : 0) * k_pad;
+    if (row >= n) return;  // waves share nothing
+    const uint8_t* rowp = blocks + row * static_cast<int64_t>(nb) * BB;
+    int8_t* outp = w8 + row * k_pad;
     float* st = lds[wave];
     const int nchunks = (nb + kChunkBlocks - 1) / kChunkBlocks;
     const int bi = lane >> 3, v = lane & 7;
 
-    float vmax = 0.0f;
+    uint8_t* chunk = raw[wave];
+    // decode chunk c into vals (lanes past the row's blocks decode nothing):
+    // its blocks are copied to the wave's LDS, the factors staged from there.
+    // The wave's LDS operations run in order, so what it wrote is read back
+    // without a barrier.
     int bad = 0;
-    float scale = 1.0f;
-    for (int pass = 0; pass < 2; ++pass) {
-        for (int c = 0; c < nchunks; ++c) {
-            const int b0 = c * kChunkBlocks;
-            const int cnt = min(kChunkBlocks, nb - b0);
-            __syncthreads();
-            if (active) stage_factors<KIND>(rowp + b0 * BB, cnt, lane, st);
-            __syncthreads();
-            if (!active || bi >= cnt) continue;
-            float vals[32];
-            decode_unit<KIND>(rowp + (b0 + bi) * BB, v, st + bi * 16, vals);
-            if (pass == 0) {
+    auto decode = [&](int c, float (&vals)[32]) -> bool {
+        const int b0 = c * kChunkBlocks;
+        const int cnt = min(kChunkBlocks, nb - b0);
+        __builtin_amdgcn_wave_barrier();
+        copy_to_lds(rowp + b0 * BB, cnt * BB, chunk, lane);
+        __builtin_amdgcn_wave_barrier();
+        bad |= stage_factors<KIND>(chunk, cnt, lane, st) ? 1 : 0;
+        __builtin_amdgcn_wave_barrier();
+        if (bi >= cnt) return false;
+        decode_unit<KIND>(chunk + bi * BB, v, st + bi * 16, vals);
+        return true;
+    };
+    float vmax = 0.0f;
+    auto track = [&](const float (&vals)[32]) {
 #pragma unroll
-                for (int i = 0; i < 32; ++i) {
-                    const float a = fabsf(vals[i]);
-                    bad |= !(a <= 3.402823466e38f);
-                    vmax = fmaxf(vmax, a);
-                }
-            } else {
-                int q[32];
+        for (int i = 0; i < 32; i += 2) vmax = fmaxf(vmax, fmaxf(fabsf(vals[i]), fabsf(vals[i + 1])));
+    };
+    float scale = 1.0f, inv = 1.0f;
+    auto finish_max = [&]() {
+        vmax = wave_max_nonneg(vmax);
+        bad = __any(bad) ? 1 : 0;
+        scale = vmax == 0.0f ? 1.0f : vmax / 127.0f;
+        inv = 1.0f / scale;
+    };
+    auto quantise_store = [&](int c, const float (&vals)[32]) {
+        int q[32];
+        quant_sym_rcp(vals, scale, inv, q);
+        if (bad) {
 #pragma unroll
-                for (int i = 0; i < 32; ++i) q[i] = bad ? 0 : quant_sym(vals[i], scale);
-                store_unit<KIND>(outp + (b0 + bi) * kQK, v, q);
-            }
+            for (int i = 0; i < 32; ++i) q[i] = 0;
         }
-        if (pass == 0) {
-            vmax = wave_max(vmax);
-            bad = wave_or(bad);
-            scale = vmax == 0.0f ? 1.0f : vmax / 127.0f;
+        store_unit<KIND>(outp + (c * kChunkBlocks + bi) * kQK, v, q);
+    };
+    if constexpr (HOLD > 0) {
+        float vals[HOLD][32];
+        bool have[HOLD];
+#pragma unroll
+        for (int c = 0; c < HOLD; ++c) {
+            have[c] = c < nchunks && decode(c, vals[c]);
+            if (have[c]) track(vals[c]);
         }
+        finish_max();
+#pragma unroll
+        for (int c = 0; c < HOLD; ++c)
+            if (have[c]) quantise_store(c, vals[c]);
+    } else {
+        float vals[32];
+        for (int c = 0; c < nchunks; ++c)
+            if (decode(c, vals)) track(vals);
+        finish_max();
+        for (int c = 0; c < nchunks; ++c)
+            if (decode(c, vals)) quantise_store(c, vals);
     }
-    if (!active) return;
     for (int64_t i = static_cast<int64_t>(nb) * kQK + 16 * lane; i < k_pad; i += 64 * 16)
         *reinterpret_cast<uint4*>(outp + i) = make_uint4(0, 0, 0, 0);
     if (lane == 0) scales[row] = bad ? __builtin_nanf("") : scale;
+}
+
+template <int KIND>
+void launch_kind(int64_t n, int nb, int64_t k_pad, const uint8_t* blocks, int8_t* w8, float* scales,
+                 hipStream_t stream) {
+    const dim3 grid(static_cast<unsigned>((n + kWaves - 1) / kWaves)), block(kWaves * 64);
+    const int nchunks = (nb + kChunkBlocks - 1) / kChunkBlocks;
+    if (nchunks == 1) repack_w8_kernel<KIND, 1><<<grid, block, 0, stream>>>(blocks, n, nb, k_pad, w8, scales);
+    else if (nchunks == 2) repack_w8_kernel<KIND, 2><<<grid, block, 0, stream>>>(blocks, n, nb, k_pad, w8, scales);
+    else repack_w8_kernel<KIND, 0><<<grid, block, 0, stream>>>(blocks, n, nb, k_pad, w8, scales);
 }
 
 }  // namespace
 
 int launch_repack_w8(int kind, const uint8_t* blocks, int64_t n, int nb, int64_t k_pad, int8_t* w8,
                      float* scales, hipStream_t stream) {
-    const dim3 grid(static_cast<unsigned>((n + kWaves - 1) / kWaves)), block(kWaves * 64);
     switch (kind) {
-    case 4: repack_w8_kernel<4><<<grid, block, 0, stream>>>(blocks, n, nb, k_pad, w8, scales); break;
-    case 5: repack_w8_kernel<5><<<grid, block, 0, stream>>>(blocks, n, nb, k_pad, w8, scales); break;
-    case 6: repack_w8_kernel<6><<<grid, block, 0, stream>>>(blocks, n, nb, k_pad, w8, scales); break;
+    case 4: launch_kind<4>(n, nb, k_pad, blocks, w8, scales, stream); break;
+    case 5: launch_kind<5>(n, nb, k_pad, blocks, w8, scales, stream); break;
+    case 6: launch_kind<6>(n, nb, k_pad, blocks, w8, scales, stream); break;
     default: return kStatusInvalid;
     }
     return hipGetLastError() == hipSuccess ? kStatusOk : kStatusExec;
