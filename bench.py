@@ -18,7 +18,8 @@ repacked Q4_K/Q6_K weights; large and batched decode GEMVs; and the CPU oracle
 timed on the host cores (all usable threads up to 16, and one) as a baseline.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--quick] [--no-cpu]
-       python bench.py --profile {gemv-q4k,gemv-q4k-m4,gemm,gemm-512,gemm-128,copy}   (workload only, for rocprofv3 counter runs)
+       python bench.py --profile {gemv-q4k,gemv-q4k-m4,gemm,gemm-512,gemm-128,repack-q4k,repack-q6k,a8-4096,a8-512,copy}
+           (workload only, for rocprofv3 counter runs)
        python bench.py --vs-hipblaslt   (W8A8 GEMM against torch._int_mm over 140 prefill shapes, one JSON line each)
 """
 from __future__ import annotations
@@ -47,7 +48,8 @@ def parse():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--quick", action="store_true", help="skip the extra W8A8 shapes and the CPU baseline")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
-    ap.add_argument("--profile", choices=["gemv-q4k", "gemv-q4k-m4", "gemm", "gemm-512", "gemm-128", "copy"],
+    ap.add_argument("--profile", choices=["gemv-q4k", "gemv-q4k-m4", "gemm", "gemm-512", "gemm-128", "copy",
+                                          "repack-q4k", "repack-q6k", "a8-4096", "a8-512"],
                     help="run one workload eagerly a few times and exit (for rocprofv3 --pmc passes)")
     ap.add_argument("--vs-hipblaslt", action="store_true",
                     help="time the W8A8 GEMM against torch._int_mm over a grid of prefill shapes and exit")
@@ -442,6 +444,17 @@ def profile_workload(torch, hip, synth, which: str) -> None:
         out = torch.empty((m, n), dtype=torch.float32, device="cuda")
         for _ in range(3):
             hip.gemm_w8a8(a8, asc, w, wsc, out=out)
+    elif which.startswith("repack"):
+        # the roofline entries' shapes: Llama-3-8B gate (Q4_K) and the Llama-3.2-1B head (Q6_K)
+        kind, n, k = (4, 14336, 4096) if which == "repack-q4k" else (6, 128256, 2048)
+        src = torch.from_numpy(synth.kquant(kind, n, k, index=63_000 + kind)).to("cuda")
+        for _ in range(3):
+            hip.repack_w8(kind, src, k, n)
+    elif which.startswith("a8"):
+        m, k = (4096, 4096) if which == "a8-4096" else (512, 5632)
+        x = torch.from_numpy(synth.activations(m, k, index=64_000)).to("cuda")
+        for _ in range(3):
+            hip.quantize_a8(x, hip.k_pad_of(k))
     else:  # a plain copy of known size: 256 MiB read, 256 MiB written
         src = torch.ones(64 << 20, dtype=torch.float32, device="cuda")
         dst = torch.empty_like(src)
