@@ -133,7 +133,9 @@ int rocknpu_hip_gemv_q_f32(uint32_t kind, size_t count, const uint8_t * const * 
  * last call, else 0, and clears the flag. The fused decode entry point of
  * the C ABI (rocknpu_matmul_q_q8k_group_f32_f32) checks it after its own
  * synchronisation and returns ROCKNPU_STATUS_EXECUTION_ERROR. The flag is
- * shared by every stream and thread of the process. No counterpart in the
+ * shared by every stream and thread of the process, and allocated by the
+ * first lane-per-block fused launch (a caller that captures launches into a
+ * HIP graph makes one launch before capturing). No counterpart in the
  * reference, whose decode GEMV runs on the CPU. */
 int rocknpu_hip_gemv_take_stall(void);
 

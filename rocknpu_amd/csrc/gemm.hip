@@ -403,8 +403,11 @@ int launch_gemm_w8a8_skinny(const int8_t* a8, int64_t lda, const int8_t* w8, int
 //   stages when 64 x 32 tiles do not fit but those do (32 x 11264 x 2048:
 //   13.8 -> 9.7 us).
 // - <= 128: 128 x 64 with four stages when 64 x 64 tiles do not fit but those
-//   do (128 x 11264 x 2048: 15.5 -> 11.8 us); else the filling choice without
-//   128-row tiles.
+//   do (128 x 11264 x 2048: 15.5 -> 11.8 us); 128 x 128 with three stages when
+//   64 x 64 tiles would be more than three per CU, 128 x 64 tiles do not fit
+//   and those do (the TinyLlama head, 128 x 32000 x 2048: 28.4 -> 23.8 us with
+//   1000 64 x 64 tiles against 250);
+//   else the filling choice without 128-row tiles.
 // - <= 256: 128 x 128 with three stages when 128 x 64 tiles do not fit but
 //   those do (256 x 11264 x 2048: 19.1 -> 15.5 us); else the filling choice.
 // - above, with a 256 x 256 tile per CU: 256 x 256 tiles, or 256 x 128 tiles
@@ -438,6 +441,7 @@ GemmTile gemm_route(int m, int n, int k, int cus) {
     }
     if (m <= 128) {
         if (tiles(64, 64) > cus && tiles(128, 64) <= cus) return GemmTile{128, 64, 4};
+        if (tiles(64, 64) > 3 * cus && tiles(128, 64) > cus && tiles(128, 128) <= cus) return GemmTile{128, 128, 3};
         return filling(false);
     }
     if (m <= 256) {

@@ -36,6 +36,7 @@ def tiles(m, n, bm, bn):
     (128, 5632, 2048, (64, 64, 4)),      # the 5632 x 2048 Q4_K weight at 128 tokens
     (128, 2048, 2048, (64, 32, 4)),
     (128, 11264, 2048, (128, 64, 4)),    # 64x64 tiles do not fit, 128x64 do
+    (128, 32000, 2048, (128, 128, 3)),   # neither 64x64 nor 128x64 fit, 128x128 do (TinyLlama head)
     (100, 16500, 128, (64, 64, 2)),
     # up to 256 rows
     (256, 11264, 2048, (128, 128, 3)),
