@@ -138,7 +138,9 @@ int rocknpu_matmul_w8a8_f32_f32_m1_nsplit(
     size_t chunk_n);
 
 /* Reference :107-119 (lib.rs:4308-4393): gate/up pair, f32 SwiGLU
- * g * (1 / (1 + exp(-g))) * u, then the down projection. */
+ * g * (1 / (1 + exp(-g))) * u, then the down projection. Here the SwiGLU runs
+ * on the device between the two W8A8 products (the device expf), so the
+ * intermediate never leaves HBM. */
 int rocknpu_matmul_w8a8_swiglu_down_f32(
     rocknpu_context * context,
     const int8_t * gate_weights_nk_i8,

@@ -199,6 +199,18 @@ __global__ void hilo_sum_kernel(float* __restrict__ out, int64_t m, int64_t n) {
     out[idx] = out[idx] + out[m * n + idx];
 }
 
+// h[i] = (g * (1 / (1 + exp(-g)))) * u with g = gu[i], u = gu[n + i]: the
+// reference's SwiGLU between the gate/up and down projections
+// (crates/rocknpu-capi/src/lib.rs:4378-4383), on the device. expf is the
+// device library's (within an ulp or two of the host's std::exp).
+__global__ void swiglu_kernel(const float* __restrict__ gu, float* __restrict__ h, int64_t n) {
+    const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    const float g = gu[i], u = gu[n + i];
+    const float sig = 1.0f / (1.0f + expf(-g));
+    h[i] = g * sig * u;
+}
+
 // Quantise host activations [m, k], run the GEMM against `w`, download and
 // scatter the columns into outs[i] ([m, ns[i]] each, ns summing to w->n).
 // `hilo_ok`: the entry point is one the two-part encoding serves.
@@ -262,21 +274,46 @@ int run_w8a8(RockNpuContext* ctx, const DeviceW8& w, const float* act, size_t m,
 // longer rows are rejected before any weight is uploaded or repacked.
 bool w8a8_k_ok(size_t k) { return round_up(k, 64) <= 133120; }
 
+// The cached W8 of one projection (M > 1 -> prompt cache, M = 1 -> decode
+// cache), built on a miss.
+int single_w8(RockNpuContext* ctx, const Source& src, bool decode, W8Ptr* w, bool* hit) {
+    auto& primary = decode ? ctx->m1 : ctx->mtile;
+    auto& other = decode ? ctx->mtile : ctx->m1;
+    *w = find_w8(primary, other, src.key);
+    *hit = *w != nullptr;
+    if (*hit) return kOk;
+    const int st = build_w8(ctx, {src}, src.key.k, w);
+    if (st != kOk) return st;
+    primary.emplace(src.key, *w);
+    return kOk;
+}
+
+// The cached concatenated W8 of a same-input group, built on a miss.
+int group_w8(RockNpuContext* ctx, const std::vector<Source>& srcs, bool decode, W8Ptr* w, bool* hit) {
+    std::vector<WeightKey> keys;
+    for (const auto& s : srcs) keys.push_back(s.key);
+    auto& cache = decode ? ctx->m1_groups : ctx->mtile_groups;
+    auto it = cache.find(keys);
+    *hit = it != cache.end();
+    if (*hit) {
+        *w = it->second;
+        return kOk;
+    }
+    const int st = build_w8(ctx, srcs, srcs[0].key.k, w);
+    if (st != kOk) return st;
+    cache.emplace(keys, *w);
+    return kOk;
+}
+
 // Cached single-projection W8A8 (M > 1 -> prompt cache, M = 1 -> decode cache).
 int exec_single(RockNpuContext* ctx, const Source& src, const float* act, float* out, size_t m,
                 bool hilo_ok = false) {
     if (!w8a8_k_ok(src.key.k)) return kInvalid;
     const bool decode = m == 1;
     const uint64_t t0 = now_ns();
-    auto& primary = decode ? ctx->m1 : ctx->mtile;
-    auto& other = decode ? ctx->mtile : ctx->m1;
-    W8Ptr w = find_w8(primary, other, src.key);
-    const bool hit = w != nullptr;
-    if (!w) {
-        const int st = build_w8(ctx, {src}, src.key.k, &w);
-        if (st != kOk) return st;
-        primary.emplace(src.key, w);
-    }
+    W8Ptr w;
+    bool hit = false;
+    if (const int st0 = single_w8(ctx, src, decode, &w, &hit); st0 != kOk) return st0;
     const uint64_t t1 = now_ns();
     const int st = run_w8a8(ctx, *w, act, m, src.key.k, {out}, {src.key.n}, decode, hilo_ok);
     const uint64_t t2 = now_ns();
@@ -303,24 +340,12 @@ int exec_group(RockNpuContext* ctx, const std::vector<Source>& srcs, const float
                const std::vector<float*>& outs, bool hilo_ok = false) {
     if (!w8a8_k_ok(srcs[0].key.k)) return kInvalid;
     const bool decode = m == 1;
-    std::vector<WeightKey> keys;
     std::vector<size_t> ns;
-    for (const auto& s : srcs) {
-        keys.push_back(s.key);
-        ns.push_back(s.key.n);
-    }
-    auto& cache = decode ? ctx->m1_groups : ctx->mtile_groups;
+    for (const auto& s : srcs) ns.push_back(s.key.n);
     const uint64_t t0 = now_ns();
     W8Ptr w;
-    auto it = cache.find(keys);
-    const bool hit = it != cache.end();
-    if (hit) {
-        w = it->second;
-    } else {
-        const int st = build_w8(ctx, srcs, srcs[0].key.k, &w);
-        if (st != kOk) return st;
-        cache.emplace(keys, w);
-    }
+    bool hit = false;
+    if (const int st0 = group_w8(ctx, srcs, decode, &w, &hit); st0 != kOk) return st0;
     const int st = run_w8a8(ctx, *w, act, m, srcs[0].key.k, outs, ns, decode, hilo_ok);
     const uint64_t t1 = now_ns();
     if (decode) {
@@ -651,17 +676,62 @@ int rocknpu_matmul_w8a8_swiglu_down_f32(rocknpu_context* ctx, const int8_t* gw, 
         output_n == 0)
         return kInvalid;
     size_t tmp;
-    if (!mul_ok(projection_k, ffn_n, &tmp) || !mul_ok(ffn_n, output_n, &tmp)) return kInvalid;
-    std::vector<float> gate(ffn_n), up(ffn_n);
-    int st = rocknpu_matmul_w8a8_pair_f32_f32_m1(ctx, gw, gs, ffn_n, uw, us, ffn_n, act, gate.data(), up.data(),
-                                                 projection_k);
+    if (!mul_ok(projection_k, ffn_n, &tmp) || !mul_ok(ffn_n, output_n, &tmp) || !scales_ok(gs, ffn_n) ||
+        !scales_ok(us, ffn_n) || !scales_ok(ds, output_n) || ffn_n > (size_t{1} << 40))
+        return kInvalid;
+    if (!w8a8_k_ok(projection_k) || !w8a8_k_ok(ffn_n)) return kInvalid;
+    // The reference runs the gate/up pair and the down projection as two M = 1
+    // calls with the SwiGLU on the host between them (lib.rs:4308-4393); here
+    // the intermediate stays on the device: one upload, one download.
+    const uint64_t t0 = now_ns();
+    W8Ptr wgu, wd;
+    bool hit_gu = false, hit_d = false;
+    int st = group_w8(ctx, {w8_source(gw, gs, projection_k, ffn_n), w8_source(uw, us, projection_k, ffn_n)}, true,
+                      &wgu, &hit_gu);
     if (st != kOk) return st;
-    for (size_t i = 0; i < ffn_n; ++i) {
-        const float g = gate[i], u = up[i];
-        const float sig = 1.0f / (1.0f + std::exp(-g));  // lib.rs:4378-4383
-        gate[i] = g * sig * u;
-    }
-    return rocknpu_matmul_w8a8_f32_f32_m1(ctx, dw, ds, gate.data(), out, ffn_n, output_n);
+    st = single_w8(ctx, w8_source(dw, ds, ffn_n, output_n), true, &wd, &hit_d);
+    if (st != kOk) return st;
+    const size_t gu_n = 2 * ffn_n, a8_bytes = std::max(wgu->k_pad, wd->k_pad);
+    if (!ctx->d_act.ensure((projection_k + ffn_n) * sizeof(float)) || !ctx->d_a8.ensure(2 * a8_bytes) ||
+        !ctx->d_as.ensure(2 * sizeof(float)) || !ctx->d_out.ensure((gu_n + output_n) * sizeof(float)) ||
+        !ctx->h_as.ensure(2 * sizeof(float)) || !ctx->h_out.ensure(output_n * sizeof(float)))
+        return kExec;
+    float* d_x = ctx->d_act.as<float>();
+    float* d_h = d_x + projection_k;
+    float* d_gu = ctx->d_out.as<float>();
+    float* d_y = d_gu + gu_n;
+    int8_t* a8 = ctx->d_a8.as<int8_t>();
+    float* as = ctx->d_as.as<float>();
+    if (!hip_ok(hipMemcpyAsync(d_x, act, projection_k * sizeof(float), hipMemcpyHostToDevice, ctx->stream), ctx,
+                "act"))
+        return kExec;
+    st = rocknpu_hip_quantize_a8(d_x, 1, projection_k, projection_k, wgu->k_pad, a8, as, ctx->stream);
+    if (st == kOk)
+        st = rocknpu_hip_gemm_w8a8(a8, as, wgu->w8, wgu->scales, 1, gu_n, wgu->k_pad, d_gu, gu_n, nullptr,
+                                   ctx->stream);
+    if (st != kOk) return st;
+    swiglu_kernel<<<static_cast<unsigned>((ffn_n + 255) / 256), 256, 0, ctx->stream>>>(d_gu, d_h,
+                                                                                      static_cast<int64_t>(ffn_n));
+    if (!hip_ok(hipGetLastError(), ctx, "swiglu")) return kExec;
+    st = rocknpu_hip_quantize_a8(d_h, 1, ffn_n, ffn_n, wd->k_pad, a8 + a8_bytes, as + 1, ctx->stream);
+    if (st == kOk)
+        st = rocknpu_hip_gemm_w8a8(a8 + a8_bytes, as + 1, wd->w8, wd->scales, 1, output_n, wd->k_pad, d_y,
+                                   output_n, nullptr, ctx->stream);
+    if (st != kOk) return st;
+    if (!hip_ok(hipMemcpyAsync(ctx->h_out.p, d_y, output_n * sizeof(float), hipMemcpyDeviceToHost, ctx->stream),
+                ctx, "download") ||
+        !hip_ok(hipMemcpyAsync(ctx->h_as.p, as, 2 * sizeof(float), hipMemcpyDeviceToHost, ctx->stream), ctx,
+                "download"))
+        return kExec;
+    run_overlap(ctx);
+    if (!hip_ok(hipStreamSynchronize(ctx->stream), ctx, "execute")) return kExec;
+    // two M = 1 calls, as the reference's pair + single
+    record_decode(ctx, hit_gu, t0);
+    record_decode(ctx, hit_d, t0);
+    const float* has = ctx->h_as.as<float>();
+    if (!std::isfinite(has[0]) || !std::isfinite(has[1])) return kInvalid;  // non-finite activation row
+    std::memcpy(out, ctx->h_out.p, output_n * sizeof(float));
+    return kOk;
 }
 
 int rocknpu_matmul_q_pair_f32_f32_mtile(rocknpu_context* ctx, const uint8_t* w1, size_t b1, uint32_t k1, size_t n1,

@@ -374,3 +374,30 @@ def test_gemv_stall_gives_nan_and_execution_error():
         ref = orc.gemv_q8_k(kind, w, k, n, q8, threads=8)
         _, _, mag = orc.gemv_block_sums(kind, w, k, n, q8[0])
         assert np.all(np.abs(h[0].astype(np.float64) - ref[0]) <= 1e-5 * mag)
+
+
+def test_swiglu_down_caches_counts_and_rejects_nonfinite():
+    """The device-side SwiGLU path keeps the reference's bookkeeping: two decode
+    calls per invocation (the pair and the down projection), misses then hits
+    on the decode caches, the same output on a repeat, and a non-finite
+    activation rejected with the output buffer left as it was."""
+    k, ffn, out_n = 1024, 512, 256
+    ws = [synth.q4_k(n, kk, index=2400 + i) for i, (n, kk) in enumerate(((ffn, k), (ffn, k), (out_n, ffn)))]
+    (g8, gs), (u8, us), (d8, ds) = (orc.repack_w8(4, ws[0], k, ffn), orc.repack_w8(4, ws[1], k, ffn),
+                                    orc.repack_w8(4, ws[2], ffn, out_n))
+    x = synth.activations(1, k, index=2410)[0]
+    with Context() as c:
+        out1 = np.zeros(out_n, np.float32)
+        assert c.matmul_w8a8_swiglu_down(g8, gs, u8, us, d8, ds, x, out1, k, ffn, out_n) == STATUS_OK
+        st1 = c.decode_cache_stats()
+        assert (st1.hits, st1.misses) == (0, 2)
+        out2 = np.zeros(out_n, np.float32)
+        assert c.matmul_w8a8_swiglu_down(g8, gs, u8, us, d8, ds, x, out2, k, ffn, out_n) == STATUS_OK
+        st2 = c.decode_cache_stats()
+        assert (st2.hits, st2.misses) == (2, 2)
+        assert np.array_equal(_bits(out1), _bits(out2))
+        bad = x.copy()
+        bad[7] = np.nan
+        out3 = np.full(out_n, 3.0, np.float32)
+        assert c.matmul_w8a8_swiglu_down(g8, gs, u8, us, d8, ds, bad, out3, k, ffn, out_n) == STATUS_INVALID_ARGUMENT
+        assert np.all(out3 == 3.0)
