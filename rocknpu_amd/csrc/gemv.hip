@@ -612,12 +612,13 @@ int launch_kind(GemvParams& p, hipStream_t stream) {
 
 int launch_gemv_mfma(int kind, bool fused, GemvParams& p, hipStream_t stream);  // gemv_mfma.hip
 
-// p.m <= 8 activation rows; LDS holds m * nb * kGemvLdsPerBlock bytes (callers
-// keep it <= 112 KiB). Q4_K with 3..8 rows and Q6_K with 5..8 rows run on the
-// matrix cores, where they are faster (TinyLlama gate+up Q4_K: 8.96 against
-// 9.23 us at 4 rows, 11.6 against 14.3 us at 8; down Q6_K: 13.6 against 20.0
-// us at 6 rows, while at 4 rows the lane-per-block kernel's 11.4 us beats
-// 12.4), except where the exact per-block sums are asked for.
+// The lane-per-block kernel takes p.m <= 8 activation rows; its LDS holds
+// m * nb * kGemvLdsPerBlock bytes (callers keep it <= 112 KiB). Q4_K with 3..16
+// rows and Q6_K with 5..8 rows run on the matrix cores, where they are faster
+// (TinyLlama gate+up Q4_K: 8.96 against 9.23 us at 4 rows, 11.6 against 14.3
+// us at 8; down Q6_K: 13.6 against 20.0 us at 6 rows, while at 4 rows the
+// lane-per-block kernel's 11.4 us beats 12.4), except where the exact
+// per-block sums are asked for.
 // Lanes per block L and waves per workgroup W of the lane-per-block kernel for
 // m activation rows, rows of nb super-blocks, and `count` projections of the
 // given rows, on `cus` CUs.
