@@ -39,9 +39,10 @@ namespace {
 // Integer sum over aligned groups of L lanes (L <= 8), in every lane of the group.
 template <int L>
 __device__ __forceinline__ int sum_lanes(int v) {
-    if constexpr (L >= 2) v += dpp<kDppXor1>(v);
-    if constexpr (L >= 4) v += dpp<kDppXor2>(v);
-    if constexpr (L >= 8) v += dpp<kDppMirror8>(v);
+    // dpp0: the moves fold into v_add_u32_dpp (every lane reads a lane)
+    if constexpr (L >= 2) v += static_cast<int>(dpp0<kDppXor1>(static_cast<unsigned>(v)));
+    if constexpr (L >= 4) v += static_cast<int>(dpp0<kDppXor2>(static_cast<unsigned>(v)));
+    if constexpr (L >= 8) v += static_cast<int>(dpp0<kDppMirror8>(static_cast<unsigned>(v)));
     return v;
 }
 // Sum over lane-index bits [lo, hi) of a value uniform over bits below lo.
@@ -198,6 +199,51 @@ __device__ __forceinline__ void lane_sums(const Piece<4, L>& k, int p, const Q8L
 
 // Q6_K quants are q - 32 with q = 0..63; bsums hold the sums of the 16
 // activation quants of each sub-block, so sum (q-32)*x = sum q*x - 32*bsum.
+// One unit (gu: half h, quarter qa, column c) of block b: 16 ql bytes, the
+// matching 16 qh bytes and the scales of its two sub-blocks s0 and s0 + 4.
+// qs0, bs0: LDS addresses of the quants and bsums of block b of activation
+// row 0 (row mi is mi * nb blocks further).
+template <int MT>
+__device__ __forceinline__ void q6_unit(const v4u& qlv, const v4u& qhv, int sc0, int sc1, int gu, uint32_t qs0,
+                                        uint32_t bs0, int nb, int m, int (&is)[MT]) {
+    const int h = gu >> 2, qa = (gu >> 1) & 1, c = gu & 1;
+    const int s0 = 8 * h + 2 * qa + c;
+    const uint32_t ql[4] = {qlv.x, qlv.y, qlv.z, qlv.w};
+    const uint32_t qh[4] = {qhv.x, qhv.y, qhv.z, qhv.w};
+    const int sh = 2 * qa;
+    // q = low nibble | 2 qh bits << 4. The qh bits of value byte k sit at bits
+    // sh, sh + 1 (low nibbles) and sh + 4, sh + 5 (high nibbles) of qh byte k,
+    // so one shift and one mask per nibble place them (sh <= 2: no bit
+    // crosses a byte).
+    uint32_t u0[4], u1[4];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+        u0[t] = (ql[t] & 0x0F0F0F0Fu) | ((qh[t] << (4 - sh)) & 0x30303030u);
+        u1[t] = ((ql[t] >> 4) & 0x0F0F0F0Fu) | ((qh[t] >> sh) & 0x30303030u);
+    }
+    // LDS addressing in 32 bits
+    const uint32_t qs = qs0 + 128 * h + 32 * qa + 16 * c;
+#pragma unroll
+    for (int mi = 0; mi < MT; ++mi) {
+        if (mi >= m) break;
+        const uint32_t xq = qs + mi * nb * kGemvLdsQsStride;
+        const v4u x0 = *lds_at<v4u>(xq);
+        const v4u x1 = *lds_at<v4u>(xq + 64);
+        int d0 = dot4(u0[0], x0.x, 0);
+        d0 = dot4(u0[1], x0.y, d0);
+        d0 = dot4(u0[2], x0.z, d0);
+        d0 = dot4(u0[3], x0.w, d0);
+        int d1 = dot4(u1[0], x1.x, 0);
+        d1 = dot4(u1[1], x1.y, d1);
+        d1 = dot4(u1[2], x1.z, d1);
+        d1 = dot4(u1[3], x1.w, d1);
+        const auto* bs = lds_at<int16_t>(bs0 + mi * nb * kGemvLdsBsStride);
+        // |d - 32 bsum| <= 16 * 63 * 128 + 32 * 2048 < 2^23 and |sc| <= 128: the
+        // 24-bit products are exact
+        is[mi] += __mul24(sc0, d0 - 32 * bs[s0]) + __mul24(sc1, d1 - 32 * bs[s0 + 4]);
+    }
+}
+
 template <int L, int MT>
 __device__ __forceinline__ void lane_sums(const Piece<6, L>& k, int p, const Q8Lds& a, int nb, int b, int m,
                                           int (&is)[MT], int (&ms)[MT]) {
@@ -211,38 +257,33 @@ __device__ __forceinline__ void lane_sums(const Piece<6, L>& k, int p, const Q8L
         const int h = gu >> 2, qa = (gu >> 1) & 1, c = gu & 1;
         const int hq = L == 1 ? 2 * h + c : (L == 8 ? 0 : c);
         const int s0 = 8 * h + 2 * qa + c;
-        const int sc0 = sbyte(scv, s0), sc1 = sbyte(scv, s0 + 4);
-        const v4u qlv = k.get_ql(u);
-        const uint32_t ql[4] = {qlv.x, qlv.y, qlv.z, qlv.w};
-        const v4u qhv = k.get_qh(hq);
-        const uint32_t qh[4] = {qhv.x, qhv.y, qhv.z, qhv.w};
-        const int sh = 2 * qa;
-        uint32_t u0[4], u1[4];
-#pragma unroll
-        for (int t = 0; t < 4; ++t) {
-            u0[t] = (ql[t] & 0x0F0F0F0Fu) | (((qh[t] >> sh) & 0x03030303u) << 4);
-            u1[t] = ((ql[t] >> 4) & 0x0F0F0F0Fu) | (((qh[t] >> (sh + 4)) & 0x03030303u) << 4);
-        }
-#pragma unroll
-        for (int mi = 0; mi < MT; ++mi) {
-            if (mi >= m) break;
-            const int blk = mi * nb + b;
-            const uint8_t* xq = a.quants(blk) + 128 * h + 32 * qa + 16 * c;
-            const v4u x0 = *reinterpret_cast<const v4u*>(xq);
-            const v4u x1 = *reinterpret_cast<const v4u*>(xq + 64);
-            int d0 = dot4(u0[0], x0.x, 0);
-            d0 = dot4(u0[1], x0.y, d0);
-            d0 = dot4(u0[2], x0.z, d0);
-            d0 = dot4(u0[3], x0.w, d0);
-            int d1 = dot4(u1[0], x1.x, 0);
-            d1 = dot4(u1[1], x1.y, d1);
-            d1 = dot4(u1[2], x1.z, d1);
-            d1 = dot4(u1[3], x1.w, d1);
-            const int16_t* bs = a.bsums(blk);
-            is[mi] += sc0 * (d0 - 32 * bs[s0]) + sc1 * (d1 - 32 * bs[s0 + 4]);
-        }
+        q6_unit<MT>(k.get_ql(u), k.get_qh(hq), sbyte(scv, s0), sbyte(scv, s0 + 4), gu,
+                    a.qs_lds() + b * kGemvLdsQsStride, a.bs_lds() + b * kGemvLdsBsStride, nb, m, is);
     }
 }
+
+// A Q6_K block as the stream kernel stages it in LDS, from a 16-byte-aligned
+// address: 14 pieces of 16 bytes, pieces 0..12 = block bytes 0..207 in place,
+// piece 13 = bytes 194..209 (so d, bytes 208..209, sits at +222). Lane p of
+// the block's 8 takes unit p: ql bytes 16p.., the qh piece 2(p/4) + p%2, the
+// scales of sub-blocks s0 = 8(p/4) + 2(p/2 % 2) + p%2 and s0 + 4.
+constexpr int kQ6Pieces = 14;
+constexpr int kQ6LdsBlock = kQ6Pieces * 16;
+struct Piece6Lds {
+    v4u ql, qh;
+    int sc0, sc1;
+    uint32_t tail;  // d in the upper half, as Piece<6, L>::tail
+    __device__ __forceinline__ void load(const uint8_t* blk, int p) {
+        const int s0 = 8 * (p >> 2) + 2 * ((p >> 1) & 1) + (p & 1);
+        ql = *reinterpret_cast<const v4u*>(blk + 16 * p);
+        qh = *reinterpret_cast<const v4u*>(blk + 128 + 16 * (2 * (p >> 2) + (p & 1)));
+        sc0 = static_cast<int8_t>(blk[192 + s0]);
+        sc1 = static_cast<int8_t>(blk[196 + s0]);
+        tail = static_cast<uint32_t>(*reinterpret_cast<const uint16_t*>(blk + 222)) << 16;
+    }
+};
+
+
 
 template <int L>
 __device__ __forceinline__ void block_scales(const Piece<4, L>& k, float& d, float& dmin) {
@@ -251,6 +292,10 @@ __device__ __forceinline__ void block_scales(const Piece<4, L>& k, float& d, flo
 }
 template <int L>
 __device__ __forceinline__ void block_scales(const Piece<6, L>& k, float& d, float& dmin) {
+    d = f16_bits_to_f32(static_cast<uint16_t>(k.tail >> 16));
+    dmin = 0.0f;
+}
+__device__ __forceinline__ void block_scales(const Piece6Lds& k, float& d, float& dmin) {
     d = f16_bits_to_f32(static_cast<uint16_t>(k.tail >> 16));
     dmin = 0.0f;
 }
@@ -287,6 +332,42 @@ struct GemvArgs {
     int spin_limit;   // fused: polls of the wait for the quantising waves
     int ready_extra;  // fused: arrivals waited for beyond the quantising waves (0; 1 tests the give-up)
 };
+
+// The activations into LDS, after the first weight loads are issued. Fused
+// launches: the quantising waves (whose activation loads went out first)
+// quantise and count themselves in `ready`; every wave (owners too: each
+// reads all blocks) waits for the count. Bounded for safety only: the owners
+// depend on nothing but their own activation loads, so the count arrives. A
+// wave that gives up reports it (host-visible flag) and gets true back, and
+// writes NaN for its outputs. Otherwise the Q8_K rows are copied.
+template <bool FUSED, int THREADS, int QP>
+__device__ __forceinline__ bool stage_activations(const GemvArgs& p, const XPre<THREADS, QP>& xpre, bool quant_wave,
+                                                  int quant_waves, const Q8Lds& a, int& ready) {
+    // The barriers here publish LDS writes only (lgkmcnt(0), then s_barrier):
+    // a fence would also wait for every direct global->LDS load in flight.
+    if constexpr (FUSED) {
+        if (threadIdx.x == 0) ready = 0;
+        asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+        if (quant_wave) {
+            xpre.quantize(p.x, p.ldx, p.m, p.nb, a);
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+            if ((threadIdx.x & 63) == 0) __hip_atomic_fetch_add(&ready, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+        }
+        const int need = quant_waves + p.ready_extra;
+        for (int spin = 0; spin < p.spin_limit; ++spin) {
+            if (__hip_atomic_load(&ready, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) >= need) break;
+            __builtin_amdgcn_s_sleep(1);
+        }
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+        const bool stalled = __hip_atomic_load(&ready, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) < need;
+        if (stalled && (threadIdx.x & 63) == 0) __hip_atomic_store(p.stall, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+        return stalled;
+    } else {
+        stage_q8k<THREADS>(p.q8k, p.ldx, p.m, p.nb, a);
+        asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+        return false;
+    }
+}
 
 // SUMS: also write every block's exact integer sums (p.isum / p.msum).
 // QP: activation quantisation passes whose loads are issued up front.
@@ -369,30 +450,7 @@ __global__ __launch_bounds__(W * 64) void gemv_kernel(const GemvArgs p) {
         load_block(lq, buf[j]);
         advance(lq);
     }
-    if constexpr (FUSED) {
-        if (threadIdx.x == 0) q8_ready = 0;
-        __syncthreads();
-        if (quant_wave) {
-            xpre.quantize(p.x, p.ldx, m, nb, a);
-            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
-            if (lane == 0) __hip_atomic_fetch_add(&q8_ready, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-        }
-        // Every wave (owners too: each reads all blocks) waits for the count.
-        // Bounded for safety only: the owners depend on nothing but their own
-        // activation loads, so the count arrives. A wave that gives up reports
-        // it (host-visible flag) and writes NaN for its outputs.
-        const int need = quant_waves + p.ready_extra;
-        for (int spin = 0; spin < p.spin_limit; ++spin) {
-            if (__hip_atomic_load(&q8_ready, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) >= need) break;
-            __builtin_amdgcn_s_sleep(1);
-        }
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
-        stalled = __hip_atomic_load(&q8_ready, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) < need;
-        if (stalled && lane == 0) __hip_atomic_store(p.stall, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
-    } else {
-        stage_q8k<W * 64>(p.q8k, p.ldx, m, nb, a);
-        __syncthreads();
-    }
+    stalled = stage_activations<FUSED>(p, xpre, quant_wave, quant_waves, a, q8_ready);
 
     float acc[MT];
 #pragma unroll
@@ -446,6 +504,227 @@ __global__ __launch_bounds__(W * 64) void gemv_kernel(const GemvArgs p) {
             advance(cq);
         }
     }
+}
+
+// Q6_K stream kernel: the lane-per-block arithmetic at L = 8 lanes per block
+// and G = 8 block slots per row (one row per row group), with the weights
+// staged in LDS instead of loaded into registers. Q6_K blocks (210 bytes) are
+// only 2-byte aligned; loaded per lane they cost several partial-line
+// requests per 16 bytes, and the L1 request rate then bounds the launch.
+// Here a stream wave moves each step (one row's 8 blocks of one iteration:
+// 1680 contiguous bytes) with two direct global->LDS loads of 16-byte pieces,
+// each piece read from its 2-byte-aligned place in the block and written to a
+// 16-byte-aligned LDS place (Piece6Lds), into a private ring of S step slots
+// kept S steps ahead. Per block the arithmetic and the order of the f32 sums
+// are those of gemv_kernel, so results are bit-identical to it.
+//
+// A workgroup has 16 waves: waves [0, WS) stream rows, waves [8, 16) first
+// stage the activations (quantise f32 rows to Q8_K in LDS, or copy Q8_K
+// rows) and count themselves in `ready`. The helpers' activation loads are
+// issued before the first barrier, so they reach the memory pipeline ahead of
+// every weight load. With WS = 8 the roles are apart: the stream waves issue
+// their first S steps at once and wait for the count. With WS = 16 the helpers
+// stream too, issuing their steps once they are done. No wave has activation
+// loads and direct loads in flight together, which keeps the compiler's
+// wait counts exact (it would otherwise wait for all of them before
+// quantising).
+constexpr int kQ6StepBytes = 8 * kQ6KBytes;      // one step: 8 blocks of a row
+constexpr int kQ6SlotBytes = 8 * kQ6LdsBlock;    // a ring slot: 112 pieces of 16 bytes
+constexpr int kQ6StreamMaxBlocks = 64;           // blocks per row
+constexpr int kQ6Waves = 16;                     // waves per workgroup
+constexpr int kQ6HelperWaves = 8;                // waves [8, 16) stage the activations
+constexpr int kQ6MaxLds = 160 * 1024;
+
+// A direct global->LDS load of 16 bytes per lane (to lds + 16 * lane) that the
+// wait-count pass does not see (inline asm): seen, every later LDS read of
+// the wave would wait for all such loads in flight. The caller waits for it
+// explicitly (wait_vm) before reading its bytes and before the wave ends.
+// The source is base (wave-uniform) + off (this lane's 32-bit offset).
+__device__ __forceinline__ void dma16_untracked(const uint8_t* base, uint32_t off, uint8_t* lds_dst) {
+    const uint32_t lds = static_cast<uint32_t>(
+        reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) uint8_t*)(lds_dst)));
+    asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(off), "s"(base), "s"(lds) : "memory");
+}
+
+// LDS: the activations of m rows (m * nb * kGemvLdsPerBlock bytes, rounded up
+// to 16), then S ring slots of WS waves.
+template <int MT, int WS, int S, bool FUSED, int QP>
+__global__ __launch_bounds__(kQ6Waves * 64) void gemv_q6_stream_kernel(const GemvArgs p) {
+    constexpr int WH = kQ6HelperWaves;
+    static_assert(WS == 8 || WS == 16, "8 or 16 stream waves");
+    static_assert(S == 2 || S == 4, "2 or 4 ring slots");
+    extern __shared__ __align__(16) uint8_t smem[];
+    __shared__ int ready;  // helper waves done staging the activations
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int nb = p.nb, m = p.m, iters = p.iters;
+    const Q8Lds a = q8_lds(smem, m, nb);
+    uint8_t* const ring_base = smem + (m * nb * kGemvLdsPerBlock + 15) / 16 * 16;
+    const bool helper = wave >= kQ6Waves - WH;
+    const int ht = threadIdx.x - (kQ6Waves - WH) * 64;  // thread index among the helpers
+
+    XPre<WH * 64, QP> xpre;
+    if constexpr (FUSED) {
+        if (helper) xpre.issue(p.x, p.ldx, m, nb, ht);
+    }
+    if (threadIdx.x == 0) ready = 0;
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+
+    const int wg = blockIdx.x;
+    const bool c1 = wg >= p.mb[0].wg_end, c2 = wg >= p.mb[1].wg_end, c3 = wg >= p.mb[2].wg_end;
+    auto pick = [&](auto v0, auto v1, auto v2, auto v3) { return c3 ? v3 : c2 ? v2 : c1 ? v1 : v0; };
+    const uint8_t* w = pick(p.mb[0].w, p.mb[1].w, p.mb[2].w, p.mb[3].w);
+    float* out = pick(p.mb[0].out, p.mb[1].out, p.mb[2].out, p.mb[3].out);
+    const int ldo = pick(p.mb[0].ldo, p.mb[1].ldo, p.mb[2].ldo, p.mb[3].ldo);
+    const int rows = pick(p.mb[0].rows, p.mb[1].rows, p.mb[2].rows, p.mb[3].rows);
+    const int wg0 = pick(0, p.mb[0].wg_end, p.mb[1].wg_end, p.mb[2].wg_end);
+    const int wg1 = pick(p.mb[0].wg_end, p.mb[1].wg_end, p.mb[2].wg_end, p.mb[3].wg_end);
+    const gbytes wg_w = reinterpret_cast<gbytes>(reinterpret_cast<uint64_t>(w));
+    const gfloats wg_out = reinterpret_cast<gfloats>(reinterpret_cast<uint64_t>(out));
+
+    const int sl = lane >> 3, pc = lane & 7;  // block slot (block of the step), lane inside the block
+    const int64_t row_bytes = static_cast<int64_t>(nb) * kQ6KBytes;
+    // this wave's rows: wave_gid, wave_gid + wave_stride, ... below `rows`
+    const int wave_gid = (wg - wg0) * WS + wave;
+    const int wave_stride = (wg1 - wg0) * WS;
+    auto advance = [=](Pos& q) {
+        if (++q.it == iters) { q.it = 0; q.gi += wave_stride; }
+    };
+    auto slot = [&](int u) { return ring_base + (u * WS + wave) * kQ6SlotBytes; };
+
+    // The pieces this lane loads in every step: pieces lane and 64 + lane
+    // (the second for lanes below 48) of the step's 8 x 14: block pb, byte po
+    // of the block, byte so = 210 pb + po of the step.
+    int pb[2], po[2], so[2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        const int q = min(64 * i + lane, 8 * kQ6Pieces - 1);
+        pb[i] = q / kQ6Pieces;
+        const int g = q - kQ6Pieces * pb[i];
+        po[i] = (g < kQ6Pieces - 1 ? 16 * g : kQ6KBytes - 16);
+        so[i] = pb[i] * kQ6KBytes + po[i];
+    }
+    // Issue step q (one of the wave's, q.gi < rows) into ring slot u: two
+    // loads from the row's start plus 32-bit offsets. In a row's last step,
+    // blocks past the row's end load the same piece of the row's block 0 (in
+    // bounds, never read).
+    auto issue = [&](const Pos& q, int u) {
+        const uint8_t* row_start =
+            reinterpret_cast<const uint8_t*>(reinterpret_cast<uint64_t>(wg_w + static_cast<int64_t>(q.gi) * row_bytes));
+        const int step0 = q.it * kQ6StepBytes;
+        uint32_t off[2];
+        if (q.it * 8 + 8 <= nb) {
+#pragma unroll
+            for (int i = 0; i < 2; ++i) off[i] = static_cast<uint32_t>(step0 + so[i]);
+        } else {
+#pragma unroll
+            for (int i = 0; i < 2; ++i) off[i] = static_cast<uint32_t>(q.it * 8 + pb[i] < nb ? step0 + so[i] : po[i]);
+        }
+        uint8_t* dst = slot(u);
+        dma16_untracked(row_start, off[0], dst);
+        if (lane < 8 * kQ6Pieces - 64) dma16_untracked(row_start, off[1], dst + 1024);
+    };
+    // Only the wave's own steps are loaded, so nothing is left in flight at
+    // its end. `ahead`: steps loaded after the current one.
+    Pos lq{wave_gid, 0};  // next step to load
+    int ahead = -1;
+    auto first_fill = [&] {
+#pragma unroll
+        for (int u = 0; u < S; ++u)
+            if (lq.gi < rows) {
+                issue(lq, u);
+                advance(lq);
+                ++ahead;
+            }
+    };
+    const bool streams = wave < WS;
+    if (streams && !helper) first_fill();
+
+    if (helper) {
+        if constexpr (FUSED) xpre.quantize(p.x, p.ldx, m, nb, a, ht);
+        else stage_q8k<WH * 64>(p.q8k, p.ldx, m, nb, a, ht);
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+        if (lane == 0) __hip_atomic_fetch_add(&ready, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+        if (!streams) return;
+        first_fill();
+    }
+
+    // Wait for the helpers. Bounded for safety only: they depend on nothing
+    // but their own activation loads, so the count arrives. A wave that gives
+    // up reports it (host-visible flag) and writes NaN for its outputs.
+    const int need = WH + p.ready_extra;
+    for (int spin = 0; spin < p.spin_limit; ++spin) {
+        if (__hip_atomic_load(&ready, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) >= need) break;
+        __builtin_amdgcn_s_sleep(1);
+    }
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+    const bool stalled = __hip_atomic_load(&ready, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) < need;
+    if (stalled && lane == 0) __hip_atomic_store(p.stall, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+
+    float acc[MT];
+#pragma unroll
+    for (int mi = 0; mi < MT; ++mi) acc[mi] = 0.0f;
+    // this lane's activation addresses for block slot sl of row 0 (the steps
+    // add uniform offsets)
+    const uint32_t lane_qs = a.qs_lds() + sl * kGemvLdsQsStride;
+    const uint32_t lane_bs = a.bs_lds() + sl * kGemvLdsBsStride;
+    const uint32_t lane_d = a.d_lds() + 4 * sl;
+    Pos cq{wave_gid, 0};  // step being multiplied
+    for (int u = 0; cq.gi < rows; u = u + 1 == S ? 0 : u + 1) {
+        // this step's two loads have landed: at most 2 * ahead loads younger
+        // than them are in flight (row-end stores only add to the count)
+        switch (ahead) {
+        case 3: wait_vm<6>(); break;
+        case 2: wait_vm<4>(); break;
+        case 1: wait_vm<2>(); break;
+        default: wait_vm<0>(); break;
+        }
+        asm volatile("" ::: "memory");
+        Piece6Lds k;
+        k.load(slot(u) + sl * kQ6LdsBlock, pc);
+        const int row = cq.gi;
+        // Lanes past the row's end (b < nb + 8) read activation bytes past
+        // their row: still inside the workgroup's LDS (the ring follows the
+        // activations), and their term is dropped by a select.
+        const int b = sl + cq.it * 8;
+        const bool have = b < nb;
+        int is[MT];
+#pragma unroll
+        for (int mi = 0; mi < MT; ++mi) is[mi] = 0;
+        const int b0 = cq.it * 8;  // uniform part of b
+        q6_unit<MT>(k.ql, k.qh, k.sc0, k.sc1, pc, lane_qs + b0 * kGemvLdsQsStride, lane_bs + b0 * kGemvLdsBsStride,
+                    nb, m, is);
+        float dw, dminw;
+        block_scales(k, dw, dminw);
+#pragma unroll
+        for (int mi = 0; mi < MT; ++mi) {
+            if (mi >= m) break;
+            const int isum = sum_lanes<8>(is[mi]);
+            const float da = *lds_at<float>(lane_d + 4 * (mi * nb + b0));
+            const float term = (dw * da) * static_cast<float>(isum);
+            acc[mi] += have ? term : 0.0f;
+        }
+        if (cq.it == iters - 1) {
+            // row done: add its 8 slot sums and store
+#pragma unroll
+            for (int mi = 0; mi < MT; ++mi) {
+                const float r = sum_bits(acc[mi], 3, 6);
+                if (lane == 0 && mi < m) wg_out[mi * ldo + row] = stalled ? __builtin_nanf("") : r;
+                acc[mi] = 0.0f;
+            }
+        }
+        // the slot's LDS reads are done before its refill is issued
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        if (lq.gi < rows) {
+            issue(lq, u);
+            advance(lq);
+        } else {
+            --ahead;
+        }
+        advance(cq);
+    }
+    // every load has landed (and been read) before the wave ends
+    wait_vm<0>();
 }
 
 // Most blocks in flight per lane, by kind and lanes per block: 64-150 bytes
@@ -532,28 +811,30 @@ int* stall_flag() {
     return flag;
 }
 
-template <int KIND, bool FUSED>
-int launch_kind(GemvParams& p, hipStream_t stream) {
-    const bool sums = !FUSED && p.isum != nullptr;
-    const int cus = device_cu_count();
-    const int mt = p.m <= 1 ? 1 : p.m <= 2 ? 2 : p.m <= 4 ? 4 : 8;
-    // At most 8 slots per row whatever L is: a row's f32 sum then runs in the
-    // same order for every L and every grouping of projections.
-    p.log2g = slots_per_row_log2(p.nb, 8);
-    const int G = 1 << p.log2g;
-    p.iters = (p.nb + G - 1) / G;
-    const GemvLanes shape = gemv_lanes(FUSED, sums, p.m, p.nb, p.rows, p.count, cus);
-    const int L = shape.lanes, W = shape.waves;
-    const int64_t max_wgs = cus;
-    const int64_t rows_per_group = 64 / L / G;
-    // Workgroups: at most one per CU and one per W row groups, split between
-    // the projections in proportion to their row groups; blocks in flight per
-    // lane = the blocks a wave ends up with, up to the kernel's most.
+// The bounded wait for the activations: the stall flag, the polls allowed,
+// and the extra arrivals a test of the give-up asks for.
+int set_wait(GemvArgs& ka) {
+    ka.stall = stall_flag();
+    if (ka.stall == nullptr) return kStatusExec;
+    const int test_spins = g_test_stall_spins.load(std::memory_order_relaxed);
+    ka.spin_limit = test_spins > 0 ? test_spins : 1 << 24;
+    ka.ready_extra = test_spins > 0 ? 1 : 0;
+    return kStatusOk;
+}
+
+// Kernel arguments for W-wave workgroups and row groups of rows_per_group
+// rows: at most one workgroup per CU and one per W row groups, split between
+// the projections in proportion to their row groups. Sets wgs and per_wave
+// (the most row groups a wave gets, times p.iters).
+template <bool FUSED>
+int plan_args(const GemvParams& p, int W, int64_t rows_per_group, int cus, GemvArgs& ka, int64_t& wgs,
+              int64_t& per_wave) {
     int64_t total_groups = 0;
     for (int i = 0; i < p.count; ++i) total_groups += (p.rows[i] + rows_per_group - 1) / rows_per_group;
-    const int64_t budget = std::max<int64_t>(p.count, std::min<int64_t>(max_wgs, (total_groups + W - 1) / W));
-    GemvArgs ka{};
-    int64_t wgs = 0, per_wave = 1;
+    const int64_t budget = std::max<int64_t>(p.count, std::min<int64_t>(cus, (total_groups + W - 1) / W));
+    ka = GemvArgs{};
+    wgs = 0;
+    per_wave = 1;
     for (int i = 0; i < p.count; ++i) {
         const int64_t groups = (p.rows[i] + rows_per_group - 1) / rows_per_group;
         int64_t n = (budget * groups + total_groups / 2) / total_groups;
@@ -577,13 +858,94 @@ int launch_kind(GemvParams& p, hipStream_t stream) {
     ka.nb = p.nb;
     ka.log2g = p.log2g;
     ka.iters = p.iters;
-    if constexpr (FUSED) {
-        ka.stall = stall_flag();
-        if (ka.stall == nullptr) return kStatusExec;
-        const int test_spins = g_test_stall_spins.load(std::memory_order_relaxed);
-        ka.spin_limit = test_spins > 0 ? test_spins : 1 << 24;
-        ka.ready_extra = test_spins > 0 ? 1 : 0;
+    if constexpr (FUSED) return set_wait(ka);
+    return kStatusOk;
+}
+
+// The Q6_K stream kernel serves up to 4 activation rows, rows of at most
+// kQ6StreamMaxBlocks blocks split into 8 slots (slots_per_row_log2 = 3), and
+// no exact-sums output.
+bool q6_stream_fits(int m, int nb, bool sums) {
+    return !sums && m >= 1 && m <= 4 && nb <= kQ6StreamMaxBlocks && slots_per_row_log2(nb, 8) == 3;
+}
+
+template <int MT, int WS, bool FUSED>
+void launch_q6_stream_ws(const GemvArgs& ka, int passes, int slots, size_t lds, dim3 grid, hipStream_t stream) {
+    const dim3 block(kQ6Waves * 64);
+    auto go = [&](auto s) {
+        constexpr int S = decltype(s)::value;
+        // activation passes loaded up front by the helpers (their VGPRs hold four)
+        if constexpr (FUSED) {
+            if (passes > 2) return gemv_q6_stream_kernel<MT, WS, S, FUSED, 4><<<grid, block, lds, stream>>>(ka);
+            if (passes > 1) return gemv_q6_stream_kernel<MT, WS, S, FUSED, 2><<<grid, block, lds, stream>>>(ka);
+        }
+        gemv_q6_stream_kernel<MT, WS, S, FUSED, 1><<<grid, block, lds, stream>>>(ka);
+    };
+    if (slots >= 4) go(std::integral_constant<int, 4>{});
+    else go(std::integral_constant<int, 2>{});
+}
+
+// One row per row group and stream wave: 16 stream waves for 2 or more
+// activation rows where the rows give every CU 16 (the helpers then stream
+// too), else 8. Ring slots: 4 where the LDS holds them beside the activations,
+// else 2. Deeper rings measured slower: the larger first burst of weight loads
+// delays the activation loads behind it in the memory system (Llama-3-8B down,
+// 4096 x 14336, one row: 13.4 us with 4 slots, 15.7 us with 8).
+// Llama-3-8B down at one row runs 13.4 us with 8 stream waves against 14.6
+// with 16 (the helpers' rows start after the quantisation and end last); at 2
+// and 4 rows 16 waves win (16.0 against 16.5 us, 22.4 against 24.8 us).
+template <bool FUSED>
+int launch_q6_stream(GemvParams& p, hipStream_t stream) {
+    const int cus = device_cu_count();
+    const int mt = p.m <= 1 ? 1 : p.m <= 2 ? 2 : 4;
+    p.log2g = 3;
+    p.iters = (p.nb + 7) / 8;
+    int64_t rows = 0;
+    for (int i = 0; i < p.count; ++i) rows += p.rows[i];
+    const int WS = p.m > 1 && rows >= 16 * static_cast<int64_t>(cus) ? 16 : 8;
+    const size_t act = (static_cast<size_t>(p.m) * p.nb * kGemvLdsPerBlock + 15) / 16 * 16;
+    const int fit = static_cast<int>((kQ6MaxLds - 64 - act) / (WS * kQ6SlotBytes));
+    const int slots = fit >= 4 ? 4 : 2;
+    if (fit < 2) return kStatusInvalid;  // q6_stream_fits keeps m * nb small enough
+    const size_t lds = act + static_cast<size_t>(slots) * WS * kQ6SlotBytes;
+    GemvArgs ka;
+    int64_t wgs = 0, per_wave = 0;
+    int st = plan_args<FUSED>(p, WS, 1, cus, ka, wgs, per_wave);
+    if (st == kStatusOk && !FUSED) st = set_wait(ka);  // Q8_K rows are staged by the helpers too
+    if (st != kStatusOk) return st;
+    const int passes = (p.m * p.nb + kQ6HelperWaves * 4 - 1) / (kQ6HelperWaves * 4);  // 16 lanes per block
+    const dim3 grid(static_cast<unsigned>(wgs));
+    if (WS == 16) {
+        if (mt == 1) launch_q6_stream_ws<1, 16, FUSED>(ka, passes, slots, lds, grid, stream);
+        else if (mt == 2) launch_q6_stream_ws<2, 16, FUSED>(ka, passes, slots, lds, grid, stream);
+        else launch_q6_stream_ws<4, 16, FUSED>(ka, passes, slots, lds, grid, stream);
+    } else {
+        if (mt == 1) launch_q6_stream_ws<1, 8, FUSED>(ka, passes, slots, lds, grid, stream);
+        else if (mt == 2) launch_q6_stream_ws<2, 8, FUSED>(ka, passes, slots, lds, grid, stream);
+        else launch_q6_stream_ws<4, 8, FUSED>(ka, passes, slots, lds, grid, stream);
     }
+    return hipGetLastError() == hipSuccess ? kStatusOk : kStatusExec;
+}
+
+template <int KIND, bool FUSED>
+int launch_kind(GemvParams& p, hipStream_t stream) {
+    const bool sums = !FUSED && p.isum != nullptr;
+    const int cus = device_cu_count();
+    const int mt = p.m <= 1 ? 1 : p.m <= 2 ? 2 : p.m <= 4 ? 4 : 8;
+    // At most 8 slots per row whatever L is: a row's f32 sum then runs in the
+    // same order for every L and every grouping of projections.
+    p.log2g = slots_per_row_log2(p.nb, 8);
+    const int G = 1 << p.log2g;
+    p.iters = (p.nb + G - 1) / G;
+    const GemvLanes shape = gemv_lanes(FUSED, sums, p.m, p.nb, p.rows, p.count, cus);
+    const int L = shape.lanes, W = shape.waves;
+    const int64_t rows_per_group = 64 / L / G;
+    // blocks in flight per lane = the blocks a wave ends up with, up to the
+    // kernel's most
+    GemvArgs ka;
+    int64_t wgs = 0, per_wave = 1;
+    const int st = plan_args<FUSED>(p, W, rows_per_group, cus, ka, wgs, per_wave);
+    if (st != kStatusOk) return st;
     // Blocks in flight per lane: one Q6_K block, and Q4_K blocks for 16 per
     // CU and lane position (two with 8 waves, one with 16). More measured
     // slower in every shape (the memory pipeline of a CU is full with fewer):
@@ -679,6 +1041,8 @@ bool gemv_uses_mfma(int kind, int m, int nb, int64_t rows, int cus) {
 int launch_gemv(int kind, bool fused, GemvParams& p, hipStream_t stream) {
     int64_t rows = 0;
     for (int i = 0; i < p.count; ++i) rows += p.rows[i];
+    if (kind == 6 && q6_stream_fits(p.m, p.nb, p.isum != nullptr))
+        return fused ? launch_q6_stream<true>(p, stream) : launch_q6_stream<false>(p, stream);
     if (gemv_uses_mfma(kind, p.m, p.nb, rows, device_cu_count()) && p.isum == nullptr)
         return launch_gemv_mfma(kind, fused, p, stream);
     if (kind == 4) return fused ? launch_kind<4, true>(p, stream) : launch_kind<4, false>(p, stream);

@@ -6,8 +6,23 @@
 
 #include "common.h"
 
+#include <utility>
+
 namespace rk {
 namespace {
+
+// Calls f(integral_constant<int, I>) for I in the sequence, in order.
+template <typename F, int... I>
+__device__ __forceinline__ void unroll_seq(F&& f, std::integer_sequence<int, I...>) {
+    (f(std::integral_constant<int, I>{}), ...);
+}
+
+// s_waitcnt with only vmcnt constrained (gfx9 encoding: vmcnt[3:0] | expcnt[6:4]
+// | lgkmcnt[11:8] | vmcnt[5:4] at bits 15:14).
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+    __builtin_amdgcn_s_waitcnt((N & 0xF) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
+}
 
 template <int CTRL>
 __device__ __forceinline__ int dpp(int v) {
@@ -59,7 +74,19 @@ struct Q8Lds {
     __device__ __forceinline__ const int16_t* bsums(int blk) const {
         return reinterpret_cast<const int16_t*>(bs + blk * kGemvLdsBsStride);
     }
+    // the arrays' LDS byte addresses, for 32-bit address arithmetic (lds_at)
+    __device__ __forceinline__ uint32_t qs_lds() const { return lds_addr(qs); }
+    __device__ __forceinline__ uint32_t bs_lds() const { return lds_addr(bs); }
+    __device__ __forceinline__ uint32_t d_lds() const { return lds_addr(d); }
+    __device__ __forceinline__ static uint32_t lds_addr(const void* p) {
+        return static_cast<uint32_t>(reinterpret_cast<uintptr_t>((const __attribute__((address_space(3))) void*)(p)));
+    }
 };
+// An LDS pointer from a 32-bit LDS byte address.
+template <typename T>
+__device__ __forceinline__ const __attribute__((address_space(3))) T* lds_at(uint32_t a) {
+    return reinterpret_cast<const __attribute__((address_space(3))) T*>(static_cast<uintptr_t>(a));
+}
 
 __device__ __forceinline__ Q8Lds q8_lds(uint8_t* smem, int mt, int nb) {
     Q8Lds a;
@@ -174,14 +201,23 @@ __device__ __forceinline__ void quantize_block_to_lds(const float4 (&f)[4], int 
 template <int THREADS, int P>
 struct XPre {
     float4 f[P][4];
+    // t: this thread's index among the THREADS that quantise (default: the
+    // workgroup's first THREADS)
     __device__ __forceinline__ void issue(const float* __restrict__ x, int64_t ldx, int m, int nb) {
-        const int slot = threadIdx.x >> 4, last = m * nb - 1;
+        issue(x, ldx, m, nb, static_cast<int>(threadIdx.x));
+    }
+    __device__ __forceinline__ void issue(const float* __restrict__ x, int64_t ldx, int m, int nb, int t) {
+        const int slot = t >> 4, last = m * nb - 1;
 #pragma unroll
         for (int i = 0; i < P; ++i) load_x16(x, ldx, nb, min(slot + i * (THREADS / 16), last), f[i]);
     }
     __device__ __forceinline__ void quantize(const float* __restrict__ x, int64_t ldx, int m, int nb,
                                              const Q8Lds& a) const {
-        const int slot = threadIdx.x >> 4;
+        quantize(x, ldx, m, nb, a, static_cast<int>(threadIdx.x));
+    }
+    __device__ __forceinline__ void quantize(const float* __restrict__ x, int64_t ldx, int m, int nb,
+                                             const Q8Lds& a, int t) const {
+        const int slot = t >> 4;
 #pragma unroll
         for (int i = 0; i < P; ++i) {
             const int qb = slot + i * (THREADS / 16);
@@ -197,11 +233,12 @@ struct XPre {
 
 // Copy Q8_K rows (292-byte blocks: f32 d, 256 quants, 16 int16 bsums) into
 // the LDS layout, one 32-bit word per thread and step.
+// t: this thread's index among the THREADS that copy.
 template <int THREADS>
 __device__ __forceinline__ void stage_q8k(const uint8_t* __restrict__ q8k, int64_t ldq, int m, int nb,
-                                          const Q8Lds& a) {
+                                          const Q8Lds& a, int t) {
     const int words = m * nb * (kQ8KBytes / 4);
-    for (int i = threadIdx.x; i < words; i += THREADS) {
+    for (int i = t; i < words; i += THREADS) {
         const int blk = i / (kQ8KBytes / 4), wi = i % (kQ8KBytes / 4);
         const int mi = blk / nb, bi = blk % nb;
         const uint32_t v = *reinterpret_cast<const uint32_t*>(q8k + mi * ldq + bi * kQ8KBytes + 4 * wi);
@@ -209,6 +246,11 @@ __device__ __forceinline__ void stage_q8k(const uint8_t* __restrict__ q8k, int64
         else if (wi <= 64) reinterpret_cast<uint32_t*>(a.qs + blk * kGemvLdsQsStride)[wi - 1] = v;
         else reinterpret_cast<uint32_t*>(a.bs + blk * kGemvLdsBsStride)[wi - 65] = v;
     }
+}
+template <int THREADS>
+__device__ __forceinline__ void stage_q8k(const uint8_t* __restrict__ q8k, int64_t ldq, int m, int nb,
+                                          const Q8Lds& a) {
+    stage_q8k<THREADS>(q8k, ldq, m, nb, a, static_cast<int>(threadIdx.x));
 }
 
 }  // namespace

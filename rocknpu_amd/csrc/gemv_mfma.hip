@@ -40,11 +40,6 @@ namespace {
 
 typedef int v4i __attribute__((ext_vector_type(4)));
 
-// Calls f(integral_constant<int, I>) for I in the sequence, in order.
-template <typename F, int... I>
-__device__ __forceinline__ void unroll_seq(F&& f, std::integer_sequence<int, I...>) {
-    (f(std::integral_constant<int, I>{}), ...);
-}
 typedef short v2s __attribute__((ext_vector_type(2)));
 
 constexpr int kTileRows = 16;
@@ -532,13 +527,6 @@ constexpr int kDmaLoads = 3;                                     // loads per wa
 __device__ __forceinline__ int stage_chunk(int r, int c) {
     const int p = c + 2 * r;
     return p >= kStageRowChunks ? p - kStageRowChunks : p;
-}
-
-// s_waitcnt with only vmcnt constrained (gfx9 encoding: vmcnt[3:0] | expcnt[6:4]
-// | lgkmcnt[11:8] | vmcnt[5:4] at bits 15:14).
-template <int N>
-__device__ __forceinline__ void wait_vm() {
-    __builtin_amdgcn_s_waitcnt((N & 0xF) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
 }
 
 // LDS of a staged launch, all of it in arrays of fixed size (a direct load's
