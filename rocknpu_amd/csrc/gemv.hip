@@ -518,21 +518,17 @@ __global__ __launch_bounds__(W * 64) void gemv_kernel(const GemvArgs p) {
 // kept S steps ahead. Per block the arithmetic and the order of the f32 sums
 // are those of gemv_kernel, so results are bit-identical to it.
 //
-// A workgroup has 16 waves: waves [0, WS) stream rows, waves [8, 16) first
-// stage the activations (quantise f32 rows to Q8_K in LDS, or copy Q8_K
-// rows) and count themselves in `ready`. The helpers' activation loads are
-// issued before the first barrier, so they reach the memory pipeline ahead of
-// every weight load. With WS = 8 the roles are apart: the stream waves issue
-// their first S steps at once and wait for the count. With WS = 16 the helpers
-// stream too, issuing their steps once they are done. No wave has activation
-// loads and direct loads in flight together, which keeps the compiler's
-// wait counts exact (it would otherwise wait for all of them before
-// quantising).
+// A workgroup has 16 waves; waves [0, WS) stream rows (WS = 8 or 16). Every
+// wave first loads its share of the activations (all passes at once), waits
+// for them, then issues its first S steps and quantises from registers (or
+// copies Q8_K rows, then issues), counts itself in `ready` and waits for all
+// 16. Activation loads thus reach the memory system before any weight load,
+// and no wave has both in flight (the compiler's wait counts would otherwise
+// wait for all of them before quantising).
 constexpr int kQ6StepBytes = 8 * kQ6KBytes;      // one step: 8 blocks of a row
 constexpr int kQ6SlotBytes = 8 * kQ6LdsBlock;    // a ring slot: 112 pieces of 16 bytes
 constexpr int kQ6StreamMaxBlocks = 64;           // blocks per row
 constexpr int kQ6Waves = 16;                     // waves per workgroup
-constexpr int kQ6HelperWaves = 8;                // waves [8, 16) stage the activations
 constexpr int kQ6MaxLds = 160 * 1024;
 
 // A direct global->LDS load of 16 bytes per lane (to lds + 16 * lane) that the
@@ -550,23 +546,18 @@ __device__ __forceinline__ void dma16_untracked(const uint8_t* base, uint32_t of
 // to 16), then S ring slots of WS waves.
 template <int MT, int WS, int S, bool FUSED, int QP>
 __global__ __launch_bounds__(kQ6Waves * 64) void gemv_q6_stream_kernel(const GemvArgs p) {
-    constexpr int WH = kQ6HelperWaves;
     static_assert(WS == 8 || WS == 16, "8 or 16 stream waves");
     static_assert(S == 2 || S == 4, "2 or 4 ring slots");
     extern __shared__ __align__(16) uint8_t smem[];
-    __shared__ int ready;  // helper waves done staging the activations
+    __shared__ int ready;  // waves done staging their share of the activations
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int nb = p.nb, m = p.m, iters = p.iters;
     const Q8Lds a = q8_lds(smem, m, nb);
     uint8_t* const ring_base = smem + (m * nb * kGemvLdsPerBlock + 15) / 16 * 16;
-    const bool helper = wave >= kQ6Waves - WH;
-    const int ht = threadIdx.x - (kQ6Waves - WH) * 64;  // thread index among the helpers
 
-    XPre<WH * 64, QP> xpre;
-    if constexpr (FUSED) {
-        if (helper) xpre.issue(p.x, p.ldx, m, nb, ht);
-    }
+    XPre<kQ6Waves * 64, QP> xpre;
+    if constexpr (FUSED) xpre.issue(p.x, p.ldx, m, nb);
     if (threadIdx.x == 0) ready = 0;
     asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 
@@ -585,7 +576,9 @@ __global__ __launch_bounds__(kQ6Waves * 64) void gemv_q6_stream_kernel(const Gem
     const int sl = lane >> 3, pc = lane & 7;  // block slot (block of the step), lane inside the block
     const int64_t row_bytes = static_cast<int64_t>(nb) * kQ6KBytes;
     // this wave's rows: wave_gid, wave_gid + wave_stride, ... below `rows`
-    const int wave_gid = (wg - wg0) * WS + wave;
+    // (none for waves WS and up)
+    const bool streams = wave < WS;
+    const int wave_gid = streams ? (wg - wg0) * WS + wave : rows;
     const int wave_stride = (wg1 - wg0) * WS;
     auto advance = [=](Pos& q) {
         if (++q.it == iters) { q.it = 0; q.gi += wave_stride; }
@@ -628,31 +621,38 @@ __global__ __launch_bounds__(kQ6Waves * 64) void gemv_q6_stream_kernel(const Gem
     // its end. `ahead`: steps loaded after the current one.
     Pos lq{wave_gid, 0};  // next step to load
     int ahead = -1;
-    auto first_fill = [&] {
-#pragma unroll
-        for (int u = 0; u < S; ++u)
+    auto fill = [&](int u0, int u1) {
+        for (int u = u0; u < u1; ++u)
             if (lq.gi < rows) {
                 issue(lq, u);
                 advance(lq);
                 ++ahead;
             }
     };
-    const bool streams = wave < WS;
-    if (streams && !helper) first_fill();
 
-    if (helper) {
-        if constexpr (FUSED) xpre.quantize(p.x, p.ldx, m, nb, a, ht);
-        else stage_q8k<WH * 64>(p.q8k, p.ldx, m, nb, a, ht);
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
-        if (lane == 0) __hip_atomic_fetch_add(&ready, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-        if (!streams) return;
-        first_fill();
+    // The first step goes out before the quantisation and the rest after:
+    // issuing all S first stalls the waves at a full memory pipeline before
+    // they quantise (TinyLlama down, 2048 x 5632: 6.2 -> 5.7 us at one row,
+    // 8.65 -> 8.15 at four).
+    if constexpr (FUSED) {
+        // the activation loads have landed (an explicit wait: the quantisation
+        // below then waits for nothing, and the direct loads are not waited for)
+        wait_vm<0>();
+        fill(0, 1);
+        xpre.quantize(p.x, p.ldx, m, nb, a);
+    } else {
+        stage_q8k<kQ6Waves * 64>(p.q8k, p.ldx, m, nb, a);
+        fill(0, 1);
     }
+    fill(1, S);
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+    if (lane == 0) __hip_atomic_fetch_add(&ready, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    if (!streams) return;
 
-    // Wait for the helpers. Bounded for safety only: they depend on nothing
-    // but their own activation loads, so the count arrives. A wave that gives
-    // up reports it (host-visible flag) and writes NaN for its outputs.
-    const int need = WH + p.ready_extra;
+    // Wait for every wave's share. Bounded for safety only: each depends on
+    // nothing but its own activation loads, so the count arrives. A wave that
+    // gives up reports it (host-visible flag) and writes NaN for its outputs.
+    const int need = kQ6Waves + p.ready_extra;
     for (int spin = 0; spin < p.spin_limit; ++spin) {
         if (__hip_atomic_load(&ready, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) >= need) break;
         __builtin_amdgcn_s_sleep(1);
@@ -874,7 +874,7 @@ void launch_q6_stream_ws(const GemvArgs& ka, int passes, int slots, size_t lds, 
     const dim3 block(kQ6Waves * 64);
     auto go = [&](auto s) {
         constexpr int S = decltype(s)::value;
-        // activation passes loaded up front by the helpers (their VGPRs hold four)
+        // activation passes, all loaded up front (q6_stream_fits keeps them <= 4)
         if constexpr (FUSED) {
             if (passes > 2) return gemv_q6_stream_kernel<MT, WS, S, FUSED, 4><<<grid, block, lds, stream>>>(ka);
             if (passes > 1) return gemv_q6_stream_kernel<MT, WS, S, FUSED, 2><<<grid, block, lds, stream>>>(ka);
@@ -886,14 +886,13 @@ void launch_q6_stream_ws(const GemvArgs& ka, int passes, int slots, size_t lds, 
 }
 
 // One row per row group and stream wave: 16 stream waves for 2 or more
-// activation rows where the rows give every CU 16 (the helpers then stream
-// too), else 8. Ring slots: 4 where the LDS holds them beside the activations,
-// else 2. Deeper rings measured slower: the larger first burst of weight loads
-// delays the activation loads behind it in the memory system (Llama-3-8B down,
-// 4096 x 14336, one row: 13.4 us with 4 slots, 15.7 us with 8).
-// Llama-3-8B down at one row runs 13.4 us with 8 stream waves against 14.6
-// with 16 (the helpers' rows start after the quantisation and end last); at 2
-// and 4 rows 16 waves win (16.0 against 16.5 us, 22.4 against 24.8 us).
+// activation rows where the rows give every CU 16, else 8. Ring slots: 4
+// where the LDS holds them beside the activations, else 2. Deeper rings
+// measured slower: the larger first burst of weight loads delays everything
+// behind it (Llama-3-8B down, 4096 x 14336, one row: 13.4 us with 4 slots,
+// 15.7 us with 8). Llama-3-8B down at one row takes 12.6 us with 8 stream
+// waves (two rows each) against 13.6 with 16; at 2 and 4 rows the arithmetic
+// per step doubles and 16 waves win.
 template <bool FUSED>
 int launch_q6_stream(GemvParams& p, hipStream_t stream) {
     const int cus = device_cu_count();
@@ -911,9 +910,9 @@ int launch_q6_stream(GemvParams& p, hipStream_t stream) {
     GemvArgs ka;
     int64_t wgs = 0, per_wave = 0;
     int st = plan_args<FUSED>(p, WS, 1, cus, ka, wgs, per_wave);
-    if (st == kStatusOk && !FUSED) st = set_wait(ka);  // Q8_K rows are staged by the helpers too
+    if (st == kStatusOk && !FUSED) st = set_wait(ka);  // the waves wait for each other's Q8_K copies too
     if (st != kStatusOk) return st;
-    const int passes = (p.m * p.nb + kQ6HelperWaves * 4 - 1) / (kQ6HelperWaves * 4);  // 16 lanes per block
+    const int passes = (p.m * p.nb + kQ6Waves * 4 - 1) / (kQ6Waves * 4);  // 16 lanes per block: at most 4
     const dim3 grid(static_cast<unsigned>(wgs));
     if (WS == 16) {
         if (mt == 1) launch_q6_stream_ws<1, 16, FUSED>(ka, passes, slots, lds, grid, stream);
