@@ -634,6 +634,8 @@ __global__ __launch_bounds__(kQ6Waves * 64) void gemv_q6_stream_kernel(const Gem
     // issuing all S first stalls the waves at a full memory pipeline before
     // they quantise (TinyLlama down, 2048 x 5632: 6.2 -> 5.7 us at one row,
     // 8.65 -> 8.15 at four).
+    // A wave counts itself in before issuing the rest of its ring: the issue
+    // can wait for room in the memory pipeline.
     if constexpr (FUSED) {
         // the activation loads have landed (an explicit wait: the quantisation
         // below then waits for nothing, and the direct loads are not waited for)
@@ -644,10 +646,10 @@ __global__ __launch_bounds__(kQ6Waves * 64) void gemv_q6_stream_kernel(const Gem
         stage_q8k<kQ6Waves * 64>(p.q8k, p.ldx, m, nb, a);
         fill(0, 1);
     }
-    fill(1, S);
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
     if (lane == 0) __hip_atomic_fetch_add(&ready, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
     if (!streams) return;
+    fill(1, S);
 
     // Wait for every wave's share. Bounded for safety only: each depends on
     // nothing but its own activation loads, so the count arrives. A wave that
