@@ -11,6 +11,16 @@
 namespace rk {
 namespace {
 
+// A direct global->LDS load of 16 bytes per lane (to lds_dst + 16 * lane,
+// lds_dst wave-uniform) from src, issued by inline asm the compiler's
+// wait-count pass does not see: the caller waits for it explicitly (wait_vm)
+// before reading its bytes and before the wave ends.
+__device__ __forceinline__ void dma16_untracked(const void* src, uint8_t* lds_dst) {
+    const uint32_t lds = static_cast<uint32_t>(
+        reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) uint8_t*)(lds_dst)));
+    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(lds) : "memory");
+}
+
 // Calls f(integral_constant<int, I>) for I in the sequence, in order.
 template <typename F, int... I>
 __device__ __forceinline__ void unroll_seq(F&& f, std::integer_sequence<int, I...>) {

@@ -604,15 +604,28 @@ __global__ __launch_bounds__(kStageBlocks * 64) void gemv_q4_staged_kernel(const
             const int rsel = to.row0 + ((row - to.row0) & keep);
             const gbytes src = w + static_cast<int64_t>(rsel) * (nb * kQ4KBytes) + c * (kStageBlocks * kQ4KBytes) +
                                ((16 * cg) & keep);
-            __builtin_amdgcn_global_load_lds(reinterpret_cast<const void*>(reinterpret_cast<uint64_t>(src)),
-                                             (__attribute__((address_space(3))) void*)(base + 1024 * j), 16, 0, 0);
+            dma16_untracked(reinterpret_cast<const void*>(reinterpret_cast<uint64_t>(src)), base + 1024 * j);
         }
     };
 
+    // The stage loads are inline asm the wait-count pass does not see (seen, a
+    // read of a stage buffer after the loop's back edge waits for all of
+    // them); their waits are the explicit wait_vm calls. With one block index
+    // per wave the activations are quantised from the registers they were
+    // loaded into: they are waited for before any stage load is issued, one
+    // stage goes out before the quantisation and the rest after. Otherwise the
+    // quantisation loads as it goes, and the stage loads follow it.
     OwnedActs<MT, W, FUSED> owned;
     owned.first(p, wave);
-    unroll_seq([&](auto u) { issue(decltype(u)::value, u); }, std::make_integer_sequence<int, R - 1>{});
-    owned.stage(p, wave, act);
+    if (iters == 1) {
+        wait_vm<0>();
+        issue(0, std::integral_constant<int, 0>{});
+        owned.stage(p, wave, act);
+        if constexpr (R > 2) issue(1, std::integral_constant<int, 1>{});
+    } else {
+        owned.stage(p, wave, act);
+        unroll_seq([&](auto u) { issue(decltype(u)::value, u); }, std::make_integer_sequence<int, R - 1>{});
+    }
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
 
     float acc[NR];
