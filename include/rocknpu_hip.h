@@ -91,7 +91,9 @@ int rocknpu_hip_gemm_route(size_t m, size_t n, size_t k_pad, int cus, int * bm, 
  * activation rows on `cus` compute units (cus <= 0: the current device's), for
  * its first launch (m beyond one launch's rows, up to 16 on the matrix-core
  * Q4_K kernel and 8 otherwise, runs in several): *mfma = 1 for the matrix-core kernel,
- * else the lane-per-block kernel with *lanes lanes per super-block and *waves
+ * *mfma = 2 for the Q6_K kernel that streams the weights through LDS (*lanes = 8
+ * lanes per super-block, *waves = its stream waves per workgroup), else 0 for
+ * the lane-per-block kernel with *lanes lanes per super-block and *waves
  * waves per workgroup. Host code only; no GPU is needed when cus > 0. No
  * counterpart in the reference, whose decode GEMV runs on the CPU. */
 int rocknpu_hip_gemv_shape(uint32_t kind, size_t m, size_t k, const size_t * n, size_t count, int fused, int cus,
@@ -124,25 +126,26 @@ int rocknpu_hip_gemv_q_f32(uint32_t kind, size_t count, const uint8_t * const * 
                            size_t ldx, size_t m, float * const * out, const size_t * ldo,
                            void * stream);
 
-/* Stall report of rocknpu_hip_gemv_q_f32. In the lane-per-block kernel
- * (rocknpu_hip_gemv_shape: *mfma == 0) a workgroup's waves wait for the waves
- * that quantise the activations with a bounded poll (about 2^24 sleeps). A
- * wave whose poll runs out writes NaN for each of its outputs and sets a
- * process-wide flag in pinned host memory. Call after synchronising the
- * streams of the launches to check: returns 1 if a launch gave up since the
- * last call, else 0, and clears the flag. The fused decode entry point of
+/* Stall report of rocknpu_hip_gemv_q_f32 and rocknpu_hip_gemv_q8_k. In the
+ * fused lane-per-block kernel (rocknpu_hip_gemv_shape: *mfma == 0) and in the
+ * Q6_K stream kernel (*mfma == 2, fused or not) a workgroup's waves wait for
+ * the waves that stage the activations with a bounded poll (about 2^24
+ * sleeps). A wave whose poll runs out writes NaN for each of its outputs and
+ * sets a process-wide flag in pinned host memory. Call after synchronising
+ * the streams of the launches to check: returns 1 if a launch gave up since
+ * the last call, else 0, and clears the flag. The fused decode entry point of
  * the C ABI (rocknpu_matmul_q_q8k_group_f32_f32) checks it after its own
  * synchronisation and returns ROCKNPU_STATUS_EXECUTION_ERROR. The flag is
  * shared by every stream and thread of the process, and allocated by the
- * first lane-per-block fused launch (a caller that captures launches into a
- * HIP graph makes one launch before capturing). No counterpart in the
- * reference, whose decode GEMV runs on the CPU. */
+ * first launch with such a wait (a caller that captures launches into a HIP
+ * graph makes one launch before capturing). No counterpart in the reference,
+ * whose decode GEMV runs on the CPU. */
 int rocknpu_hip_gemv_take_stall(void);
 
-/* Test hook for the stall path: with spins > 0, later lane-per-block fused
- * launches wait for one more quantising wave than exists and give up after
- * `spins` polls (every wave then exits normally, outputs NaN, flag set);
- * spins == 0 restores normal launches. Returns 0, or -1 for spins < 0. */
+/* Test hook for the stall path: with spins > 0, later launches with the wait
+ * above wait for one more arrival than exists and give up after `spins` polls
+ * (every wave then exits normally, outputs NaN, flag set); spins == 0 restores
+ * normal launches. Returns 0, or -1 for spins < 0. */
 int rocknpu_hip_gemv_test_stall(int spins);
 
 #ifdef __cplusplus

@@ -47,6 +47,9 @@ struct GemvLanes {
 };
 GemvLanes gemv_lanes(bool fused, bool sums, int m, int nb, const int64_t* rows, int count, int cus);  // gemv.hip
 bool gemv_uses_mfma(int kind, int m, int nb, int64_t rows, int cus);                                  // gemv.hip
+// Stream waves per workgroup of the Q6_K LDS-stream kernel for such a launch,
+// or 0 when another kernel runs it. Defined in gemv.hip.
+int gemv_stream_waves(int kind, int m, int nb, int64_t rows, bool sums, int cus);
 // Activation rows per launch the matrix-core GEMV holds for rows of nb blocks
 // (0: none). Defined in gemv_mfma.hip.
 int gemv_mfma_rows(int kind, int nb);

@@ -887,6 +887,18 @@ void launch_q6_stream_ws(const GemvArgs& ka, int passes, int slots, size_t lds, 
     else go(std::integral_constant<int, 2>{});
 }
 
+}  // namespace
+
+// Stream waves per workgroup of the Q6_K stream kernel for a launch of m
+// activation rows over `rows` weight rows of nb blocks, or 0 when another
+// kernel runs it.
+int gemv_stream_waves(int kind, int m, int nb, int64_t rows, bool sums, int cus) {
+    if (kind != 6 || !q6_stream_fits(m, nb, sums)) return 0;
+    return m > 1 && rows >= 16 * static_cast<int64_t>(cus) ? 16 : 8;
+}
+
+namespace {
+
 // One row per row group and stream wave: 16 stream waves for 2 or more
 // activation rows where the rows give every CU 16, else 8. Ring slots: 4
 // where the LDS holds them beside the activations, else 2. Deeper rings
@@ -903,7 +915,8 @@ int launch_q6_stream(GemvParams& p, hipStream_t stream) {
     p.iters = (p.nb + 7) / 8;
     int64_t rows = 0;
     for (int i = 0; i < p.count; ++i) rows += p.rows[i];
-    const int WS = p.m > 1 && rows >= 16 * static_cast<int64_t>(cus) ? 16 : 8;
+    const int WS = gemv_stream_waves(6, p.m, p.nb, rows, false, cus);
+    if (WS == 0) return kStatusInvalid;
     const size_t act = (static_cast<size_t>(p.m) * p.nb * kGemvLdsPerBlock + 15) / 16 * 16;
     const int fit = static_cast<int>((kQ6MaxLds - 64 - act) / (WS * kQ6SlotBytes));
     const int slots = fit >= 4 ? 4 : 2;
@@ -1042,7 +1055,7 @@ bool gemv_uses_mfma(int kind, int m, int nb, int64_t rows, int cus) {
 int launch_gemv(int kind, bool fused, GemvParams& p, hipStream_t stream) {
     int64_t rows = 0;
     for (int i = 0; i < p.count; ++i) rows += p.rows[i];
-    if (kind == 6 && q6_stream_fits(p.m, p.nb, p.isum != nullptr))
+    if (gemv_stream_waves(kind, p.m, p.nb, rows, p.isum != nullptr, device_cu_count()) != 0)
         return fused ? launch_q6_stream<true>(p, stream) : launch_q6_stream<false>(p, stream);
     if (gemv_uses_mfma(kind, p.m, p.nb, rows, device_cu_count()) && p.isum == nullptr)
         return launch_gemv_mfma(kind, fused, p, stream);

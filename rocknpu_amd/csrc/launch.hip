@@ -127,6 +127,13 @@ extern "C" int rocknpu_hip_gemv_shape(uint32_t kind, size_t m, size_t k, const s
     }
     // the first launch's rows
     const int rows0 = static_cast<int>(gemv_rows_per_launch(kind, nb, m, total, false, cus));
+    const int stream_waves = rk::gemv_stream_waves(static_cast<int>(kind), rows0, static_cast<int>(nb), total, false, cus);
+    if (stream_waves != 0) {
+        *mfma = 2;
+        *lanes = 8;
+        *waves = stream_waves;
+        return rk::kStatusOk;
+    }
     *mfma = rk::gemv_uses_mfma(static_cast<int>(kind), rows0, static_cast<int>(nb), total, cus) ? 1 : 0;
     const rk::GemvLanes l = rk::gemv_lanes(fused != 0, false, rows0, static_cast<int>(nb), rows,
                                            static_cast<int>(count), cus);

@@ -140,13 +140,13 @@ def gemv_q_f32(kind: int, weights, k: int, ns, x: torch.Tensor, outs=None):
 
 
 def gemv_take_stall() -> bool:
-    """Whether a fused lane-per-block GEMV launch gave up its wait for the
-    activation quantisation since the last call (call after synchronising);
-    clears the flag."""
+    """Whether a GEMV launch with a bounded wait for the activations (the fused
+    lane-per-block kernel, the Q6_K stream kernel) gave up since the last call
+    (call after synchronising); clears the flag."""
     return bool(_lib.load().rocknpu_hip_gemv_take_stall())
 
 
 def gemv_test_stall(spins: int) -> None:
-    """Test hook: spins > 0 makes later fused lane-per-block launches wait for
-    an arrival that never comes and give up after `spins` polls; 0 restores."""
+    """Test hook: spins > 0 makes later launches with that wait wait for an
+    arrival that never comes and give up after `spins` polls; 0 restores."""
     _check(_lib.load().rocknpu_hip_gemv_test_stall(spins), "gemv_test_stall")

@@ -328,6 +328,11 @@ def test_gemv_m_chunking():
     # Q4_K rows longer than one 8-block stage: LDS-staged weights at 4, 16 and 8 rows,
     # then rows too long for the staged kernel's LDS (the unstaged matrix-core kernel)
     (4, (1000, 3000), 4096, 4), (4, (700,), 3072, 13), (4, (256, 4100), 6144, 8), (4, (256, 4100), 14336, 8),
+    # Q6_K on the LDS stream: 57 blocks per row (every other row starts 2 bytes
+    # off a 4-byte boundary; the last step of a row is partial), 16 stream waves
+    # at 2 rows with a ragged last workgroup, and 4 rows of 64 blocks on a wide
+    # weight (a two-slot ring beside the activations)
+    (6, (333,), 14592, 1), (6, (4101,), 14592, 2), (6, (4096,), 16384, 4),
 ])
 def test_gemv_fused_grouped(kind, ns, k, m):
     """Fused Q8_K quant + grouped GEMV == separate quant + per-member GEMV, bit for bit,
@@ -350,3 +355,53 @@ def test_gemv_fused_grouped(kind, ns, k, m):
         for mi in range(m):
             _, _, mag = orc.gemv_block_sums(kind, w, k, n, q8_ref[mi])
             assert np.all(np.abs(got[mi].astype(np.float64) - ref[mi]) <= 1e-5 * mag)
+
+
+@pytest.mark.parametrize("m", [1, 4])
+def test_gemv_q6_stream_stall(m):
+    """The Q6_K stream kernel's waves wait for the activations with a bounded
+    poll. Forced from the host to give up (test hook: one arrival more than the
+    workgroup has, 8 polls; every wave still exits), fused and Q8_K-input
+    launches write NaN and set the stall flag; with the hook off they match
+    each other bit for bit and the oracle, and leave the flag clear."""
+    import ctypes
+
+    from rocknpu_amd import _lib
+
+    kind, n, k = 6, 2048, 2048
+    mf, lanes, waves = ctypes.c_int(), ctypes.c_int(), ctypes.c_int()
+    arr = (ctypes.c_size_t * 1)(n)
+    assert _lib.load().rocknpu_hip_gemv_shape(kind, m, k, arr, 1, 1, 0, ctypes.byref(mf), ctypes.byref(lanes),
+                                              ctypes.byref(waves)) == 0
+    assert mf.value == 2  # the stream kernel
+    w = synth.kquant(kind, n, k, index=2400 + m)
+    x = synth.activations(m, k, index=2410 + m)
+    dw, dx = _dev(w), _dev(x)
+    q8 = hip.quantize_q8_k(dx)
+    torch.cuda.synchronize()
+    assert not hip.gemv_take_stall()
+    print(f"q6 stream stall hook on m={m}", flush=True)
+    hip.gemv_test_stall(8)
+    try:
+        fused = hip.gemv_q_f32(kind, [dw], k, [n], dx)[0]
+        torch.cuda.synchronize()
+        assert np.isnan(fused.cpu().numpy()).all()
+        assert hip.gemv_take_stall()
+        sep = hip.gemv_q8_k(kind, dw, k, n, q8)
+        torch.cuda.synchronize()
+        assert np.isnan(sep.cpu().numpy()).all()
+        assert hip.gemv_take_stall()
+    finally:
+        hip.gemv_test_stall(0)
+    print(f"q6 stream stall hook off m={m}", flush=True)
+    fused = hip.gemv_q_f32(kind, [dw], k, [n], dx)[0]
+    sep = hip.gemv_q8_k(kind, dw, k, n, q8)
+    torch.cuda.synchronize()
+    assert not hip.gemv_take_stall()
+    got = fused.cpu().numpy()
+    assert np.array_equal(got.view(np.uint32), sep.cpu().numpy().view(np.uint32))
+    q8_ref = orc.quantize_q8_k(x)
+    ref = orc.gemv_q8_k(kind, w, k, n, q8_ref, threads=8)
+    for mi in range(m):
+        _, _, mag = orc.gemv_block_sums(kind, w, k, n, q8_ref[mi])
+        assert np.all(np.abs(got[mi].astype(np.float64) - ref[mi]) <= 1e-5 * mag)
