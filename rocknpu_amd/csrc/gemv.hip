@@ -178,10 +178,11 @@ __device__ __forceinline__ void lane_sums(const Piece<4, L>& k, int p, const Q8L
 #pragma unroll
         for (int mi = 0; mi < MT; ++mi) {
             if (mi >= m) break;
-            const int blk = mi * nb + b;
-            const uint8_t* xq = a.quants(blk);
-            const v4u x0 = *reinterpret_cast<const v4u*>(xq + 64 * j + 16 * hh);
-            const v4u x1 = *reinterpret_cast<const v4u*>(xq + 64 * j + 32 + 16 * hh);
+            // LDS addresses in 32 bits (full-rate 24-bit index products)
+            const uint32_t blk = static_cast<uint32_t>(mi * nb + b);
+            const uint32_t xq = a.qs_lds() + __umul24(blk, kGemvLdsQsStride) + 64 * j + 16 * hh;
+            const v4u x0 = *lds_at<v4u>(xq);
+            const v4u x1 = *lds_at<v4u>(xq + 32);
             int d0 = dot4(lo[0], x0.x, 0);
             d0 = dot4(lo[1], x0.y, d0);
             d0 = dot4(lo[2], x0.z, d0);
@@ -190,9 +191,10 @@ __device__ __forceinline__ void lane_sums(const Piece<4, L>& k, int p, const Q8L
             d1 = dot4(hi[1], x1.y, d1);
             d1 = dot4(hi[2], x1.z, d1);
             d1 = dot4(hi[3], x1.w, d1);
-            const int16_t* bs = a.bsums(blk);
-            is[mi] += sc0 * d0 + sc1 * d1;
-            ms[mi] += mn0 * bs[4 * j + hh] + mn1 * bs[4 * j + 2 + hh];
+            const auto* bs = lds_at<int16_t>(a.bs_lds() + __umul24(blk, kGemvLdsBsStride));
+            // |d| <= 16 * 15 * 128 and sc, mn < 64: the 24-bit products are exact
+            is[mi] += __mul24(sc0, d0) + __mul24(sc1, d1);
+            ms[mi] += __mul24(mn0, bs[4 * j + hh]) + __mul24(mn1, bs[4 * j + 2 + hh]);
         }
     }
 }
@@ -258,7 +260,8 @@ __device__ __forceinline__ void lane_sums(const Piece<6, L>& k, int p, const Q8L
         const int hq = L == 1 ? 2 * h + c : (L == 8 ? 0 : c);
         const int s0 = 8 * h + 2 * qa + c;
         q6_unit<MT>(k.get_ql(u), k.get_qh(hq), sbyte(scv, s0), sbyte(scv, s0 + 4), gu,
-                    a.qs_lds() + b * kGemvLdsQsStride, a.bs_lds() + b * kGemvLdsBsStride, nb, m, is);
+                    a.qs_lds() + __umul24(static_cast<uint32_t>(b), kGemvLdsQsStride),
+                    a.bs_lds() + __umul24(static_cast<uint32_t>(b), kGemvLdsBsStride), nb, m, is);
     }
 }
 
@@ -425,7 +428,10 @@ __global__ __launch_bounds__(W * 64) void gemv_kernel(const GemvArgs p) {
             row = home_row;
             b = home_b;
         }
-        k.load(wg_w + row * row_bytes + b * BB, pc);
+        // row, b >= 0 and row_bytes < 2^32: one 32 x 32 -> 64-bit product
+        k.load(wg_w + static_cast<uint64_t>(static_cast<uint32_t>(row)) * static_cast<uint32_t>(row_bytes) +
+                   __umul24(static_cast<uint32_t>(b), static_cast<uint32_t>(BB)),
+               pc);
     };
 
     // Issue order: the owners of quantisation blocks load their activations
@@ -475,7 +481,7 @@ __global__ __launch_bounds__(W * 64) void gemv_kernel(const GemvArgs p) {
                     if (mi >= m) break;
                     const int isum = sum_lanes<L>(is[mi]);
                     const int msum = KIND == 4 ? sum_lanes<L>(ms[mi]) : 0;
-                    const float da = a.d[mi * nb + bk];
+                    const float da = *lds_at<float>(a.d_lds() + 4 * __umul24(static_cast<uint32_t>(mi * nb + bk), 1u));
                     float term = (dw * da) * static_cast<float>(isum);
                     if constexpr (KIND == 4) term = term - (dminw * da) * static_cast<float>(msum);
                     acc[mi] += have ? term : 0.0f;
