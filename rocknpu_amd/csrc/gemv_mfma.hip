@@ -758,15 +758,18 @@ size_t gemv_mfma_lds(int mt, int nb, int w) {
     return ((static_cast<size_t>(nb) * mt * kPerRowBlock + 15) & ~size_t{15}) + 2 * static_cast<size_t>(w) * 64 * (mt / 4) * 4;
 }
 
-// Whether the staged kernel takes a Q4_K launch of mt-row tiles: rows of more
-// than one stage (nb > 8), whose LDS holds rows of nb blocks and `tiles` tiles
-// per workgroup. With one stage per tile the unstaged kernel is faster (its
-// operand loads start without a barrier): TinyLlama o (2048 x 2048) at 4 rows
-// 4.94 against 5.21 us, at 8 rows 5.72 against 6.06 us; with two or more the
-// staged one (Llama-3-8B gate+up, 2 x 14336 x 4096, at 4 rows 24.8 -> 22.5 us,
-// at 8 rows 27.1 -> 26.2 us).
+// Whether the staged kernel takes a Q4_K launch of mt-row tiles, `tiles` tiles
+// per workgroup, whose LDS holds rows of nb blocks: rows of more than one stage
+// (nb > 8), and at 4 rows also rows of one stage when a workgroup walks two or
+// more tiles. With one stage per tile and one tile per workgroup the unstaged
+// kernel is faster (its operand loads start without a barrier): TinyLlama o
+// (2048 x 2048) at 4 rows 4.94 against 5.21 us, at 8 rows 5.72 against 6.06 us.
+// With several one-stage tiles the staged one is faster at 4 rows (TinyLlama
+// gate+up, 2 x 5632 x 2048: 8.46 -> 8.1-8.2 us) and slower at 8 (8.5 against
+// 9.8 us). With two or more stages per tile it is faster (Llama-3-8B gate+up,
+// 2 x 14336 x 4096, at 4 rows 24.8 -> 22.5 us, at 8 rows 27.1 -> 26.2 us).
 bool gemv_staged_fits(int mt, int nb, int tiles) {
-    if (nb <= kStageBlocks) return false;
+    if (nb <= kStageBlocks && (mt != 4 || tiles < 2)) return false;
     if (mt == 4) return nb <= StagedCfg<4>::NB && tiles <= StagedCfg<4>::TILES;
     if (mt == 8) return nb <= StagedCfg<8>::NB && tiles <= StagedCfg<8>::TILES;
     return nb <= StagedCfg<16>::NB && tiles <= StagedCfg<16>::TILES;

@@ -273,11 +273,12 @@ def test_gemv_q8_k(kind, n, k, m):
 
 
 @pytest.mark.parametrize("n,k,m", [(16, 256, 2), (40, 1024, 3), (2048, 2048, 4), (130, 5632, 5), (300, 2048, 8),
-                                   (17, 14336, 3), (1000, 4096, 7), (33, 256, 6)])
+                                   (17, 14336, 3), (1000, 4096, 7), (33, 256, 6), (8200, 1024, 3), (11264, 2048, 4)])
 def test_gemv_q4k_multi_row(n, k, m):
     """Q4_K at 2..8 activation rows without the exact-sums outputs (3..8 rows run on the
     matrix-core kernel) against the oracle: ragged tiles of 16 weight rows, blocks per row
-    not a multiple of 8, padded activation rows."""
+    not a multiple of 8, padded activation rows; rows of one LDS stage with several tiles
+    per workgroup at 3..4 rows (8200 x 1024, 11264 x 2048) take the staged kernel."""
     print(f"gemv multi-row n={n} k={k} m={m}", flush=True)
     w = synth.kquant(4, n, k, index=800 + n + m)
     x = synth.activations(m, k, index=801 + k)
