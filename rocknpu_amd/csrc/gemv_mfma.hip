@@ -399,8 +399,8 @@ __global__ __launch_bounds__(W * 64) void gemv_mfma_kernel(const MfmaArgs p) {
     const int n = lane & 15, q = lane >> 4;  // B column (weight row in the tile), K slot group
 
     // Items: (tile t = blockIdx.x + k * gridDim.x, iteration it < iters), walked
-    // with counters. Loads past the last item re-read the last tile's first
-    // block (in bounds) and are never used.
+    // with counters. With more than one block in flight, loads past the last
+    // item re-read the last tile's first block (in bounds) and are never used.
     struct Pos {
         int t;
         int it;
@@ -471,7 +471,13 @@ __global__ __launch_bounds__(W * 64) void gemv_mfma_kernel(const MfmaArgs p) {
                 block_terms<KIND, MT>(buf[j], areg, bsreg, dareg, term);
 #pragma unroll
                 for (int lr = 0; lr < NR; ++lr) acc[lr] += have ? term[lr] : 0.0f;
-                load(lq, buf[j]);
+                // With one block in flight a load past the last item is skipped:
+                // issued, it queues ahead of the tile's barrier and the wave's
+                // end (TinyLlama o and qkv at 4 rows, one tile per workgroup:
+                // 4.45 -> 3.9 us). With more in flight the loads stay
+                // unconditional, so the wait counts cover exactly the block each
+                // value needs.
+                if (D > 1 || lq.t < p.tiles) load(lq, buf[j]);
                 advance(lq);
                 if (it == iters - 1) {
                     // tile done: partial sums to LDS, then one wave adds them in wave order
@@ -579,11 +585,12 @@ __global__ __launch_bounds__(kStageBlocks * 64) void gemv_q4_staged_kernel(const
     // Every wave issues three (waves 2..7 repeat load 16 or 17: the same bytes to
     // the same place), all lanes active, so the wait counts are uniform.
     auto issue = [&](int s, auto u) {
-        // past the end: one 16-byte chunk of the last stage for every lane (the
-        // loads keep the wait counts uniform; their bytes are never read)
-        const bool real = s < ns;
-        const int ss = min(s, ns - 1);
-        const int k = ss / iters, c = ss - k * iters;
+        // a stage past the end issues nothing (the waits below count one stage
+        // fewer in flight then): issued, its loads queue ahead of the last
+        // stages' barriers and the wave's end (TinyLlama gate+up at 4 rows
+        // 8.17 -> 7.75 us)
+        if (s >= ns) return;
+        const int k = s / iters, c = s - k * iters;
         const int t = bid + k * grid;
         const TileOut to = tile_out(p, t);
         const gbytes w = reinterpret_cast<gbytes>(reinterpret_cast<uint64_t>(tile_weights(p, t)));
@@ -598,12 +605,7 @@ __global__ __launch_bounds__(kStageBlocks * 64) void gemv_q4_staged_kernel(const
             cg = cg < 0 ? cg + kStageRowChunks : cg;
             cg = cg < valid ? cg : 0;
             const int row = min(to.row0 + r, to.rows - 1);
-            // masks, not selects: a select on a uniform condition may become a
-            // branch, and a join
-            const int keep = -static_cast<int>(real);
-            const int rsel = to.row0 + ((row - to.row0) & keep);
-            const gbytes src = w + static_cast<int64_t>(rsel) * (nb * kQ4KBytes) + c * (kStageBlocks * kQ4KBytes) +
-                               ((16 * cg) & keep);
+            const gbytes src = w + static_cast<int64_t>(row) * (nb * kQ4KBytes) + c * (kStageBlocks * kQ4KBytes) + 16 * cg;
             dma16_untracked(reinterpret_cast<const void*>(reinterpret_cast<uint64_t>(src)), base + 1024 * j);
         }
     };
@@ -652,7 +654,11 @@ __global__ __launch_bounds__(kStageBlocks * 64) void gemv_q4_staged_kernel(const
     // stage past the end.
     auto step = [&](auto uu, int s) {
         constexpr int U = decltype(uu)::value;
-        wait_vm<(R - 2) * kDmaLoads>();  // this wave's loads of stage s
+        // this wave's loads of stage s: the stage after it (R = 3) is in flight
+        // unless s is the last
+        static_assert(R <= 3, "one stage younger at most");
+        if (R > 2 && s + 1 < ns) wait_vm<(R - 2) * kDmaLoads>();
+        else wait_vm<0>();
         // everyone's, and every wave's LDS writes (partial sums); stage s - 1 is
         // then free. A compiler memory barrier too.
         asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
