@@ -51,12 +51,49 @@ int rocknpu_hip_gemm_w8a8(const int8_t * a8, const float * a_scales, const int8_
                           const float * w_scales, size_t m, size_t n, size_t k_pad, float * out,
                           size_t ldo, int32_t * out_i32, void * stream);
 
+/* rocknpu_hip_gemm_w8a8 with a caller workspace, which lets the GEMM split
+ * each tile's K range over several workgroups where its tiles would fill at
+ * most half the GPU (rocknpu_hip_gemm_workspace says when, and how many bytes).
+ * The split workgroups add their int32 partial tiles (exact, so the results
+ * are bit-identical to the unsplit call's). The workspace is device memory,
+ * 256-byte aligned, whose first 16 KiB hold the tile counters: they must be
+ * zero when the call starts, and every call that completes leaves them zero
+ * (whatever shapes share the workspace), so zero a workspace once after
+ * allocating it. A workspace smaller than the
+ * route asks for (or NULL with 0 bytes) runs the GEMM unsplit. Calls that
+ * overlap (other streams) need workspaces of their own. No counterpart in the
+ * reference (its NPU K-split, crates/rocknpu-capi/src/lib.rs:1885-1926, adds
+ * int32 partials on the host); the product is that of rocknpu_hip_gemm_w8a8. */
+int rocknpu_hip_gemm_w8a8_ws(const int8_t * a8, const float * a_scales, const int8_t * w8,
+                             const float * w_scales, size_t m, size_t n, size_t k_pad, float * out,
+                             size_t ldo, int32_t * out_i32, void * workspace, size_t workspace_bytes,
+                             void * stream);
+
+/* The workspace rocknpu_hip_gemm_w8a8_ws uses for an M x N x k_pad product on
+ * a GPU of `cus` compute units (cus <= 0: the current device's): *bytes (0 when
+ * the product runs unsplit) and the K split *splits (1: none). Host code only;
+ * no GPU is needed when cus > 0. No counterpart in the reference. */
+int rocknpu_hip_gemm_workspace(size_t m, size_t n, size_t k_pad, int cus, size_t * bytes, int * splits);
+
+/* The W8A8 GEMM on a given tile (bm x bn: 64x32 and 64x64 with 2 or 4 stages,
+ * 128x64 with 2 or 4, 128x128 with 2 or 3, 256x128 with 3, 256x256 with 2;
+ * bm = 0: the weight-streaming kernel, m <= 16) and K split (1 to 16; above 1
+ * the workspace must hold 16 KiB of zero counters, one per tile and at most
+ * 4096 tiles, then splits x bm x bn int32 per tile). For tests and tuning:
+ * every choice gives the same bits. No
+ * counterpart in the reference. */
+int rocknpu_hip_gemm_w8a8_tile(int bm, int bn, int stages, int splits, const int8_t * a8,
+                               const float * a_scales, const int8_t * w8, const float * w_scales, size_t m,
+                               size_t n, size_t k_pad, float * out, size_t ldo, int32_t * out_i32,
+                               void * workspace, size_t workspace_bytes, void * stream);
+
 /* Kernels (b) + (c): the W8A8 prompt route on device buffers. A [m, lda] f32
  * (first k columns) is quantised per token into an int8 workspace, then
  * out[m, ldo] = (f32(A8 W8^T) * a_scale[m]) * w_scales[n] against the resident
  * W8 [n, k_pad] (16-byte aligned, k_pad a multiple of 64, at most 133120).
- * The library allocates the workspace (m * k_pad bytes + m scales) on
- * `stream`, stream-ordered, and releases it behind the GEMM. Replaces the
+ * The library allocates the workspace (m * k_pad bytes + m scales, and the
+ * GEMM's K-split workspace where the route splits) on `stream`, stream-ordered,
+ * and releases it behind the GEMM. Replaces the
  * quantise / i32 GEMM / rescale sequence of execute_cached_w8a8_mtile_pool_padded
  * (crates/rocknpu-capi/src/lib.rs:1776-1791, :1868-1884) without its weight
  * cache. Results equal rocknpu_hip_quantize_a8 followed by rocknpu_hip_gemm_w8a8. */
@@ -68,7 +105,8 @@ int rocknpu_hip_matmul_w8a8_f32(const float * a, size_t m, size_t k, size_t lda,
  * reference. For callers that cannot allocate device memory (code under HIP
  * graph capture, tight serving loops, harnesses that forbid hipMalloc). The
  * workspace is a fixed array in the library's device memory, one copy per GPU
- * the library runs on, held until the process ends: at most 16384 rows and
+ * the library runs on, held until the process ends (64 KiB of scales, 32 MiB
+ * of A8 and 4 MiB + 16 KiB for the GEMM's K split): at most 16384 rows and
  * m * k_pad <= 32 MiB; beyond that the call returns
  * ROCKNPU_STATUS_INVALID_ARGUMENT and prints the limit on stderr. Every call on
  * one GPU uses that GPU's copy, so calls that overlap on one GPU (other

@@ -21,6 +21,7 @@
 #include <unordered_map>
 #include <vector>
 
+#include "common.h"
 #include "context.h"
 #include "rocknpu.h"
 #include "rocknpu_ggml.h"
@@ -226,10 +227,20 @@ int run_w8a8(RockNpuContext* ctx, const DeviceW8& w, const float* act, size_t m,
         !ctx->d_as.ensure(rows * sizeof(float)) || !ctx->d_out.ensure(o_rows * sizeof(float)) ||
         !ctx->h_out.ensure(o_elems * sizeof(float)) || !ctx->h_as.ensure(rows * sizeof(float)))
         return kExec;
+    // the GEMM's K-split workspace; the (first) quantisation clears its counters
+    const rk::GemmTile route = rk::gemm_route(static_cast<int>(rows), static_cast<int>(w.n),
+                                              static_cast<int>(w.k_pad), rk::device_cu_count());
+    const size_t split = rk::gemm_workspace_bytes(route, static_cast<int>(rows), static_cast<int>(w.n));
+    if (split > 0 && !ctx->d_split.ensure(split)) return kExec;
     if (!hip_ok(hipMemcpyAsync(ctx->d_act.p, act, a_bytes, hipMemcpyHostToDevice, ctx->stream), ctx, "act"))
         return kExec;
-    int st = rocknpu_hip_quantize_a8(ctx->d_act.as<float>(), m, k, k, w.k_pad, ctx->d_a8.as<int8_t>(),
-                                     ctx->d_as.as<float>(), ctx->stream);
+    int st = rk::launch_quantize_a8(ctx->d_act.as<float>(), static_cast<int64_t>(m), static_cast<int64_t>(k),
+                                    static_cast<int64_t>(k), static_cast<int64_t>(w.k_pad), ctx->d_a8.as<int8_t>(),
+                                    ctx->d_as.as<float>(), split > 0 ? ctx->d_split.as<uint32_t>() : nullptr,
+                                    split > 0 ? rk::gemm_workspace_counters(route, static_cast<int>(rows),
+                                                                            static_cast<int>(w.n))
+                                              : 0,
+                                    ctx->stream);
     if (st != kOk) return st;
     if (hilo) {
         const int64_t total = static_cast<int64_t>(m * k);
@@ -241,8 +252,9 @@ int run_w8a8(RockNpuContext* ctx, const DeviceW8& w, const float* act, size_t m,
                                      ctx->d_as.as<float>() + m, ctx->stream);
         if (st != kOk) return st;
     }
-    st = rocknpu_hip_gemm_w8a8(ctx->d_a8.as<int8_t>(), ctx->d_as.as<float>(), w.w8, w.scales, rows, w.n, w.k_pad,
-                               ctx->d_out.as<float>(), w.n, nullptr, ctx->stream);
+    st = rocknpu_hip_gemm_w8a8_ws(ctx->d_a8.as<int8_t>(), ctx->d_as.as<float>(), w.w8, w.scales, rows, w.n, w.k_pad,
+                                  ctx->d_out.as<float>(), w.n, nullptr, split > 0 ? ctx->d_split.p : nullptr, split,
+                                  ctx->stream);
     if (st != kOk) return st;
     if (hilo) {
         const int64_t total = static_cast<int64_t>(o_elems);

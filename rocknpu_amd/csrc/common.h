@@ -35,11 +35,35 @@ constexpr int kMaxExactK = 133120;
 // Rows of A8 (m * k_pad bytes) the weight-streaming GEMM stages in LDS at most.
 constexpr int kSkinnyMaxA8 = 112 * 1024;
 // A W8A8 GEMM launch: tile bm x bn with `stages` K stages of 128 bytes (bm = 0:
-// the weight-streaming kernel for up to 16 rows).
+// the weight-streaming kernel for up to 16 rows), K split over `splits`
+// workgroups per tile (their i32 partials meet in a workspace).
 struct GemmTile {
     int bm, bn, stages;
+    int splits = 1;
 };
 GemmTile gemm_route(int m, int n, int k, int cus);  // gemm.hip
+// A K-split workspace starts with a fixed block of kSplitCounters tile
+// counters (whatever the shape, so a workspace reused for other shapes never
+// finds another shape's partials in its counters), then the i32 partial tiles.
+constexpr int kSplitCounters = 4096;
+constexpr size_t kSplitCounterBytes = kSplitCounters * 4;
+// Workspace bytes a split-K launch of `tile` needs for an m x n product.
+size_t gemm_workspace_bytes(const GemmTile& tile, int m, int n);  // gemm.hip
+// Counter words at the start of that workspace (what must be zero at entry).
+int gemm_workspace_counters(const GemmTile& tile, int m, int n);  // gemm.hip
+// Per-token A8 quantisation; workgroup 0 also clears `nzero` words at
+// zero_words (nullptr, 0: none). quant.hip.
+int launch_quantize_a8(const float* a, int64_t m, int64_t k, int64_t lda, int64_t k_pad, int8_t* a8,
+                       float* scales, uint32_t* zero_words, int nzero, hipStream_t stream);
+// The W8A8 GEMM on the routed tile; the routed K split runs when `workspace`
+// holds gemm_workspace_bytes of it with zero counters, else unsplit. gemm.hip.
+int launch_gemm_w8a8(const int8_t* a8, int64_t lda, const int8_t* w8, int64_t ldw, const float* as,
+                     const float* ws, int m, int n, int k, float* out, int64_t ldo, int32_t* oi,
+                     int64_t ldoi, uint8_t* workspace, size_t workspace_bytes, hipStream_t stream);
+// The same on a given tile, stage count and split. gemm.hip.
+int launch_gemm_w8a8_tile(const GemmTile& r, const int8_t* a8, int64_t lda, const int8_t* w8, int64_t ldw,
+                          const float* as, const float* ws, int m, int n, int k, float* out, int64_t ldo,
+                          int32_t* oi, int64_t ldoi, uint8_t* workspace, hipStream_t stream);
 // Decode GEMV launch shape: lanes per super-block and waves per workgroup of
 // the lane-per-block kernel, and whether the matrix-core kernel runs instead.
 struct GemvLanes {

@@ -152,6 +152,7 @@ struct RockNpuContext {
     // raw K-quant blocks resident for the Q8_K decode GEMV
     std::unordered_map<rk::WeightKey, std::shared_ptr<rk::DevBuf>, rk::KeyHash> raw;
     rk::DevBuf d_raw, d_act, d_a8, d_as, d_out, d_q8k;
+    rk::DevBuf d_split;  // the W8A8 GEMM's K-split workspace (counters cleared per call)
     rk::PinnedBuf h_out, h_as;
     size_t hits = 0, misses = 0, m1_calls = 0;
     uint64_t hit_ns = 0, miss_ns = 0;

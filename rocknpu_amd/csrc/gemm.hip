@@ -14,6 +14,7 @@
 // weight-streaming kernel of gemm_skinny.hip runs instead.
 #include "common.h"
 
+#include <algorithm>
 #include <type_traits>
 #include <utility>
 
@@ -76,11 +77,26 @@ __device__ __forceinline__ void unroll_seq(F&& f, std::integer_sequence<int, I..
     (f(std::integral_constant<int, I>{}), ...);
 }
 
-template <int BM, int BN, int WM, int WN, int ST, int KB>
+// Split-K (SK): the grid holds `splits` workgroups per tile, workgroup s of a
+// tile taking K bytes [s * k_split, (s + 1) * k_split). Each writes its i32
+// partial tile to `partials` in the accumulator layout (lane-contiguous, so
+// every store is a full 256-byte row), then counts itself in at the tile's
+// counter; the last to arrive adds the other partials to its own (int32
+// addition: exact and order-free) and runs the epilogue, and resets the
+// counter to zero, so a workspace whose counters start at zero ends every
+// call with them at zero.
+//
+// The partials and counters are device-scope atomics (relaxed), which on a
+// gfx950 write through and read past the XCDs' separate L2s; each wave waits
+// for its partial stores to complete before the count. A device-scope fence
+// instead would write back and invalidate the whole L2 of the XCD, which cost
+// 50 us per launch at 352 workgroups.
+template <int BM, int BN, int WM, int WN, int ST, int KB, bool SK>
 __global__ __launch_bounds__(WM* WN * 64) void gemm_w8a8_dma_kernel(
     const int8_t* __restrict__ a8, int64_t lda, const int8_t* __restrict__ w8, int64_t ldw,
     const float* __restrict__ a_scales, const float* __restrict__ w_scales, int m, int n, int k,
-    float* __restrict__ out, int64_t ldo, int32_t* __restrict__ out_i32, int64_t ldo_i32) {
+    float* __restrict__ out, int64_t ldo, int32_t* __restrict__ out_i32, int64_t ldo_i32, int splits,
+    int k_split, int32_t* __restrict__ partials, uint32_t* __restrict__ counters) {
     using Cfg = DmaTile<BM, BN, WM, WN, KB>;
     constexpr int TM = BM / WM, TN = BN / WN;
     constexpr int FM = TM / 32, FN = TN / 32;  // 32x32 fragments
@@ -122,10 +138,22 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_w8a8_dma_kernel(
     // XCD-aware tile order: workgroup b runs on XCD b % 8, so each XCD takes a
     // contiguous range of tile indices, walked in groups of 4 tile rows; the
     // 32 tiles an XCD runs at once then share A rows and W rows in its L2.
+    // With split-K the (tile, split) pairs are ordered tile-major, so a tile's
+    // splits run on one XCD and exchange their partials through its L2.
     const int tiles_m = (m + BM - 1) / BM, tiles_n = (n + BN - 1) / BN;
     const int tiles = tiles_m * tiles_n;
-    const int bid = blockIdx.x, xcd = bid & 7, per = tiles >> 3, rem = tiles & 7;
-    const int t = xcd * per + min(xcd, rem) + (bid >> 3);
+    const int total = SK ? tiles * splits : tiles;
+    const int bid = blockIdx.x, xcd = bid & 7, per = total >> 3, rem = total & 7;
+    const int v = xcd * per + min(xcd, rem) + (bid >> 3);
+    const int t = SK ? v / splits : v;
+    const int split = SK ? v - t * splits : 0;
+    if constexpr (SK) {
+        // this split's K range: operands start k0 bytes in, k bytes long
+        const int k0 = split * k_split;
+        a8 += k0;
+        w8 += k0;
+        k = min(k - k0, k_split);
+    }
     constexpr int GM = 4;
     const int group = t / (GM * tiles_n), first_m = group * GM;
     const int gsize = min(tiles_m - first_m, GM);
@@ -281,6 +309,44 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_w8a8_dma_kernel(
     wait_lgkm0();
     __builtin_amdgcn_s_barrier();
 
+    if constexpr (SK) {
+        constexpr int PART = FM * FN * 16 * 64;  // ints of one wave's partial
+        __shared__ int last;
+        int32_t* mine = partials + (static_cast<int64_t>(t) * splits + split) * (WM * WN * PART) + wave * PART;
+#pragma unroll
+        for (int i = 0; i < FM; ++i)
+#pragma unroll
+            for (int j = 0; j < FN; ++j)
+#pragma unroll
+                for (int e = 0; e < 16; ++e)
+                    __hip_atomic_store(mine + ((i * FN + j) * 16 + e) * 64 + lane, acc[i][j][e], __ATOMIC_RELAXED,
+                                       __HIP_MEMORY_SCOPE_AGENT);
+        // every wave's partial has reached the device-coherent level before the count
+        wait_vm<0>();
+        __syncthreads();
+        if (threadIdx.x == 0)
+            last = __hip_atomic_fetch_add(counters + t, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+                   static_cast<uint32_t>(splits - 1);
+        __syncthreads();
+        if (!last) return;
+        // the other splits counted in after their partials completed; read them
+        // at device scope (past this XCD's L2)
+        for (int s2 = 0; s2 < splits; ++s2) {
+            if (s2 == split) continue;
+            int32_t* other =
+                partials + (static_cast<int64_t>(t) * splits + s2) * (WM * WN * PART) + wave * PART;
+#pragma unroll
+            for (int i = 0; i < FM; ++i)
+#pragma unroll
+                for (int j = 0; j < FN; ++j)
+#pragma unroll
+                    for (int e = 0; e < 16; ++e)
+                        acc[i][j][e] += __hip_atomic_load(other + ((i * FN + j) * 16 + e) * 64 + lane,
+                                                          __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        if (threadIdx.x == 0) __hip_atomic_store(counters + t, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+
     // Epilogue. lane l holds column l%32 of each 32x32 fragment, rows
     // (e%4) + 4*(l/32) + 8*(e/4). Each fragment is scaled, written to an
     // HR x 40 f32 tile of the wave's own stage buffer (HR = 32 rows, or 16 in
@@ -363,18 +429,40 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_w8a8_dma_kernel(
     }
 }
 
+// Splits that get K stages when `splits` are asked for over `ks` stages, and
+// the stages of each (the last may have fewer).
+struct SplitK {
+    int splits, stages_per;
+};
+SplitK split_k(int ks, int splits) {
+    if (splits <= 1 || ks <= 1) return {1, ks};
+    const int per = (ks + splits - 1) / splits;
+    return {(ks + per - 1) / per, per};
+}
+
 template <int BM, int BN, int WM, int WN, int ST, int KB = 64>
 int launch_dma(const int8_t* a8, int64_t lda, const int8_t* w8, int64_t ldw, const float* as,
                const float* ws, int m, int n, int k, float* out, int64_t ldo, int32_t* oi,
-               int64_t ldoi, hipStream_t stream) {
+               int64_t ldoi, int splits, uint8_t* workspace, hipStream_t stream) {
     // 128-byte stages need K % 128 == 0 (a stage never reads past a row)
     if constexpr (KB != 64)
         if (k % KB != 0)
             return launch_dma<BM, BN, WM, WN, (ST < 4 ? 4 : ST), 64>(a8, lda, w8, ldw, as, ws, m, n, k, out, ldo, oi,
-                                                                     ldoi, stream);
+                                                                     ldoi, splits, workspace, stream);
     const int64_t tiles = static_cast<int64_t>((m + BM - 1) / BM) * ((n + BN - 1) / BN);
-    gemm_w8a8_dma_kernel<BM, BN, WM, WN, ST, KB><<<dim3(static_cast<unsigned>(tiles)), dim3(WM * WN * 64), 0, stream>>>(
-        a8, lda, w8, ldw, as, ws, m, n, k, out, ldo, oi, ldoi);
+    const SplitK sk = split_k(k / KB, workspace && tiles <= kSplitCounters ? splits : 1);
+    if (sk.splits > 1) {
+        uint32_t* counters = reinterpret_cast<uint32_t*>(workspace);
+        int32_t* partials = reinterpret_cast<int32_t*>(workspace + kSplitCounterBytes);
+        gemm_w8a8_dma_kernel<BM, BN, WM, WN, ST, KB, true>
+            <<<dim3(static_cast<unsigned>(tiles * sk.splits)), dim3(WM * WN * 64), 0, stream>>>(
+                a8, lda, w8, ldw, as, ws, m, n, k, out, ldo, oi, ldoi, sk.splits, sk.stages_per * KB, partials,
+                counters);
+    } else {
+        gemm_w8a8_dma_kernel<BM, BN, WM, WN, ST, KB, false><<<dim3(static_cast<unsigned>(tiles)), dim3(WM * WN * 64), 0,
+                                                              stream>>>(a8, lda, w8, ldw, as, ws, m, n, k, out, ldo,
+                                                                        oi, ldoi, 1, k, nullptr, nullptr);
+    }
     return hipGetLastError() == hipSuccess ? kStatusOk : kStatusExec;
 }
 
@@ -383,6 +471,7 @@ int launch_dma(const int8_t* a8, int64_t lda, const int8_t* w8, int64_t ldw, con
 int launch_gemm_w8a8_skinny(const int8_t* a8, int64_t lda, const int8_t* w8, int64_t ldw, const float* as,
                             const float* ws, int m, int n, int k, float* out, int64_t ldo, int32_t* oi,
                             int64_t ldoi, hipStream_t stream);  // gemm_skinny.hip
+GemmTile gemm_tile(int m, int n, int k, int cus);
 
 // Tile and stage count of the GEMM for an M x N x K product on `cus` CUs
 // (bm = 0: the weight-streaming kernel of gemm_skinny.hip). "Fits" below
@@ -424,7 +513,28 @@ int launch_gemm_w8a8_skinny(const int8_t* a8, int64_t lda, const int8_t* w8, int
 //   (512 x 2048 x 5632: 21.9 -> 16.5 us; 1024 x 2560 x 4096: 29.9 -> 23.5 us).
 // Tiles that need a second round where smaller or larger ones fit in one
 // measured slower, which is why each rule asks for one round.
+//
+// K split (with a workspace): when the chosen tiles are at most 64 x 64 and
+// fill at most half the CUs, each tile's K range is split over
+// min(cus / tiles, stages / 8, 4) workgroups, so the units fill the CUs with
+// at least 8 stages each (128 x 2048 x 2048: 8.19 -> 7.56 us; 128 x 2048 x
+// 5632: 13.6 -> 10.7 us; 128 x 2048 x 8192: 18.1 -> 12.9 us). Larger tiles,
+// and tiles filling more than half the CUs, measured slower split (128 x 5632
+// x 2048 on 176 64 x 64 tiles: 8.4 -> 12.0 us at two splits; 1024 x 8192 x
+// 4096 on 128 256 x 256 tiles: 58.5 -> 63.9 us).
 GemmTile gemm_route(int m, int n, int k, int cus) {
+    GemmTile r = gemm_tile(m, n, k, cus);
+    if (r.bm == 0 || r.bm * r.bn > 64 * 64) return r;
+    const int64_t tiles = static_cast<int64_t>((m + r.bm - 1) / r.bm) * ((n + r.bn - 1) / r.bn);
+    const int stages = k % 128 == 0 ? k / 128 : k / 64;
+    if (2 * tiles > cus || tiles > kSplitCounters) return r;
+    const int s = static_cast<int>(std::min<int64_t>(std::min(cus / tiles, static_cast<int64_t>(stages / 8)), 4));
+    if (s >= 2) r.splits = s;
+    return r;
+}
+
+// The tile and stage count (no split) of gemm_route.
+GemmTile gemm_tile(int m, int n, int k, int cus) {
     auto tiles = [&](int bm, int bn) { return static_cast<int64_t>((m + bm - 1) / bm) * ((n + bn - 1) / bn); };
     auto by_tiles = [&](int bm, int bn) { return GemmTile{bm, bn, tiles(bm, bn) > cus ? 2 : 4}; };
     auto rounds = [&](int64_t t, int per_cu) { return (t + per_cu * cus - 1) / (per_cu * cus); };
@@ -460,12 +570,26 @@ GemmTile gemm_route(int m, int n, int k, int cus) {
     return filling(true);
 }
 
-int launch_gemm_w8a8(const int8_t* a8, int64_t lda, const int8_t* w8, int64_t ldw, const float* as,
-                     const float* ws, int m, int n, int k, float* out, int64_t ldo, int32_t* oi,
-                     int64_t ldoi, hipStream_t stream) {
-    const GemmTile r = gemm_route(m, n, k, device_cu_count());
+int gemm_workspace_counters(const GemmTile& tile, int m, int n) {
+    if (tile.bm == 0 || tile.splits <= 1) return 0;
+    return ((m + tile.bm - 1) / tile.bm) * ((n + tile.bn - 1) / tile.bn);
+}
+
+size_t gemm_workspace_bytes(const GemmTile& tile, int m, int n) {
+    const size_t tiles = static_cast<size_t>(gemm_workspace_counters(tile, m, n));
+    if (tiles == 0) return 0;
+    return kSplitCounterBytes + tiles * tile.splits * tile.bm * tile.bn * 4;
+}
+
+// The GEMM on a given tile, stage count and split (splits > 1 needs a
+// workspace of gemm_workspace_bytes(r, m, n) whose counters are zero; else it
+// runs unsplit).
+int launch_gemm_w8a8_tile(const GemmTile& r, const int8_t* a8, int64_t lda, const int8_t* w8, int64_t ldw,
+                          const float* as, const float* ws, int m, int n, int k, float* out, int64_t ldo,
+                          int32_t* oi, int64_t ldoi, uint8_t* workspace, hipStream_t stream) {
+    const int sp = r.splits;
 #define RK_GEMM(BM, BN, WM, WN, ST) \
-    launch_dma<BM, BN, WM, WN, ST, 128>(a8, lda, w8, ldw, as, ws, m, n, k, out, ldo, oi, ldoi, stream)
+    launch_dma<BM, BN, WM, WN, ST, 128>(a8, lda, w8, ldw, as, ws, m, n, k, out, ldo, oi, ldoi, sp, workspace, stream)
     if (r.bm == 0) return launch_gemm_w8a8_skinny(a8, lda, w8, ldw, as, ws, m, n, k, out, ldo, oi, ldoi, stream);
     if (r.bm == 64 && r.bn == 32) return r.stages == 2 ? RK_GEMM(64, 32, 2, 1, 2) : RK_GEMM(64, 32, 2, 1, 4);
     if (r.bm == 64) return r.stages == 2 ? RK_GEMM(64, 64, 2, 2, 2) : RK_GEMM(64, 64, 2, 2, 4);
@@ -474,6 +598,14 @@ int launch_gemm_w8a8(const int8_t* a8, int64_t lda, const int8_t* w8, int64_t ld
     if (r.bn == 128) return RK_GEMM(256, 128, 4, 2, 3);
     return RK_GEMM(256, 256, 2, 2, 2);
 #undef RK_GEMM
+}
+
+int launch_gemm_w8a8(const int8_t* a8, int64_t lda, const int8_t* w8, int64_t ldw, const float* as,
+                     const float* ws, int m, int n, int k, float* out, int64_t ldo, int32_t* oi,
+                     int64_t ldoi, uint8_t* workspace, size_t workspace_bytes, hipStream_t stream) {
+    GemmTile r = gemm_route(m, n, k, device_cu_count());
+    if (!workspace || workspace_bytes < gemm_workspace_bytes(r, m, n)) r.splits = 1;
+    return launch_gemm_w8a8_tile(r, a8, lda, w8, ldw, as, ws, m, n, k, out, ldo, oi, ldoi, workspace, stream);
 }
 
 }  // namespace rk

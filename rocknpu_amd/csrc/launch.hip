@@ -10,13 +10,8 @@
 namespace rk {
 int launch_repack_w8(int kind, const uint8_t* blocks, int64_t n, int nb, int64_t k_pad, int8_t* w8,
                      float* scales, hipStream_t stream);
-int launch_quantize_a8(const float* a, int64_t m, int64_t k, int64_t lda, int64_t k_pad, int8_t* a8,
-                       float* scales, hipStream_t stream);
 int launch_quantize_q8_k(const float* x, int64_t m, int64_t k, int64_t ldx, uint8_t* y,
                          hipStream_t stream);
-int launch_gemm_w8a8(const int8_t* a8, int64_t lda, const int8_t* w8, int64_t ldw, const float* as,
-                     const float* ws, int m, int n, int k, float* out, int64_t ldo, int32_t* oi,
-                     int64_t ldoi, hipStream_t stream);
 int launch_gemv(int kind, bool fused, GemvParams& p, hipStream_t stream);
 
 int device_cu_count() {
@@ -79,23 +74,76 @@ extern "C" int rocknpu_hip_quantize_a8(const float* a, size_t m, size_t k, size_
     if (!a || !a8 || !scales || m == 0 || k == 0 || lda < k || k_pad < k || m > kMaxGrid)
         return rk::kStatusInvalid;
     return rk::launch_quantize_a8(a, static_cast<int64_t>(m), static_cast<int64_t>(k),
-                                  static_cast<int64_t>(lda), static_cast<int64_t>(k_pad), a8, scales,
+                                  static_cast<int64_t>(lda), static_cast<int64_t>(k_pad), a8, scales, nullptr, 0,
                                   static_cast<hipStream_t>(stream));
+}
+
+namespace {
+bool gemm_args_ok(const int8_t* a8, const float* a_scales, const int8_t* w8, const float* w_scales, size_t m,
+                  size_t n, size_t k_pad, const float* out, size_t ldo) {
+    if (!a8 || !a_scales || !w8 || !w_scales || !out || m == 0 || n == 0 || k_pad == 0 || k_pad % 64 != 0 ||
+        ldo < n || m > INT_MAX || n > INT_MAX || k_pad > rk::kMaxExactK)
+        return false;
+    if (!aligned(a8, 16) || !aligned(w8, 16)) return false;
+    // worst-case tile count (16-row tiles, 64-column tiles) must fit one grid;
+    // routed K splits only run on tiles filling at most half the CUs
+    return ((m + 15) / 16) * ((n + 63) / 64) <= kMaxGrid;
+}
+}  // namespace
+
+extern "C" int rocknpu_hip_gemm_w8a8_ws(const int8_t* a8, const float* a_scales, const int8_t* w8,
+                                        const float* w_scales, size_t m, size_t n, size_t k_pad, float* out,
+                                        size_t ldo, int32_t* out_i32, void* workspace, size_t workspace_bytes,
+                                        void* stream) {
+    if (!gemm_args_ok(a8, a_scales, w8, w_scales, m, n, k_pad, out, ldo)) return rk::kStatusInvalid;
+    if (workspace_bytes > 0 && (!workspace || !aligned(workspace, 256))) return rk::kStatusInvalid;
+    return rk::launch_gemm_w8a8(a8, static_cast<int64_t>(k_pad), w8, static_cast<int64_t>(k_pad), a_scales,
+                                w_scales, static_cast<int>(m), static_cast<int>(n), static_cast<int>(k_pad), out,
+                                static_cast<int64_t>(ldo), out_i32, static_cast<int64_t>(n),
+                                static_cast<uint8_t*>(workspace), workspace_bytes, static_cast<hipStream_t>(stream));
 }
 
 extern "C" int rocknpu_hip_gemm_w8a8(const int8_t* a8, const float* a_scales, const int8_t* w8,
                                      const float* w_scales, size_t m, size_t n, size_t k_pad, float* out,
                                      size_t ldo, int32_t* out_i32, void* stream) {
-    if (!a8 || !a_scales || !w8 || !w_scales || !out || m == 0 || n == 0 || k_pad == 0 || k_pad % 64 != 0 ||
-        ldo < n || m > INT_MAX || n > INT_MAX || k_pad > rk::kMaxExactK)
+    return rocknpu_hip_gemm_w8a8_ws(a8, a_scales, w8, w_scales, m, n, k_pad, out, ldo, out_i32, nullptr, 0, stream);
+}
+
+extern "C" int rocknpu_hip_gemm_w8a8_tile(int bm, int bn, int stages, int splits, const int8_t* a8,
+                                          const float* a_scales, const int8_t* w8, const float* w_scales, size_t m,
+                                          size_t n, size_t k_pad, float* out, size_t ldo, int32_t* out_i32,
+                                          void* workspace, size_t workspace_bytes, void* stream) {
+    if (!gemm_args_ok(a8, a_scales, w8, w_scales, m, n, k_pad, out, ldo)) return rk::kStatusInvalid;
+    // the tiles and stage counts the launcher instantiates
+    const bool known = (bm == 0 && m <= 16 && m * k_pad <= static_cast<size_t>(rk::kSkinnyMaxA8)) ||
+                       (bm == 64 && bn == 32 && (stages == 2 || stages == 4)) ||
+                       (bm == 64 && bn == 64 && (stages == 2 || stages == 4)) ||
+                       (bm == 128 && bn == 64 && (stages == 2 || stages == 4)) ||
+                       (bm == 128 && bn == 128 && (stages == 2 || stages == 3)) ||
+                       (bm == 256 && bn == 128 && stages == 3) || (bm == 256 && bn == 256 && stages == 2);
+    if (!known || splits < 1 || splits > 16) return rk::kStatusInvalid;
+    rk::GemmTile r{bm, bn, stages};
+    r.splits = bm == 0 ? 1 : splits;
+    if (r.splits > 1 &&
+        (!workspace || !aligned(workspace, 256) ||
+         workspace_bytes < rk::gemm_workspace_bytes(r, static_cast<int>(m), static_cast<int>(n)) ||
+         rk::gemm_workspace_counters(r, static_cast<int>(m), static_cast<int>(n)) > rk::kSplitCounters))
         return rk::kStatusInvalid;
-    if (!aligned(a8, 16) || !aligned(w8, 16)) return rk::kStatusInvalid;
-    // worst-case tile count (16-row tiles, 64-column tiles) must fit one grid
-    if (((m + 15) / 16) * ((n + 63) / 64) > kMaxGrid) return rk::kStatusInvalid;
-    return rk::launch_gemm_w8a8(a8, static_cast<int64_t>(k_pad), w8, static_cast<int64_t>(k_pad), a_scales,
-                                w_scales, static_cast<int>(m), static_cast<int>(n), static_cast<int>(k_pad),
-                                out, static_cast<int64_t>(ldo), out_i32, static_cast<int64_t>(n),
-                                static_cast<hipStream_t>(stream));
+    return rk::launch_gemm_w8a8_tile(r, a8, static_cast<int64_t>(k_pad), w8, static_cast<int64_t>(k_pad), a_scales,
+                                     w_scales, static_cast<int>(m), static_cast<int>(n), static_cast<int>(k_pad), out,
+                                     static_cast<int64_t>(ldo), out_i32, static_cast<int64_t>(n),
+                                     static_cast<uint8_t*>(workspace), static_cast<hipStream_t>(stream));
+}
+
+extern "C" int rocknpu_hip_gemm_workspace(size_t m, size_t n, size_t k_pad, int cus, size_t* bytes, int* splits) {
+    if (!bytes || !splits || m == 0 || n == 0 || k_pad == 0 || k_pad % 64 != 0 || m > INT_MAX || n > INT_MAX ||
+        k_pad > INT_MAX)
+        return rk::kStatusInvalid;
+    if (cus <= 0) cus = rk::device_cu_count();
+    const rk::GemmTile r = rk::gemm_route(static_cast<int>(m), static_cast<int>(n), static_cast<int>(k_pad), cus);
+    *bytes = rk::gemm_workspace_bytes(r, static_cast<int>(m), static_cast<int>(n));
+    *splits = r.splits;
+    return rk::kStatusOk;
 }
 
 extern "C" int rocknpu_hip_gemm_route(size_t m, size_t n, size_t k_pad, int cus, int* bm, int* bn, int* stages) {

@@ -35,6 +35,13 @@ __device__ __forceinline__ uint32_t pack4(int a, int b, int c, int d) {
     return (a & 0xFF) | (b & 0xFF) << 8 | (c & 0xFF) << 16 | static_cast<uint32_t>(d & 0xFF) << 24;
 }
 
+// Workgroup 0 clears `nzero` words (the split-K counters of the GEMM that
+// follows on the stream), so the prompt route needs no separate fill launch.
+__device__ __forceinline__ void zero_counters(uint32_t* words, int nzero) {
+    if (blockIdx.x == 0)
+        for (int i = threadIdx.x; i < nzero; i += blockDim.x) words[i] = 0;
+}
+
 // One workgroup per activation row. VEC: k, lda and k_pad are multiples of 4
 // and both base pointers are 16-byte aligned.
 template <bool VEC>
@@ -42,8 +49,9 @@ __global__ __launch_bounds__(kA8Threads) void quantize_a8_kernel(const float* __
                                                                  int64_t k, int64_t lda,
                                                                  int64_t k_pad,
                                                                  int8_t* __restrict__ a8,
-                                                                 float* __restrict__ scales) {
+                                                                 float* __restrict__ scales, uint32_t* __restrict__ zero_words, int nzero) {
     __shared__ float red[kA8Threads / 64];
+    zero_counters(zero_words, nzero);
     const int64_t row = blockIdx.x;
     const float* x = a + row * lda;
     int8_t* q = a8 + row * k_pad;
@@ -104,8 +112,9 @@ __global__ __launch_bounds__(kA8Threads) void quantize_a8_regs_kernel(const floa
                                                                       int64_t k, int64_t lda,
                                                                       int64_t k_pad,
                                                                       int8_t* __restrict__ a8,
-                                                                      float* __restrict__ scales) {
+                                                                      float* __restrict__ scales, uint32_t* __restrict__ zero_words, int nzero) {
     __shared__ float red[kA8Threads / 64];
+    zero_counters(zero_words, nzero);
     const int64_t row = blockIdx.x;
     const float4* x = reinterpret_cast<const float4*>(a + row * lda);
     uint32_t* q = reinterpret_cast<uint32_t*>(a8 + row * k_pad);
@@ -202,22 +211,22 @@ __global__ __launch_bounds__(256) void quantize_q8_k_kernel(const float* __restr
 }  // namespace
 
 int launch_quantize_a8(const float* a, int64_t m, int64_t k, int64_t lda, int64_t k_pad, int8_t* a8,
-                       float* scales, hipStream_t stream) {
+                       float* scales, uint32_t* zero_words, int nzero, hipStream_t stream) {
     const bool vec = k % 4 == 0 && lda % 4 == 0 && k_pad % 4 == 0 &&
                      reinterpret_cast<uintptr_t>(a) % 16 == 0 && reinterpret_cast<uintptr_t>(a8) % 16 == 0;
     const dim3 grid(static_cast<unsigned>(m)), block(kA8Threads);
     // float4 per thread that hold the row
     const int64_t per = (k / 4 + kA8Threads - 1) / kA8Threads;
     if (vec && per <= 16) {
-        if (per <= 1) quantize_a8_regs_kernel<1><<<grid, block, 0, stream>>>(a, k, lda, k_pad, a8, scales);
-        else if (per <= 2) quantize_a8_regs_kernel<2><<<grid, block, 0, stream>>>(a, k, lda, k_pad, a8, scales);
-        else if (per <= 4) quantize_a8_regs_kernel<4><<<grid, block, 0, stream>>>(a, k, lda, k_pad, a8, scales);
-        else if (per <= 6) quantize_a8_regs_kernel<6><<<grid, block, 0, stream>>>(a, k, lda, k_pad, a8, scales);
-        else if (per <= 8) quantize_a8_regs_kernel<8><<<grid, block, 0, stream>>>(a, k, lda, k_pad, a8, scales);
-        else if (per <= 12) quantize_a8_regs_kernel<12><<<grid, block, 0, stream>>>(a, k, lda, k_pad, a8, scales);
-        else quantize_a8_regs_kernel<16><<<grid, block, 0, stream>>>(a, k, lda, k_pad, a8, scales);
-    } else if (vec) quantize_a8_kernel<true><<<grid, block, 0, stream>>>(a, k, lda, k_pad, a8, scales);
-    else quantize_a8_kernel<false><<<grid, block, 0, stream>>>(a, k, lda, k_pad, a8, scales);
+        if (per <= 1) quantize_a8_regs_kernel<1><<<grid, block, 0, stream>>>(a, k, lda, k_pad, a8, scales, zero_words, nzero);
+        else if (per <= 2) quantize_a8_regs_kernel<2><<<grid, block, 0, stream>>>(a, k, lda, k_pad, a8, scales, zero_words, nzero);
+        else if (per <= 4) quantize_a8_regs_kernel<4><<<grid, block, 0, stream>>>(a, k, lda, k_pad, a8, scales, zero_words, nzero);
+        else if (per <= 6) quantize_a8_regs_kernel<6><<<grid, block, 0, stream>>>(a, k, lda, k_pad, a8, scales, zero_words, nzero);
+        else if (per <= 8) quantize_a8_regs_kernel<8><<<grid, block, 0, stream>>>(a, k, lda, k_pad, a8, scales, zero_words, nzero);
+        else if (per <= 12) quantize_a8_regs_kernel<12><<<grid, block, 0, stream>>>(a, k, lda, k_pad, a8, scales, zero_words, nzero);
+        else quantize_a8_regs_kernel<16><<<grid, block, 0, stream>>>(a, k, lda, k_pad, a8, scales, zero_words, nzero);
+    } else if (vec) quantize_a8_kernel<true><<<grid, block, 0, stream>>>(a, k, lda, k_pad, a8, scales, zero_words, nzero);
+    else quantize_a8_kernel<false><<<grid, block, 0, stream>>>(a, k, lda, k_pad, a8, scales, zero_words, nzero);
     return hipGetLastError() == hipSuccess ? kStatusOk : kStatusExec;
 }
 

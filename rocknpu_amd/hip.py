@@ -73,16 +73,71 @@ def quantize_a8(a: torch.Tensor, k_pad: int | None = None, a8: torch.Tensor | No
     return a8, scales
 
 
+def gemm_workspace(m: int, n: int, k_pad: int, cus: int = 0) -> tuple[int, int]:
+    """(bytes, K splits) of the workspace the GEMM's route uses for m x n x k_pad."""
+    nb = ctypes.c_size_t()
+    sp = ctypes.c_int()
+    _check(_lib.load().rocknpu_hip_gemm_workspace(m, n, k_pad, cus, ctypes.byref(nb), ctypes.byref(sp)),
+           "gemm_workspace")
+    return nb.value, sp.value
+
+
+# Zeroed K-split workspaces, one per device: the GEMM leaves their counters
+# at zero. Calls that use it must not overlap (one stream, or streams ordered
+# with each other); overlapping calls pass workspaces of their own.
+_workspaces: dict[int, torch.Tensor] = {}
+
+
+def workspace_for(device: torch.device, nbytes: int) -> torch.Tensor:
+    """This module's zeroed workspace of at least nbytes on `device`."""
+    key = torch.device(device).index or 0
+    ws = _workspaces.get(key)
+    if ws is None or ws.numel() < nbytes:
+        ws = torch.zeros(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
+        _workspaces[key] = ws
+    return ws
+
+
 def gemm_w8a8(a8: torch.Tensor, a_scales: torch.Tensor, w8: torch.Tensor, w_scales: torch.Tensor,
-              out: torch.Tensor | None = None, out_i32: torch.Tensor | None = None) -> torch.Tensor:
-    """Kernel (c): out[m, n] = (f32(A8 W8^T) * a_scales) * w_scales."""
+              out: torch.Tensor | None = None, out_i32: torch.Tensor | None = None,
+              workspace: torch.Tensor | bool | None = True) -> torch.Tensor:
+    """Kernel (c): out[m, n] = (f32(A8 W8^T) * a_scales) * w_scales.
+
+    workspace: True (default) splits K where the route does, in this module's
+    zeroed workspace for the current stream; a uint8 device tensor supplies
+    one (zeroed once by the caller); None or False runs the call without one
+    (rocknpu_hip_gemm_w8a8, never split). The bits are the same either way."""
     m, kp = a8.shape
     n = w8.shape[0]
     assert w8.shape[1] == kp and a8.is_contiguous() and w8.is_contiguous()
     if out is None:
         out = torch.empty((m, n), dtype=torch.float32, device=a8.device)
-    _check(_lib.load().rocknpu_hip_gemm_w8a8(_ptr(a8), _ptr(a_scales), _ptr(w8), _ptr(w_scales), m, n, kp,
-                                             _ptr(out), _ld(out), _ptr(out_i32), _stream()), "gemm_w8a8")
+    lib = _lib.load()
+    if workspace is None or workspace is False:
+        _check(lib.rocknpu_hip_gemm_w8a8(_ptr(a8), _ptr(a_scales), _ptr(w8), _ptr(w_scales), m, n, kp,
+                                         _ptr(out), _ld(out), _ptr(out_i32), _stream()), "gemm_w8a8")
+        return out
+    if workspace is True:
+        nbytes, _ = gemm_workspace(m, n, kp)
+        workspace = workspace_for(a8.device, nbytes) if nbytes else None
+    _check(lib.rocknpu_hip_gemm_w8a8_ws(_ptr(a8), _ptr(a_scales), _ptr(w8), _ptr(w_scales), m, n, kp, _ptr(out),
+                                        _ld(out), _ptr(out_i32), _ptr(workspace),
+                                        0 if workspace is None else workspace.numel(), _stream()), "gemm_w8a8_ws")
+    return out
+
+
+def gemm_w8a8_tile(bm: int, bn: int, stages: int, splits: int, a8: torch.Tensor, a_scales: torch.Tensor,
+                   w8: torch.Tensor, w_scales: torch.Tensor, out: torch.Tensor | None = None,
+                   out_i32: torch.Tensor | None = None, workspace: torch.Tensor | None = None) -> torch.Tensor:
+    """Kernel (c) on a given tile, stage count and K split (tests and tuning)."""
+    m, kp = a8.shape
+    n = w8.shape[0]
+    if out is None:
+        out = torch.empty((m, n), dtype=torch.float32, device=a8.device)
+    _check(_lib.load().rocknpu_hip_gemm_w8a8_tile(bm, bn, stages, splits, _ptr(a8), _ptr(a_scales), _ptr(w8),
+                                                  _ptr(w_scales), m, n, kp, _ptr(out), _ld(out), _ptr(out_i32),
+                                                  _ptr(workspace), 0 if workspace is None else workspace.numel(),
+                                                  _stream()), "gemm_w8a8_tile")
     return out
 
 

@@ -101,3 +101,74 @@ def test_fewer_cus_and_bad_arguments():
     assert lib.rocknpu_hip_gemm_route(0, 64, 64, CUS, *ptrs) == -1
     assert lib.rocknpu_hip_gemm_route(4, 64, 100, CUS, *ptrs) == -1  # k_pad % 64 != 0
     assert lib.rocknpu_hip_gemm_route(4, 64, 64, CUS, None, ptrs[1], ptrs[2]) == -1
+
+
+def workspace(m, n, k, cus=CUS):
+    nb, sp = ctypes.c_size_t(), ctypes.c_int()
+    assert _lib.load().rocknpu_hip_gemm_workspace(m, n, k, cus, ctypes.byref(nb), ctypes.byref(sp)) == 0
+    return nb.value, sp.value
+
+
+@pytest.mark.parametrize("m,n,k,splits", [
+    # 64 x 32 tiles on half the CUs, long K: split so the units fill the CUs
+    (128, 2048, 2048, 2),    # TinyLlama o at 128 tokens: 8.19 -> 7.56 us
+    (128, 2048, 5632, 2),    # TinyLlama down: 13.6 -> 10.7 us
+    (128, 2048, 8192, 2),    # Llama-3.2-1B down: 18.1 -> 12.9 us
+    (64, 4096, 14336, 2),
+    (32, 2048, 8192, 4),     # 32 tiles: four splits of 16 stages
+    # measured slower split, or not under-filled: unsplit
+    (128, 5632, 2048, 1),    # 176 64 x 64 tiles (8.4 against 12.0 us split)
+    (128, 2560, 2048, 1),    # 160 tiles: more than half the CUs
+    (1024, 8192, 4096, 1),   # 256 x 256 tiles (58.5 against 63.9 us split)
+    (512, 11264, 2048, 1),
+    (4096, 14336, 4096, 1),
+    (128, 2048, 256, 1),     # two stages: nothing to split
+    (8, 2048, 8192, 1),      # the weight-streaming kernel
+])
+def test_split_rule(m, n, k, splits):
+    nb, sp = workspace(m, n, k)
+    assert sp == splits
+    bm, bn, _ = route(m, n, k)
+    if sp == 1:
+        assert nb == 0
+    else:
+        t = tiles(m, n, bm, bn)
+        # the fixed 16 KiB counter block, then splits x bm x bn int32 per tile
+        assert nb == 16384 + t * sp * bm * bn * 4
+
+
+def test_split_invariants_over_a_grid():
+    ms = (1, 16, 17, 32, 64, 100, 128, 200, 256, 512, 1024, 4096)
+    ns = (16, 100, 1024, 2048, 2560, 4096, 5632, 11264, 32000)
+    ks = (64, 256, 1024, 2048, 5632, 8192, 14336)
+    for m, n, k in itertools.product(ms, ns, ks):
+        nb, sp = workspace(m, n, k)
+        bm, bn, _ = route(m, n, k)
+        if sp == 1:
+            assert nb == 0
+            continue
+        t = tiles(m, n, bm, bn)
+        stages = k // 128 if k % 128 == 0 else k // 64
+        assert bm * bn <= 64 * 64 and 2 * t <= CUS, (m, n, k)
+        assert 2 <= sp <= 4 and t * sp <= CUS and stages // sp >= 8, (m, n, k, sp)
+        # the no-allocation entry's fixed split workspace holds every routed split on 256 CUs
+        assert nb <= (4 << 20) + 16384, (m, n, k, nb)
+
+
+def test_workspace_and_tile_bad_arguments():
+    lib = _lib.load()
+    nb, sp = ctypes.c_size_t(), ctypes.c_int()
+    assert lib.rocknpu_hip_gemm_workspace(0, 64, 64, CUS, ctypes.byref(nb), ctypes.byref(sp)) == -1
+    assert lib.rocknpu_hip_gemm_workspace(4, 64, 100, CUS, ctypes.byref(nb), ctypes.byref(sp)) == -1
+    assert lib.rocknpu_hip_gemm_workspace(4, 64, 64, CUS, None, ctypes.byref(sp)) == -1
+    # every check below fails on the host, before any GPU call
+    p = ctypes.c_void_p(1 << 20)  # never dereferenced
+    args = (p, p, p, p, 128, 2048, 2048, p, 2048, None)
+    assert lib.rocknpu_hip_gemm_w8a8_tile(64, 48, 4, 1, *args, None, 0, None) == -1   # no such tile
+    assert lib.rocknpu_hip_gemm_w8a8_tile(64, 64, 3, 1, *args, None, 0, None) == -1   # no such stage count
+    assert lib.rocknpu_hip_gemm_w8a8_tile(64, 32, 4, 0, *args, None, 0, None) == -1   # splits < 1
+    assert lib.rocknpu_hip_gemm_w8a8_tile(64, 32, 4, 2, *args, None, 0, None) == -1   # split without workspace
+    small = 16384 + (128 // 64) * (2048 // 32) * 2 * 64 * 32 * 4 - 4  # four bytes short
+    assert lib.rocknpu_hip_gemm_w8a8_tile(64, 32, 4, 2, *args, p, small, None) == -1
+    assert lib.rocknpu_hip_gemm_w8a8_ws(*args, ctypes.c_void_p((1 << 20) + 16), 4096, None) == -1  # unaligned
+    assert lib.rocknpu_hip_gemm_w8a8_ws(*args, None, 4096, None) == -1

@@ -1,0 +1,124 @@
+"""K-split W8A8 GEMM on the GPU (rocknpu_hip_gemm_w8a8_ws / _tile): every tile
+and split count gives the oracle's int32 accumulators and f32 outputs bit for
+bit and leaves the workspace counters at zero; routed splits agree through the
+launch layer, the device-pointer prompt route and the C ABI; graph replays of
+split launches agree with the eager result."""
+import numpy as np
+import pytest
+import torch
+
+from oracle import oracle as orc
+from rocknpu_amd import hip, synth
+from rocknpu_amd.capi import Context
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+TILES = [(64, 32, 4), (64, 32, 2), (64, 64, 4), (64, 64, 2), (128, 64, 4), (128, 64, 2), (128, 128, 3),
+         (128, 128, 2), (256, 128, 3), (256, 256, 2)]
+
+
+def _bits(x):
+    return np.ascontiguousarray(x, np.float32).view(np.uint32)
+
+
+def _operands(m, n, k, seed):
+    g = np.random.default_rng(seed)
+    a8 = g.integers(-127, 128, (m, k), dtype=np.int8)
+    w8 = g.integers(-127, 128, (n, k), dtype=np.int8)
+    as_ = (g.random(m, dtype=np.float32) + np.float32(0.01)) / np.float32(127)
+    ws = (g.random(n, dtype=np.float32) + np.float32(0.01)) / np.float32(127)
+    return a8, w8, as_, ws
+
+
+def _counter_bytes(m, n, bm, bn):
+    return 16384, -(-m // bm) * -(-n // bn)
+
+
+@pytest.mark.parametrize("m,n,k", [
+    (128, 512, 2048),   # 16 stages of 128 bytes
+    (100, 300, 5632),   # ragged edges, 44 stages
+    (37, 200, 1088),    # K % 128 != 0: 17 stages of 64 bytes (seven splits become six)
+    (64, 256, 8192),
+    (260, 130, 1024),   # 256-row tiles past the edge
+])
+def test_split_every_tile_bit_exact(m, n, k):
+    a8, w8, as_, ws = _operands(m, n, k, m * 7 + n + k)
+    c_ref = orc.gemm_i32(a8, w8, threads=8)
+    out_ref = _bits(orc.rescale(c_ref, as_, ws))
+    d = [torch.from_numpy(x).to(DEV) for x in (a8, as_, w8, ws)]
+    for bm, bn, st in TILES:
+        cb, t = _counter_bytes(m, n, bm, bn)
+        for sp in (1, 2, 3, 4, 7):
+            print(f"split gemm m={m} n={n} k={k} tile={bm}x{bn}/{st} splits={sp}", flush=True)
+            work = torch.zeros(cb + t * sp * bm * bn * 4, dtype=torch.uint8, device=DEV) if sp > 1 else None
+            c = torch.full((m, n), -1, dtype=torch.int32, device=DEV)
+            out = hip.gemm_w8a8_tile(bm, bn, st, sp, d[0], d[1], d[2], d[3], out_i32=c, workspace=work)
+            torch.cuda.synchronize()
+            assert np.array_equal(c.cpu().numpy(), c_ref), (bm, bn, st, sp)
+            assert np.array_equal(_bits(out.cpu().numpy()), out_ref), (bm, bn, st, sp)
+            if work is not None:
+                assert not work[:cb].any().item(), "counters not left at zero"
+
+
+def test_routed_split_through_every_entry():
+    """128 x 2048 x 5632 (TinyLlama down at 128 tokens) splits K in two on the
+    route: launch layer with and without a workspace, the prompt route and the
+    C ABI agree with the oracle; calls of another shape in between."""
+    m, k, n = 128, 5632, 2048
+    nbytes, splits = hip.gemm_workspace(m, n, k)
+    assert splits == 2 and nbytes > 0
+    blocks = synth.q6_k(n, k, index=40)
+    act = synth.activations(m, k, index=41)
+    ref = orc.matmul_q_w8a8(6, blocks, act, n, threads=8)
+    w8, wsc = hip.repack_w8(6, torch.from_numpy(blocks).to(DEV), k, n)
+    a = torch.from_numpy(act).to(DEV)
+    a8, asc = hip.quantize_a8(a)
+    work = torch.zeros(nbytes, dtype=torch.uint8, device=DEV)
+    outs = []
+    for step in range(3):
+        print(f"routed split step {step}", flush=True)
+        outs.append(hip.gemm_w8a8(a8, asc, w8, wsc, workspace=work))
+        outs.append(hip.gemm_w8a8(a8, asc, w8, wsc, workspace=None))
+        outs.append(hip.matmul_w8a8_f32(a, w8, wsc))
+        # a smaller split shape in between, on the same workspace
+        hip.gemm_w8a8(a8[:32], asc[:32], w8[:1024], wsc[:1024], workspace=work)
+    torch.cuda.synchronize()
+    assert not work[:16384].any().item()
+    for o in outs:
+        assert np.array_equal(_bits(o.cpu().numpy()), _bits(ref))
+    with Context() as ctx:
+        host = np.empty((m, n), np.float32)
+        for _ in range(2):
+            assert ctx.matmul_q(6, blocks, act, host, k, n) == 0
+            assert np.array_equal(_bits(host), _bits(ref))
+
+
+def test_split_graph_replays_match_eager():
+    m, n, k = 128, 2048, 8192
+    assert hip.gemm_workspace(m, n, k)[1] > 1
+    a8, w8, as_, ws = _operands(m, n, k, 5)
+    d = [torch.from_numpy(x).to(DEV) for x in (a8, as_, w8, ws)]
+    eager = hip.gemm_w8a8(*d)
+    torch.cuda.synchronize()
+    want = _bits(eager.cpu().numpy())
+    out = torch.empty_like(eager)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        hip.gemm_w8a8(*d, out=out)
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        hip.gemm_w8a8(*d, out=out)
+        hip.gemm_w8a8(*d, out=out)
+    for rep in range(4):
+        print(f"split graph replay {rep}", flush=True)
+        out.fill_(float("nan"))
+        g.replay()
+        torch.cuda.synchronize()
+        assert np.array_equal(_bits(out.cpu().numpy()), want), rep
+        # eager work between replays
+        hip.gemm_w8a8(d[0][:64], d[1][:64], d[2], d[3])
+        torch.cuda.synchronize()
