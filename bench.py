@@ -183,7 +183,8 @@ def w8a8_gemm(torch, hip, synth, m: int, n: int, k: int, reps: int, rotate_bytes
     byts = n * kp + m * kp + 4 * (m + n) + 4 * m * n
     tops = ops / (per * 1e-3) / 1e12
     bound_tops = min(INT8_PEAK_TOPS, HBM_PEAK_GBS * ops / byts / 1e3)
-    return {"m": m, "n": n, "k": k, "us": round(per * 1e3, 3), "tops": round(tops, 2),
+    return {"m": m, "n": n, "k": k, "k_splits": hip.gemm_workspace(m, n, kp)[1], "us": round(per * 1e3, 3),
+            "tops": round(tops, 2),
             "frac_int8_peak": round(tops / INT8_PEAK_TOPS, 4),
             "roofline_tops": round(bound_tops, 1), "frac_roofline": round(tops / bound_tops, 4),
             "bound": "mfma" if bound_tops >= INT8_PEAK_TOPS else "hbm", "weight_copies": copies}
@@ -640,7 +641,8 @@ def main():
                    "layers": synth.TINYLLAMA_LAYERS, "m": [1, 4], "launches_per_step": n_gemv,
                    "bytes_per_step": step_bytes},
         "roofline": {"bound": "hbm", "kernel": "Q4_K x Q8_K decode GEMV at M=4 on the matrix cores with fused "
-                                               "Q8_K quant (gemv_mfma_kernel<4,4,true,...>), the 66 Q4_K launches "
+                                               "Q8_K quant (gemv_mfma_kernel<4,4,true,...> for q/k/v and o, "
+                                               "gemv_q4_staged_kernel<4,true> for gate+up), the 66 Q4_K launches "
                                                "of a step",
                      "achieved": round(m4_achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(m4_achieved / HBM_PEAK_GBS, 4), "traffic": measured_traffic("gemv_q4k_m4"),
