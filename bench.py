@@ -20,7 +20,7 @@ timed on the host cores (all usable threads up to 16, and one) as a baseline.
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--quick] [--no-cpu]
        python bench.py --profile {gemv-q4k,gemv-q4k-m4,gemm,gemm-512,gemm-128,repack-q4k,repack-q6k,a8-4096,a8-512,copy}
            (workload only, for rocprofv3 counter runs)
-       python bench.py --vs-hipblaslt   (W8A8 GEMM against torch._int_mm over 140 prefill shapes, one JSON line each)
+       python bench.py --vs-hipblaslt   (W8A8 GEMM against torch._int_mm over 155 prefill shapes, one JSON line each)
 """
 from __future__ import annotations
 
@@ -409,25 +409,28 @@ def vs_hipblaslt(torch, hip, synth) -> None:
     """One line per shape: this GEMM (rescale fused, f32 out) against
     hipBLASLt's int8 GEMM through torch._int_mm (i32 out, no rescale), both
     on weight copies rotating through >= 512 MiB, M x N x K over prefill
-    sizes of the TinyLlama, Llama-3.2-1B and Llama-3-8B projections."""
+    sizes of the TinyLlama, Llama-3.2-1B and Llama-3-8B projections, and
+    their down projections' long K."""
     rotate = 512 << 20
-    for m in (64, 128, 256, 384, 512, 768, 1024, 1536, 2048, 4096):
-        for n in (2048, 2560, 4096, 5632, 11264, 14336, 28672):
-            for k in (2048, 4096):
-                ours = w8a8_gemm(torch, hip, synth, m, n, k, reps=20, rotate_bytes=rotate)["us"]
-                copies = max(1, min(64, rotate // (n * k) + 1))
-                ws = [torch.randint(-127, 128, (n, k), dtype=torch.int8, device="cuda") for _ in range(copies)]
-                a = torch.randint(-127, 128, (max(m, 17), k), dtype=torch.int8, device="cuda")  # _int_mm needs m > 16
+    shapes = [(m, n, k) for m in (64, 128, 256, 384, 512, 768, 1024, 1536, 2048, 4096)
+              for n in (2048, 2560, 4096, 5632, 11264, 14336, 28672) for k in (2048, 4096)]
+    # the down projections' long K (TinyLlama 5632, Llama-3.2-1B 8192, Llama-3-8B 14336)
+    shapes += [(m, n, k) for m in (64, 128, 256, 512, 2048) for n, k in ((2048, 5632), (2048, 8192), (4096, 14336))]
+    for m, n, k in shapes:
+        ours = w8a8_gemm(torch, hip, synth, m, n, k, reps=20, rotate_bytes=rotate)["us"]
+        copies = max(1, min(64, rotate // (n * k) + 1))
+        ws = [torch.randint(-127, 128, (n, k), dtype=torch.int8, device="cuda") for _ in range(copies)]
+        a = torch.randint(-127, 128, (max(m, 17), k), dtype=torch.int8, device="cuda")  # _int_mm needs m > 16
 
-                def run():
-                    for w in ws:
-                        torch._int_mm(a, w.t())
+        def run():
+            for w in ws:
+                torch._int_mm(a, w.t())
 
-                ms, _ = time_graph(torch, run, max(1, 20 // copies), 2)
-                theirs = ms * 1e3 / copies
-                print(json.dumps({"m": m, "n": n, "k": k, "us": ours, "int_mm_us": round(theirs, 3),
-                                  "speedup": round(theirs / ours, 3)}), flush=True)
-                del ws
+        ms, _ = time_graph(torch, run, max(1, 20 // copies), 2)
+        theirs = ms * 1e3 / copies
+        print(json.dumps({"m": m, "n": n, "k": k, "k_splits": hip.gemm_workspace(m, n, k)[1], "us": ours,
+                          "int_mm_us": round(theirs, 3), "speedup": round(theirs / ours, 3)}), flush=True)
+        del ws
 
 
 def profile_workload(torch, hip, synth, which: str) -> None:
