@@ -659,7 +659,7 @@ def main():
     if not args.quick:
         rot = 1 << 30
         result["w8a8"] = {
-            "config0_m128": w8a8_gemm(torch, hip, synth, 128, 5632, 2048, 200, rot),
+            "q4k_5632x2048_m128": w8a8_gemm(torch, hip, synth, 128, 5632, 2048, 200, rot),
             "tinyllama_gateup_m512": w8a8_gemm(torch, hip, synth, 512, 11264, 2048, 100, rot),
             "llama3_8b_ffn_m4096": w8a8_gemm(torch, hip, synth, 4096, 14336, 4096, 8, rot),
         }

@@ -203,7 +203,7 @@ def test_gemm_reference_kats():
     assert np.array_equal(c, np.broadcast_to(exp, (m, n)))
 
 
-def test_w8a8_pipeline_config0():
+def test_w8a8_pipeline_q4k_5632x2048_128_tokens():
     """Repack -> A8 quant -> GEMM for the 5632x2048 Q4_K weight and 128 tokens."""
     m, k, n = 128, 2048, 5632
     blocks = synth.q4_k(n, k, index=0)
