@@ -18,7 +18,7 @@ repacked Q4_K/Q6_K weights; large and batched decode GEMVs; and the CPU oracle
 timed on the host cores (all usable threads up to 16, and one) as a baseline.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--quick] [--no-cpu]
-       python bench.py --profile {gemv-q4k,gemv-q4k-m4,gemm,gemm-512,gemm-128,repack-q4k,repack-q6k,a8-4096,a8-512,copy}
+       python bench.py --profile {gemv-q4k,gemv-q4k-m4,gemm,gemm-512,gemm-128,gemm-128-split,repack-q4k,repack-q6k,a8-4096,a8-512,copy}
            (workload only, for rocprofv3 counter runs)
        python bench.py --vs-hipblaslt   (W8A8 GEMM against torch._int_mm over 155 prefill shapes, one JSON line each)
 """
@@ -48,7 +48,7 @@ def parse():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--quick", action="store_true", help="skip the extra W8A8 shapes and the CPU baseline")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
-    ap.add_argument("--profile", choices=["gemv-q4k", "gemv-q4k-m4", "gemm", "gemm-512", "gemm-128", "copy",
+    ap.add_argument("--profile", choices=["gemv-q4k", "gemv-q4k-m4", "gemm", "gemm-512", "gemm-128", "gemm-128-split", "copy",
                                           "repack-q4k", "repack-q6k", "a8-4096", "a8-512"],
                     help="run one workload eagerly a few times and exit (for rocprofv3 --pmc passes)")
     ap.add_argument("--vs-hipblaslt", action="store_true",
@@ -440,8 +440,10 @@ def profile_workload(torch, hip, synth, which: str) -> None:
         for _ in range(3):
             ds.step(only_kind=4, only_m=1 if which == "gemv-q4k" else 4)
     elif which.startswith("gemm"):
-        # Llama-3-8B FFN at M=4096; TinyLlama gate+up at M=512; 128 x 5632 x 2048
-        m, n, k = {"gemm": (4096, 14336, 4096), "gemm-512": (512, 11264, 2048), "gemm-128": (128, 5632, 2048)}[which]
+        # Llama-3-8B FFN at M=4096; TinyLlama gate+up at M=512; 128 x 5632 x 2048; TinyLlama
+        # down at M=128 (K split in two)
+        m, n, k = {"gemm": (4096, 14336, 4096), "gemm-512": (512, 11264, 2048), "gemm-128": (128, 5632, 2048),
+                   "gemm-128-split": (128, 2048, 5632)}[which]
         w = torch.randint(-127, 128, (n, k), dtype=torch.int8, device="cuda")
         wsc = torch.rand(n, device="cuda") / 127 + 1e-3
         a8, asc = hip.quantize_a8(torch.from_numpy(synth.activations(m, k, index=5)).to("cuda"), k)
