@@ -618,14 +618,20 @@ def main():
     # dominant kernel: the Q4_K x Q8_K GEMV at M=4 on the matrix cores (the
     # largest share of a step), its launches timed alone in the same sequence;
     # the single-row launches of the same weights are timed beside it
-    def kernel_rate(only_m):
-        b, launches = ds.bytes_per_step(only_kind=4, only_m=only_m)
-        t_ms, _ = time_graph(torch, lambda: ds.step(only_kind=4, only_m=only_m), args.steps, args.warmup)
+    def kernel_rate(only_m, kind=4):
+        b, launches = ds.bytes_per_step(only_kind=kind, only_m=only_m)
+        t_ms, _ = time_graph(torch, lambda: ds.step(only_kind=kind, only_m=only_m), args.steps, args.warmup)
         us = t_ms * 1e3 / launches
         return b // launches, us, b / launches / (us * 1e-6) / 1e9
 
     q4_bpl, q4_us, achieved = kernel_rate(1)
     m4_bpl, m4_us, m4_achieved = kernel_rate(4)
+    # the Q6_K down projections of the same step (the other kind), for where the time goes
+    q6 = {}
+    for m in (1, 4):
+        bpl, us, gbs = kernel_rate(m, kind=6)
+        q6[f"m{m}"] = {"achieved": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4), "avg_launch_us": round(us, 3),
+                       "bytes_per_launch": bpl, "launches_per_step": synth.TINYLLAMA_LAYERS}
 
     result = {
         "metric": METRIC,
@@ -657,6 +663,9 @@ def main():
                         "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                         "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": measured_traffic("gemv_q4k"),
                         "avg_launch_us": round(q4_us, 3), "bytes_per_launch": q4_bpl},
+        "decode_q6k_down": {"kernel": "Q6_K x Q8_K decode GEMV with fused Q8_K quant (gemv_q6_stream_kernel), "
+                                      "the 22 down launches of a step at each M", "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                            **q6},
     }
     if not args.quick:
         rot = 1 << 30
