@@ -21,6 +21,7 @@ Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--quick] [--no-cpu]
        python bench.py --profile {gemv-q4k,gemv-q4k-m4,gemm,gemm-512,gemm-128,gemm-128-split,repack-q4k,repack-q6k,a8-4096,a8-512,copy}
            (workload only, for rocprofv3 counter runs)
        python bench.py --vs-hipblaslt   (W8A8 GEMM against torch._int_mm over 155 prefill shapes, one JSON line each)
+       python bench.py --gemv-shapes    (single decode GEMV launches per shape and row count, one JSON line each)
 """
 from __future__ import annotations
 
@@ -53,6 +54,9 @@ def parse():
                     help="run one workload eagerly a few times and exit (for rocprofv3 --pmc passes)")
     ap.add_argument("--vs-hipblaslt", action="store_true",
                     help="time the W8A8 GEMM against torch._int_mm over a grid of prefill shapes and exit")
+    ap.add_argument("--gemv-shapes", action="store_true",
+                    help="time single decode GEMV launches per projection shape and row count, one JSON line each, "
+                         "and exit")
     return ap.parse_args()
 
 
@@ -433,6 +437,36 @@ def vs_hipblaslt(torch, hip, synth) -> None:
         del ws
 
 
+def gemv_shapes(torch, hip, synth) -> None:
+    """One line per decode shape and row count: single fused launches (Q8_K
+    quantisation in-kernel) of the TinyLlama projections and the Llama-3-8B
+    FFN, replayed in a graph on weight copies rotating through >= 1 GiB."""
+    shapes = [("o", 4, 2048, [2048]), ("qkv", 4, 2048, [2048, 256, 256]), ("gate+up", 4, 2048, [5632, 5632]),
+              ("down", 6, 5632, [2048]), ("llama3_8b gate+up", 4, 4096, [14336, 14336]),
+              ("llama3_8b down", 6, 14336, [4096])]
+    for name, kind, k, ns in shapes:
+        per = sum(n * (k // synth.QK) * hip.BLOCK_BYTES[kind] for n in ns)
+        copies = max(2, (1 << 30) // per + 1)
+        base = [[torch.from_numpy(synth.kquant(kind, n, k, index=500 + c * 8 + i)).to("cuda")
+                 for i, n in enumerate(ns)] for c in range(min(copies, 4))]
+        sets = [base[c] if c < len(base) else [t.clone() for t in base[c % len(base)]] for c in range(copies)]
+        for m in ((1, 2, 4, 8) if name.startswith("llama3_8b") else (1, 4, 8)):
+            x = torch.from_numpy(synth.activations(m, k, index=900 + m)).to("cuda")
+            outs = [torch.empty((m, n), device="cuda") for n in ns]
+
+            def run():
+                for ws in sets:
+                    hip.gemv_q_f32(kind, ws, k, ns, x, outs=outs)
+
+            ms, _ = time_graph(torch, run, max(1, 100 // copies), 2)
+            us = ms * 1e3 / copies
+            byts = per + m * k * 4 + m * sum(ns) * 4
+            print(json.dumps({"shape": name, "kind": kind, "m": m, "k": k, "n": ns, "us": round(us, 3),
+                              "gb_s": round(byts / us / 1e3, 1), "weight_mb": round(per / 1e6, 2)}), flush=True)
+        del sets, base
+        torch.cuda.empty_cache()
+
+
 def profile_workload(torch, hip, synth, which: str) -> None:
     """Run one workload eagerly (3 times) for rocprofv3 counter passes."""
     if which in ("gemv-q4k", "gemv-q4k-m4"):
@@ -599,6 +633,9 @@ def main():
         return
     if args.vs_hipblaslt:
         vs_hipblaslt(torch, hip, synth)
+        return
+    if args.gemv_shapes:
+        gemv_shapes(torch, hip, synth)
         return
 
     ds = DecodeSet(torch, hip, synth, synth.TINYLLAMA_LAYERS)
