@@ -122,3 +122,31 @@ def test_split_graph_replays_match_eager():
         # eager work between replays
         hip.gemm_w8a8(d[0][:64], d[1][:64], d[2], d[3])
         torch.cuda.synchronize()
+
+
+def test_split_extreme_magnitudes_at_the_largest_exact_k():
+    """|C| = 127^2 * K at K = 133120, the largest K whose int32 sums are exact
+    (127 * 127 * 133120 = 2,147,092,480 < 2^31): the split partials and their sum
+    stay exact, on the routed split and on 16 splits."""
+    m, n, k = 64, 256, 133120
+    nbytes, splits = hip.gemm_workspace(m, n, k)
+    assert splits > 1
+    a8 = torch.full((m, k), -127, dtype=torch.int8, device=DEV)
+    w8 = torch.full((n, k), 127, dtype=torch.int8, device=DEV)
+    w8[1::2] = -127
+    ones_m = torch.ones(m, device=DEV)
+    ones_n = torch.ones(n, device=DEV)
+    exp = np.where(np.arange(n) % 2 == 0, -127 * 127 * k, 127 * 127 * k).astype(np.int32)
+    exp = np.broadcast_to(exp, (m, n))
+    c = torch.empty((m, n), dtype=torch.int32, device=DEV)
+    out = hip.gemm_w8a8(a8, ones_m, w8, ones_n, out_i32=c, workspace=torch.zeros(nbytes, dtype=torch.uint8, device=DEV))
+    torch.cuda.synchronize()
+    assert np.array_equal(c.cpu().numpy(), exp)
+    assert np.array_equal(_bits(out.cpu().numpy()), _bits(orc.rescale(exp, np.ones(m, np.float32), np.ones(n, np.float32))))
+    t = (m // 64) * (n // 32)
+    work = torch.zeros(16384 + t * 16 * 64 * 32 * 4, dtype=torch.uint8, device=DEV)
+    c.fill_(0)
+    hip.gemm_w8a8_tile(64, 32, 4, 16, a8, ones_m, w8, ones_n, out_i32=c, workspace=work)
+    torch.cuda.synchronize()
+    assert np.array_equal(c.cpu().numpy(), exp)
+    assert not work[:16384].any().item()
