@@ -78,3 +78,40 @@ def test_fused_gemv_random_shape(kind, ns, k, m):
             _, _, mag = orc.gemv_block_sums(kind, w, k, n, q8[mi])
             err = np.abs(got[mi].astype(np.float64) - ref[mi])
             assert np.all(err <= 1e-5 * mag), f"member n={n} row {mi}: max err/mag {np.max(err / mag)}"
+
+
+def _capi_cases(count=24, seed=99):
+    g = np.random.default_rng(seed)
+    out = []
+    for i in range(count):
+        kind = int(g.choice([4, 5, 6]))
+        m = int(g.choice([1, int(g.integers(2, 17)), int(g.integers(17, 300))]))
+        if kind == 5 and m == 1:
+            m = 2  # the reference rejects Q5_K at one row
+        k = 256 * int(g.integers(1, 25))
+        # the grouped entry takes Q4_K and Q6_K only, as the reference's (lib.rs:2573-2577)
+        ns = tuple(int(g.integers(1, 2500)) for _ in range(1 if kind == 5 else int(g.integers(1, 4))))
+        out.append((kind, m, k, ns))
+    return out
+
+
+@pytest.mark.parametrize("kind,m,k,ns", _capi_cases())
+def test_capi_random_shape_bit_exact(kind, m, k, ns):
+    """The reference C ABI on host buffers (rocknpu_matmul_q{4,5,6}_k_f32_f32 for one
+    projection, rocknpu_matmul_q_concat_f32_f32_mtile for several sharing the
+    activations): the W8A8 route, bit for bit against the oracle."""
+    from rocknpu_amd.capi import STATUS_OK, Context
+
+    print(f"random capi kind={kind} m={m} k={k} ns={ns}", flush=True)
+    ws = [synth.kquant(kind, n, k, index=9500 + i * 13 + n) for i, n in enumerate(ns)]
+    a = synth.activations(m, k, index=9600 + m + k)
+    with Context() as ctx:
+        if len(ns) == 1:
+            out = np.empty((m, ns[0]), np.float32)
+            assert ctx.matmul_q(kind, ws[0], a, out, k, ns[0]) == STATUS_OK
+            outs = [out]
+        else:
+            outs = [np.empty((m, n), np.float32) for n in ns]
+            assert ctx.matmul_q_concat(ws, [kind] * len(ns), list(ns), a, outs, k) == STATUS_OK
+        for w, n, o in zip(ws, ns, outs):
+            assert np.array_equal(_bits(o), _bits(orc.matmul_q_w8a8(kind, w, a, n, threads=8))), f"member n={n}"
