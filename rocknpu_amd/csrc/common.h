@@ -143,6 +143,45 @@ __device__ __forceinline__ void quant_sym_rcp(const float (&v)[N], float s, floa
     }
 }
 
+// quant_sym_rcp with the int8 results packed four to a word (value 4 i + b in
+// byte b of word i), for callers whose scale s is a normal float (`fast`).
+// Then |v| <= 127 s gives |r| <= 127 (1 + 3 * 2^-24) < 127.5 for
+// r = f32(v * inv), and u = f32(r + 1.5 * 2^23) is rint(r) (ties to even)
+// offset into the low mantissa bits, two's complement, so u's low byte is the
+// int8 value; u - 1.5 * 2^23 and r - rint(r) are exact. The same rule as
+// quant_sym_rcp picks the lane's fallback to quant_sym: the largest
+// |r - rint(r)| over its values reaching 0.5 - 2^-15, or !fast.
+template <int N>
+__device__ __forceinline__ void quant_sym_rcp_packed(const float (&v)[N], float s, float inv, bool fast,
+                                                     uint32_t (&w)[N / 4]) {
+    constexpr float kRound = 12582912.0f;
+    uint32_t u[N];
+    float err = 0.0f;
+#pragma unroll
+    for (int i = 0; i < N; ++i) {
+        const float r = v[i] * inv;
+        const float ur = r + kRound;
+        u[i] = __float_as_uint(ur);
+        err = fmaxf(err, fabsf(r - (ur - kRound)));
+    }
+#pragma unroll
+    for (int i = 0; i < N / 4; ++i) {
+        const uint32_t lo = __builtin_amdgcn_perm(u[4 * i + 1], u[4 * i], 0x0C0C0400u);
+        const uint32_t hi = __builtin_amdgcn_perm(u[4 * i + 3], u[4 * i + 2], 0x0C0C0400u);
+        w[i] = __builtin_amdgcn_perm(hi, lo, 0x05040100u);
+    }
+    // a wave-uniform branch (a lane's fallback costs the wave the same either
+    // way): the compiler then keeps the divisions out of the common path
+    if (__builtin_expect(__any(!(fast && err < 0.5f - 0x1p-15f)), 0)) {
+#pragma unroll
+        for (int i = 0; i < N / 4; ++i) {
+            w[i] = 0;
+#pragma unroll
+            for (int b = 0; b < 4; ++b) w[i] |= static_cast<uint32_t>(quant_sym(v[4 * i + b], s) & 0xFF) << (8 * b);
+        }
+    }
+}
+
 // Max over the wave of non-negative floats (their bit patterns order as the
 // values): DPP steps across lane bits 0-3 (0 is the identity of an unsigned
 // max, so each move folds into v_max_u32_dpp), then the four 16-lane rows by

@@ -21,6 +21,8 @@
 // the product is within 2^-15 of a rounding boundary (quant_sym_rcp).
 #include "common.h"
 
+#include <algorithm>
+
 namespace rk {
 namespace {
 
@@ -137,35 +139,19 @@ __device__ __forceinline__ void decode_unit(const uint8_t* blk, int v, const flo
     }
 }
 
+// Store unit v's 32 int8 values, packed four to a word in decode_unit's
+// order (w[i] holds vals[4 i .. 4 i + 3]), at their row positions.
 template <int KIND>
-__device__ __forceinline__ void store_unit(int8_t* out_blk, int v, const int (&q)[32]) {
+__device__ __forceinline__ void store_unit(int8_t* out_blk, int v, const uint32_t (&w)[8]) {
     if constexpr (KIND == 4 || KIND == 5) {
         const int j = v >> 1, h = v & 1;
-        uint32_t lo[4], hi[4];
-#pragma unroll
-        for (int w = 0; w < 4; ++w) {
-            lo[w] = (q[4 * w] & 0xFF) | (q[4 * w + 1] & 0xFF) << 8 | (q[4 * w + 2] & 0xFF) << 16 |
-                    static_cast<uint32_t>(q[4 * w + 3] & 0xFF) << 24;
-            hi[w] = (q[16 + 4 * w] & 0xFF) | (q[16 + 4 * w + 1] & 0xFF) << 8 |
-                    (q[16 + 4 * w + 2] & 0xFF) << 16 |
-                    static_cast<uint32_t>(q[16 + 4 * w + 3] & 0xFF) << 24;
-        }
-        *reinterpret_cast<uint4*>(out_blk + 64 * j + 16 * h) = make_uint4(lo[0], lo[1], lo[2], lo[3]);
-        *reinterpret_cast<uint4*>(out_blk + 64 * j + 32 + 16 * h) =
-            make_uint4(hi[0], hi[1], hi[2], hi[3]);
+        *reinterpret_cast<uint4*>(out_blk + 64 * j + 16 * h) = make_uint4(w[0], w[1], w[2], w[3]);
+        *reinterpret_cast<uint4*>(out_blk + 64 * j + 32 + 16 * h) = make_uint4(w[4], w[5], w[6], w[7]);
     } else {
         const int half = v >> 2, g = v & 3;
 #pragma unroll
-        for (int qd = 0; qd < 4; ++qd) {
-            uint32_t w[2];
-#pragma unroll
-            for (int t = 0; t < 2; ++t) {
-                const int* s = &q[8 * qd + 4 * t];
-                w[t] = (s[0] & 0xFF) | (s[1] & 0xFF) << 8 | (s[2] & 0xFF) << 16 |
-                       static_cast<uint32_t>(s[3] & 0xFF) << 24;
-            }
-            *reinterpret_cast<uint2*>(out_blk + 128 * half + 32 * qd + 8 * g) = make_uint2(w[0], w[1]);
-        }
+        for (int qd = 0; qd < 4; ++qd)
+            *reinterpret_cast<uint2*>(out_blk + 128 * half + 32 * qd + 8 * g) = make_uint2(w[2 * qd], w[2 * qd + 1]);
     }
 }
 
@@ -228,20 +214,22 @@ __global__ __launch_bounds__(kWaves * 64) void repack_w8_kernel(const uint8_t* _
         for (int i = 0; i < 32; i += 2) vmax = fmaxf(vmax, fmaxf(fabsf(vals[i]), fabsf(vals[i + 1])));
     };
     float scale = 1.0f, inv = 1.0f;
+    bool fast = true;
     auto finish_max = [&]() {
         vmax = wave_max_nonneg(vmax);
         bad = __any(bad) ? 1 : 0;
         scale = vmax == 0.0f ? 1.0f : vmax / 127.0f;
         inv = 1.0f / scale;
+        fast = scale >= 1.175494351e-38f;  // a normal scale (not one of a subnormal max)
     };
     auto quantise_store = [&](int c, const float (&vals)[32]) {
-        int q[32];
-        quant_sym_rcp(vals, scale, inv, q);
+        uint32_t w[8];
+        quant_sym_rcp_packed(vals, scale, inv, fast, w);
         if (bad) {
 #pragma unroll
-            for (int i = 0; i < 32; ++i) q[i] = 0;
+            for (int i = 0; i < 8; ++i) w[i] = 0;
         }
-        store_unit<KIND>(outp + (c * kChunkBlocks + bi) * kQK, v, q);
+        store_unit<KIND>(outp + (c * kChunkBlocks + bi) * kQK, v, w);
     };
     if constexpr (HOLD > 0) {
         float vals[HOLD][32];
@@ -268,12 +256,83 @@ __global__ __launch_bounds__(kWaves * 64) void repack_w8_kernel(const uint8_t* _
     if (lane == 0) scales[row] = bad ? __builtin_nanf("") : scale;
 }
 
+// Rows of one chunk (nb <= 8) whose blocks start 16-byte aligned: each wave
+// walks rows r, r + (all waves), ... and holds the next row's blocks in
+// registers (at most 105 16-byte pieces, two per lane) while it repacks the
+// current one, so a row's loads are in flight during the previous row's
+// arithmetic instead of after it. The arithmetic per row is repack_w8_kernel's.
+template <int KIND>
+__global__ __launch_bounds__(kWaves * 64) void repack_w8_stream_kernel(const uint8_t* __restrict__ blocks,
+                                                                       int64_t n, int nb, int64_t k_pad,
+                                                                       int8_t* __restrict__ w8,
+                                                                       float* __restrict__ scales) {
+    constexpr int BB = block_bytes(KIND);
+    static_assert(kChunkBlocks * BB <= 128 * 16, "a row's pieces fit two per lane");
+    __shared__ float lds[kWaves][kChunkBlocks * 16];
+    __shared__ __align__(16) uint8_t raw[kWaves][kChunkBlocks * BB];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int64_t stride = static_cast<int64_t>(gridDim.x) * kWaves;
+    int64_t row = static_cast<int64_t>(blockIdx.x) * kWaves + wave;
+    const int pieces = nb * BB / 16;
+    const int64_t row_bytes = static_cast<int64_t>(nb) * BB;
+    float* st = lds[wave];
+    uint8_t* chunk = raw[wave];
+    const int bi = lane >> 3, v = lane & 7;
+    uint4 p0 = make_uint4(0, 0, 0, 0), p1 = make_uint4(0, 0, 0, 0);
+    auto fetch = [&](int64_t r) {
+        const uint4* src = reinterpret_cast<const uint4*>(blocks + r * row_bytes);
+        if (lane < pieces) p0 = src[lane];
+        if (lane + 64 < pieces) p1 = src[lane + 64];
+    };
+    if (row < n) fetch(row);
+    for (; row < n; row += stride) {
+        __builtin_amdgcn_wave_barrier();
+        if (lane < pieces) reinterpret_cast<uint4*>(chunk)[lane] = p0;
+        if (lane + 64 < pieces) reinterpret_cast<uint4*>(chunk)[lane + 64] = p1;
+        __builtin_amdgcn_wave_barrier();
+        if (row + stride < n) fetch(row + stride);
+        int bad = stage_factors<KIND>(chunk, nb, lane, st) ? 1 : 0;
+        __builtin_amdgcn_wave_barrier();
+        float vals[32];
+        float vmax = 0.0f;
+        const bool have = bi < nb;
+        if (have) {
+            decode_unit<KIND>(chunk + bi * BB, v, st + bi * 16, vals);
+#pragma unroll
+            for (int i = 0; i < 32; i += 2) vmax = fmaxf(vmax, fmaxf(fabsf(vals[i]), fabsf(vals[i + 1])));
+        }
+        vmax = wave_max_nonneg(vmax);
+        bad = __any(bad) ? 1 : 0;
+        const float scale = vmax == 0.0f ? 1.0f : vmax / 127.0f;
+        const float inv = 1.0f / scale;
+        int8_t* outp = w8 + row * k_pad;
+        if (have) {
+            uint32_t w[8];
+            quant_sym_rcp_packed(vals, scale, inv, scale >= 1.175494351e-38f, w);
+            if (bad) {
+#pragma unroll
+                for (int i = 0; i < 8; ++i) w[i] = 0;
+            }
+            store_unit<KIND>(outp + bi * kQK, v, w);
+        }
+        for (int64_t i = static_cast<int64_t>(nb) * kQK + 16 * lane; i < k_pad; i += 64 * 16)
+            *reinterpret_cast<uint4*>(outp + i) = make_uint4(0, 0, 0, 0);
+        if (lane == 0) scales[row] = bad ? __builtin_nanf("") : scale;
+    }
+}
+
 template <int KIND>
 void launch_kind(int64_t n, int nb, int64_t k_pad, const uint8_t* blocks, int8_t* w8, float* scales,
                  hipStream_t stream) {
     const dim3 grid(static_cast<unsigned>((n + kWaves - 1) / kWaves)), block(kWaves * 64);
     const int nchunks = (nb + kChunkBlocks - 1) / kChunkBlocks;
-    if (nchunks == 1) repack_w8_kernel<KIND, 1><<<grid, block, 0, stream>>>(blocks, n, nb, k_pad, w8, scales);
+    if (nchunks == 1 && (reinterpret_cast<uintptr_t>(blocks) & 15) == 0 &&
+        (static_cast<int64_t>(nb) * block_bytes(KIND)) % 16 == 0) {
+        // six workgroups per CU at most; each wave walks rows from there
+        const int64_t wgs = std::min<int64_t>((n + kWaves - 1) / kWaves, static_cast<int64_t>(device_cu_count()) * 6);
+        repack_w8_stream_kernel<KIND><<<dim3(static_cast<unsigned>(wgs)), block, 0, stream>>>(blocks, n, nb, k_pad,
+                                                                                            w8, scales);
+    } else if (nchunks == 1) repack_w8_kernel<KIND, 1><<<grid, block, 0, stream>>>(blocks, n, nb, k_pad, w8, scales);
     else if (nchunks == 2) repack_w8_kernel<KIND, 2><<<grid, block, 0, stream>>>(blocks, n, nb, k_pad, w8, scales);
     else repack_w8_kernel<KIND, 0><<<grid, block, 0, stream>>>(blocks, n, nb, k_pad, w8, scales);
 }

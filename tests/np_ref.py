@@ -174,3 +174,44 @@ def source_sample_fnv1a64(raw: bytes) -> int:
             h ^= v
             h = (h * 1099511628211) & mask
     return h
+
+
+def tie_rows(kind: int, n: int, k: int, seed: int) -> np.ndarray:
+    """K-quant rows whose symmetric scale is a power of two, so that many
+    v / scale land exactly on half-integers, where rounding half to even and
+    half away from zero differ on every other one.
+    Q4_K/Q5_K: d = 1/4, dmin = 127/64, sub-block 0 of each block has scale 1
+    and min 32 (values q/4 - 63.5, the row's largest magnitude 63.5 at q = 0,
+    placed in block 0), the other sub-blocks scales 1..16 (Q5_K 1..8) and min 0: scale
+    0.5, v / scale = sc * q / 2. Q6_K: d = 1, sub-block 0 has scale 127 and a
+    quant of -32 at value 0 (magnitude 4064), the others odd scales 1..61:
+    scale 32, v / scale = sc * q / 32, a tie wherever q = +-16."""
+    g = np.random.default_rng(seed)
+    nbt = n * (k // QK)
+    bb = {4: 144, 5: 176, 6: 210}[kind]
+    blk = np.empty((nbt, bb), np.uint8)
+    if kind in (4, 5):
+        from rocknpu_amd import synth
+        blk[:, 0:2] = np.frombuffer(np.float16(0.25).tobytes(), np.uint8)
+        blk[:, 2:4] = np.frombuffer(np.float16(127 / 64).tobytes(), np.uint8)
+        sc = g.integers(1, 17 if kind == 4 else 9, (nbt, 8))  # |d sc q| <= 60 / 62 < 63.5
+        mn = np.zeros((nbt, 8), np.int64)
+        sc[:, 0] = 1
+        mn[:, 0] = 32
+        blk[:, 4:16] = synth.pack_scales_k4(sc, mn)
+        blk[:, 16:] = g.integers(0, 256, (nbt, bb - 16), dtype=np.uint8)
+        blk = blk.reshape(n, -1, bb)
+        # value 0 of block 0: low nibble of the first quant byte (and its Q5_K high bit) zero
+        blk[:, 0, 16 if kind == 4 else 48] &= 0xF0
+        if kind == 5:
+            blk[:, 0, 16] &= 0xFE
+    else:
+        blk[:, 0:192] = g.integers(0, 256, (nbt, 192), dtype=np.uint8)
+        sc = (2 * g.integers(0, 31, (nbt, 16)) + 1).astype(np.int8)
+        sc[:, 0] = 127
+        blk[:, 192:208] = sc.view(np.uint8)
+        blk[:, 208:210] = np.frombuffer(np.float16(1.0).tobytes(), np.uint8)
+        blk = blk.reshape(n, -1, bb)
+        blk[:, 0, 0] &= 0xF0    # value 0: low nibble 0
+        blk[:, 0, 128] &= 0xFC  # and high bits 0, so q = -32
+    return np.ascontiguousarray(blk.reshape(-1))

@@ -26,6 +26,8 @@ def _bits(x: np.ndarray) -> np.ndarray:
     (4, 1, 256), (4, 67, 2048), (4, 130, 5632), (4, 5632, 2048),
     (5, 48, 2048), (5, 9, 768),
     (6, 1, 256), (6, 33, 2048), (6, 70, 5632), (6, 2048, 5632),
+    # one-chunk rows streamed by waves that walk several rows each (more rows than waves)
+    (6, 7001, 2048), (4, 13003, 1024), (5, 6500, 512),
 ])
 def test_repack_w8_bit_exact(kind, n, k):
     print(f"repack kind={kind} n={n} k={k}", flush=True)
@@ -52,6 +54,22 @@ def test_repack_zero_and_nonfinite_rows():
     assert np.isnan(sc[2])
     w8_ref, sc_ref = orc.repack_w8(4, np.ascontiguousarray(blocks[:2].reshape(-1)), k, 2)
     assert np.array_equal(w8[:2, :k], w8_ref) and np.array_equal(_bits(sc[:2]), _bits(sc_ref))
+
+
+@pytest.mark.parametrize("kind,n,k", [(4, 96, 2048), (4, 40, 4096), (5, 33, 2048), (6, 96, 2048), (6, 20, 5632)])
+def test_repack_exact_ties(kind, n, k):
+    """Rows whose scale is a power of two, so that many values sit exactly on
+    half-integers after scaling: every lane holding one takes the exact
+    division and rounds half away from zero, bit for bit with the oracle."""
+    print(f"repack ties kind={kind} n={n} k={k}", flush=True)
+    from . import np_ref
+
+    blocks = np_ref.tie_rows(kind, n, k, seed=300 + kind + n)
+    w8_ref, sc_ref = orc.repack_w8(kind, blocks, k, n)
+    w8, sc = hip.repack_w8(kind, _dev(blocks), k, n)
+    torch.cuda.synchronize()
+    assert np.array_equal(w8.cpu().numpy()[:, :k], w8_ref)
+    assert np.array_equal(_bits(sc.cpu().numpy()), _bits(sc_ref))
 
 
 # ---------------------------------------------------------------- kernel (b)

@@ -165,6 +165,25 @@ def test_repack_matches_numpy(kind):
     assert np.array_equal(w8, qn) and np.array_equal(_bits(sc), _bits(sn))
 
 
+@pytest.mark.parametrize("kind", [4, 5, 6])
+def test_repack_exact_ties_round_half_away(kind):
+    """Rows whose scale is a power of two put many v / scale exactly on
+    half-integers; the oracle rounds them half away from zero as numpy's
+    floor-based restatement does, and a planted half-to-even rounding fails."""
+    n, k = 6, 512
+    blocks = np_ref.tie_rows(kind, n, k, seed=kind)
+    vals = np_ref.dequant(kind, blocks, n, k)
+    w8, sc = orc.repack_w8(kind, blocks, k, n)
+    assert np.all(sc == np.float32(0.5 if kind != 6 else 32.0))
+    r = vals / sc[:, None]
+    ties = (r - np.floor(r)) == 0.5
+    even_differs = ties & (np.rint(r) != np_ref.round_half_away(r))
+    assert even_differs.sum() > 20, "the rows must hold ties where the two roundings differ"
+    qn, sn = np_ref.quantize_symmetric(vals)
+    assert np.array_equal(w8, qn) and np.array_equal(_bits(sc), _bits(sn))
+    assert not np.array_equal(w8, np.clip(np.rint(r), -127, 127).astype(np.int8))
+
+
 def test_repack_rejects_bad_sizes():
     blocks = synth.q4_k(2, 512, index=1)
     with pytest.raises(orc.OracleError):
