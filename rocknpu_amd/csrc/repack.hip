@@ -328,8 +328,8 @@ void launch_kind(int64_t n, int nb, int64_t k_pad, const uint8_t* blocks, int8_t
     const int nchunks = (nb + kChunkBlocks - 1) / kChunkBlocks;
     if (nchunks == 1 && (reinterpret_cast<uintptr_t>(blocks) & 15) == 0 &&
         (static_cast<int64_t>(nb) * block_bytes(KIND)) % 16 == 0) {
-        // six workgroups per CU at most; each wave walks rows from there
-        const int64_t wgs = std::min<int64_t>((n + kWaves - 1) / kWaves, static_cast<int64_t>(device_cu_count()) * 6);
+        // twelve workgroups per CU at most; each wave walks rows from there
+        const int64_t wgs = std::min<int64_t>((n + kWaves - 1) / kWaves, static_cast<int64_t>(device_cu_count()) * 12);
         repack_w8_stream_kernel<KIND><<<dim3(static_cast<unsigned>(wgs)), block, 0, stream>>>(blocks, n, nb, k_pad,
                                                                                             w8, scales);
     } else if (nchunks == 1) repack_w8_kernel<KIND, 1><<<grid, block, 0, stream>>>(blocks, n, nb, k_pad, w8, scales);
