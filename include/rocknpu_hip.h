@@ -56,12 +56,18 @@ int rocknpu_hip_gemm_w8a8(const int8_t * a8, const float * a_scales, const int8_
  * most half the GPU (rocknpu_hip_gemm_workspace says when, and how many bytes).
  * The split workgroups add their int32 partial tiles (exact, so the results
  * are bit-identical to the unsplit call's). The workspace is device memory,
- * 256-byte aligned, whose first 16 KiB hold the tile counters: they must be
- * zero when the call starts, and every call that completes leaves them zero
- * (whatever shapes share the workspace), so zero a workspace once after
- * allocating it. A workspace smaller than the
- * route asks for (or NULL with 0 bytes) runs the GEMM unsplit. Calls that
- * overlap (other streams) need workspaces of their own. No counterpart in the
+ * 256-byte aligned, whose first 16 KiB hold the tile counters and an error
+ * word, followed by the partial tiles and per-split arrival stamps: zero a
+ * workspace once after allocating it, and every call that completes leaves it
+ * zeroed (whatever shapes share it). A call that finds its counters not zero
+ * (a workspace never zeroed, a call that did not complete, calls overlapping
+ * on one workspace) writes NaN for the f32 results of the tiles concerned and
+ * sets the error word, which rocknpu_hip_gemm_workspace_check reports; such a
+ * workspace stays flagged until it is zeroed again. A workspace smaller than
+ * the route asks for (or NULL with 0 bytes) runs the GEMM unsplit, and so does
+ * a device other than gfx950 (the exchange between the split workgroups is
+ * checked there only). Calls that overlap (other streams) need workspaces of
+ * their own. No counterpart in the
  * reference (its NPU K-split, crates/rocknpu-capi/src/lib.rs:1885-1926, adds
  * int32 partials on the host); the product is that of rocknpu_hip_gemm_w8a8. */
 int rocknpu_hip_gemm_w8a8_ws(const int8_t * a8, const float * a_scales, const int8_t * w8,
@@ -75,11 +81,20 @@ int rocknpu_hip_gemm_w8a8_ws(const int8_t * a8, const float * a_scales, const in
  * no GPU is needed when cus > 0. No counterpart in the reference. */
 int rocknpu_hip_gemm_workspace(size_t m, size_t n, size_t k_pad, int cus, size_t * bytes, int * splits);
 
+/* Waits for `stream`, then reads and clears the error word of a K-split
+ * workspace: 0 when no call on it since the last check found dirty counters,
+ * -3 (ROCKNPU_STATUS_EXECUTION_ERROR) when one did (the f32 results of its
+ * affected tiles are NaN; zero the workspace before using it again), -1 for a
+ * NULL workspace. No counterpart in the reference. */
+int rocknpu_hip_gemm_workspace_check(void * workspace, void * stream);
+
 /* The W8A8 GEMM on a given tile (bm x bn: 64x32 and 64x64 with 2 or 4 stages,
  * 128x64 with 2 or 4, 128x128 with 2 or 3, 256x128 with 3, 256x256 with 2;
  * bm = 0: the weight-streaming kernel, m <= 16) and K split (1 to 16; above 1
- * the workspace must hold 16 KiB of zero counters, one per tile and at most
- * 4096 tiles, then splits x bm x bn int32 per tile). For tests and tuning:
+ * the workspace must be a zeroed one of rocknpu_hip_gemm_w8a8_ws's layout: the
+ * 16 KiB counter block, one counter per tile and at most 4095 tiles, then
+ * splits x bm x bn int32 per tile, then splits x tiles stamps rounded up to
+ * 256 bytes). For tests and tuning:
  * every choice gives the same bits. No
  * counterpart in the reference. */
 int rocknpu_hip_gemm_w8a8_tile(int bm, int bn, int stages, int splits, const int8_t * a8,
@@ -106,7 +121,7 @@ int rocknpu_hip_matmul_w8a8_f32(const float * a, size_t m, size_t k, size_t lda,
  * graph capture, tight serving loops, harnesses that forbid hipMalloc). The
  * workspace is a fixed array in the library's device memory, one copy per GPU
  * the library runs on, held until the process ends (64 KiB of scales, 32 MiB
- * of A8 and 4 MiB + 16 KiB for the GEMM's K split): at most 16384 rows and
+ * of A8 and 4 MiB + 17 KiB for the GEMM's K split): at most 16384 rows and
  * m * k_pad <= 32 MiB; beyond that the call returns
  * ROCKNPU_STATUS_INVALID_ARGUMENT and prints the limit on stderr. Every call on
  * one GPU uses that GPU's copy, so calls that overlap on one GPU (other

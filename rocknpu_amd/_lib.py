@@ -66,6 +66,7 @@ SIGNATURES = {
     "rocknpu_hip_gemm_route": (_i, [_sz, _sz, _sz, _i, _vp, _vp, _vp]),
     "rocknpu_hip_gemm_w8a8_ws": (_i, [_vp, _vp, _vp, _vp, _sz, _sz, _sz, _vp, _sz, _vp, _vp, _sz, _vp]),
     "rocknpu_hip_gemm_workspace": (_i, [_sz, _sz, _sz, _i, _vp, _vp]),
+    "rocknpu_hip_gemm_workspace_check": (_i, [_vp, _vp]),
     "rocknpu_hip_gemm_w8a8_tile": (_i, [_i, _i, _i, _i, _vp, _vp, _vp, _vp, _sz, _sz, _sz, _vp, _sz, _vp, _vp, _sz,
                                         _vp]),
     "rocknpu_hip_gemv_shape": (_i, [ctypes.c_uint32, _sz, _sz, _vp, _sz, _i, _i, _vp, _vp, _vp]),

@@ -227,20 +227,18 @@ int run_w8a8(RockNpuContext* ctx, const DeviceW8& w, const float* act, size_t m,
         !ctx->d_as.ensure(rows * sizeof(float)) || !ctx->d_out.ensure(o_rows * sizeof(float)) ||
         !ctx->h_out.ensure(o_elems * sizeof(float)) || !ctx->h_as.ensure(rows * sizeof(float)))
         return kExec;
-    // the GEMM's K-split workspace; the (first) quantisation clears its counters
+    // the GEMM's K-split workspace; the (first) quantisation clears its
+    // counters and error word
     const rk::GemmTile route = rk::gemm_route(static_cast<int>(rows), static_cast<int>(w.n),
                                               static_cast<int>(w.k_pad), rk::device_cu_count());
     const size_t split = rk::gemm_workspace_bytes(route, static_cast<int>(rows), static_cast<int>(w.n));
-    if (split > 0 && !ctx->d_split.ensure(split)) return kExec;
+    if (split > 0 && (!ctx->d_split.ensure(split) || !ctx->h_err.ensure(sizeof(uint32_t)))) return kExec;
     if (!hip_ok(hipMemcpyAsync(ctx->d_act.p, act, a_bytes, hipMemcpyHostToDevice, ctx->stream), ctx, "act"))
         return kExec;
     int st = rk::launch_quantize_a8(ctx->d_act.as<float>(), static_cast<int64_t>(m), static_cast<int64_t>(k),
                                     static_cast<int64_t>(k), static_cast<int64_t>(w.k_pad), ctx->d_a8.as<int8_t>(),
                                     ctx->d_as.as<float>(), split > 0 ? ctx->d_split.as<uint32_t>() : nullptr,
-                                    split > 0 ? rk::gemm_workspace_counters(route, static_cast<int>(rows),
-                                                                            static_cast<int>(w.n))
-                                              : 0,
-                                    ctx->stream);
+                                    split > 0 ? rk::kSplitCounterWords : 0, ctx->stream);
     if (st != kOk) return st;
     if (hilo) {
         const int64_t total = static_cast<int64_t>(m * k);
@@ -256,6 +254,11 @@ int run_w8a8(RockNpuContext* ctx, const DeviceW8& w, const float* act, size_t m,
                                   ctx->d_out.as<float>(), w.n, nullptr, split > 0 ? ctx->d_split.p : nullptr, split,
                                   ctx->stream);
     if (st != kOk) return st;
+    // a split GEMM that found dirty counters set the workspace's error word
+    if (split > 0 && !hip_ok(hipMemcpyAsync(ctx->h_err.p, ctx->d_split.as<uint32_t>() + rk::kSplitErrorWord,
+                                            sizeof(uint32_t), hipMemcpyDeviceToHost, ctx->stream),
+                             ctx, "download"))
+        return kExec;
     if (hilo) {
         const int64_t total = static_cast<int64_t>(o_elems);
         hilo_sum_kernel<<<static_cast<unsigned>((total + 255) / 256), 256, 0, ctx->stream>>>(
@@ -270,6 +273,10 @@ int run_w8a8(RockNpuContext* ctx, const DeviceW8& w, const float* act, size_t m,
         return kExec;
     if (decode) run_overlap(ctx);
     if (!hip_ok(hipStreamSynchronize(ctx->stream), ctx, "execute")) return kExec;
+    if (split > 0 && *ctx->h_err.as<uint32_t>() != 0) {
+        if (ctx->trace) std::fprintf(stderr, "rocknpu: K-split workspace counters were not zero\n");
+        return kExec;
+    }
     const float* as = ctx->h_as.as<float>();
     for (size_t r = 0; r < rows; ++r)
         if (!std::isfinite(as[r])) return kInvalid;  // non-finite activation row

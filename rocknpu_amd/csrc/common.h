@@ -42,13 +42,21 @@ struct GemmTile {
     int splits = 1;
 };
 GemmTile gemm_route(int m, int n, int k, int cus);  // gemm.hip
-// A K-split workspace starts with a fixed block of kSplitCounters tile
+// A K-split workspace starts with a fixed 16 KiB block: kSplitCounters tile
 // counters (whatever the shape, so a workspace reused for other shapes never
-// finds another shape's partials in its counters), then the i32 partial tiles.
-constexpr int kSplitCounters = 4096;
-constexpr size_t kSplitCounterBytes = kSplitCounters * 4;
+// finds another shape's partials in its counters) and, in its last word, a
+// sticky error flag that a launch sets when it finds its counters dirty. Then
+// the i32 partial tiles, then one arrival stamp per (tile, split).
+constexpr int kSplitCounterWords = 4096;
+constexpr int kSplitCounters = kSplitCounterWords - 1;
+constexpr int kSplitErrorWord = kSplitCounters;
+constexpr size_t kSplitCounterBytes = kSplitCounterWords * 4;
 // Workspace bytes a split-K launch of `tile` needs for an m x n product.
 size_t gemm_workspace_bytes(const GemmTile& tile, int m, int n);  // gemm.hip
+// Whether the K split's exchange (relaxed agent-scope atomics, see gemm.hip)
+// has been checked on the current device's architecture: gfx950 only. Other
+// devices run every GEMM unsplit. gemm.hip.
+bool gemm_split_supported();
 // Counter words at the start of that workspace (what must be zero at entry).
 int gemm_workspace_counters(const GemmTile& tile, int m, int n);  // gemm.hip
 // Per-token A8 quantisation; workgroup 0 also clears `nzero` words at

@@ -15,6 +15,8 @@
 #include "common.h"
 
 #include <algorithm>
+#include <atomic>
+#include <cstring>
 #include <type_traits>
 #include <utility>
 
@@ -80,23 +82,42 @@ __device__ __forceinline__ void unroll_seq(F&& f, std::integer_sequence<int, I..
 // Split-K (SK): the grid holds `splits` workgroups per tile, workgroup s of a
 // tile taking K bytes [s * k_split, (s + 1) * k_split). Each writes its i32
 // partial tile to `partials` in the accumulator layout (lane-contiguous, so
-// every store is a full 256-byte row), then counts itself in at the tile's
-// counter; the last to arrive adds the other partials to its own (int32
-// addition: exact and order-free) and runs the epilogue, and resets the
-// counter to zero, so a workspace whose counters start at zero ends every
-// call with them at zero.
+// every store is a full 256-byte row) and its arrival stamp (the launch's
+// generation `gen`, never 0), then counts itself in at the tile's counter; the
+// last to arrive adds the other partials to its own (int32 addition: exact and
+// order-free), runs the epilogue, and resets the tile's stamps and counter to
+// zero, so a workspace that starts zeroed ends every call zeroed.
 //
-// The partials and counters are device-scope atomics (relaxed), which on a
-// gfx950 write through and read past the XCDs' separate L2s; each wave waits
-// for its partial stores to complete before the count. A device-scope fence
-// instead would write back and invalidate the whole L2 of the XCD, which cost
-// 50 us per launch at 352 workgroups.
+// A counter that was not zero at entry (a workspace never zeroed, a call that
+// did not complete, two calls overlapping on one workspace) is detected rather
+// than trusted: an arrival that finds the count at or above `splits`, or a
+// last arrival that finds another split's stamp different from `gen`, writes
+// NaN for the tile's f32 results and sets the workspace's sticky error word
+// (rocknpu_hip_gemm_workspace_check reads and clears it).
+//
+// Memory ordering. A tile's splits can run on different XCDs (at the edges of
+// an XCD's range of the bid mapping below), and each XCD has its own L2, so
+// the exchange must bypass those L2s. The partials, stamps and counters are
+// relaxed agent-scope atomics: gfx950 compiles these stores and loads with
+// the sc1 bit, which writes through to and reads from the device-coherent
+// level past the XCD's L2. Each wave then waits for its own stores to complete
+// (s_waitcnt vmcnt(0): on gfx9 stores count in vmcnt) before the workgroup
+// barrier and the relaxed fetch_add that counts it in. That ordering is a
+// property of how gfx950 lowers these operations, not of the HIP memory model
+// (which would need release/acquire); it is checked on gfx950 only, and
+// gemm_split_supported() keeps every other architecture unsplit. A
+// device-scope fence instead would write back and invalidate the whole L2 of
+// the XCD, which cost 50 us per launch at 352 workgroups.
+#if defined(__HIP_DEVICE_COMPILE__) && !defined(__gfx950__)
+#error "the K-split exchange of gemm_w8a8_dma_kernel is checked on gfx950 only"
+#endif
 template <int BM, int BN, int WM, int WN, int ST, int KB, bool SK>
 __global__ __launch_bounds__(WM* WN * 64) void gemm_w8a8_dma_kernel(
     const int8_t* __restrict__ a8, int64_t lda, const int8_t* __restrict__ w8, int64_t ldw,
     const float* __restrict__ a_scales, const float* __restrict__ w_scales, int m, int n, int k,
     float* __restrict__ out, int64_t ldo, int32_t* __restrict__ out_i32, int64_t ldo_i32, int splits,
-    int k_split, int32_t* __restrict__ partials, uint32_t* __restrict__ counters) {
+    int k_split, int32_t* __restrict__ partials, uint32_t* __restrict__ counters, uint32_t* __restrict__ stamps,
+    uint32_t gen) {
     using Cfg = DmaTile<BM, BN, WM, WN, KB>;
     constexpr int TM = BM / WM, TN = BN / WN;
     constexpr int FM = TM / 32, FN = TN / 32;  // 32x32 fragments
@@ -138,8 +159,10 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_w8a8_dma_kernel(
     // XCD-aware tile order: workgroup b runs on XCD b % 8, so each XCD takes a
     // contiguous range of tile indices, walked in groups of 4 tile rows; the
     // 32 tiles an XCD runs at once then share A rows and W rows in its L2.
-    // With split-K the (tile, split) pairs are ordered tile-major, so a tile's
-    // splits run on one XCD and exchange their partials through its L2.
+    // With split-K the (tile, split) pairs are ordered tile-major, so most of
+    // a tile's splits run on one XCD; a tile whose splits straddle the end of
+    // an XCD's range has them on two, which is why the exchange above goes
+    // past the L2s.
     const int tiles_m = (m + BM - 1) / BM, tiles_n = (n + BN - 1) / BN;
     const int tiles = tiles_m * tiles_n;
     const int total = SK ? tiles * splits : tiles;
@@ -309,9 +332,10 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_w8a8_dma_kernel(
     wait_lgkm0();
     __builtin_amdgcn_s_barrier();
 
+    bool poison = false;  // this tile's counters were dirty: its f32 results are NaN
     if constexpr (SK) {
         constexpr int PART = FM * FN * 16 * 64;  // ints of one wave's partial
-        __shared__ int last;
+        __shared__ int verdict;                  // 0: not last, 1: last, 2: dirty counters
         int32_t* mine = partials + (static_cast<int64_t>(t) * splits + split) * (WM * WN * PART) + wave * PART;
 #pragma unroll
         for (int i = 0; i < FM; ++i)
@@ -324,27 +348,45 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_w8a8_dma_kernel(
         // every wave's partial has reached the device-coherent level before the count
         wait_vm<0>();
         __syncthreads();
-        if (threadIdx.x == 0)
-            last = __hip_atomic_fetch_add(counters + t, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
-                   static_cast<uint32_t>(splits - 1);
-        __syncthreads();
-        if (!last) return;
-        // the other splits counted in after their partials completed; read them
-        // at device scope (past this XCD's L2)
-        for (int s2 = 0; s2 < splits; ++s2) {
-            if (s2 == split) continue;
-            int32_t* other =
-                partials + (static_cast<int64_t>(t) * splits + s2) * (WM * WN * PART) + wave * PART;
-#pragma unroll
-            for (int i = 0; i < FM; ++i)
-#pragma unroll
-                for (int j = 0; j < FN; ++j)
-#pragma unroll
-                    for (int e = 0; e < 16; ++e)
-                        acc[i][j][e] += __hip_atomic_load(other + ((i * FN + j) * 16 + e) * 64 + lane,
-                                                          __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        uint32_t* tile_stamps = stamps + static_cast<int64_t>(t) * splits;
+        if (threadIdx.x == 0) {
+            __hip_atomic_store(tile_stamps + split, gen, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            wait_vm<0>();  // the stamp, like the partials, lands before the count
+            const uint32_t old = __hip_atomic_fetch_add(counters + t, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            int v = old == static_cast<uint32_t>(splits - 1) ? 1 : old >= static_cast<uint32_t>(splits) ? 2 : 0;
+            if (v == 1)  // every split of this call has counted in, or the count started dirty
+                for (int s2 = 0; s2 < splits; ++s2)
+                    if (__hip_atomic_load(tile_stamps + s2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != gen) v = 2;
+            if (v == 2)
+                __hip_atomic_store(counters + kSplitErrorWord, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            verdict = v;
         }
-        if (threadIdx.x == 0) __hip_atomic_store(counters + t, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __syncthreads();
+        const int v = verdict;
+        if (v == 0) return;
+        poison = v == 2;
+        if (!poison) {
+            // the other splits counted in after their partials completed; read
+            // them at device scope (past this XCD's L2)
+            for (int s2 = 0; s2 < splits; ++s2) {
+                if (s2 == split) continue;
+                int32_t* other =
+                    partials + (static_cast<int64_t>(t) * splits + s2) * (WM * WN * PART) + wave * PART;
+#pragma unroll
+                for (int i = 0; i < FM; ++i)
+#pragma unroll
+                    for (int j = 0; j < FN; ++j)
+#pragma unroll
+                        for (int e = 0; e < 16; ++e)
+                            acc[i][j][e] += __hip_atomic_load(other + ((i * FN + j) * 16 + e) * 64 + lane,
+                                                              __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
+            // a dirty tile keeps its state, so every later call on the
+            // workspace reports it until the caller zeroes the workspace
+            if (threadIdx.x < splits)
+                __hip_atomic_store(tile_stamps + threadIdx.x, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            if (threadIdx.x == 0) __hip_atomic_store(counters + t, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
     }
 
     // Epilogue. lane l holds column l%32 of each 32x32 fragment, rows
@@ -384,6 +426,10 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_w8a8_dma_kernel(
                 for (int e = 0; e < 4; ++e) rs[4 * q + e] = r + e < m ? a_scales[r + e] : 0.0f;
             }
         }
+        if constexpr (SK)
+            if (poison)
+#pragma unroll
+                for (int e = 0; e < 16; ++e) rs[e] = __builtin_nanf("");
 #pragma unroll
         for (int j = 0; j < FN; ++j) {
             const int c0 = n0 + wn * TN + j * 32;
@@ -429,6 +475,16 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_w8a8_dma_kernel(
     }
 }
 
+// The generation a split launch stamps its arrivals with: distinct for every
+// launch of the process (until it wraps after 2^32 - 1 of them), never 0,
+// which is what a zeroed or reset stamp holds.
+uint32_t next_split_generation() {
+    static std::atomic<uint32_t> gen{0};
+    uint32_t g = gen.fetch_add(1, std::memory_order_relaxed) + 1;
+    while (g == 0) g = gen.fetch_add(1, std::memory_order_relaxed) + 1;
+    return g;
+}
+
 // Splits that get K stages when `splits` are asked for over `ks` stages, and
 // the stages of each (the last may have fewer).
 struct SplitK {
@@ -450,18 +506,20 @@ int launch_dma(const int8_t* a8, int64_t lda, const int8_t* w8, int64_t ldw, con
             return launch_dma<BM, BN, WM, WN, (ST < 4 ? 4 : ST), 64>(a8, lda, w8, ldw, as, ws, m, n, k, out, ldo, oi,
                                                                      ldoi, splits, workspace, stream);
     const int64_t tiles = static_cast<int64_t>((m + BM - 1) / BM) * ((n + BN - 1) / BN);
-    const SplitK sk = split_k(k / KB, workspace && tiles <= kSplitCounters ? splits : 1);
+    const SplitK sk =
+        split_k(k / KB, workspace && tiles <= kSplitCounters && gemm_split_supported() ? splits : 1);
     if (sk.splits > 1) {
         uint32_t* counters = reinterpret_cast<uint32_t*>(workspace);
         int32_t* partials = reinterpret_cast<int32_t*>(workspace + kSplitCounterBytes);
+        uint32_t* stamps = reinterpret_cast<uint32_t*>(partials + tiles * sk.splits * BM * BN);
         gemm_w8a8_dma_kernel<BM, BN, WM, WN, ST, KB, true>
             <<<dim3(static_cast<unsigned>(tiles * sk.splits)), dim3(WM * WN * 64), 0, stream>>>(
                 a8, lda, w8, ldw, as, ws, m, n, k, out, ldo, oi, ldoi, sk.splits, sk.stages_per * KB, partials,
-                counters);
+                counters, stamps, next_split_generation());
     } else {
         gemm_w8a8_dma_kernel<BM, BN, WM, WN, ST, KB, false><<<dim3(static_cast<unsigned>(tiles)), dim3(WM * WN * 64), 0,
                                                               stream>>>(a8, lda, w8, ldw, as, ws, m, n, k, out, ldo,
-                                                                        oi, ldoi, 1, k, nullptr, nullptr);
+                                                                        oi, ldoi, 1, k, nullptr, nullptr, nullptr, 0);
     }
     return hipGetLastError() == hipSuccess ? kStatusOk : kStatusExec;
 }
@@ -578,7 +636,23 @@ int gemm_workspace_counters(const GemmTile& tile, int m, int n) {
 size_t gemm_workspace_bytes(const GemmTile& tile, int m, int n) {
     const size_t tiles = static_cast<size_t>(gemm_workspace_counters(tile, m, n));
     if (tiles == 0) return 0;
-    return kSplitCounterBytes + tiles * tile.splits * tile.bm * tile.bn * 4;
+    const size_t units = tiles * tile.splits;
+    // counter block, i32 partial tiles, one stamp per unit (256-byte rounded)
+    return kSplitCounterBytes + units * tile.bm * tile.bn * 4 + (units * 4 + 255) / 256 * 256;
+}
+
+bool gemm_split_supported() {
+    static int cached[64] = {};  // 0 unknown, 1 yes, 2 no
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return false;
+    if (cached[dev] == 0) {
+        hipDeviceProp_t prop{};
+        const bool ok = hipGetDeviceProperties(&prop, dev) == hipSuccess &&
+                        std::strncmp(prop.gcnArchName, "gfx950", 6) == 0 &&
+                        (prop.gcnArchName[6] == '\0' || prop.gcnArchName[6] == ':');
+        cached[dev] = ok ? 1 : 2;
+    }
+    return cached[dev] == 1;
 }
 
 // The GEMM on a given tile, stage count and split (splits > 1 needs a

@@ -146,6 +146,22 @@ extern "C" int rocknpu_hip_gemm_workspace(size_t m, size_t n, size_t k_pad, int 
     return rk::kStatusOk;
 }
 
+extern "C" int rocknpu_hip_gemm_workspace_check(void* workspace, void* stream) {
+    if (!workspace) return rk::kStatusInvalid;
+    const hipStream_t s = static_cast<hipStream_t>(stream);
+    uint32_t* word = static_cast<uint32_t*>(workspace) + rk::kSplitErrorWord;
+    uint32_t flag = 0;
+    if (hipMemcpyAsync(&flag, word, sizeof flag, hipMemcpyDeviceToHost, s) != hipSuccess ||
+        hipStreamSynchronize(s) != hipSuccess)
+        return rk::kStatusExec;
+    if (flag == 0) return rk::kStatusOk;
+    static const uint32_t zero = 0;
+    if (hipMemcpyAsync(word, &zero, sizeof zero, hipMemcpyHostToDevice, s) != hipSuccess ||
+        hipStreamSynchronize(s) != hipSuccess)
+        return rk::kStatusExec;
+    return rk::kStatusExec;
+}
+
 extern "C" int rocknpu_hip_gemm_route(size_t m, size_t n, size_t k_pad, int cus, int* bm, int* bn, int* stages) {
     if (!bm || !bn || !stages || m == 0 || n == 0 || k_pad == 0 || k_pad % 64 != 0 || m > INT_MAX || n > INT_MAX ||
         k_pad > INT_MAX)

@@ -58,12 +58,12 @@ int run(const float* a, size_t m, size_t k, size_t lda, const int8_t* w8, const 
 // copy per GPU, held until the process ends. Scales of at most kNoAllocRows
 // rows, then A8 of at most kNoAllocA8Bytes (the layout above: A8 starts at
 // scales_bytes(m) <= kNoAllocRows * 4).
-// Then the GEMM's K-split workspace: 4 MiB + 16 KiB holds every split the
+// Then the GEMM's K-split workspace: 4 MiB + 17 KiB holds every split the
 // route takes on up to 256 CUs (the counter block, then at most 256 units of a
-// 64 x 64 i32 tile); a larger split runs unsplit instead.
+// 64 x 64 i32 tile and their 256 stamps); a larger split runs unsplit instead.
 constexpr size_t kNoAllocRows = 16384;
 constexpr size_t kNoAllocA8Bytes = size_t{32} << 20;
-constexpr size_t kNoAllocSplitBytes = (size_t{4} << 20) + rk::kSplitCounterBytes;
+constexpr size_t kNoAllocSplitBytes = (size_t{4} << 20) + rk::kSplitCounterBytes + 1024;
 constexpr size_t kScratchBytes = kNoAllocRows * sizeof(float) + kNoAllocA8Bytes + kNoAllocSplitBytes;
 static __device__ __align__(256) uint8_t scratch[kScratchBytes];
 

@@ -82,20 +82,45 @@ def gemm_workspace(m: int, n: int, k_pad: int, cus: int = 0) -> tuple[int, int]:
     return nb.value, sp.value
 
 
-# Zeroed K-split workspaces, one per device: the GEMM leaves their counters
-# at zero. Calls that use it must not overlap (one stream, or streams ordered
-# with each other); overlapping calls pass workspaces of their own.
-_workspaces: dict[int, torch.Tensor] = {}
+# Zeroed K-split workspaces, one per (device, stream): the GEMM leaves them
+# zeroed, so each is zeroed once, when it is made. Calls on one stream are
+# ordered with each other, so they can share its workspace; calls on other
+# streams get their own. Under HIP graph capture none is made or grown (the
+# zeroing would run only at replay, and eager calls would find the counters
+# dirty); a captured call runs unsplit unless the stream already has a large
+# enough workspace, which the graph then reuses on every replay.
+_workspaces: dict[tuple[int, int], torch.Tensor] = {}
 
 
-def workspace_for(device: torch.device, nbytes: int) -> torch.Tensor:
-    """This module's zeroed workspace of at least nbytes on `device`."""
-    key = torch.device(device).index or 0
+def workspace_for(device: torch.device, nbytes: int) -> torch.Tensor | None:
+    """This module's zeroed workspace of at least nbytes for the current
+    stream on `device`; None when one would have to be made or grown during
+    graph capture."""
+    dev = torch.device(device)
+    index = dev.index if dev.index is not None else torch.cuda.current_device()
+    stream = torch.cuda.current_stream(index)
+    key = (index, stream.cuda_stream)
     ws = _workspaces.get(key)
-    if ws is None or ws.numel() < nbytes:
-        ws = torch.zeros(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
-        _workspaces[key] = ws
-    return ws
+    if ws is not None and ws.numel() >= nbytes:
+        return ws
+    if torch.cuda.is_current_stream_capturing():
+        return None
+    new = torch.zeros(max(nbytes, 1 << 20), dtype=torch.uint8, device=torch.device("cuda", index))
+    if ws is not None:
+        # the old buffer may still be read by work queued on this stream
+        ws.record_stream(stream)
+    _workspaces[key] = new
+    return new
+
+
+def gemm_workspace_check(workspace: torch.Tensor) -> bool:
+    """Waits for the current stream and reads and clears the workspace's error
+    word: True when no split GEMM on it found dirty counters since the last
+    check. A False workspace must be zeroed before it is used again."""
+    st = _lib.load().rocknpu_hip_gemm_workspace_check(_ptr(workspace), _stream())
+    if st not in (0, -3):
+        raise LaunchError(f"gemm_workspace_check returned status {st}")
+    return st == 0
 
 
 def gemm_w8a8(a8: torch.Tensor, a_scales: torch.Tensor, w8: torch.Tensor, w_scales: torch.Tensor,
@@ -104,25 +129,27 @@ def gemm_w8a8(a8: torch.Tensor, a_scales: torch.Tensor, w8: torch.Tensor, w_scal
     """Kernel (c): out[m, n] = (f32(A8 W8^T) * a_scales) * w_scales.
 
     workspace: True (default) splits K where the route does, in this module's
-    zeroed workspace for the current stream; a uint8 device tensor supplies
-    one (zeroed once by the caller); None or False runs the call without one
-    (rocknpu_hip_gemm_w8a8, never split). The bits are the same either way."""
+    zeroed workspace for the current stream (none under graph capture unless
+    the stream already has one; the call then runs unsplit); a uint8 device
+    tensor supplies one (zeroed once by the caller, used by one stream at a
+    time); None or False runs the call without one (rocknpu_hip_gemm_w8a8,
+    never split). The bits are the same either way."""
     m, kp = a8.shape
     n = w8.shape[0]
     assert w8.shape[1] == kp and a8.is_contiguous() and w8.is_contiguous()
     if out is None:
         out = torch.empty((m, n), dtype=torch.float32, device=a8.device)
     lib = _lib.load()
+    if workspace is True:
+        nbytes, _ = gemm_workspace(m, n, kp)
+        workspace = workspace_for(a8.device, nbytes) if nbytes else None
     if workspace is None or workspace is False:
         _check(lib.rocknpu_hip_gemm_w8a8(_ptr(a8), _ptr(a_scales), _ptr(w8), _ptr(w_scales), m, n, kp,
                                          _ptr(out), _ld(out), _ptr(out_i32), _stream()), "gemm_w8a8")
         return out
-    if workspace is True:
-        nbytes, _ = gemm_workspace(m, n, kp)
-        workspace = workspace_for(a8.device, nbytes) if nbytes else None
     _check(lib.rocknpu_hip_gemm_w8a8_ws(_ptr(a8), _ptr(a_scales), _ptr(w8), _ptr(w_scales), m, n, kp, _ptr(out),
-                                        _ld(out), _ptr(out_i32), _ptr(workspace),
-                                        0 if workspace is None else workspace.numel(), _stream()), "gemm_w8a8_ws")
+                                        _ld(out), _ptr(out_i32), _ptr(workspace), workspace.numel(), _stream()),
+           "gemm_w8a8_ws")
     return out
 
 

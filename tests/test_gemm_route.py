@@ -133,8 +133,9 @@ def test_split_rule(m, n, k, splits):
         assert nb == 0
     else:
         t = tiles(m, n, bm, bn)
-        # the fixed 16 KiB counter block, then splits x bm x bn int32 per tile
-        assert nb == 16384 + t * sp * bm * bn * 4
+        # the fixed 16 KiB counter block, then splits x bm x bn int32 per tile,
+        # then one 4-byte stamp per (tile, split) rounded up to 256 bytes
+        assert nb == 16384 + t * sp * bm * bn * 4 + -(-t * sp * 4 // 256) * 256
 
 
 def test_split_invariants_over_a_grid():
@@ -152,7 +153,7 @@ def test_split_invariants_over_a_grid():
         assert bm * bn <= 64 * 64 and 2 * t <= CUS, (m, n, k)
         assert 2 <= sp <= 4 and t * sp <= CUS and stages // sp >= 8, (m, n, k, sp)
         # the no-allocation entry's fixed split workspace holds every routed split on 256 CUs
-        assert nb <= (4 << 20) + 16384, (m, n, k, nb)
+        assert nb <= (4 << 20) + 16384 + 1024, (m, n, k, nb)
 
 
 def test_workspace_and_tile_bad_arguments():
@@ -168,7 +169,8 @@ def test_workspace_and_tile_bad_arguments():
     assert lib.rocknpu_hip_gemm_w8a8_tile(64, 64, 3, 1, *args, None, 0, None) == -1   # no such stage count
     assert lib.rocknpu_hip_gemm_w8a8_tile(64, 32, 4, 0, *args, None, 0, None) == -1   # splits < 1
     assert lib.rocknpu_hip_gemm_w8a8_tile(64, 32, 4, 2, *args, None, 0, None) == -1   # split without workspace
-    small = 16384 + (128 // 64) * (2048 // 32) * 2 * 64 * 32 * 4 - 4  # four bytes short
+    units = (128 // 64) * (2048 // 32) * 2
+    small = 16384 + units * 64 * 32 * 4 + units * 4 - 4  # four bytes short
     assert lib.rocknpu_hip_gemm_w8a8_tile(64, 32, 4, 2, *args, p, small, None) == -1
     assert lib.rocknpu_hip_gemm_w8a8_ws(*args, ctypes.c_void_p((1 << 20) + 16), 4096, None) == -1  # unaligned
     assert lib.rocknpu_hip_gemm_w8a8_ws(*args, None, 4096, None) == -1
