@@ -88,6 +88,10 @@ class DecodeSet:
                 blocks = synth.kquant(kind, n, k, index=10_000 + li * 16 + pi)
                 lw[name] = (torch.from_numpy(blocks).to(dev), k, n, kind)
             self.layers.append(lw)
+        # the decode cache's tile-interleaved copies, written once before any
+        # timing (the C ABI builds them on a weight's first call of 2+ rows)
+        self.tiled = [{name: hip.gemv_tile_weights(kind, w, k, n) for name, (w, k, n, kind) in lw.items()}
+                      for lw in self.layers]
         # activations: one input per distinct projection input, per M
         self.inputs = {}
         self.outs = {}
@@ -113,17 +117,22 @@ class DecodeSet:
 
     def step(self, only_kind: int | None = None, only_m: int | None = None):
         """One pass: per layer and M, one fused launch per shared input
-        (q/k/v, o, gate/up, down), each quantising its f32 input to Q8_K."""
+        (q/k/v, o, gate/up, down), each quantising its f32 input to Q8_K; the
+        raw rows or the tiled copies as the library's rule picks (tiled from
+        2 rows), as the C ABI's decode entries do."""
         hip = self.hip
         for m, li, tag, names, kind in self._launches(only_kind, only_m):
-            lw = self.layers[li]
+            lw, lt = self.layers[li], self.tiled[li]
             k = lw[names[0]][1]
-            hip.gemv_q_f32(kind, [lw[nm][0] for nm in names], k, [lw[nm][2] for nm in names],
-                           self.inputs[(m, tag)], outs=[self.outs[(m, li, nm)] for nm in names])
+            hip.gemv_decode(kind, [lw[nm][0] for nm in names], [lt[nm] for nm in names], k,
+                            [lw[nm][2] for nm in names], self.inputs[(m, tag)],
+                            outs=[self.outs[(m, li, nm)] for nm in names])
 
     def bytes_per_step(self, only_kind: int | None = None, only_m: int | None = None) -> tuple[int, int]:
         """(algorithmic HBM bytes, launches) per step: each launch reads its
-        weights and the f32 activation rows once and writes the f32 outputs."""
+        weights (the raw GGUF bytes; every TinyLlama projection has a multiple
+        of 16 rows, so its tiled copy holds exactly those bytes) and the f32
+        activation rows once and writes the f32 outputs."""
         total = 0
         launches = 0
         for m, li, tag, names, kind in self._launches(only_kind, only_m):
@@ -351,21 +360,27 @@ def decode_large(torch, hip, synth) -> dict:
     for name, kind, ns, k in (("gate_up_q4k", 4, (14336, 14336), 4096), ("down_q6k", 6, (4096,), 14336)):
         wbytes = sum(n * k // 256 * synth.BLOCK_BYTES[kind] for n in ns)
         copies = max(2, min(24, int(1.2e9 // wbytes)))
-        W = [[torch.from_numpy(synth.kquant(kind, n, k, index=50_000 + 8 * c + j)).to(dev)
-              for j, n in enumerate(ns)] for c in range(copies)]
+        tiled = hip.gemv_tiled_preferred(kind, 1, k)
+        W = []
+        for c in range(copies):
+            ws = []
+            for j, n in enumerate(ns):
+                raw = torch.from_numpy(synth.kquant(kind, n, k, index=50_000 + 8 * c + j)).to(dev)
+                ws.append(hip.gemv_tile_weights(kind, raw, k, n) if tiled else raw)
+            W.append(ws)
         x = torch.from_numpy(synth.activations(1, k, index=51_000 + k)).to(dev)
         outs = [torch.empty((1, n), dtype=torch.float32, device=dev) for n in ns]
 
         def run():
             for ws in W:
-                hip.gemv_q_f32(kind, ws, k, list(ns), x, outs=outs)
+                hip.gemv_decode(kind, ws, ws, k, list(ns), x, outs=outs)
 
         ms, _ = time_graph(torch, run, 5, 2)
         us = ms * 1e3 / copies
         byts = wbytes + k * 4 + sum(ns) * 4
         gbs = byts / (us * 1e-6) / 1e9
-        res[name] = {"kind": kind, "n": list(ns), "k": k, "us": round(us, 3), "gb_s": round(gbs, 1),
-                     "frac_hbm_peak": round(gbs / HBM_PEAK_GBS, 4), "weight_copies": copies}
+        res[name] = {"kind": kind, "n": list(ns), "k": k, "layout": "tiled" if tiled else "raw", "us": round(us, 3),
+                     "gb_s": round(gbs, 1), "frac_hbm_peak": round(gbs / HBM_PEAK_GBS, 4), "weight_copies": copies}
         del W
         torch.cuda.empty_cache()
     return res
@@ -373,8 +388,8 @@ def decode_large(torch, hip, synth) -> dict:
 
 def decode_crossover(torch, hip, synth) -> dict:
     """Llama-3-8B gate+up (2 x [14336 x 4096] Q4_K) at batched decode sizes:
-    the GEMV route (f32 activations quantised to Q8_K in-kernel, Q4_K weights
-    read as they are) against the W8A8 route (per-token A8 quant + int8 GEMM
+    the GEMV route (f32 activations quantised to Q8_K in-kernel, the Q4_K
+    weights' tiled copy) against the W8A8 route (per-token A8 quant + int8 GEMM
     on weights repacked once to W8), to locate the batch where the GEMM takes
     over. Weight copies rotate through > 256 MB for both routes."""
     dev = "cuda"
@@ -382,6 +397,7 @@ def decode_crossover(torch, hip, synth) -> dict:
     res = {}
     wq = [[torch.from_numpy(synth.kquant(4, n, k, index=52_000 + 2 * c + j)).to(dev) for j in range(2)]
           for c in range(4)]
+    wt = [[hip.gemv_tile_weights(4, blk, k, n) for blk in pair] for pair in wq]
     w8 = []
     for pair in wq[:3]:
         parts = [hip.repack_w8(4, blk, k, n) for blk in pair]
@@ -394,8 +410,8 @@ def decode_crossover(torch, hip, synth) -> dict:
         out = torch.empty((m, 2 * n), dtype=torch.float32, device=dev)
 
         def gemv():
-            for pair in wq:
-                hip.gemv_q_f32(4, pair, k, [n, n], x, outs=outs)
+            for pair, tpair in zip(wq, wt):
+                hip.gemv_decode(4, pair, tpair, k, [n, n], x, outs=outs)
 
         def gemm():
             for w, wsc in w8:
@@ -438,9 +454,11 @@ def vs_hipblaslt(torch, hip, synth) -> None:
 
 
 def gemv_shapes(torch, hip, synth) -> None:
-    """One line per decode shape and row count: single fused launches (Q8_K
-    quantisation in-kernel) of the TinyLlama projections and the Llama-3-8B
-    FFN, replayed in a graph on weight copies rotating through >= 1 GiB."""
+    """One line per decode shape, row count and weight layout (raw GGUF rows,
+    the tiled copy): single fused launches (Q8_K quantisation in-kernel) of the
+    TinyLlama projections and the Llama-3-8B FFN, replayed in a graph on weight
+    copies rotating through >= 1 GiB; `picked` marks the layout the library's
+    rule takes."""
     shapes = [("o", 4, 2048, [2048]), ("qkv", 4, 2048, [2048, 256, 256]), ("gate+up", 4, 2048, [5632, 5632]),
               ("down", 6, 5632, [2048]), ("llama3_8b gate+up", 4, 4096, [14336, 14336]),
               ("llama3_8b down", 6, 14336, [4096])]
@@ -448,22 +466,28 @@ def gemv_shapes(torch, hip, synth) -> None:
         per = sum(n * (k // synth.QK) * hip.BLOCK_BYTES[kind] for n in ns)
         copies = max(2, (1 << 30) // per + 1)
         base = [[torch.from_numpy(synth.kquant(kind, n, k, index=500 + c * 8 + i)).to("cuda")
-                 for i, n in enumerate(ns)] for c in range(min(copies, 4))]
-        sets = [base[c] if c < len(base) else [t.clone() for t in base[c % len(base)]] for c in range(copies)]
-        for m in ((1, 2, 4, 8) if name.startswith("llama3_8b") else (1, 4, 8)):
-            x = torch.from_numpy(synth.activations(m, k, index=900 + m)).to("cuda")
-            outs = [torch.empty((m, n), device="cuda") for n in ns]
+                 for i, n in enumerate(ns)] for c in range(min(copies, 2))]
+        tbase = [[hip.gemv_tile_weights(kind, w, k, n) for w, n in zip(ws, ns)] for ws in base]
+        for layout, src in (("raw", base), ("tiled", tbase)):
+            sets = [src[c] if c < len(src) else [t.clone() for t in src[c % len(src)]] for c in range(copies)]
+            for m in ((1, 2, 4, 8) if name.startswith("llama3_8b") else (1, 2, 4, 8)):
+                x = torch.from_numpy(synth.activations(m, k, index=900 + m)).to("cuda")
+                outs = [torch.empty((m, n), device="cuda") for n in ns]
+                call = hip.gemv_q_f32 if layout == "raw" else hip.gemv_q_f32_tiled
 
-            def run():
-                for ws in sets:
-                    hip.gemv_q_f32(kind, ws, k, ns, x, outs=outs)
+                def run():
+                    for ws in sets:
+                        call(kind, ws, k, ns, x, outs=outs)
 
-            ms, _ = time_graph(torch, run, max(1, 100 // copies), 2)
-            us = ms * 1e3 / copies
-            byts = per + m * k * 4 + m * sum(ns) * 4
-            print(json.dumps({"shape": name, "kind": kind, "m": m, "k": k, "n": ns, "us": round(us, 3),
-                              "gb_s": round(byts / us / 1e3, 1), "weight_mb": round(per / 1e6, 2)}), flush=True)
-        del sets, base
+                ms, _ = time_graph(torch, run, max(1, 100 // copies), 2)
+                us = ms * 1e3 / copies
+                byts = per + m * k * 4 + m * sum(ns) * 4
+                print(json.dumps({"shape": name, "kind": kind, "m": m, "k": k, "n": ns, "layout": layout,
+                                  "picked": hip.gemv_tiled_preferred(kind, m, k) == (layout == "tiled"),
+                                  "us": round(us, 3), "gb_s": round(byts / us / 1e3, 1),
+                                  "weight_mb": round(per / 1e6, 2)}), flush=True)
+            del sets
+        del base, tbase
         torch.cuda.empty_cache()
 
 
@@ -685,13 +709,14 @@ def main():
         "data": "synthetic (seeded Q4_K/Q6_K weights, N(0,1) activations)",
         "config": {"workload": "decode GEMV set: TinyLlama-1.1B projections x 22 layers, M=1 and M=4, "
                                "Q8_K activation quant fused into the Q4_K/Q6_K x Q8_K GEMV, one launch per "
-                               "shared input (qkv, o, gate+up, down), HIP graph",
+                               "shared input (qkv, o, gate+up, down), raw rows at M=1 and the decode cache's "
+                               "tiled copies at M=4, HIP graph",
                    "layers": synth.TINYLLAMA_LAYERS, "m": [1, 4], "launches_per_step": n_gemv,
                    "bytes_per_step": step_bytes},
-        "roofline": {"bound": "hbm", "kernel": "Q4_K x Q8_K decode GEMV at M=4 on the matrix cores with fused "
-                                               "Q8_K quant (gemv_mfma_kernel<4,4,true,...> for q/k/v and o, "
-                                               "gemv_q4_staged_kernel<4,true> for gate+up), the 66 Q4_K launches "
-                                               "of a step",
+        "roofline": {"bound": "hbm", "kernel": "Q4_K x Q8_K decode GEMV at M=4 on the matrix cores over the "
+                                               "tiled copies, fused Q8_K quant (gemv_tiled_kernel<4,4,true,8,true,1,1> "
+                                               "for q/k/v and o, gemv_tiled_kernel<4,4,true,8,true,3,2> for "
+                                               "gate+up), the 66 Q4_K launches of a step",
                      "achieved": round(m4_achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(m4_achieved / HBM_PEAK_GBS, 4), "traffic": measured_traffic("gemv_q4k_m4"),
                      "avg_launch_us": round(m4_us, 3), "bytes_per_launch": m4_bpl},
@@ -700,8 +725,10 @@ def main():
                         "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                         "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": measured_traffic("gemv_q4k"),
                         "avg_launch_us": round(q4_us, 3), "bytes_per_launch": q4_bpl},
-        "decode_q6k_down": {"kernel": "Q6_K x Q8_K decode GEMV with fused Q8_K quant (gemv_q6_stream_kernel), "
-                                      "the 22 down launches of a step at each M", "peak": HBM_PEAK_GBS, "unit": "GB/s",
+        "decode_q6k_down": {"kernel": "Q6_K x Q8_K decode GEMV with fused Q8_K quant (M=1: gemv_q6_stream_kernel "
+                                      "on raw rows; M=4: gemv_tiled_kernel<6,4,true,8,false,3,2> on the tiled "
+                                      "copies), the 22 down launches of a step at each M", "peak": HBM_PEAK_GBS,
+                            "unit": "GB/s",
                             **q6},
     }
     if not args.quick:

@@ -179,6 +179,47 @@ int rocknpu_hip_gemv_q_f32(uint32_t kind, size_t count, const uint8_t * const * 
                            size_t ldx, size_t m, float * const * out, const size_t * ldo,
                            void * stream);
 
+/* Bytes of the decode cache's tile-interleaved copy of a Q4_K (kind 4) or Q6_K
+ * (kind 6) weight of n rows and K = k (a multiple of 256): whole 16-row tiles
+ * of k/256 blocks each, ceil(n / 16) * 16 * (k / 256) * block bytes (the last
+ * tile's missing rows are zero blocks). 0 for an invalid kind or shape. Host
+ * code only. No counterpart in the reference, whose decode GEMV runs on the
+ * CPU on ggml's row-major blocks. */
+size_t rocknpu_hip_gemv_tiled_bytes(uint32_t kind, size_t k, size_t n);
+
+/* Writes the tile-interleaved copy of the raw row-major GGUF blocks `w`
+ * (w_bytes = n * k/256 * block bytes, 2-byte aligned) to `tiled` (16-byte
+ * aligned, tiled_bytes >= rocknpu_hip_gemv_tiled_bytes): 16 rows' block b
+ * together, each wave lane's operand bytes contiguous, so the decode GEMV
+ * loads whole cache lines. The same bytes in another order (a one-time
+ * conversion, like the W8 repack); the GEMV's results on the copy equal those
+ * on the raw blocks bit for bit. No counterpart in the reference. */
+int rocknpu_hip_gemv_tile_weights(uint32_t kind, const uint8_t * w, size_t w_bytes, size_t k, size_t n,
+                                  uint8_t * tiled, size_t tiled_bytes, void * stream);
+
+/* rocknpu_hip_gemv_q_f32 and rocknpu_hip_gemv_q8_k on tiled copies
+ * (rocknpu_hip_gemv_tile_weights; w_bytes[i] = rocknpu_hip_gemv_tiled_bytes of
+ * member i): the matrix-core GEMV with whole-line weight loads at every m
+ * (launches of up to 16 rows for Q4_K, 8 for Q6_K). A row's f32 sum runs in the
+ * order of the matrix-core kernel on raw blocks, so results equal
+ * rocknpu_hip_gemv_q_f32 / _q8_k wherever that kernel serves the call, and
+ * fused, grouped and Q8_K-input calls agree bit for bit. No counterpart in the
+ * reference. */
+int rocknpu_hip_gemv_q_f32_tiled(uint32_t kind, size_t count, const uint8_t * const * w,
+                                 const size_t * w_bytes, const size_t * n, size_t k, const float * x,
+                                 size_t ldx, size_t m, float * const * out, const size_t * ldo,
+                                 void * stream);
+int rocknpu_hip_gemv_q8_k_tiled(uint32_t kind, const uint8_t * w, size_t w_bytes, size_t k, size_t n,
+                                const uint8_t * q8k, size_t m, float * out, size_t ldo, void * stream);
+
+/* Whether a decode GEMV of m activation rows over Q4_K (kind 4) or Q6_K
+ * (kind 6) rows of K = k runs faster on the tiled copy (1) or on the raw rows
+ * (0): the tiled copy from two rows, and at one row for Q4_K rows of 16 or more
+ * blocks; one-row launches of shorter Q4_K rows and of Q6_K rows keep the
+ * lane-per-block and LDS-stream kernels on raw rows. Host code only. No
+ * counterpart in the reference. */
+int rocknpu_hip_gemv_tiled_preferred(uint32_t kind, size_t m, size_t k);
+
 /* Stall report of rocknpu_hip_gemv_q_f32 and rocknpu_hip_gemv_q8_k. In the
  * fused lane-per-block kernel (rocknpu_hip_gemv_shape: *mfma == 0) and in the
  * Q6_K stream kernel (*mfma == 2, fused or not) a workgroup's waves wait for

@@ -40,7 +40,7 @@ CFLAGS = [
     f"-I{CSRC}",
 ]
 
-SOURCES = ["repack.hip", "quant.hip", "gemm.hip", "gemm_skinny.hip", "gemv.hip", "gemv_mfma.hip", "launch.hip", "matmul.hip", "capi.hip", "sidecar.hip", "route.hip"]
+SOURCES = ["repack.hip", "quant.hip", "gemm.hip", "gemm_skinny.hip", "gemv.hip", "gemv_mfma.hip", "gemv_tiled.hip", "launch.hip", "matmul.hip", "capi.hip", "sidecar.hip", "route.hip"]
 
 
 def _run(cmd: list[str]) -> None:

@@ -50,6 +50,7 @@ uint64_t now_ns() {
                                      .count());
 }
 
+using rk::DecodeWeight;
 using rk::DevBuf;
 using rk::DeviceW8;
 using rk::KeyHash;
@@ -458,20 +459,41 @@ int context_repack_to_host(rocknpu_context* ctx, uint32_t kind, const uint8_t* s
 }  // namespace rk
 
 namespace {
-// The raw K-quant blocks of a weight, resident on the device under the
-// reference's cache key; uploaded on first use.
-std::shared_ptr<DevBuf> raw_weights(RockNpuContext* ctx, const uint8_t* w, size_t bytes, size_t k, size_t n,
-                                    uint32_t kind, bool* hit) {
+// The K-quant blocks of a weight, resident on the device under the
+// reference's cache key: the raw rows uploaded on first use, and for calls of
+// two or more rows (`tiled`) their tile-interleaved copy, written once on the
+// device from the raw rows.
+std::shared_ptr<DecodeWeight> raw_weights(RockNpuContext* ctx, const uint8_t* w, size_t bytes, size_t k, size_t n,
+                                          uint32_t kind, bool tiled, bool* hit) {
     const WeightKey key{reinterpret_cast<uintptr_t>(w), bytes, k, n, kind};
+    std::shared_ptr<DecodeWeight> dw;
     auto it = ctx->raw.find(key);
-    if (it != ctx->raw.end()) return it->second;
-    *hit = false;
-    auto dw = std::make_shared<DevBuf>();
-    if (!dw->ensure(bytes) || !hip_ok(hipMemcpyAsync(dw->p, w, bytes, hipMemcpyHostToDevice, ctx->stream), ctx, "raw"))
-        return nullptr;
-    ctx->raw.emplace(key, dw);
+    if (it != ctx->raw.end()) {
+        dw = it->second;
+    } else {
+        *hit = false;
+        dw = std::make_shared<DecodeWeight>();
+        if (!dw->raw.ensure(bytes) ||
+            !hip_ok(hipMemcpyAsync(dw->raw.p, w, bytes, hipMemcpyHostToDevice, ctx->stream), ctx, "raw"))
+            return nullptr;
+        dw->raw_bytes = bytes;
+        ctx->raw.emplace(key, dw);
+    }
+    if (tiled && dw->tiled_bytes == 0) {
+        *hit = false;
+        const size_t tb = rocknpu_hip_gemv_tiled_bytes(kind, k, n);
+        if (tb == 0 || !dw->tiled.ensure(tb) ||
+            rocknpu_hip_gemv_tile_weights(kind, dw->raw.as<uint8_t>(), bytes, k, n, dw->tiled.as<uint8_t>(), tb,
+                                          ctx->stream) != kOk)
+            return nullptr;
+        dw->tiled_bytes = tb;
+    }
     return dw;
 }
+
+// Whether a decode call reads the tiled copies (rocknpu_hip_gemv_tiled_preferred:
+// from two rows, and Q4_K rows of 16 or more blocks at one row).
+bool decode_tiled(uint32_t kind, size_t m, size_t k) { return rocknpu_hip_gemv_tiled_preferred(kind, m, k) != 0; }
 
 // Decode-cache accounting of one decode call (the reference's
 // decode_cache_hits / misses and their ns, lib.rs:3821-3826): a hit when every
@@ -519,7 +541,7 @@ int rocknpu_context_decode_cache_stats(const rocknpu_context* ctx, rocknpu_decod
     size_t resident = 0;
     for (const auto& e : ctx->m1) resident += e.second->resident_bytes();
     for (const auto& e : ctx->m1_groups) resident += e.second->resident_bytes();
-    for (const auto& e : ctx->raw) resident += e.first.bytes;
+    for (const auto& e : ctx->raw) resident += e.second->raw_bytes + e.second->tiled_bytes;
     rocknpu_decode_cache_stats s{};
     s.hits = ctx->hits;
     s.misses = ctx->misses;
@@ -813,7 +835,8 @@ int rocknpu_matmul_q_q8k_f32_f32(rocknpu_context* ctx, uint32_t kind, const uint
         if (!std::isfinite(act[i])) return kInvalid;
     const uint64_t t0 = now_ns();
     bool hit = true;
-    const std::shared_ptr<DevBuf> dw = raw_weights(ctx, w, bytes, k, n, kind, &hit);
+    const bool tiled = decode_tiled(kind, m, k);
+    const std::shared_ptr<DecodeWeight> dw = raw_weights(ctx, w, bytes, k, n, kind, tiled, &hit);
     if (!dw) return kExec;
     const size_t q8_bytes = m * (k / kQK) * 292;
     if (!ctx->d_act.ensure(a_elems * 4) || !ctx->d_q8k.ensure(q8_bytes) || !ctx->d_out.ensure(o_elems * 4))
@@ -822,8 +845,10 @@ int rocknpu_matmul_q_q8k_f32_f32(rocknpu_context* ctx, uint32_t kind, const uint
         return kExec;
     int st = rocknpu_hip_quantize_q8_k(ctx->d_act.as<float>(), m, k, k, ctx->d_q8k.as<uint8_t>(), ctx->stream);
     if (st != kOk) return st;
-    st = rocknpu_hip_gemv_q8_k(kind, dw->as<uint8_t>(), bytes, k, n, ctx->d_q8k.as<uint8_t>(), m,
-                               ctx->d_out.as<float>(), n, nullptr, nullptr, ctx->stream);
+    st = tiled ? rocknpu_hip_gemv_q8_k_tiled(kind, dw->tiled.as<uint8_t>(), dw->tiled_bytes, k, n,
+                                             ctx->d_q8k.as<uint8_t>(), m, ctx->d_out.as<float>(), n, ctx->stream)
+               : rocknpu_hip_gemv_q8_k(kind, dw->raw.as<uint8_t>(), bytes, k, n, ctx->d_q8k.as<uint8_t>(), m,
+                                       ctx->d_out.as<float>(), n, nullptr, nullptr, ctx->stream);
     if (st != kOk) return st;
     if (!hip_ok(hipMemcpyAsync(out, ctx->d_out.p, o_elems * 4, hipMemcpyDeviceToHost, ctx->stream), ctx, "out") ||
         !hip_ok(hipStreamSynchronize(ctx->stream), ctx, "gemv"))
@@ -852,9 +877,10 @@ int rocknpu_matmul_q_q8k_group_f32_f32(rocknpu_context* ctx, size_t count, const
         if (!std::isfinite(act[i])) return kInvalid;
     const uint64_t t0 = now_ns();
     bool hit = true;
-    std::shared_ptr<DevBuf> dw[4];
+    std::shared_ptr<DecodeWeight> dw[4];
     for (size_t i = 0; i < count; ++i)
-        if (!(dw[i] = raw_weights(ctx, weights[i], bytes[i], k, ns[i], kinds[i], &hit))) return kExec;
+        if (!(dw[i] = raw_weights(ctx, weights[i], bytes[i], k, ns[i], kinds[i], decode_tiled(kinds[i], m, k), &hit)))
+            return kExec;
     if (!ctx->d_act.ensure(a_elems * 4) || !ctx->d_out.ensure(o_elems * 4)) return kExec;
     if (!hip_ok(hipMemcpyAsync(ctx->d_act.p, act, a_elems * 4, hipMemcpyHostToDevice, ctx->stream), ctx, "act"))
         return kExec;
@@ -863,22 +889,25 @@ int rocknpu_matmul_q_q8k_group_f32_f32(rocknpu_context* ctx, size_t count, const
     size_t off[4];
     for (size_t i = 0, o = 0; i < count; o += m * ns[i], ++i) off[i] = o;
     for (uint32_t kind : {4u, 6u}) {
+        const bool tiled = decode_tiled(kind, m, k);
         const uint8_t* w[4];
         size_t wb[4], wn[4], ldo[4];
         float* out[4];
         size_t c = 0;
         for (size_t i = 0; i < count; ++i) {
             if (kinds[i] != kind) continue;
-            w[c] = dw[i]->as<uint8_t>();
-            wb[c] = bytes[i];
+            w[c] = tiled ? dw[i]->tiled.as<uint8_t>() : dw[i]->raw.as<uint8_t>();
+            wb[c] = tiled ? dw[i]->tiled_bytes : bytes[i];
             wn[c] = ns[i];
             ldo[c] = ns[i];
             out[c] = ctx->d_out.as<float>() + off[i];
             ++c;
         }
         if (c == 0) continue;
-        const int st = rocknpu_hip_gemv_q_f32(kind, c, w, wb, wn, k, ctx->d_act.as<float>(), k, m, out, ldo,
-                                              ctx->stream);
+        const int st = tiled ? rocknpu_hip_gemv_q_f32_tiled(kind, c, w, wb, wn, k, ctx->d_act.as<float>(), k, m, out,
+                                                            ldo, ctx->stream)
+                             : rocknpu_hip_gemv_q_f32(kind, c, w, wb, wn, k, ctx->d_act.as<float>(), k, m, out, ldo,
+                                                      ctx->stream);
         if (st != kOk) return st;
     }
     for (size_t i = 0; i < count; ++i)

@@ -237,4 +237,11 @@ struct GemvParams {
     int32_t* msum;
 };
 
+// The decode cache's tile-interleaved weight layout (gemv_mfma.hip): bytes of
+// the tiled copy of n rows of nb blocks, the conversion from raw GGUF blocks,
+// and the matrix-core GEMV on such copies (1 <= p.m <= gemv_mfma_rows).
+size_t gemv_tiled_bytes(int kind, int64_t n, int nb);
+int launch_gemv_tile_weights(int kind, const uint8_t* src, int64_t n, int nb, uint8_t* dst, hipStream_t stream);
+int launch_gemv_tiled(int kind, bool fused, GemvParams& p, hipStream_t stream);
+
 }  // namespace rk

@@ -86,6 +86,14 @@ struct DevBuf {
     T* as() const { return static_cast<T*>(p); }
 };
 
+// A weight resident for the Q8_K decode GEMV: its raw K-quant rows (read by
+// the one-row kernels) and, built on the first call of two or more rows, the
+// tile-interleaved copy the matrix-core kernels read with whole-line loads.
+struct DecodeWeight {
+    DevBuf raw, tiled;
+    size_t raw_bytes = 0, tiled_bytes = 0;
+};
+
 struct PinnedBuf {
     void* p = nullptr;
     size_t cap = 0;
@@ -149,8 +157,8 @@ struct RockNpuContext {
     // decode (M = 1) caches, kept across releases
     std::unordered_map<rk::WeightKey, rk::W8Ptr, rk::KeyHash> m1;
     std::map<std::vector<rk::WeightKey>, rk::W8Ptr> m1_groups;
-    // raw K-quant blocks resident for the Q8_K decode GEMV
-    std::unordered_map<rk::WeightKey, std::shared_ptr<rk::DevBuf>, rk::KeyHash> raw;
+    // K-quant weights resident for the Q8_K decode GEMV (raw and tiled)
+    std::unordered_map<rk::WeightKey, std::shared_ptr<rk::DecodeWeight>, rk::KeyHash> raw;
     rk::DevBuf d_raw, d_act, d_a8, d_as, d_out, d_q8k;
     rk::DevBuf d_split;  // the W8A8 GEMM's K-split workspace (counters cleared per call)
     rk::PinnedBuf h_out, h_as, h_err;  // h_err: the K-split workspace's error word

@@ -1,0 +1,290 @@
+// Kernel (d) on the decode cache's tiled copies of Q4_K/Q6_K weights: the
+// layout and its conversion from raw GGUF rows, and the matrix-core GEMV of
+// gemv_mfma.h reading them with whole-line loads.
+//
+// In the tiled copy the 16 rows of a tile have block b in one contiguous run
+// whose bytes sit in the order the lanes take them: the 16 rows' headers, then
+// each lane's operand bytes together. A wave then loads a tile's block with
+// three (Q4_K) or five (Q6_K) whole-line instructions instead of 16 partly
+// used lines per instruction, into the same registers, so the arithmetic and
+// its results are those of the kernel on raw rows.
+#include "gemv_mfma.h"
+
+namespace rk {
+namespace {
+
+// ------------------------------------------------------------ tiled, pipelined
+// The matrix-core GEMV on tiled weights with NI items per wave (an item is a
+// tile of the workgroup and one of the wave's block indices) known at compile
+// time and D of them in flight. The item loop is unrolled into straight-line
+// code: in gemv_mfma_kernel's loop the compiler waits for every load in flight
+// at the loop's head, so a second block in flight was waited for together with
+// the first. The tile sums go to LDS and are stored after the loop, so no store
+// sits among the loads either. A row's arithmetic and f32 order are those of
+// gemv_mfma_kernel (wave g adds blocks g, g + W, .. in order; the W partial
+// sums are added in wave order), so the results are the same bits.
+template <int KIND, int MT, bool FUSED, int W, bool AREG, int NI, int D>
+__global__ __launch_bounds__(W * 64) void gemv_tiled_kernel(const MfmaArgs p) {
+    constexpr int BB = block_bytes(KIND);
+    constexpr int NR = MT / 4;
+    static_assert(D >= 1 && D <= NI, "one to NI items in flight");
+    using Piece = typename PieceOf<KIND, true>::type;
+    extern __shared__ __align__(16) uint8_t smem[];
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int nb = p.nb, m = p.m, iters = p.iters;
+    const ActLds<MT> act{smem, nb};
+    // partial sums [2][W][64][NR], then the tile sums [NI][64][NR]
+    float* part = reinterpret_cast<float*>(smem + ((nb * MT * kPerRowBlock + 15) & ~15));
+    float* res = part + 2 * W * 64 * NR;
+    const int n = lane & 15, q = lane >> 4;
+    const int grid = gridDim.x, bid = blockIdx.x;
+    const int ntile = (p.tiles - bid + grid - 1) / grid;  // tiles bid, bid + grid, ..
+    const int items = ntile * iters;                       // <= NI (the host's choice)
+    // item i: tile i / iters of the workgroup, block index i % iters; items
+    // past the workgroup's last re-read its last one (in bounds) and are dropped
+    auto load_item = [&](int i, Piece& k) {
+        const int ic = min(i, items - 1);
+        const int kt = ic / iters, it = ic - kt * iters;
+        const int t = bid + kt * grid;
+        const TileOut to = tile_out(p, t);
+        const int b = min(wave + W * it, nb - 1);
+        const gbytes w = reinterpret_cast<gbytes>(reinterpret_cast<uint64_t>(tile_weights(p, t)));
+        k.load_tiled(w + (static_cast<int64_t>(to.row0 / kTileRows) * nb + b) * (kTileRows * BB), lane);
+    };
+
+    OwnedActs<MT, W, FUSED> owned;
+    owned.first(p, wave);
+    // every wave's activation loads ahead of any weight load (gemv_mfma_kernel)
+    __builtin_amdgcn_s_barrier();
+    Piece buf[D];
+    load_item(0, buf[0]);
+    owned.template stage<AREG>(p, wave, act);
+#pragma unroll
+    for (int j = 1; j < D; ++j) load_item(j, buf[j]);
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+
+    uint64_t areg[8];
+    uint32_t bsreg[NR][8];
+    float dareg[NR];
+    if constexpr (AREG) {
+        const int b = min(wave, nb - 1);
+        a_operands<KIND, MT>(act, b, lane, areg);
+        row_data<KIND, MT>(act, b, lane, bsreg, dareg);
+    }
+    float acc[NR];
+#pragma unroll
+    for (int lr = 0; lr < NR; ++lr) acc[lr] = 0.0f;
+#pragma unroll
+    for (int i = 0; i < NI; ++i) {
+        const int kt = i / iters, it = i - kt * iters;
+        const int b = wave + W * it;
+        if constexpr (!AREG) {
+            a_operands<KIND, MT>(act, min(b, nb - 1), lane, areg);
+            row_data<KIND, MT>(act, min(b, nb - 1), lane, bsreg, dareg);
+        }
+        float term[NR];
+        block_terms<KIND, MT>(buf[i % D], areg, bsreg, dareg, term);
+        if (i + D < NI) load_item(i + D, buf[i % D]);
+        const bool have = b < nb && i < items;  // uniform
+#pragma unroll
+        for (int lr = 0; lr < NR; ++lr) acc[lr] += have ? term[lr] : 0.0f;
+        if (it == iters - 1) {  // uniform: tile kt done
+            float* pb = part + (kt & 1) * (W * 64 * NR);
+#pragma unroll
+            for (int lr = 0; lr < NR; ++lr) {
+                pb[(wave * 64 + lane) * NR + lr] = acc[lr];
+                acc[lr] = 0.0f;
+            }
+            asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+            if (wave == (kt & (W - 1))) {
+#pragma unroll
+                for (int lr = 0; lr < NR; ++lr) {
+                    res[(kt * 64 + lane) * NR + lr] = tile_row_sum<W, NR>(pb, lane, lr, iters);
+                }
+            }
+        }
+    }
+    __syncthreads();
+    for (int kt = wave; kt < ntile; kt += W) {
+        const TileOut to = tile_out(p, bid + kt * grid);
+        const int row = to.row0 + n;
+#pragma unroll
+        for (int lr = 0; lr < NR; ++lr) {
+            const int mo = NR * q + lr;
+            if (mo < m && row < to.rows)
+                reinterpret_cast<gfloats>(reinterpret_cast<uint64_t>(to.out))[mo * to.ldo + row] =
+                    res[(kt * 64 + lane) * NR + lr];
+        }
+    }
+}
+
+}  // namespace
+
+// ------------------------------------------------------------ tiled layout
+// The decode cache's copy of a weight: tiles of 16 rows (the last padded with
+// zero rows), each tile's nb blocks one after another, and each block of the
+// tile one run of 16 * B_blk bytes in the order the lanes of a wave take them
+// (tile block, byte u):
+//   Q4_K (2304 bytes): u < 256 row u / 16's 16-byte header (d, dmin, 12 scale
+//     bytes); else lane l = (u - 256) / 32, with row n = l % 16 and K group
+//     q = l / 16: the quant bytes 32 j + 8 q .. + 7 of row n, j = 0..3.
+//   Q6_K (3360 bytes): u < 256 row u / 16's 16 scales; u < 288 row (u - 256)
+//     / 2's fp16 d; else lane l = (u - 288) / 48: the ql runs 64 h + 32 i + 8 q
+//     (in the order 2 h + i) and the qh runs 128 + 32 h + 8 q, 8 bytes each.
+// A bijection of the raw bytes (plus the zero rows), so the GEMV's results on
+// it are those on the raw blocks.
+size_t gemv_tiled_bytes(int kind, int64_t n, int nb) {
+    return static_cast<size_t>((n + kTileRows - 1) / kTileRows) * kTileRows * nb * block_bytes(kind);
+}
+
+namespace {
+// One 2-byte unit of the tiled copy per thread: every run above starts at an
+// even byte and has an even length, so a unit's bytes are one aligned 2-byte
+// piece of one raw block (blocks are 2-byte aligned).
+template <int KIND>
+__global__ __launch_bounds__(256) void gemv_tile_weights_kernel(const uint8_t* __restrict__ src, int64_t n, int nb,
+                                                                uint16_t* __restrict__ dst, int64_t units) {
+    constexpr int BB = block_bytes(KIND), TB = kTileRows * BB;
+    for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < units;
+         i += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+        const int64_t o = 2 * i, tbi = o / TB;
+        const int u = static_cast<int>(o - tbi * TB);
+        const int64_t t = tbi / nb;
+        const int b = static_cast<int>(tbi - t * nb);
+        int r, off;
+        if constexpr (KIND == 4) {
+            if (u < 256) {
+                r = u >> 4;
+                off = u & 15;
+            } else {
+                const int v = u - 256, l = v >> 5, w = v & 31;
+                r = l & 15;
+                off = 16 + 32 * (w >> 3) + 8 * (l >> 4) + (w & 7);
+            }
+        } else {
+            if (u < 256) {
+                r = u >> 4;
+                off = 192 + (u & 15);
+            } else if (u < 288) {
+                r = (u - 256) >> 1;
+                off = 208;
+            } else {
+                const int v = u - 288, l = v / 48, w = v - 48 * l, q = l >> 4;
+                r = l & 15;
+                off = w < 32 ? 64 * (w >> 4) + 32 * ((w >> 3) & 1) + 8 * q + (w & 7)
+                             : 128 + 32 * ((w - 32) >> 3) + 8 * q + (w & 7);
+            }
+        }
+        const int64_t row = t * kTileRows + r;
+        dst[i] = row < n ? *reinterpret_cast<const uint16_t*>(src + (row * nb + b) * BB + off) : uint16_t{0};
+    }
+}
+}  // namespace
+
+int launch_gemv_tile_weights(int kind, const uint8_t* src, int64_t n, int nb, uint8_t* dst, hipStream_t stream) {
+    const int64_t units = static_cast<int64_t>(gemv_tiled_bytes(kind, n, nb) / 2);
+    const int64_t want = (units + 255) / 256;
+    const dim3 grid(static_cast<unsigned>(std::min<int64_t>(want, 65536)));
+    if (kind == 4)
+        gemv_tile_weights_kernel<4><<<grid, dim3(256), 0, stream>>>(src, n, nb, reinterpret_cast<uint16_t*>(dst), units);
+    else if (kind == 6)
+        gemv_tile_weights_kernel<6><<<grid, dim3(256), 0, stream>>>(src, n, nb, reinterpret_cast<uint16_t*>(dst), units);
+    else
+        return kStatusInvalid;
+    return hipGetLastError() == hipSuccess ? kStatusOk : kStatusExec;
+}
+
+namespace {
+// Pipelined kernel, NI items per wave: two in flight for two or three items
+// (TinyLlama gate+up, 2 x 5632 x 2048, three tiles per workgroup at 4 rows:
+// 5.32 us against 5.51 with one; TinyLlama down, 2048 x 5632 on 8 waves, three
+// blocks per wave: 6.95 against 7.46), one for four (Llama-3-8B down, 4096 x
+// 14336 on 16 waves: 14.8 against 14.8-15.1 us with two or four).
+template <int KIND, int MT, bool FUSED, int W, bool AREG>
+void launch_pipe(int ni, const MfmaArgs& p, dim3 grid, size_t lds, hipStream_t stream) {
+    const dim3 block(W * 64);
+    if (ni == 1) gemv_tiled_kernel<KIND, MT, FUSED, W, AREG, 1, 1><<<grid, block, lds, stream>>>(p);
+    else if (ni == 2) gemv_tiled_kernel<KIND, MT, FUSED, W, AREG, 2, 2><<<grid, block, lds, stream>>>(p);
+    else if (ni == 3) gemv_tiled_kernel<KIND, MT, FUSED, W, AREG, 3, 2><<<grid, block, lds, stream>>>(p);
+    else gemv_tiled_kernel<KIND, MT, FUSED, W, AREG, 4, 1><<<grid, block, lds, stream>>>(p);
+}
+
+template <int KIND, int MT, bool FUSED, int W>
+void launch_tiled_w(int ni, const MfmaArgs& p, dim3 grid, size_t lds_loop, size_t lds_pipe, hipStream_t stream) {
+    if constexpr (MT <= 8) {
+        if (ni <= 4) {
+            if (p.iters == 1) launch_pipe<KIND, MT, FUSED, W, true>(ni, p, grid, lds_pipe, stream);
+            else launch_pipe<KIND, MT, FUSED, W, false>(ni, p, grid, lds_pipe, stream);
+            return;
+        }
+    }
+    {
+        // more items per wave than the pipelined kernel unrolls: the item loop
+        // with one block in flight (two or four measured slower there)
+        if (p.iters == 1) gemv_mfma_kernel<KIND, MT, FUSED, W, true, 1, true><<<grid, dim3(W * 64), lds_loop, stream>>>(p);
+        else gemv_mfma_kernel<KIND, MT, FUSED, W, false, 1, true><<<grid, dim3(W * 64), lds_loop, stream>>>(p);
+    }
+}
+
+template <int KIND, bool FUSED>
+void launch_tiled_kind(int mt, int w, int ni, const MfmaArgs& p, dim3 grid, size_t lds_loop, size_t lds_pipe,
+                       hipStream_t stream) {
+#define RK_TW(MT)                                                                                   \
+    (w == 16 ? launch_tiled_w<KIND, MT, FUSED, 16>(ni, p, grid, lds_loop, lds_pipe, stream)         \
+             : launch_tiled_w<KIND, MT, FUSED, 8>(ni, p, grid, lds_loop, lds_pipe, stream))
+    if (mt == 4) RK_TW(4);
+    else if (mt == 8) RK_TW(8);
+    else if constexpr (KIND == 4) RK_TW(16);
+#undef RK_TW
+}
+}  // namespace
+
+// Waves per workgroup of a tiled launch. A row's f32 order must not depend on
+// how many projections share the launch (grouped and separate calls agree bit
+// for bit), so where the wave count changes the order it follows from the row
+// length alone: rows of more than 16 blocks take 16 waves from 32 blocks
+// (Llama-3-8B down, 4096 x 14336: 14.3 us against 16.4 with 8) and 8 below
+// (TinyLlama down, 2048 x 5632: 6.9 against 7.4 us with 16). Rows of at most
+// 16 blocks give the same bits with 8 or 16 waves (tile_row_sum), so there the
+// launch's tiles decide: 16 waves for 16-block rows making four or more tiles
+// per CU (Llama-3-8B gate+up, 2 x 14336 x 4096: 13.3 against 18.3 us), else 8.
+// Rows shorter than 8 blocks leave waves without a block; they compute block
+// nb - 1 and drop it, adding +0.0 to the row's sum.
+int tiled_waves(int nb, int64_t tiles, int cus) {
+    if (nb > 16) return nb >= 32 ? 16 : 8;
+    return nb == 16 && tiles >= 4 * int64_t{cus} ? 16 : 8;
+}
+
+// The matrix-core GEMV on tiled weights (p.w[i] each a tiled copy of its
+// member's rows): Q4_K or Q6_K, 1 <= p.m <= gemv_mfma_rows(kind, p.nb). One
+// workgroup per CU at most, each walking its tiles; one block in flight per
+// wave in the item loop, or the pipelined kernel where a wave has at most four
+// items and the launch at most 8 rows.
+int launch_gemv_tiled(int kind, bool fused, GemvParams& p, hipStream_t stream) {
+    if ((kind != 4 && kind != 6) || p.m < 1 || p.m > gemv_mfma_rows(kind, p.nb)) return kStatusInvalid;
+    const int mt = p.m <= 4 ? 4 : p.m <= 8 ? 8 : 16;
+    const int cus = device_cu_count();
+    int64_t tiles = 0;
+    for (int i = 0; i < p.count; ++i) tiles += (p.rows[i] + kTileRows - 1) / kTileRows;
+    const int w = tiled_waves(p.nb, tiles, cus);
+    MfmaArgs ka;
+    if (mfma_args(p, w, ka) != kStatusOk) return kStatusInvalid;
+    const int wgs = std::min(ka.tiles, cus);
+    const dim3 grid(static_cast<unsigned>(wgs));
+    const int ni = (ka.tiles + wgs - 1) / wgs * ka.iters;
+    const size_t lds_loop = gemv_mfma_lds(mt, p.nb, w);
+    // the pipelined kernel keeps each tile's sums in LDS until its stores
+    const size_t lds_pipe = lds_loop + static_cast<size_t>(std::min(ni, 4)) * 64 * (mt / 4) * 4;
+    if (lds_pipe > static_cast<size_t>(kLdsMax)) return kStatusInvalid;
+    if (kind == 4) {
+        if (fused) launch_tiled_kind<4, true>(mt, w, ni, ka, grid, lds_loop, lds_pipe, stream);
+        else launch_tiled_kind<4, false>(mt, w, ni, ka, grid, lds_loop, lds_pipe, stream);
+    } else {
+        if (fused) launch_tiled_kind<6, true>(mt, w, ni, ka, grid, lds_loop, lds_pipe, stream);
+        else launch_tiled_kind<6, false>(mt, w, ni, ka, grid, lds_loop, lds_pipe, stream);
+    }
+    return hipGetLastError() == hipSuccess ? kStatusOk : kStatusExec;
+}
+
+}  // namespace rk

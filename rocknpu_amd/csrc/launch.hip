@@ -248,6 +248,108 @@ extern "C" int rocknpu_hip_gemv_q8_k(uint32_t kind, const uint8_t* w, size_t w_b
     return rk::kStatusOk;
 }
 
+extern "C" size_t rocknpu_hip_gemv_tiled_bytes(uint32_t kind, size_t k, size_t n) {
+    if ((kind != 4 && kind != 6) || k == 0 || k % rk::kQK != 0 || n == 0 || n > INT32_MAX / 2 ||
+        k / rk::kQK > INT_MAX)
+        return 0;
+    return rk::gemv_tiled_bytes(static_cast<int>(kind), static_cast<int64_t>(n), static_cast<int>(k / rk::kQK));
+}
+
+extern "C" int rocknpu_hip_gemv_tile_weights(uint32_t kind, const uint8_t* w, size_t w_bytes, size_t k, size_t n,
+                                             uint8_t* tiled, size_t tiled_bytes, void* stream) {
+    const size_t need = rocknpu_hip_gemv_tiled_bytes(kind, k, n);
+    if (need == 0 || !w || !tiled || tiled_bytes < need) return rk::kStatusInvalid;
+    const size_t bb = rk::block_bytes(static_cast<int>(kind)), nb = k / rk::kQK;
+    if (w_bytes != n * nb * bb || !aligned(w, 2) || !aligned(tiled, 16)) return rk::kStatusInvalid;
+    return rk::launch_gemv_tile_weights(static_cast<int>(kind), w, static_cast<int64_t>(n), static_cast<int>(nb),
+                                        tiled, static_cast<hipStream_t>(stream));
+}
+
+// Measured on the decode shapes (HIP graph, weights rotating through > 1 GB):
+// at one row the raw-row kernels win for TinyLlama o (3.47 against 3.60 us),
+// gate+up (5.15 against 5.30) and down (Q6_K LDS stream, 5.6 against 6.9), and
+// Llama-3-8B down (12.6 against 14.3); the tiled copy wins for Llama-3-8B
+// gate+up (16 blocks per row: 13.3 against 14.4 us) and from two rows on
+// every shape (TinyLlama o at 4 rows 3.63 against 4.19 us, gate+up 5.32
+// against 7.48, down 6.95 against 7.90).
+extern "C" int rocknpu_hip_gemv_tiled_preferred(uint32_t kind, size_t m, size_t k) {
+    if ((kind != 4 && kind != 6) || m == 0 || k == 0 || k % rk::kQK != 0) return 0;
+    return m >= 2 || (kind == 4 && k / rk::kQK >= 16) ? 1 : 0;
+}
+
+namespace {
+// Activation rows per launch of the tiled GEMV: the matrix-core kernel's most.
+size_t tiled_rows_per_launch(uint32_t kind, size_t nb) {
+    return static_cast<size_t>(rk::gemv_mfma_rows(static_cast<int>(kind), static_cast<int>(nb)));
+}
+}  // namespace
+
+extern "C" int rocknpu_hip_gemv_q8_k_tiled(uint32_t kind, const uint8_t* w, size_t w_bytes, size_t k, size_t n,
+                                           const uint8_t* q8k, size_t m, float* out, size_t ldo, void* stream) {
+    if ((kind != 4 && kind != 6) || !w || !q8k || !out || k == 0 || k % rk::kQK != 0 || n == 0 || m == 0 ||
+        ldo < n || n > INT32_MAX / 2)
+        return rk::kStatusInvalid;
+    const size_t nb = k / rk::kQK;
+    if (w_bytes != rocknpu_hip_gemv_tiled_bytes(kind, k, n) || !aligned(w, 16) || !aligned(q8k, 4))
+        return rk::kStatusInvalid;
+    const size_t per_row = nb * rk::kQ8KBytes, chunk = tiled_rows_per_launch(kind, nb);
+    if (chunk == 0) return rk::kStatusInvalid;
+    const hipStream_t s = static_cast<hipStream_t>(stream);
+    for (size_t m0 = 0; m0 < m; m0 += chunk) {
+        rk::GemvParams p{};
+        p.count = 1;
+        p.w[0] = w;
+        p.out[0] = out + m0 * ldo;
+        p.ldo[0] = static_cast<int64_t>(ldo);
+        p.rows[0] = static_cast<int64_t>(n);
+        p.q8k = q8k + m0 * per_row;
+        p.ldx = static_cast<int64_t>(per_row);
+        p.m = static_cast<int>(std::min(chunk, m - m0));
+        p.nb = static_cast<int>(nb);
+        const int st = rk::launch_gemv_tiled(static_cast<int>(kind), false, p, s);
+        if (st != rk::kStatusOk) return st;
+    }
+    return rk::kStatusOk;
+}
+
+extern "C" int rocknpu_hip_gemv_q_f32_tiled(uint32_t kind, size_t count, const uint8_t* const* w,
+                                            const size_t* w_bytes, const size_t* n, size_t k, const float* x,
+                                            size_t ldx, size_t m, float* const* out, const size_t* ldo,
+                                            void* stream) {
+    if ((kind != 4 && kind != 6) || count < 1 || count > static_cast<size_t>(rk::kGemvMaxMembers) || !w ||
+        !w_bytes || !n || !x || !out || !ldo || k == 0 || k % rk::kQK != 0 || m == 0 || ldx < k)
+        return rk::kStatusInvalid;
+    if (ldx % 4 != 0 || !aligned(x, 16)) return rk::kStatusInvalid;
+    const size_t nb = k / rk::kQK, chunk = tiled_rows_per_launch(kind, nb);
+    if (chunk == 0) return rk::kStatusInvalid;
+    size_t total = 0;
+    for (size_t i = 0; i < count; ++i) {
+        if (!w[i] || !out[i] || n[i] == 0 || ldo[i] < n[i] || n[i] > INT32_MAX / 2 ||
+            w_bytes[i] != rocknpu_hip_gemv_tiled_bytes(kind, k, n[i]) || !aligned(w[i], 16))
+            return rk::kStatusInvalid;
+        total += n[i];
+    }
+    if (total > INT_MAX) return rk::kStatusInvalid;
+    const hipStream_t s = static_cast<hipStream_t>(stream);
+    for (size_t m0 = 0; m0 < m; m0 += chunk) {
+        rk::GemvParams p{};
+        p.count = static_cast<int>(count);
+        for (size_t i = 0; i < count; ++i) {
+            p.w[i] = w[i];
+            p.out[i] = out[i] + m0 * ldo[i];
+            p.ldo[i] = static_cast<int64_t>(ldo[i]);
+            p.rows[i] = static_cast<int64_t>(n[i]);
+        }
+        p.x = x + m0 * ldx;
+        p.ldx = static_cast<int64_t>(ldx);
+        p.m = static_cast<int>(std::min(chunk, m - m0));
+        p.nb = static_cast<int>(nb);
+        const int st = rk::launch_gemv_tiled(static_cast<int>(kind), true, p, s);
+        if (st != rk::kStatusOk) return st;
+    }
+    return rk::kStatusOk;
+}
+
 extern "C" int rocknpu_hip_gemv_q_f32(uint32_t kind, size_t count, const uint8_t* const* w, const size_t* w_bytes,
                                       const size_t* n, size_t k, const float* x, size_t ldx, size_t m,
                                       float* const* out, const size_t* ldo, void* stream) {

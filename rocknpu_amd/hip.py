@@ -221,6 +221,67 @@ def gemv_q_f32(kind: int, weights, k: int, ns, x: torch.Tensor, outs=None):
     return outs
 
 
+def gemv_tiled_bytes(kind: int, k: int, n: int) -> int:
+    """Bytes of the tile-interleaved decode copy of an n x k Q4_K/Q6_K weight."""
+    nb = _lib.load().rocknpu_hip_gemv_tiled_bytes(kind, k, n)
+    if nb == 0:
+        raise LaunchError(f"gemv_tiled_bytes: invalid kind {kind} or shape {n} x {k}")
+    return nb
+
+
+def gemv_tile_weights(kind: int, w: torch.Tensor, k: int, n: int, tiled: torch.Tensor | None = None) -> torch.Tensor:
+    """Raw GGUF blocks [n rows of k/256 blocks] -> their tile-interleaved copy
+    (uint8, gemv_tiled_bytes long) for the tiled decode GEMV."""
+    nbytes = gemv_tiled_bytes(kind, k, n)
+    if tiled is None:
+        tiled = torch.empty(nbytes, dtype=torch.uint8, device=w.device)
+    _check(_lib.load().rocknpu_hip_gemv_tile_weights(kind, _ptr(w), w.numel(), k, n, _ptr(tiled), tiled.numel(),
+                                                     _stream()), "gemv_tile_weights")
+    return tiled
+
+
+def gemv_q_f32_tiled(kind: int, weights, k: int, ns, x: torch.Tensor, outs=None):
+    """gemv_q_f32 on tiled copies (gemv_tile_weights) of 1..4 projections."""
+    m = x.shape[0]
+    count = len(weights)
+    if outs is None:
+        outs = [torch.empty((m, n), dtype=torch.float32, device=x.device) for n in ns]
+    w_arr = (ctypes.c_void_p * count)(*[w.data_ptr() for w in weights])
+    b_arr = (ctypes.c_size_t * count)(*[w.numel() for w in weights])
+    n_arr = (ctypes.c_size_t * count)(*ns)
+    o_arr = (ctypes.c_void_p * count)(*[o.data_ptr() for o in outs])
+    l_arr = (ctypes.c_size_t * count)(*[_ld(o) for o in outs])
+    _check(_lib.load().rocknpu_hip_gemv_q_f32_tiled(kind, count, w_arr, b_arr, n_arr, k, _ptr(x), _ld(x), m,
+                                                    o_arr, l_arr, _stream()), "gemv_q_f32_tiled")
+    return outs
+
+
+def gemv_q8_k_tiled(kind: int, w: torch.Tensor, k: int, n: int, q8k: torch.Tensor,
+                    out: torch.Tensor | None = None) -> torch.Tensor:
+    """gemv_q8_k on a tiled copy (gemv_tile_weights)."""
+    m = q8k.shape[0]
+    if out is None:
+        out = torch.empty((m, n), dtype=torch.float32, device=q8k.device)
+    _check(_lib.load().rocknpu_hip_gemv_q8_k_tiled(kind, _ptr(w), w.numel(), k, n, _ptr(q8k), m, _ptr(out),
+                                                   _ld(out), _stream()), "gemv_q8_k_tiled")
+    return out
+
+
+def gemv_tiled_preferred(kind: int, m: int, k: int) -> bool:
+    """Whether an m-row decode GEMV over K = k runs faster on the tiled copy
+    (from two rows; Q4_K rows of 16 or more blocks at one row) than on raw rows."""
+    return bool(_lib.load().rocknpu_hip_gemv_tiled_preferred(kind, m, k))
+
+
+def gemv_decode(kind: int, raw, tiled, k: int, ns, x: torch.Tensor, outs=None):
+    """The fused decode GEMV on whichever copy gemv_tiled_preferred picks:
+    `raw` and `tiled` are the members' raw GGUF rows and their tiled copies
+    (either list may be None when the rule never picks it for this call)."""
+    if gemv_tiled_preferred(kind, x.shape[0], k):
+        return gemv_q_f32_tiled(kind, tiled, k, ns, x, outs=outs)
+    return gemv_q_f32(kind, raw, k, ns, x, outs=outs)
+
+
 def gemv_take_stall() -> bool:
     """Whether a GEMV launch with a bounded wait for the activations (the fused
     lane-per-block kernel, the Q6_K stream kernel) gave up since the last call

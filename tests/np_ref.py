@@ -215,3 +215,35 @@ def tie_rows(kind: int, n: int, k: int, seed: int) -> np.ndarray:
         blk[:, 0, 0] &= 0xF0    # value 0: low nibble 0
         blk[:, 0, 128] &= 0xFC  # and high bits 0, so q = -32
     return np.ascontiguousarray(blk.reshape(-1))
+
+
+def tile_weights(kind: int, blocks: np.ndarray, n: int, k: int) -> np.ndarray:
+    """The decode cache's tile-interleaved copy of n rows of k/256 blocks,
+    built with array reshapes (no per-byte index arithmetic): tiles of 16 rows
+    (zero rows past n), each tile's blocks in order, and for tile t, block b:
+    Q4_K: the 16 rows' 16-byte headers, then for lane l = 16 q + r the quant
+    bytes 32 j + 8 q .. + 7 of row r, j = 0..3;
+    Q6_K: the 16 rows' 16 scale bytes, their 2-byte d, then for lane
+    l = 16 q + r the ql runs 64 h + 32 i + 8 q (order 2 h + i) and the qh runs
+    128 + 32 h + 8 q, 8 bytes each."""
+    bb = 144 if kind == 4 else 210
+    nb = k // QK
+    tiles = -(-n // 16)
+    b = np.zeros((tiles * 16, nb, bb), np.uint8)
+    b[:n] = blocks.reshape(n, nb, bb)
+    b = b.reshape(tiles, 16, nb, bb).transpose(0, 2, 1, 3)  # [tile][block][row][byte]
+    if kind == 4:
+        head = b[..., :16].reshape(tiles, nb, 256)
+        qs = b[..., 16:].reshape(tiles, nb, 16, 4, 4, 8)         # [row][j][q][8]
+        lanes = qs.transpose(0, 1, 4, 2, 3, 5).reshape(tiles, nb, 2048)  # [q][row][j][8]
+        out = np.concatenate([head, lanes], axis=2)
+    else:
+        sc = b[..., 192:208].reshape(tiles, nb, 256)
+        d = b[..., 208:210].reshape(tiles, nb, 32)
+        ql = b[..., :128].reshape(tiles, nb, 16, 2, 2, 4, 8)     # [row][h][i][q][8]
+        ql = ql.transpose(0, 1, 5, 2, 3, 4, 6).reshape(tiles, nb, 4, 16, 32)  # [q][row][h i 8]
+        qh = b[..., 128:192].reshape(tiles, nb, 16, 2, 4, 8)     # [row][h][q][8]
+        qh = qh.transpose(0, 1, 4, 2, 3, 5).reshape(tiles, nb, 4, 16, 16)     # [q][row][h 8]
+        lanes = np.concatenate([ql, qh], axis=4).reshape(tiles, nb, 3072)
+        out = np.concatenate([sc, d, lanes], axis=2)
+    return np.ascontiguousarray(out).reshape(-1)

@@ -103,3 +103,35 @@ def test_gemv_stall_report_host_side():
     assert lib.rocknpu_hip_gemv_test_stall(-1) == -1
     assert lib.rocknpu_hip_gemv_test_stall(0) == 0
     assert lib.rocknpu_hip_gemv_take_stall() == 0
+
+
+def test_tiled_decode_layout_host_side():
+    """Bytes of the tiled decode copies (whole 16-row tiles of k/256 blocks), and
+    the tiled entries' argument checks, all answered on the host."""
+    lib = _lib.load()
+    assert lib.rocknpu_hip_gemv_tiled_bytes(4, 2048, 2048) == 2048 * 8 * 144
+    assert lib.rocknpu_hip_gemv_tiled_bytes(6, 5632, 2048) == 2048 * 22 * 210
+    assert lib.rocknpu_hip_gemv_tiled_bytes(4, 2048, 17) == 32 * 8 * 144   # ragged rows pad to a tile
+    assert lib.rocknpu_hip_gemv_tiled_bytes(6, 256, 1) == 16 * 210
+    assert lib.rocknpu_hip_gemv_tiled_bytes(5, 2048, 16) == 0               # no Q5_K GEMV
+    assert lib.rocknpu_hip_gemv_tiled_bytes(4, 100, 16) == 0                # K not a multiple of 256
+    assert lib.rocknpu_hip_gemv_tiled_bytes(4, 256, 0) == 0
+    p = ctypes.c_void_p(1 << 20)  # never dereferenced
+    raw = 16 * 144
+    tb = lib.rocknpu_hip_gemv_tiled_bytes(4, 256, 16)
+    assert lib.rocknpu_hip_gemv_tile_weights(4, p, raw, 256, 16, p, tb - 1, None) == -1     # copy too small
+    assert lib.rocknpu_hip_gemv_tile_weights(4, p, raw - 144, 256, 16, p, tb, None) == -1   # raw bytes != n rows
+    assert lib.rocknpu_hip_gemv_tile_weights(4, p, raw, 256, 16, ctypes.c_void_p((1 << 20) + 8), tb, None) == -1
+    assert lib.rocknpu_hip_gemv_tile_weights(4, None, raw, 256, 16, p, tb, None) == -1
+    out = ctypes.c_void_p(1 << 21)
+    assert lib.rocknpu_hip_gemv_q8_k_tiled(4, p, 17 * 144, 256, 17, p, 1, out, 17, None) == -1  # raw size, not tiled
+    assert lib.rocknpu_hip_gemv_q8_k_tiled(4, p, tb, 256, 16, p, 1, out, 8, None) == -1     # ldo < n
+    w_arr = (ctypes.c_void_p * 1)(1 << 20)
+    b_arr = (ctypes.c_size_t * 1)(tb)
+    n_arr = (ctypes.c_size_t * 1)(16)
+    o_arr = (ctypes.c_void_p * 1)(1 << 21)
+    l_arr = (ctypes.c_size_t * 1)(16)
+    assert lib.rocknpu_hip_gemv_q_f32_tiled(4, 1, w_arr, b_arr, n_arr, 256, p, 255, 1, o_arr, l_arr, None) == -1
+    assert lib.rocknpu_hip_gemv_q_f32_tiled(4, 5, w_arr, b_arr, n_arr, 256, p, 256, 1, o_arr, l_arr, None) == -1
+    b_arr[0], n_arr[0], l_arr[0] = 17 * 144, 17, 17  # raw size of 17 rows, not the tiled 32
+    assert lib.rocknpu_hip_gemv_q_f32_tiled(4, 1, w_arr, b_arr, n_arr, 256, p, 256, 1, o_arr, l_arr, None) == -1
