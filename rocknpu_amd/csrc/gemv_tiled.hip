@@ -23,7 +23,48 @@ namespace {
 // sits among the loads either. A row's arithmetic and f32 order are those of
 // gemv_mfma_kernel (wave g adds blocks g, g + W, .. in order; the W partial
 // sums are added in wave order), so the results are the same bits.
-template <int KIND, int MT, bool FUSED, int W, bool AREG, int NI, int D>
+// The activation blocks a wave owns (block indices wave + W * it, it < IT,
+// of rows < m) with every f32 load issued up front: later block indices no
+// longer wait, one after another, for loads issued while the one before is
+// quantised. Past `iters` (or nb, or m) the loads re-read a valid block and
+// nothing is quantised from them; Q8_K rows are copied as OwnedActs does.
+template <int MT, int W, bool FUSED, int IT>
+struct AllActs {
+    static constexpr int QP = MT / 4;
+    float4 xf[FUSED ? IT : 1][FUSED ? QP : 1][4];
+    __device__ __forceinline__ void first(const MfmaArgs& p, int wave) {
+        if constexpr (FUSED) {
+            const int qslot = (threadIdx.x & 63) >> 4;
+#pragma unroll
+            for (int it = 0; it < IT; ++it)
+#pragma unroll
+                for (int i = 0; i < QP; ++i)
+                    load_x16(p.x, p.ldx, p.nb, min(4 * i + qslot, p.m - 1) * p.nb + min(wave + W * it, p.nb - 1),
+                             xf[it][i]);
+        }
+    }
+    __device__ __forceinline__ void stage(const MfmaArgs& p, int wave, const ActLds<MT>& act) {
+        if constexpr (FUSED) {
+            const int qslot = (threadIdx.x & 63) >> 4;
+#pragma unroll
+            for (int it = 0; it < IT; ++it) {
+                const int b = wave + W * it;
+#pragma unroll
+                for (int i = 0; i < QP; ++i) {
+                    const int mi = 4 * i + qslot;
+                    if (it < p.iters && mi < p.m && b < p.nb)
+                        quantize_block(xf[it][i], act.quants(b, mi), reinterpret_cast<int16_t*>(act.bsums(b, mi)),
+                                       act.d(b, mi));
+                }
+            }
+        } else {
+            OwnedActs<MT, W, false> o;
+            o.stage(p, wave, act);
+        }
+    }
+};
+
+template <int KIND, int MT, bool FUSED, int W, bool AREG, int NI, int D, int IT>
 __global__ __launch_bounds__(W * 64) void gemv_tiled_kernel(const MfmaArgs p) {
     constexpr int BB = block_bytes(KIND);
     constexpr int NR = MT / 4;
@@ -53,13 +94,22 @@ __global__ __launch_bounds__(W * 64) void gemv_tiled_kernel(const MfmaArgs p) {
         k.load_tiled(w + (static_cast<int64_t>(to.row0 / kTileRows) * nb + b) * (kTileRows * BB), lane);
     };
 
+    // The activations of the wave's IT = iters block indices: with one, as
+    // gemv_mfma_kernel loads them; with two to four, all loaded up front
+    // (TinyLlama down, 2048 x 5632, three per wave: 6.93 -> 6.72 us at one row;
+    // Llama-3-8B down, 4096 x 14336, four per wave: 14.4 -> 13.4 us).
+    static_assert(AREG == (IT == 1), "one block index per wave keeps its operands in registers");
     OwnedActs<MT, W, FUSED> owned;
-    owned.first(p, wave);
-    // every wave's activation loads ahead of any weight load (gemv_mfma_kernel)
+    AllActs<MT, W, FUSED, IT> all;
+    if constexpr (IT == 1) owned.first(p, wave);
+    else all.first(p, wave);
+    // every wave's activation loads ahead of any weight load (gemv_mfma_kernel;
+    // without this barrier TinyLlama o takes 4.1 instead of 3.6 us)
     __builtin_amdgcn_s_barrier();
     Piece buf[D];
     load_item(0, buf[0]);
-    owned.template stage<AREG>(p, wave, act);
+    if constexpr (IT == 1) owned.template stage<true>(p, wave, act);
+    else all.stage(p, wave, act);
 #pragma unroll
     for (int j = 1; j < D; ++j) load_item(j, buf[j]);
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
@@ -196,26 +246,35 @@ int launch_gemv_tile_weights(int kind, const uint8_t* src, int64_t n, int nb, ui
 }
 
 namespace {
-// Pipelined kernel, NI items per wave: two in flight for two or three items
-// (TinyLlama gate+up, 2 x 5632 x 2048, three tiles per workgroup at 4 rows:
-// 5.32 us against 5.51 with one; TinyLlama down, 2048 x 5632 on 8 waves, three
-// blocks per wave: 6.95 against 7.46), one for four (Llama-3-8B down, 4096 x
-// 14336 on 16 waves: 14.8 against 14.8-15.1 us with two or four).
-template <int KIND, int MT, bool FUSED, int W, bool AREG>
-void launch_pipe(int ni, const MfmaArgs& p, dim3 grid, size_t lds, hipStream_t stream) {
+// Pipelined kernel, NI items per wave (ni tiles of iters block indices): two
+// in flight for two or three items (TinyLlama gate+up, 2 x 5632 x 2048, three
+// tiles per workgroup at 4 rows: 5.32 us against 5.51 with one and 5.42 with
+// three; TinyLlama down, 2048 x 5632 on 8 waves, three blocks per wave: 6.95
+// against 7.46 with one), one for four (Llama-3-8B down, 4096 x 14336 on 16
+// waves: 14.8 against 14.8-15.1 us with two or four).
+template <int KIND, int MT, bool FUSED, int W>
+void launch_pipe(int ni, int iters, const MfmaArgs& p, dim3 grid, size_t lds, hipStream_t stream) {
     const dim3 block(W * 64);
-    if (ni == 1) gemv_tiled_kernel<KIND, MT, FUSED, W, AREG, 1, 1><<<grid, block, lds, stream>>>(p);
-    else if (ni == 2) gemv_tiled_kernel<KIND, MT, FUSED, W, AREG, 2, 2><<<grid, block, lds, stream>>>(p);
-    else if (ni == 3) gemv_tiled_kernel<KIND, MT, FUSED, W, AREG, 3, 2><<<grid, block, lds, stream>>>(p);
-    else gemv_tiled_kernel<KIND, MT, FUSED, W, AREG, 4, 1><<<grid, block, lds, stream>>>(p);
+    if (iters == 1) {
+        if (ni == 1) gemv_tiled_kernel<KIND, MT, FUSED, W, true, 1, 1, 1><<<grid, block, lds, stream>>>(p);
+        else if (ni == 2) gemv_tiled_kernel<KIND, MT, FUSED, W, true, 2, 2, 1><<<grid, block, lds, stream>>>(p);
+        else if (ni == 3) gemv_tiled_kernel<KIND, MT, FUSED, W, true, 3, 2, 1><<<grid, block, lds, stream>>>(p);
+        else gemv_tiled_kernel<KIND, MT, FUSED, W, true, 4, 1, 1><<<grid, block, lds, stream>>>(p);
+    } else if (iters == 2) {
+        if (ni == 2) gemv_tiled_kernel<KIND, MT, FUSED, W, false, 2, 2, 2><<<grid, block, lds, stream>>>(p);
+        else gemv_tiled_kernel<KIND, MT, FUSED, W, false, 4, 1, 2><<<grid, block, lds, stream>>>(p);
+    } else if (iters == 3) {
+        gemv_tiled_kernel<KIND, MT, FUSED, W, false, 3, 2, 3><<<grid, block, lds, stream>>>(p);
+    } else {
+        gemv_tiled_kernel<KIND, MT, FUSED, W, false, 4, 1, 4><<<grid, block, lds, stream>>>(p);
+    }
 }
 
 template <int KIND, int MT, bool FUSED, int W>
 void launch_tiled_w(int ni, const MfmaArgs& p, dim3 grid, size_t lds_loop, size_t lds_pipe, hipStream_t stream) {
     if constexpr (MT <= 8) {
         if (ni <= 4) {
-            if (p.iters == 1) launch_pipe<KIND, MT, FUSED, W, true>(ni, p, grid, lds_pipe, stream);
-            else launch_pipe<KIND, MT, FUSED, W, false>(ni, p, grid, lds_pipe, stream);
+            launch_pipe<KIND, MT, FUSED, W>(ni, p.iters, p, grid, lds_pipe, stream);
             return;
         }
     }
