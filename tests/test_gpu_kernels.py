@@ -279,6 +279,7 @@ def _gemv_check(kind, n, k, m, index):
         assert np.array_equal(msum[mi], rms), f"msum row {mi}"
         err = np.abs(out[mi].astype(np.float64) - ref[mi])
         assert np.all(err <= 1e-5 * mag), f"row {mi}: max err/mag {np.max(err / mag)}"
+        assert err.max() <= 1e-5 * np.abs(ref[mi]).max(), "normwise max|err| / max|y|"
 
 
 @pytest.mark.parametrize("kind,n,k,m", [
@@ -309,6 +310,7 @@ def test_gemv_q4k_multi_row(n, k, m):
         _, _, mag = orc.gemv_block_sums(4, w, k, n, q8[mi])
         err = np.abs(got[mi].astype(np.float64) - ref[mi])
         assert np.all(err <= 1e-5 * mag), f"row {mi}: max err/mag {np.max(err / mag)}"
+        assert err.max() <= 1e-5 * np.abs(ref[mi]).max(), "normwise max|err| / max|y|"
 
 
 @pytest.mark.parametrize("n,k,m", [(16, 256, 5), (40, 1024, 4), (2048, 5632, 6), (130, 5632, 5), (300, 2048, 8),
@@ -332,6 +334,7 @@ def test_gemv_q6k_multi_row(n, k, m):
         _, _, mag = orc.gemv_block_sums(6, w, k, n, q8[mi])
         err = np.abs(got[mi].astype(np.float64) - ref[mi])
         assert np.all(err <= 1e-5 * mag), f"row {mi}: max err/mag {np.max(err / mag)}"
+        assert err.max() <= 1e-5 * np.abs(ref[mi]).max(), "normwise max|err| / max|y|"
 
 
 def test_gemv_m_chunking():
@@ -373,7 +376,9 @@ def test_gemv_fused_grouped(kind, ns, k, m):
         ref = orc.gemv_q8_k(kind, w, k, n, q8_ref, threads=8)
         for mi in range(m):
             _, _, mag = orc.gemv_block_sums(kind, w, k, n, q8_ref[mi])
-            assert np.all(np.abs(got[mi].astype(np.float64) - ref[mi]) <= 1e-5 * mag)
+            err = np.abs(got[mi].astype(np.float64) - ref[mi])
+            assert np.all(err <= 1e-5 * mag)
+            assert err.max() <= 1e-5 * np.abs(ref[mi]).max(), "normwise max|err| / max|y|"
 
 
 @pytest.mark.parametrize("m", [1, 4])
@@ -423,4 +428,6 @@ def test_gemv_q6_stream_stall(m):
     ref = orc.gemv_q8_k(kind, w, k, n, q8_ref, threads=8)
     for mi in range(m):
         _, _, mag = orc.gemv_block_sums(kind, w, k, n, q8_ref[mi])
-        assert np.all(np.abs(got[mi].astype(np.float64) - ref[mi]) <= 1e-5 * mag)
+        err = np.abs(got[mi].astype(np.float64) - ref[mi])
+        assert np.all(err <= 1e-5 * mag)
+        assert err.max() <= 1e-5 * np.abs(ref[mi]).max(), "normwise max|err| / max|y|"

@@ -11,10 +11,11 @@ them over; each node's output is checked bit for bit against the oracle's W8A8
 route on sampled activation rows (rows are independent: per-token quantisation,
 one i32 dot product per output). The launch layer's repack and int32
 accumulators are checked bit-exact on the largest shapes (the 128256 x 2048 Q6_K
-head, the 4096 x 14336 x 4096 GEMM) on sampled row blocks. Batched decode on
-Llama-3-8B gate+up (2 x 14336 x 4096) runs through both routes: W8A8 (exact) and
-the Q8_K GEMV (within 1e-5 of the sum of the block terms' magnitudes, and of
-max |y| per row).
+head, the Llama-3-8B 128256 x 4096 Q6_K head, the 4096 x 14336 x 4096 GEMM) on
+sampled row blocks. Batched decode on every Llama-3-8B projection (q/k/v, o,
+gate+up, the Q6_K down) runs through both routes: W8A8 (exact) and the Q8_K
+GEMV (within 1e-5 of the sum of the block terms' magnitudes, and of max |y|
+per row).
 
 Activations of the nodes are distinct windows of one random pool (distinct
 pointers, as distinct graph tensors are), so the routing groups only what a
@@ -222,37 +223,79 @@ def test_llama3_8b_prefill_4096_gemm_i32_exact(kind, n, k):
     assert np.array_equal(_bits(out[idx].cpu().numpy()), _bits(orc.rescale(rc, ras, rsc)))
 
 
+def test_llama3_8b_head_repack_and_i32_exact():
+    """The Llama-3-8B output head (Q6_K 128256 x 4096, the vocabulary head the
+    reference leaves on the CPU, ggml-rocknpu.cpp:644-650): the GPU repack
+    bit-exact against the oracle's on every row, and the 4096-token GEMM's int32
+    accumulators and f32 outputs exact on four 16-row blocks (one per quarter
+    of M)."""
+    vocab, hidden, m = 128256, 4096, 4096
+    blocks = synth.kquant(6, vocab, hidden, index=47000)
+    a = synth.activations(m, hidden, index=47001)
+    print("llama3-8b head repack", flush=True)
+    w8, wsc = hip.repack_w8(6, torch.from_numpy(blocks).to("cuda"), hidden, vocab)
+    a8, asc = hip.quantize_a8(torch.from_numpy(a).to("cuda"))
+    c = torch.empty((m, vocab), dtype=torch.int32, device="cuda")
+    out = hip.gemm_w8a8(a8, asc, w8, wsc, out_i32=c)
+    torch.cuda.synchronize()
+    rw8, rsc = orc.repack_w8(6, blocks, hidden, vocab, threads=THREADS)
+    assert np.array_equal(w8.cpu().numpy(), rw8)
+    assert np.array_equal(_bits(wsc.cpu().numpy()), _bits(rsc))
+    del blocks
+    g = np.random.default_rng(47002)
+    rows = np.concatenate([np.arange(b, b + 16) for b in
+                           [0] + [q * 1024 + 16 * int(g.integers(0, 64)) for q in (1, 2)] + [m - 16]])
+    ra8, ras = orc.quantize_a8(a[rows])
+    idx = torch.from_numpy(rows).to("cuda")
+    assert np.array_equal(a8[idx].cpu().numpy(), ra8)
+    rc = orc.gemm_i32(ra8, rw8, threads=THREADS)
+    assert np.array_equal(c[idx].cpu().numpy(), rc)
+    assert np.array_equal(_bits(out[idx].cpu().numpy()), _bits(orc.rescale(rc, ras, rsc)))
+
+
 def test_llama3_8b_prefill_layer_sequence():
     """Llama-3-8B at 4096 tokens: two layers' projections (q/k/v grouped, o,
     gate/up grouped, down) through one routing call, sampled rows exact."""
     _prefill_sequence("llama3_8b", 4096, 2, False, seed=45000)
 
 
+# Llama-3-8B decode projections: (name, kinds, rows per member, K)
+L3_DECODE = {
+    "qkv": ((4, 4, 4), (4096, 1024, 1024), 4096),
+    "o": ((4,), (4096,), 4096),
+    "gate_up": ((4, 4), (14336, 14336), 4096),
+    "down": ((6,), (4096,), 14336),
+}
+
+
+@pytest.mark.parametrize("proj", list(L3_DECODE))
 @pytest.mark.parametrize("m", [1, 8, 32, 64])
-def test_llama3_8b_batched_decode_both_routes(m):
-    """Decode at batch 1, 8, 32, 64 on Llama-3-8B gate+up (2 x 14336 x 4096): the W8A8 route
-    (concat call) and the Q8_K GEMV route (grouped call), on sampled rows: the
-    first exact, the second within 1e-5 of the block terms' magnitude and of
-    max |y| per row."""
-    n, k = 14336, 4096
-    ws = [synth.kquant(4, n, k, index=46000 + i) for i in range(2)]
-    x = synth.activations(m, k, index=46010 + m)
-    print(f"llama3-8b batched decode m={m}", flush=True)
+def test_llama3_8b_batched_decode_both_routes(proj, m):
+    """Decode at batch 1, 8, 32, 64 on every Llama-3-8B projection (q/k/v and
+    gate+up as one call each, o, and the Q6_K down): the W8A8 route (concat
+    call) and the Q8_K GEMV route (grouped call, the decode cache's tiled
+    copies from two rows), on sampled rows: the first exact, the second within
+    1e-5 of the block terms' magnitude and of max |y| per row."""
+    kinds, ns, k = L3_DECODE[proj]
+    ws = [synth.kquant(kind, n, k, index=46000 + 10 * list(L3_DECODE).index(proj) + i)
+          for i, (kind, n) in enumerate(zip(kinds, ns))]
+    x = synth.activations(m, k, index=46010 + m + k)
+    print(f"llama3-8b batched decode {proj} m={m}", flush=True)
     with Context() as ctx:
-        w8a8 = [np.full((m, n), np.nan, np.float32) for _ in ws]
-        assert ctx.matmul_q_concat(ws, [4, 4], [n, n], x, w8a8, k) == STATUS_OK
-        q8route = [np.full((m, n), np.nan, np.float32) for _ in ws]
-        assert ctx.matmul_q_q8k_group(ws, [4, 4], [n, n], x, q8route, k) == STATUS_OK
+        w8a8 = [np.full((m, n), np.nan, np.float32) for n in ns]
+        assert ctx.matmul_q_concat(ws, list(kinds), list(ns), x, w8a8, k) == STATUS_OK
+        q8route = [np.full((m, n), np.nan, np.float32) for n in ns]
+        assert ctx.matmul_q_q8k_group(ws, list(kinds), list(ns), x, q8route, k) == STATUS_OK
     rows = _sample_rows(m, 8, 46020 + m)
     q8 = orc.quantize_q8_k(x[rows])
     worst = 0.0
-    for w, o1, o2 in zip(ws, w8a8, q8route):
-        _check_w8a8_rows(4, w, k, n, x, o1, rows, f"w8a8 m={m}")
-        ref = orc.gemv_q8_k(4, w, k, n, q8, threads=THREADS)
+    for kind, n, w, o1, o2 in zip(kinds, ns, ws, w8a8, q8route):
+        _check_w8a8_rows(kind, w, k, n, x, o1, rows, f"w8a8 {proj} m={m}")
+        ref = orc.gemv_q8_k(kind, w, k, n, q8, threads=THREADS)
         for i, mi in enumerate(rows):
-            _, _, mag = orc.gemv_block_sums(4, w, k, n, q8[i])
+            _, _, mag = orc.gemv_block_sums(kind, w, k, n, q8[i])
             err = np.abs(o2[mi].astype(np.float64) - ref[i])
-            assert np.all(err <= 1e-5 * mag), mi
+            assert np.all(err <= 1e-5 * mag), (proj, mi)
             worst = max(worst, float(err.max() / np.abs(ref[i]).max()))
-    print(f"q8k route m={m}: max |err| / max |y| = {worst:.3g}", flush=True)
+    print(f"q8k route {proj} m={m}: max |err| / max |y| = {worst:.3g}", flush=True)
     assert worst <= 1e-5

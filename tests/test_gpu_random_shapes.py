@@ -78,6 +78,7 @@ def test_fused_gemv_random_shape(kind, ns, k, m):
             _, _, mag = orc.gemv_block_sums(kind, w, k, n, q8[mi])
             err = np.abs(got[mi].astype(np.float64) - ref[mi])
             assert np.all(err <= 1e-5 * mag), f"member n={n} row {mi}: max err/mag {np.max(err / mag)}"
+            assert err.max() <= 1e-5 * np.abs(ref[mi]).max(), "normwise max|err| / max|y|"
 
 
 def _capi_cases(count=24, seed=99):
