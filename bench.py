@@ -780,8 +780,8 @@ def main():
                    "layers": synth.TINYLLAMA_LAYERS, "m": [1, 4], "launches_per_step": n_gemv,
                    "bytes_per_step": step_bytes},
         "roofline": {"bound": "hbm", "kernel": "Q4_K x Q8_K decode GEMV at M=4 on the matrix cores over the "
-                                               "tiled copies, fused Q8_K quant (gemv_tiled_kernel<4,4,true,8,true,1,1> "
-                                               "for q/k/v and o, gemv_tiled_kernel<4,4,true,8,true,3,2> for "
+                                               "tiled copies, fused Q8_K quant (gemv_tiled_kernel<4,4,true,8,true,1,1,1> "
+                                               "for q/k/v and o, gemv_tiled_kernel<4,4,true,8,true,3,2,1> for "
                                                "gate+up), the 66 Q4_K launches of a step",
                      "achieved": round(m4_achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(m4_achieved / HBM_PEAK_GBS, 4), "traffic": measured_traffic("gemv_q4k_m4"),
@@ -792,7 +792,7 @@ def main():
                         "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": measured_traffic("gemv_q4k"),
                         "avg_launch_us": round(q4_us, 3), "bytes_per_launch": q4_bpl},
         "decode_q6k_down": {"kernel": "Q6_K x Q8_K decode GEMV with fused Q8_K quant (M=1: gemv_q6_stream_kernel "
-                                      "on raw rows; M=4: gemv_tiled_kernel<6,4,true,8,false,3,2> on the tiled "
+                                      "on raw rows; M=4: gemv_tiled_kernel<6,4,true,8,false,3,2,3> on the tiled "
                                       "copies), the 22 down launches of a step at each M", "peak": HBM_PEAK_GBS,
                             "unit": "GB/s",
                             **q6},
