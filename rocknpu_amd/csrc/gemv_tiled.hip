@@ -43,20 +43,22 @@ struct AllActs {
                              xf[it][i]);
         }
     }
+    // the wave's block index `it` (< IT, a constant once unrolled) into LDS
+    __device__ __forceinline__ void quantise_one(const MfmaArgs& p, int wave, const ActLds<MT>& act, int it) {
+        const int qslot = (threadIdx.x & 63) >> 4;
+        const int b = wave + W * it;
+#pragma unroll
+        for (int i = 0; i < QP; ++i) {
+            const int mi = 4 * i + qslot;
+            if (it < p.iters && mi < p.m && b < p.nb)
+                quantize_block(xf[it][i], act.quants(b, mi), reinterpret_cast<int16_t*>(act.bsums(b, mi)),
+                               act.d(b, mi));
+        }
+    }
     __device__ __forceinline__ void stage(const MfmaArgs& p, int wave, const ActLds<MT>& act) {
         if constexpr (FUSED) {
-            const int qslot = (threadIdx.x & 63) >> 4;
 #pragma unroll
-            for (int it = 0; it < IT; ++it) {
-                const int b = wave + W * it;
-#pragma unroll
-                for (int i = 0; i < QP; ++i) {
-                    const int mi = 4 * i + qslot;
-                    if (it < p.iters && mi < p.m && b < p.nb)
-                        quantize_block(xf[it][i], act.quants(b, mi), reinterpret_cast<int16_t*>(act.bsums(b, mi)),
-                                       act.d(b, mi));
-                }
-            }
+            for (int it = 0; it < IT; ++it) quantise_one(p, wave, act, it);
         } else {
             OwnedActs<MT, W, false> o;
             o.stage(p, wave, act);
@@ -64,7 +66,7 @@ struct AllActs {
     }
 };
 
-template <int KIND, int MT, bool FUSED, int W, bool AREG, int NI, int D, int IT>
+template <int KIND, int MT, bool FUSED, int W, bool AREG, int NI, int D, int IT, bool LAZY = false>
 __global__ __launch_bounds__(W * 64) void gemv_tiled_kernel(const MfmaArgs p) {
     constexpr int BB = block_bytes(KIND);
     constexpr int NR = MT / 4;
@@ -108,7 +110,13 @@ __global__ __launch_bounds__(W * 64) void gemv_tiled_kernel(const MfmaArgs p) {
     __builtin_amdgcn_s_barrier();
     Piece buf[D];
     load_item(0, buf[0]);
+    // LAZY: only block index 0 quantised here, block index i (< IT) just
+    // before item i, the first that reads it, so item 0's terms wait for one
+    // quantisation instead of IT (each wave quantises and reads only its own
+    // block indices, so no barrier is needed between)
+    constexpr bool lazy = LAZY && FUSED && IT > 1;
     if constexpr (IT == 1) owned.template stage<true>(p, wave, act);
+    else if constexpr (lazy) all.quantise_one(p, wave, act, 0);
     else all.stage(p, wave, act);
 #pragma unroll
     for (int j = 1; j < D; ++j) load_item(j, buf[j]);
@@ -127,6 +135,12 @@ __global__ __launch_bounds__(W * 64) void gemv_tiled_kernel(const MfmaArgs p) {
     for (int lr = 0; lr < NR; ++lr) acc[lr] = 0.0f;
 #pragma unroll
     for (int i = 0; i < NI; ++i) {
+        if constexpr (lazy) {
+            if (i >= 1 && i < IT) {  // block index i, first used by item i
+                all.quantise_one(p, wave, act, i);
+                asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+            }
+        }
         const int kt = i / iters, it = i - kt * iters;
         const int b = wave + W * it;
         if constexpr (!AREG) {
@@ -261,8 +275,10 @@ void launch_pipe(int ni, int iters, const MfmaArgs& p, dim3 grid, size_t lds, hi
         else if (ni == 3) gemv_tiled_kernel<KIND, MT, FUSED, W, true, 3, 2, 1><<<grid, block, lds, stream>>>(p);
         else gemv_tiled_kernel<KIND, MT, FUSED, W, true, 4, 1, 1><<<grid, block, lds, stream>>>(p);
     } else if (iters == 2) {
-        if (ni == 2) gemv_tiled_kernel<KIND, MT, FUSED, W, false, 2, 2, 2><<<grid, block, lds, stream>>>(p);
-        else gemv_tiled_kernel<KIND, MT, FUSED, W, false, 4, 1, 2><<<grid, block, lds, stream>>>(p);
+        // block index 1 quantised after item 0's terms (Llama-3-8B q/o, 4096 x
+        // 4096: 5.37 -> 5.19 us; q/k/v, 6144 x 4096: 7.17 -> 6.76 us)
+        if (ni == 2) gemv_tiled_kernel<KIND, MT, FUSED, W, false, 2, 2, 2, true><<<grid, block, lds, stream>>>(p);
+        else gemv_tiled_kernel<KIND, MT, FUSED, W, false, 4, 1, 2, true><<<grid, block, lds, stream>>>(p);
     } else if (iters == 3) {
         gemv_tiled_kernel<KIND, MT, FUSED, W, false, 3, 2, 3><<<grid, block, lds, stream>>>(p);
     } else {
@@ -272,8 +288,13 @@ void launch_pipe(int ni, int iters, const MfmaArgs& p, dim3 grid, size_t lds, hi
 
 template <int KIND, int MT, bool FUSED, int W>
 void launch_tiled_w(int ni, const MfmaArgs& p, dim3 grid, size_t lds_loop, size_t lds_pipe, hipStream_t stream) {
+    // Eight rows on 16 waves with three or four block indices a wave: the
+    // activations loaded up front do not fit the 128 registers of a 1024-lane
+    // workgroup and spill (Llama-3-8B down, 4096 x 14336, eight rows: 33.1 us
+    // against 20.0 in the item loop)
     if constexpr (MT <= 8) {
-        if (ni <= 4) {
+        const bool spills = MT == 8 && W == 16 && p.iters >= 3;
+        if (ni <= 4 && !spills) {
             launch_pipe<KIND, MT, FUSED, W>(ni, p.iters, p, grid, lds_pipe, stream);
             return;
         }

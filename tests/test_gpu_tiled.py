@@ -62,17 +62,22 @@ def test_tile_weights_equal_the_restatement(kind, k, n):
 
 
 # (kind, k, member rows, activation rows): TinyLlama o, qkv, gate+up and down
-# (one, one, three and three items per wave), Llama-3-8B gate+up (16 waves,
-# seven tiles per workgroup: the item loop) and down (16 waves, four blocks
-# per wave), rows shorter than eight blocks, a single block, ragged N; 9-16
-# activation rows run the item loop on 16-row register tiles.
+# (one, one, three and three items per wave), Llama-3-8B q/o and q/k/v (two
+# block indices per wave, the second quantised after the first item), gate+up
+# (16 waves, seven tiles per workgroup: the item loop) and down (16 waves, four
+# blocks per wave; at 5-8 rows the item loop), rows shorter than eight blocks,
+# a single block, ragged N; 9-16 activation rows run the item loop on 16-row
+# register tiles.
 CASES = [
     (4, 2048, [2048], (1, 2, 3, 4, 8, 16)),
     (4, 2048, [2048, 256, 256], (2, 4, 5, 9)),
     (4, 2048, [5632, 5632], (2, 4, 8)),
     (6, 5632, [2048], (1, 2, 4, 6, 8)),
     (4, 4096, [14336, 14336], (1, 4)),
-    (6, 14336, [4096], (1, 4)),
+    (4, 4096, [4096], (1, 2, 4, 8)),
+    (4, 4096, [4096, 1024, 1024], (3, 6)),
+    (6, 4096, [1000], (2, 7)),
+    (6, 14336, [4096], (1, 4, 5, 8)),
     (4, 512, [100], (1, 3)),
     (6, 256, [40], (1, 2)),
     (4, 2048, [1000, 17], (4, 13)),
