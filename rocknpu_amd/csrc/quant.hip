@@ -14,6 +14,8 @@
 // d = 1/iscale. An all-zero block stores d = 0, zero quants and zero bsums.
 #include "common.h"
 
+#include <algorithm>
+
 namespace rk {
 namespace {
 
@@ -103,54 +105,56 @@ __global__ __launch_bounds__(kA8Threads) void quantize_a8_kernel(const float* __
 }
 
 // The same for rows of up to 16 * 1024 values with k, lda and k_pad multiples
-// of 4 and 16-byte aligned bases: each thread keeps its R float4 of the row in
-// registers, so the row is read once, not once per pass. The max is
-// order-independent and every value takes the same quant_sym_rcp, so the output
-// is bit-identical to quantize_a8_kernel's.
+// of 4 and 16-byte aligned bases, one row per workgroup of blockDim.x threads
+// (whole waves, at most 1024): each thread keeps its R float4 of the row
+// (float4 t + blockDim.x * j) in registers, so the row is read once. The max
+// of |x| is an unsigned max of the bit patterns with the sign cleared (NaN
+// patterns order above +inf, so the one reduction also finds non-finite
+// rows), and the values are quantised four to a word by quant_sym_rcp_packed.
+// The max is order-independent and every value takes quant_sym's result, so
+// the output is bit-identical to quantize_a8_kernel's.
 template <int R>
-__global__ __launch_bounds__(kA8Threads) void quantize_a8_regs_kernel(const float* __restrict__ a,
-                                                                      int64_t k, int64_t lda,
-                                                                      int64_t k_pad,
-                                                                      int8_t* __restrict__ a8,
-                                                                      float* __restrict__ scales, uint32_t* __restrict__ zero_words, int nzero) {
-    __shared__ float red[kA8Threads / 64];
+__global__ __launch_bounds__(1024) void quantize_a8_regs_kernel(const float* __restrict__ a, int64_t k,
+                                                                int64_t lda, int64_t k_pad,
+                                                                int8_t* __restrict__ a8,
+                                                                float* __restrict__ scales, uint32_t* __restrict__ zero_words, int nzero) {
+    __shared__ uint32_t red[16];
     zero_counters(zero_words, nzero);
     const int64_t row = blockIdx.x;
     const float4* x = reinterpret_cast<const float4*>(a + row * lda);
     uint32_t* q = reinterpret_cast<uint32_t*>(a8 + row * k_pad);
-    const int t = threadIdx.x;
+    const int t = threadIdx.x, nt = blockDim.x;
     const int k4 = static_cast<int>(k / 4);
-    float4 v[R];
+    float vals[4 * R];
 #pragma unroll
     for (int j = 0; j < R; ++j) {
-        const int i = t + j * kA8Threads;
-        v[j] = i < k4 ? x[i] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        const int i = t + j * nt;
+        const float4 v = i < k4 ? x[i] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        vals[4 * j] = v.x;
+        vals[4 * j + 1] = v.y;
+        vals[4 * j + 2] = v.z;
+        vals[4 * j + 3] = v.w;
     }
-    float vmax = 0.0f;
+    uint32_t um = 0;
 #pragma unroll
-    for (int j = 0; j < R; ++j) {
-        const float e[4] = {v[j].x, v[j].y, v[j].z, v[j].w};
-#pragma unroll
-        for (int c = 0; c < 4; ++c) {
-            const float m = fabsf(e[c]);
-            vmax = fmaxf(vmax, (m <= 3.402823466e38f) ? m : __builtin_inff());
-        }
-    }
-    vmax = block_max(vmax, red);
-    const bool bad = !(vmax <= 3.402823466e38f);
-    const float scale = vmax == 0.0f ? 1.0f : vmax / 127.0f;
+    for (int i = 0; i < 4 * R; ++i) um = max(um, __float_as_uint(vals[i]) & 0x7fffffffu);
+    um = __float_as_uint(wave_max_nonneg(__uint_as_float(um)));
+    if ((t & 63) == 0) red[t >> 6] = um;
+    __syncthreads();
+    um = red[0];
+    for (int w = 1; w < nt / 64; ++w) um = max(um, red[w]);
+    const bool bad = um > 0x7f7fffffu;  // an Inf or NaN in the row
+    const float vmax = __uint_as_float(um);
+    const float scale = bad || vmax == 0.0f ? 1.0f : vmax / 127.0f;
     const float inv = 1.0f / scale;
+    uint32_t w[R];
+    quant_sym_rcp_packed(vals, scale, inv, scale >= 1.175494351e-38f, w);
 #pragma unroll
     for (int j = 0; j < R; ++j) {
-        const int i = t + j * kA8Threads;
-        if (i < k4) {
-            const float e[4] = {v[j].x, v[j].y, v[j].z, v[j].w};
-            int qq[4];
-            quant_sym_rcp(e, scale, inv, qq);
-            q[i] = bad ? 0u : pack4(qq[0], qq[1], qq[2], qq[3]);
-        }
+        const int i = t + j * nt;
+        if (i < k4) q[i] = bad ? 0u : w[j];
     }
-    for (int64_t i = k4 + t; i < k_pad / 4; i += kA8Threads) q[i] = 0;
+    for (int64_t i = k4 + t; i < k_pad / 4; i += nt) q[i] = 0;
     if (t == 0) scales[row] = bad ? __builtin_nanf("") : scale;
 }
 
@@ -215,16 +219,21 @@ int launch_quantize_a8(const float* a, int64_t m, int64_t k, int64_t lda, int64_
     const bool vec = k % 4 == 0 && lda % 4 == 0 && k_pad % 4 == 0 &&
                      reinterpret_cast<uintptr_t>(a) % 16 == 0 && reinterpret_cast<uintptr_t>(a8) % 16 == 0;
     const dim3 grid(static_cast<unsigned>(m)), block(kA8Threads);
-    // float4 per thread that hold the row
-    const int64_t per = (k / 4 + kA8Threads - 1) / kA8Threads;
-    if (vec && per <= 16) {
-        if (per <= 1) quantize_a8_regs_kernel<1><<<grid, block, 0, stream>>>(a, k, lda, k_pad, a8, scales, zero_words, nzero);
-        else if (per <= 2) quantize_a8_regs_kernel<2><<<grid, block, 0, stream>>>(a, k, lda, k_pad, a8, scales, zero_words, nzero);
-        else if (per <= 4) quantize_a8_regs_kernel<4><<<grid, block, 0, stream>>>(a, k, lda, k_pad, a8, scales, zero_words, nzero);
-        else if (per <= 6) quantize_a8_regs_kernel<6><<<grid, block, 0, stream>>>(a, k, lda, k_pad, a8, scales, zero_words, nzero);
-        else if (per <= 8) quantize_a8_regs_kernel<8><<<grid, block, 0, stream>>>(a, k, lda, k_pad, a8, scales, zero_words, nzero);
-        else if (per <= 12) quantize_a8_regs_kernel<12><<<grid, block, 0, stream>>>(a, k, lda, k_pad, a8, scales, zero_words, nzero);
-        else quantize_a8_regs_kernel<16><<<grid, block, 0, stream>>>(a, k, lda, k_pad, a8, scales, zero_words, nzero);
+    // Threads per row: two float4 each (one for at most 512 rows of at most
+    // 4096 values), in whole waves, at most 1024. Sweeps over 256-1024
+    // threads: 512 x 5632 takes 5.85 us (6.87 with 256 threads and six float4
+    // each), 128 x 2048 2.55 (2.97), 2048 x 2048 6.83 (7.36), 4096 x 4096 17.2
+    // (17.7), 4096 x 14336 54.0 (58.0).
+    const int64_t k4 = k / 4;
+    const int64_t per = m <= 512 && k4 <= 1024 ? 1 : 2;
+    const int64_t nt = std::min<int64_t>(1024, std::max<int64_t>(64, (k4 + per - 1) / per + 63) / 64 * 64);
+    const int64_t r = (k4 + nt - 1) / nt;
+    if (vec && r <= 4) {
+        const dim3 rb(static_cast<unsigned>(nt));
+        if (r <= 1) quantize_a8_regs_kernel<1><<<grid, rb, 0, stream>>>(a, k, lda, k_pad, a8, scales, zero_words, nzero);
+        else if (r <= 2) quantize_a8_regs_kernel<2><<<grid, rb, 0, stream>>>(a, k, lda, k_pad, a8, scales, zero_words, nzero);
+        else if (r <= 3) quantize_a8_regs_kernel<3><<<grid, rb, 0, stream>>>(a, k, lda, k_pad, a8, scales, zero_words, nzero);
+        else quantize_a8_regs_kernel<4><<<grid, rb, 0, stream>>>(a, k, lda, k_pad, a8, scales, zero_words, nzero);
     } else if (vec) quantize_a8_kernel<true><<<grid, block, 0, stream>>>(a, k, lda, k_pad, a8, scales, zero_words, nzero);
     else quantize_a8_kernel<false><<<grid, block, 0, stream>>>(a, k, lda, k_pad, a8, scales, zero_words, nzero);
     return hipGetLastError() == hipSuccess ? kStatusOk : kStatusExec;
