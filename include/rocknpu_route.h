@@ -53,9 +53,20 @@ typedef struct rocknpu_mul_mat_node {
 } rocknpu_mul_mat_node;
 
 /* Dispatch counters of the routing over one context (the plugin's TRACE
- * summary counters, ggml-rocknpu.cpp:721-736). Printed to stderr when the
- * context is destroyed if ROCKNPU_GGML_TRACE or ROCKNPU_DISPATCH_SUMMARY is
- * set. */
+ * summary counters, ggml-rocknpu.cpp:721-736, and its split-profile counters,
+ * :758-818). Printed to stderr when the context is destroyed if
+ * ROCKNPU_GGML_TRACE or ROCKNPU_DISPATCH_SUMMARY is set.
+ *
+ * ROCKNPU_SPLIT_PROFILE (ggml-rocknpu.cpp:758-818, :1080-1092, :1623-1632):
+ * every rocknpu_route_run call's wall time is kept as a sample, and from the
+ * 112th call on every projection run on its own is timed per "M=.. K=.. N=.."
+ * shape. At destroy the context prints one "ROCKNPU SHAPE PROFILE" line per
+ * shape and one "ROCKNPU SPLIT PROFILE" line: calls, nodes, total and mean
+ * times, the counters below, the samples of 5 ms and 20 ms or more, the last
+ * 5 ms sample, the longest, the first 111 calls against the rest, and the four
+ * quarters of the samples (time and 20 ms samples each), in the plugin's
+ * format. The entry points return once the results are in host memory, so
+ * the wall times are the GPU work's. */
 typedef struct rocknpu_route_stats {
     size_t graph_calls;        /* rocknpu_route_run calls */
     size_t q4_k_mul_mat;       /* projections run, by weight type */
@@ -67,6 +78,16 @@ typedef struct rocknpu_route_stats {
     size_t mtile_group_calls;  /* same-input group calls (2..4 projections, M > 1) */
     size_t qkv_triple_calls;   /* Q nodes run as Q+K+V with K/V stashed */
     size_t qkv_stash_hits;     /* K/V nodes served from the stash */
+    size_t graph_nodes;        /* nodes passed to rocknpu_route_run */
+    uint64_t graph_ns;         /* wall time in rocknpu_route_run */
+    /* projections by M: single projections of M 4, 8, 12, 16 and any other M;
+     * the members of same-input groups with M > 1 count as "other", and
+     * single-token groups in none (the plugin's m4 .. m_other counters) */
+    size_t m4_mul_mat;
+    size_t m8_mul_mat;
+    size_t m12_mul_mat;
+    size_t m16_mul_mat;
+    size_t m_other_mul_mat;
 } rocknpu_route_stats;
 
 /* Where single-token (M = 1) MUL_MATs go (ROCKNPU_DECODE, ggml-rocknpu.cpp:305-322). */

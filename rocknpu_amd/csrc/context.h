@@ -10,6 +10,7 @@
 #include <cstdint>
 #include <map>
 #include <memory>
+#include <string>
 #include <unordered_map>
 #include <vector>
 
@@ -144,6 +145,10 @@ constexpr size_t kQkvMaxLayers = 256;
 struct RouteState {
     std::unordered_map<size_t, QkvLayer> qkv;
     rocknpu_route_stats stats{};
+    // ROCKNPU_SPLIT_PROFILE: per rocknpu_route_run call, and per shape of a
+    // projection run on its own ({calls, ns})
+    std::vector<uint64_t> samples_ns;
+    std::map<std::string, std::pair<size_t, uint64_t>> shapes;
 };
 
 }  // namespace rk

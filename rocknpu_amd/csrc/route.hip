@@ -5,6 +5,8 @@
 // rocknpu_mtile_group (:856-976, with the cross-partition Q/K/V stash of
 // :871-928) and graph_compute (:978-1650), made from plain node descriptions
 // instead of ggml tensors. Host code only.
+#include <algorithm>
+#include <chrono>
 #include <cstdint>
 #include <cstdio>
 #include <cstdlib>
@@ -141,6 +143,17 @@ bool attention_layer(const rocknpu_mul_mat_node& nd, const char* needle, size_t*
     return true;
 }
 
+// A projection run on its own, by M (the plugin counts every M here, 1 included).
+void count_m(rocknpu_route_stats& st, int64_t m) {
+    (m == 4 ? st.m4_mul_mat : m == 8 ? st.m8_mul_mat : m == 12 ? st.m12_mul_mat : m == 16 ? st.m16_mul_mat
+                                                                                        : st.m_other_mul_mat)++;
+}
+
+uint64_t since_ns(std::chrono::steady_clock::time_point t0) {
+    return static_cast<uint64_t>(
+        std::chrono::duration_cast<std::chrono::nanoseconds>(std::chrono::steady_clock::now() - t0).count());
+}
+
 void count_run(rocknpu_route_stats& st, const rocknpu_mul_mat_node& nd, int32_t decode) {
     switch (nd.weight_type) {
     case ROCKNPU_TYPE_Q4_K: st.q4_k_mul_mat++; break;
@@ -204,6 +217,7 @@ int qkv_stash(rocknpu_context* ctx, const rocknpu_mul_mat_node* const* g, size_t
     st.rows = m;
     st.k_pending = st.v_pending = true;
     rs.stats.qkv_triple_calls++;
+    rs.stats.m_other_mul_mat += 3;
     for (int32_t t : {lead.weight_type, st.wk.type, st.wv.type})
         (t == ROCKNPU_TYPE_Q4_K ? rs.stats.q4_k_mul_mat : rs.stats.q6_k_mul_mat)++;
     if (!st.released) {
@@ -221,11 +235,58 @@ int qkv_stash(rocknpu_context* ctx, const rocknpu_mul_mat_node* const* g, size_t
 }  // namespace
 
 namespace rk {
+namespace {
+// The ROCKNPU_SPLIT_PROFILE report (ggml-rocknpu.cpp:758-818): the shapes,
+// then the calls' summary, field for field in the plugin's format, so logs
+// read the same. The first 111 calls are the plugin's warm-up batch; the
+// shape timings start after it.
+constexpr size_t kWarmCalls = 111;
+void split_profile_print(const RouteState& rs) {
+    const rocknpu_route_stats& s = rs.stats;
+    const std::vector<uint64_t>& v = rs.samples_ns;
+    size_t slow5 = 0, slow20 = 0, last_slow5 = 0;
+    uint64_t max_ns = 0, first_ns = 0, rest_ns = 0, q_ns[4] = {0, 0, 0, 0};
+    size_t q_slow20[4] = {0, 0, 0, 0};
+    for (size_t i = 0; i < v.size(); ++i) {
+        const uint64_t ns = v[i];
+        const bool s20 = ns >= 20000000u;
+        max_ns = std::max(max_ns, ns);
+        if (ns >= 5000000u) {
+            ++slow5;
+            last_slow5 = i + 1;
+        }
+        slow20 += s20 ? 1 : 0;
+        const size_t q = std::min<size_t>(3, i * 4 / v.size());
+        q_ns[q] += ns;
+        q_slow20[q] += s20 ? 1 : 0;
+        (i < kWarmCalls ? first_ns : rest_ns) += ns;
+    }
+    for (const auto& e : rs.shapes)
+        std::fprintf(stderr, "ROCKNPU SHAPE PROFILE %s calls=%zu total_ms=%.3f avg_ms=%.3f\n", e.first.c_str(),
+                     e.second.first, e.second.second / 1e6, e.second.second / 1e6 / static_cast<double>(e.second.first));
+    const double graph_ms = s.graph_ns / 1e6, calls = static_cast<double>(s.graph_calls);
+    // cpu_fallback and native_w8 stay 0: unsupported nodes never reach this
+    // routing (rocknpu_route_run rejects them), and f32 weights are not taken
+    std::fprintf(stderr,
+                 "ROCKNPU SPLIT PROFILE graph_calls=%zu graph_nodes=%zu graph_ms=%.3f avg_call_ms=%.3f "
+                 "avg_nodes=%.2f cpu_fallback=%zu q4=%zu q6=%zu f16=%zu native_w8=%zu "
+                 "m=[4:%zu,8:%zu,12:%zu,16:%zu,other:%zu] slow5=%zu slow20=%zu last_slow5=%zu max_ms=%.3f "
+                 "first111_ms=%.3f rest_ms=%.3f q_ms=[%.3f,%.3f,%.3f,%.3f] q_slow20=[%zu,%zu,%zu,%zu]\n",
+                 s.graph_calls, s.graph_nodes, graph_ms, s.graph_calls ? graph_ms / calls : 0.0,
+                 s.graph_calls ? static_cast<double>(s.graph_nodes) / calls : 0.0, size_t{0}, s.q4_k_mul_mat,
+                 s.q6_k_mul_mat, s.f16_mul_mat, size_t{0}, s.m4_mul_mat, s.m8_mul_mat, s.m12_mul_mat,
+                 s.m16_mul_mat, s.m_other_mul_mat, slow5, slow20, last_slow5, max_ns / 1e6, first_ns / 1e6,
+                 rest_ns / 1e6, q_ns[0] / 1e6, q_ns[1] / 1e6, q_ns[2] / 1e6, q_ns[3] / 1e6, q_slow20[0],
+                 q_slow20[1], q_slow20[2], q_slow20[3]);
+}
+}  // namespace
+
 // Called from rocknpu_context_destroy: the plugin's TRACE summary line
-// (ggml-rocknpu.cpp:721-736).
+// (ggml-rocknpu.cpp:721-736) and the split profile.
 void route_print_summary(const RockNpuContext* ctx) {
-    if (!env_on("ROCKNPU_GGML_TRACE") && !env_on("ROCKNPU_DISPATCH_SUMMARY")) return;
     const rocknpu_route_stats& s = ctx->route.stats;
+    if (env_on("ROCKNPU_SPLIT_PROFILE")) split_profile_print(ctx->route);
+    if (!env_on("ROCKNPU_GGML_TRACE") && !env_on("ROCKNPU_DISPATCH_SUMMARY")) return;
     if (s.graph_calls == 0) return;
     std::fprintf(stderr,
                  "ROCKNPU GGML TRACE summary graph_calls=%zu q4_K_mul_mat=%zu q5_K_mul_mat=%zu q6_K_mul_mat=%zu "
@@ -263,6 +324,20 @@ int rocknpu_route_run(rocknpu_context* ctx, const rocknpu_mul_mat_node* nodes, s
         if (!supported(nodes[i], decode_route)) return kInvalid;
     rocknpu_route_stats& stats = ctx->route.stats;
     stats.graph_calls++;
+    stats.graph_nodes += count;
+    const bool profile = env_on("ROCKNPU_SPLIT_PROFILE");
+    // the call's wall time, on every return
+    struct CallTimer {
+        rk::RouteState& rs;
+        bool keep;
+        std::chrono::steady_clock::time_point t0 = std::chrono::steady_clock::now();
+        ~CallTimer() {
+            const uint64_t ns = since_ns(t0);
+            rs.stats.graph_ns += ns;
+            if (keep) rs.samples_ns.push_back(ns);
+        }
+    } timer{ctx->route, profile};
+    const bool shape_profile = profile && stats.graph_calls > rk::kWarmCalls;
     const bool trace = env_on("ROCKNPU_GGML_TRACE");
     const bool qkv = env_default_on("ROCKNPU_MTILE_QKV");
     // the plan's groups, walked in lead order
@@ -300,6 +375,7 @@ int rocknpu_route_run(rocknpu_context* ctx, const rocknpu_mul_mat_node* nodes, s
                 st = rocknpu_matmul_q_concat_f32_f32_mtile(ctx, c, w, bytes, kinds, ns, lead.activations, outs,
                                                            m, k);
                 stats.mtile_group_calls++;
+                stats.m_other_mul_mat += c;
                 if (trace)
                     std::fprintf(stderr, "ROCKNPU GGML TRACE mtile_group lead=%s count=%zu M=%zu K=%zu N=%zu\n",
                                  lead.weight_name ? lead.weight_name : "?", c, m, k, total_n);
@@ -321,6 +397,7 @@ int rocknpu_route_run(rocknpu_context* ctx, const rocknpu_mul_mat_node* nodes, s
         } else {
             const size_t n = static_cast<size_t>(n_of(lead));
             const uint8_t* w = static_cast<const uint8_t*>(lead.weights);
+            const auto t0 = std::chrono::steady_clock::now();
             if (lead.weight_type == ROCKNPU_TYPE_F16)
                 st = rocknpu_matmul_f16_f32_f32(ctx, static_cast<const uint16_t*>(lead.weights), lead.activations,
                                                 lead.output, m, k, n);
@@ -333,7 +410,17 @@ int rocknpu_route_run(rocknpu_context* ctx, const rocknpu_mul_mat_node* nodes, s
                 st = rocknpu_matmul_q5_k_f32_f32(ctx, w, lead.weight_bytes, lead.activations, lead.output, m, k, n);
             else
                 st = rocknpu_matmul_q6_k_f32_f32(ctx, w, lead.weight_bytes, lead.activations, lead.output, m, k, n);
-            if (st == kOk) count_run(stats, lead, decode_route);
+            if (st == kOk) {
+                count_run(stats, lead, decode_route);
+                count_m(stats, static_cast<int64_t>(m));
+            }
+            if (shape_profile) {
+                char key[96];
+                std::snprintf(key, sizeof(key), "M=%zu K=%zu N=%zu", m, k, n);
+                auto& e = ctx->route.shapes[key];
+                e.first++;
+                e.second += since_ns(t0);
+            }
         }
         if (st != kOk) return st;
     }

@@ -35,7 +35,10 @@ class RouteStats(ctypes.Structure):
 
     _fields_ = [(name, ctypes.c_size_t) for name in (
         "graph_calls", "q4_k_mul_mat", "q5_k_mul_mat", "q6_k_mul_mat", "f16_mul_mat", "q8k_m1_mul_mat",
-        "w8a8_m1_mul_mat", "mtile_group_calls", "qkv_triple_calls", "qkv_stash_hits")]
+        "w8a8_m1_mul_mat", "mtile_group_calls", "qkv_triple_calls", "qkv_stash_hits", "graph_nodes")]
+    _fields_ += [("graph_ns", ctypes.c_uint64)]
+    _fields_ += [(name, ctypes.c_size_t) for name in (
+        "m4_mul_mat", "m8_mul_mat", "m12_mul_mat", "m16_mul_mat", "m_other_mul_mat")]
 
     def as_dict(self) -> dict:
         return {name: getattr(self, name) for name, _ in self._fields_}

@@ -148,3 +148,56 @@ def test_qkv_stash_across_separate_calls():
             r2 = np.zeros((m, n), np.float32)
             assert ctx.matmul_q(kind, ws[name], x2, r2, k, n) == 0
             assert np.array_equal(_bits(outs2[name]), _bits(r2)), name
+
+
+def test_split_profile(monkeypatch, capfd):
+    """ROCKNPU_SPLIT_PROFILE (ggml-rocknpu.cpp:758-818, :1080-1092,
+    :1623-1632): calls, nodes and the M buckets in the stats; at destroy one
+    SHAPE PROFILE line per single projection shape timed after the 111
+    warm-up calls, and the SPLIT PROFILE line whose first-111/rest and
+    quarter times add up to the total."""
+    import re
+    monkeypatch.setenv("ROCKNPU_SPLIT_PROFILE", "1")
+    k, calls = 256, 115
+    xa, xg, xd = (synth.activations(m, k, index=7000 + m) for m in (4, 5, 8))
+    wa, wb, wc, wd = (synth.kquant(kind, n, k, index=7010 + i) for i, (kind, n) in
+                      enumerate(((4, 32), (4, 48), (6, 16), (6, 64))))
+    outs = [np.zeros((m, n), np.float32) for m, n in ((4, 32), (5, 48), (5, 16), (8, 64))]
+    nodes = [R.node(R.Q4_K, wa, k, 32, xa, outs[0]),          # alone, M = 4
+             R.node(R.Q4_K, wb, k, 48, xg, outs[1]),          # a same-input pair, M = 5
+             R.node(R.Q6_K, wc, k, 16, xg, outs[2]),
+             R.node(R.Q6_K, wd, k, 64, xd, outs[3])]          # alone, M = 8
+    with Context() as ctx:
+        for i in range(calls):
+            if i % 20 == 0:
+                print(f"split profile call {i}", flush=True)
+            assert R.run(ctx, nodes, R.DECODE_GGML) == 0
+        s = R.stats(ctx)
+        assert (s["graph_calls"], s["graph_nodes"]) == (calls, 4 * calls)
+        assert (s["m4_mul_mat"], s["m8_mul_mat"], s["m12_mul_mat"], s["m16_mul_mat"], s["m_other_mul_mat"]) == \
+            (calls, calls, 0, 0, 2 * calls)
+        assert s["graph_ns"] > 0
+        capfd.readouterr()
+    err = capfd.readouterr().err
+    shapes = re.findall(r"ROCKNPU SHAPE PROFILE M=(\d+) K=(\d+) N=(\d+) calls=(\d+)", err)
+    assert sorted(shapes) == sorted([("4", "256", "32", str(calls - 111)), ("8", "256", "64", str(calls - 111))])
+    line = re.search(r"ROCKNPU SPLIT PROFILE (.*)", err).group(1)
+    f = dict(kv.split("=", 1) for kv in line.split())
+    assert (f["graph_calls"], f["graph_nodes"], f["q4"], f["q6"]) == (str(calls), str(4 * calls), str(2 * calls),
+                                                                      str(2 * calls))
+    assert f["m"] == f"[4:{calls},8:{calls},12:0,16:0,other:{2 * calls}]"
+    total = float(f["graph_ms"])
+    assert abs(float(f["first111_ms"]) + float(f["rest_ms"]) - total) <= 0.01 + 1e-3 * total
+    assert abs(sum(float(v) for v in f["q_ms"].strip("[]").split(",")) - total) <= 0.01 + 1e-3 * total
+    assert 0 <= int(f["slow20"]) <= int(f["slow5"]) <= calls and float(f["max_ms"]) <= total
+
+
+def test_no_split_profile_without_the_variable(monkeypatch, capfd):
+    monkeypatch.delenv("ROCKNPU_SPLIT_PROFILE", raising=False)
+    x = synth.activations(4, 256, index=7100)
+    w = synth.kquant(4, 32, 256, index=7101)
+    out = np.zeros((4, 32), np.float32)
+    with Context() as ctx:
+        assert R.run(ctx, [R.node(R.Q4_K, w, 256, 32, x, out)], R.DECODE_GGML) == 0
+        assert R.stats(ctx)["m4_mul_mat"] == 1
+    assert "SPLIT PROFILE" not in capfd.readouterr().err

@@ -68,3 +68,22 @@ def test_c_program_links_and_calls(tmp_path):
     assert s1 == -1  # ROCKNPU_STATUS_INVALID_ARGUMENT
     assert (s2, bm, bn, st) == (0, 256, 256, 2)
     assert count >= 0
+
+
+def test_route_stats_layout_matches_the_python_mirror(tmp_path):
+    """rocknpu_route_stats as C lays it out equals route.RouteStats (ctypes):
+    size and every field's offset."""
+    from rocknpu_amd import route
+    fields = [name for name, _ in route.RouteStats._fields_]
+    src = tmp_path / "layout.c"
+    body = "".join(f'    printf("%zu\\n", offsetof(rocknpu_route_stats, {f}));\n' for f in fields)
+    src.write_text('#include <stddef.h>\n#include <stdio.h>\n#include "rocknpu_route.h"\nint main(void) {\n'
+                   '    printf("%zu\\n", sizeof(rocknpu_route_stats));\n' + body + "    return 0;\n}\n")
+    exe = tmp_path / "layout"
+    r = subprocess.run(["gcc", "-std=c99", "-Wall", "-Werror", f"-I{ROOT / 'include'}", str(src), "-o", str(exe)],
+                       capture_output=True, text=True)
+    assert r.returncode == 0, r.stderr
+    got = [int(v) for v in subprocess.run([str(exe)], capture_output=True, text=True, check=True).stdout.split()]
+    import ctypes
+    want = [ctypes.sizeof(route.RouteStats)] + [getattr(route.RouteStats, f).offset for f in fields]
+    assert got == want
