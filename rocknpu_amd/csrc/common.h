@@ -163,19 +163,21 @@ template <int N>
 __device__ __forceinline__ void quant_sym_rcp_packed(const float (&v)[N], float s, float inv, bool fast,
                                                      uint32_t (&w)[N / 4]) {
     constexpr float kRound = 12582912.0f;
-    uint32_t u[N];
     float err = 0.0f;
-#pragma unroll
-    for (int i = 0; i < N; ++i) {
-        const float r = v[i] * inv;
-        const float ur = r + kRound;
-        u[i] = __float_as_uint(ur);
-        err = fmaxf(err, fabsf(r - (ur - kRound)));
-    }
+    // four values at a time, packed as soon as they are rounded, so only four
+    // rounded values are live at once
 #pragma unroll
     for (int i = 0; i < N / 4; ++i) {
-        const uint32_t lo = __builtin_amdgcn_perm(u[4 * i + 1], u[4 * i], 0x0C0C0400u);
-        const uint32_t hi = __builtin_amdgcn_perm(u[4 * i + 3], u[4 * i + 2], 0x0C0C0400u);
+        uint32_t u[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const float r = v[4 * i + e] * inv;
+            const float ur = r + kRound;
+            u[e] = __float_as_uint(ur);
+            err = fmaxf(err, fabsf(r - (ur - kRound)));
+        }
+        const uint32_t lo = __builtin_amdgcn_perm(u[1], u[0], 0x0C0C0400u);
+        const uint32_t hi = __builtin_amdgcn_perm(u[3], u[2], 0x0C0C0400u);
         w[i] = __builtin_amdgcn_perm(hi, lo, 0x05040100u);
     }
     // a wave-uniform branch (a lane's fallback costs the wave the same either
