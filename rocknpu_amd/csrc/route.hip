@@ -375,7 +375,7 @@ int rocknpu_route_run(rocknpu_context* ctx, const rocknpu_mul_mat_node* nodes, s
                 st = rocknpu_matmul_q_concat_f32_f32_mtile(ctx, c, w, bytes, kinds, ns, lead.activations, outs,
                                                            m, k);
                 stats.mtile_group_calls++;
-                stats.m_other_mul_mat += c;
+                if (st == kOk) stats.m_other_mul_mat += c;
                 if (trace)
                     std::fprintf(stderr, "ROCKNPU GGML TRACE mtile_group lead=%s count=%zu M=%zu K=%zu N=%zu\n",
                                  lead.weight_name ? lead.weight_name : "?", c, m, k, total_n);

@@ -85,9 +85,15 @@ def _rounding_kat_row() -> np.ndarray:
     return np.array(vals, np.float32)
 
 
+# The register kernel sizes its workgroup to the row: one float4 a thread for
+# at most 512 rows of at most 4096 values, else two, up to 1024 threads, so
+# rows of 2049-3072 float4 take three a thread and longer ones four.
 @pytest.mark.parametrize("m,k,k_pad", [(1, 2048, 2048), (128, 2048, 2048), (7, 5632, 5632), (3, 300, 320),
                                        (5, 1001, 1024), (2, 2064, 2112),
-                                       (4, 14336, 14336),    # row in registers, 14 of 16 float4 per thread
+                                       (600, 2048, 2048),    # over 512 rows: two float4 a thread
+                                       (1, 64, 64), (2, 4, 64),  # one wave
+                                       (3, 11264, 11264),    # three float4 a thread
+                                       (4, 14336, 14336),    # four float4 a thread, 1024 threads
                                        (2, 16384, 16384),    # the longest row kept in registers
                                        (3, 16388, 16448)])   # longer: two passes over the row
 def test_quantize_a8_bit_exact(m, k, k_pad):
@@ -100,7 +106,8 @@ def test_quantize_a8_bit_exact(m, k, k_pad):
     assert np.array_equal(_bits(sc.cpu().numpy()), _bits(sc_ref))
 
 
-@pytest.mark.parametrize("k", [2051, 2048, 16388])  # scalar path; row in registers; two vector passes
+# scalar path; row in registers at one to four float4 a thread; two vector passes
+@pytest.mark.parametrize("k", [2051, 2048, 5632, 11264, 14336, 16388])
 def test_quantize_a8_edge_rows(k):
     print(f"a8 edge rows k={k}", flush=True)
     kat = np.resize(_rounding_kat_row(), k)
