@@ -146,17 +146,25 @@ class DecodeSet:
         return total, launches
 
 
+_SIDE_STREAM = None
+
+
 def time_graph(torch, fn, steps: int, warmup: int) -> tuple[float, object]:
     """Capture fn() in a HIP graph, replay warmup + steps times; returns
-    (ms per replay over the timed steps, graph)."""
-    s = torch.cuda.Stream()
+    (ms per replay over the timed steps, graph). Every capture runs on one
+    side stream, so the library's per-stream K-split workspaces are made once."""
+    global _SIDE_STREAM
+    if _SIDE_STREAM is None:
+        _SIDE_STREAM = torch.cuda.Stream()
+    s = _SIDE_STREAM
     s.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(s):
-        fn()  # eager warm-up on the side stream (loads code objects)
+        fn()  # eager warm-up on the side stream (loads code objects, makes its split workspaces)
     torch.cuda.current_stream().wait_stream(s)
     torch.cuda.synchronize()
     g = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(g):
+    # captured on the warm-up's stream, whose K-split workspaces the graph reuses
+    with torch.cuda.graph(g, stream=s):
         fn()
     for _ in range(warmup):
         g.replay()

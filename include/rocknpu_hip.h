@@ -203,14 +203,39 @@ int rocknpu_hip_gemv_tile_weights(uint32_t kind, const uint8_t * w, size_t w_byt
  * (launches of up to 16 rows for Q4_K, 8 for Q6_K). A row's f32 sum runs in the
  * order of the matrix-core kernel on raw blocks, so results equal
  * rocknpu_hip_gemv_q_f32 / _q8_k wherever that kernel serves the call, and
- * fused, grouped and Q8_K-input calls agree bit for bit. No counterpart in the
+ * fused, grouped and Q8_K-input calls agree bit for bit.
+ *
+ * K split: launches of 2 to 8 rows over rows of 17 to 31 blocks (K 4352 to
+ * 7936, e.g. a 5632-wide down projection) split each 16-row tile's blocks into
+ * two ranges on two workgroups, whose partial sums meet in the workspace
+ * (rocknpu_hip_gemv_tiled_workspace_bytes for the call's m, k and total rows;
+ * 256-byte aligned; zeroed before its first use). Such a row's sum is the two
+ * ranges' sums added, the same bits in grouped, separate, fused and Q8_K-input
+ * calls, but not those of the unsplit kernels. Every completed call leaves the
+ * workspace as it found it; calls that share one must not overlap (one per
+ * stream). A call that finds it not clear writes NaN where it did and sets
+ * its error word (rocknpu_hip_gemv_tiled_workspace_check). Calls that do not
+ * split ignore workspace (it may be null); a split call without one large
+ * enough returns ROCKNPU_STATUS_INVALID_ARGUMENT. No counterpart in the
  * reference. */
 int rocknpu_hip_gemv_q_f32_tiled(uint32_t kind, size_t count, const uint8_t * const * w,
                                  const size_t * w_bytes, const size_t * n, size_t k, const float * x,
                                  size_t ldx, size_t m, float * const * out, const size_t * ldo,
-                                 void * stream);
+                                 void * workspace, size_t workspace_bytes, void * stream);
 int rocknpu_hip_gemv_q8_k_tiled(uint32_t kind, const uint8_t * w, size_t w_bytes, size_t k, size_t n,
-                                const uint8_t * q8k, size_t m, float * out, size_t ldo, void * stream);
+                                const uint8_t * q8k, size_t m, float * out, size_t ldo, void * workspace,
+                                size_t workspace_bytes, void * stream);
+
+/* Bytes of the K-split workspace a tiled call of m activation rows over K = k
+ * and `rows` output rows in all (the members' n summed) needs; 0 when none of
+ * its launches splits. Host code only. No counterpart in the reference. */
+size_t rocknpu_hip_gemv_tiled_workspace_bytes(uint32_t kind, size_t m, size_t k, size_t rows);
+
+/* Waits for `stream`, then reads and clears the workspace's error word:
+ * ROCKNPU_STATUS_OK when no split call on it found it not clear since the last
+ * check, else ROCKNPU_STATUS_EXECUTION_ERROR, and the workspace must be zeroed
+ * before it is used again. No counterpart in the reference. */
+int rocknpu_hip_gemv_tiled_workspace_check(void * workspace, void * stream);
 
 /* Whether a decode GEMV of m activation rows over Q4_K (kind 4) or Q6_K
  * (kind 6) rows of K = k runs faster on the tiled copy (1) or on the raw rows

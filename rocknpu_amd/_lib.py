@@ -77,8 +77,10 @@ SIGNATURES = {
     "rocknpu_hip_matmul_w8a8_f32_noalloc": (_i, [_vp, _sz, _sz, _sz, _vp, _vp, _sz, _sz, _vp, _sz, _vp]),
     "rocknpu_hip_gemv_tiled_bytes": (_sz, [_u32, _sz, _sz]),
     "rocknpu_hip_gemv_tile_weights": (_i, [_u32, _vp, _sz, _sz, _sz, _vp, _sz, _vp]),
-    "rocknpu_hip_gemv_q_f32_tiled": (_i, [_u32, _sz, _vp, _vp, _vp, _sz, _vp, _sz, _sz, _vp, _vp, _vp]),
-    "rocknpu_hip_gemv_q8_k_tiled": (_i, [_u32, _vp, _sz, _sz, _sz, _vp, _sz, _vp, _sz, _vp]),
+    "rocknpu_hip_gemv_q_f32_tiled": (_i, [_u32, _sz, _vp, _vp, _vp, _sz, _vp, _sz, _sz, _vp, _vp, _vp, _sz, _vp]),
+    "rocknpu_hip_gemv_q8_k_tiled": (_i, [_u32, _vp, _sz, _sz, _sz, _vp, _sz, _vp, _sz, _vp, _sz, _vp]),
+    "rocknpu_hip_gemv_tiled_workspace_bytes": (_sz, [_u32, _sz, _sz, _sz]),
+    "rocknpu_hip_gemv_tiled_workspace_check": (_i, [_vp, _vp]),
     "rocknpu_hip_gemv_tiled_preferred": (_i, [_u32, _sz, _sz]),
     "rocknpu_hip_gemv_take_stall": (_i, []),
     "rocknpu_hip_gemv_test_stall": (_i, [_i]),

@@ -495,6 +495,39 @@ std::shared_ptr<DecodeWeight> raw_weights(RockNpuContext* ctx, const uint8_t* w,
 // from two rows, and Q4_K rows of 16 or more blocks at one row).
 bool decode_tiled(uint32_t kind, size_t m, size_t k) { return rocknpu_hip_gemv_tiled_preferred(kind, m, k) != 0; }
 
+// The tiled GEMV's K-split workspace for a launch of m rows over `rows` output
+// rows: null when that launch does not split. Zeroed when (re)allocated; every
+// completed launch leaves it zero, and gemv_split_failed zeroes it again after
+// a launch that found it dirty.
+bool gemv_split_ws(RockNpuContext* ctx, uint32_t kind, size_t m, size_t k, size_t rows, void** ws, size_t* bytes) {
+    *bytes = rocknpu_hip_gemv_tiled_workspace_bytes(kind, m, k, rows);
+    *ws = nullptr;
+    if (*bytes == 0) return true;
+    const size_t before = ctx->d_gemv_split.cap;
+    if (!ctx->d_gemv_split.ensure(*bytes) || !ctx->h_err.ensure(sizeof(uint32_t))) return false;
+    if (ctx->d_gemv_split.cap != before &&
+        !hip_ok(hipMemsetAsync(ctx->d_gemv_split.p, 0, ctx->d_gemv_split.cap, ctx->stream), ctx, "gemv split"))
+        return false;
+    *ws = ctx->d_gemv_split.p;
+    *bytes = ctx->d_gemv_split.cap;
+    return true;
+}
+// Queues the download of the workspace's error word (read after the sync).
+bool gemv_split_queue_check(RockNpuContext* ctx) {
+    return hip_ok(hipMemcpyAsync(ctx->h_err.p, ctx->d_gemv_split.p, sizeof(uint32_t), hipMemcpyDeviceToHost,
+                                 ctx->stream),
+                  ctx, "gemv split");
+}
+// After the sync: whether a split launch found the workspace dirty (its
+// results are NaN where it did); the workspace is zeroed again then.
+bool gemv_split_failed(RockNpuContext* ctx) {
+    if (*ctx->h_err.as<uint32_t>() == 0) return false;
+    if (ctx->trace) std::fprintf(stderr, "ROCKNPU DECODE ERROR gemv: K-split workspace was not clear\n");
+    (void)hipMemsetAsync(ctx->d_gemv_split.p, 0, ctx->d_gemv_split.cap, ctx->stream);
+    (void)hipStreamSynchronize(ctx->stream);
+    return true;
+}
+
 // Decode-cache accounting of one decode call (the reference's
 // decode_cache_hits / misses and their ns, lib.rs:3821-3826): a hit when every
 // weight was resident.
@@ -843,16 +876,22 @@ int rocknpu_matmul_q_q8k_f32_f32(rocknpu_context* ctx, uint32_t kind, const uint
         return kExec;
     if (!hip_ok(hipMemcpyAsync(ctx->d_act.p, act, a_elems * 4, hipMemcpyHostToDevice, ctx->stream), ctx, "act"))
         return kExec;
+    void* ws = nullptr;
+    size_t ws_bytes = 0;
+    if (tiled && !gemv_split_ws(ctx, kind, m, k, n, &ws, &ws_bytes)) return kExec;
     int st = rocknpu_hip_quantize_q8_k(ctx->d_act.as<float>(), m, k, k, ctx->d_q8k.as<uint8_t>(), ctx->stream);
     if (st != kOk) return st;
     st = tiled ? rocknpu_hip_gemv_q8_k_tiled(kind, dw->tiled.as<uint8_t>(), dw->tiled_bytes, k, n,
-                                             ctx->d_q8k.as<uint8_t>(), m, ctx->d_out.as<float>(), n, ctx->stream)
+                                             ctx->d_q8k.as<uint8_t>(), m, ctx->d_out.as<float>(), n, ws, ws_bytes,
+                                             ctx->stream)
                : rocknpu_hip_gemv_q8_k(kind, dw->raw.as<uint8_t>(), bytes, k, n, ctx->d_q8k.as<uint8_t>(), m,
                                        ctx->d_out.as<float>(), n, nullptr, nullptr, ctx->stream);
     if (st != kOk) return st;
+    if (ws && !gemv_split_queue_check(ctx)) return kExec;
     if (!hip_ok(hipMemcpyAsync(out, ctx->d_out.p, o_elems * 4, hipMemcpyDeviceToHost, ctx->stream), ctx, "out") ||
         !hip_ok(hipStreamSynchronize(ctx->stream), ctx, "gemv"))
         return kExec;
+    if (ws && gemv_split_failed(ctx)) return kExec;
     record_decode(ctx, hit, t0);
     return kOk;
 }
@@ -888,6 +927,7 @@ int rocknpu_matmul_q_q8k_group_f32_f32(rocknpu_context* ctx, size_t count, const
     // launch per kind over that kind's members, in member order
     size_t off[4];
     for (size_t i = 0, o = 0; i < count; o += m * ns[i], ++i) off[i] = o;
+    bool split = false;
     for (uint32_t kind : {4u, 6u}) {
         const bool tiled = decode_tiled(kind, m, k);
         const uint8_t* w[4];
@@ -904,18 +944,25 @@ int rocknpu_matmul_q_q8k_group_f32_f32(rocknpu_context* ctx, size_t count, const
             ++c;
         }
         if (c == 0) continue;
+        void* ws = nullptr;
+        size_t ws_bytes = 0, rows = 0;
+        for (size_t i = 0; i < c; ++i) rows += wn[i];
+        if (tiled && !gemv_split_ws(ctx, kind, m, k, rows, &ws, &ws_bytes)) return kExec;
+        split |= ws != nullptr;
         const int st = tiled ? rocknpu_hip_gemv_q_f32_tiled(kind, c, w, wb, wn, k, ctx->d_act.as<float>(), k, m, out,
-                                                            ldo, ctx->stream)
+                                                            ldo, ws, ws_bytes, ctx->stream)
                              : rocknpu_hip_gemv_q_f32(kind, c, w, wb, wn, k, ctx->d_act.as<float>(), k, m, out, ldo,
                                                       ctx->stream);
         if (st != kOk) return st;
     }
+    if (split && !gemv_split_queue_check(ctx)) return kExec;
     for (size_t i = 0; i < count; ++i)
         if (!hip_ok(hipMemcpyAsync(outputs[i], ctx->d_out.as<float>() + off[i], m * ns[i] * 4, hipMemcpyDeviceToHost,
                                    ctx->stream),
                     ctx, "out"))
             return kExec;
     if (!hip_ok(hipStreamSynchronize(ctx->stream), ctx, "gemv")) return kExec;
+    if (split && gemv_split_failed(ctx)) return kExec;
     // a fused launch whose wait for its quantising waves gave up wrote NaN
     if (rocknpu_hip_gemv_take_stall()) {
         if (ctx->trace) std::fprintf(stderr, "ROCKNPU DECODE ERROR gemv: activation quantisation wait gave up\n");

@@ -237,6 +237,10 @@ struct GemvParams {
     int iters;           // blocks per slot per row group
     int32_t* isum;       // optional exact per-(mi, row, block) sums (count == 1)
     int32_t* msum;
+    // the tiled GEMV's K-split exchange (gemv_tiled_split): zeroed slots and
+    // error word, gemv_tiled_split_bytes long; null where no split applies
+    void* split_ws;
+    size_t split_ws_bytes;
 };
 
 // The decode cache's tile-interleaved weight layout (gemv_mfma.hip): bytes of
@@ -245,5 +249,14 @@ struct GemvParams {
 size_t gemv_tiled_bytes(int kind, int64_t n, int nb);
 int launch_gemv_tile_weights(int kind, const uint8_t* src, int64_t n, int nb, uint8_t* dst, hipStream_t stream);
 int launch_gemv_tiled(int kind, bool fused, GemvParams& p, hipStream_t stream);
+// Whether a tiled launch of m activation rows over rows of nb blocks splits
+// each tile's blocks over two workgroups (a function of these alone, so a
+// row's f32 order does not depend on the projections sharing the launch), and
+// the workspace such a launch over `tiles` 16-row tiles needs (0 without a
+// split): one 8-byte slot per tile, lane and register row, then the error word.
+bool gemv_tiled_split(int kind, int m, int nb);
+size_t gemv_tiled_split_bytes(int kind, int m, int nb, int64_t tiles);
+// The generation a split launch (GEMM or GEMV) tags its arrivals with.
+uint32_t next_split_generation();
 
 }  // namespace rk

@@ -166,6 +166,7 @@ struct RockNpuContext {
     std::unordered_map<rk::WeightKey, std::shared_ptr<rk::DecodeWeight>, rk::KeyHash> raw;
     rk::DevBuf d_raw, d_act, d_a8, d_as, d_out, d_q8k;
     rk::DevBuf d_split;  // the W8A8 GEMM's K-split workspace (counters cleared per call)
+    rk::DevBuf d_gemv_split;  // the tiled decode GEMV's K-split slots and error word (zero between calls)
     rk::PinnedBuf h_out, h_as, h_err;  // h_err: the K-split workspace's error word
     size_t hits = 0, misses = 0, m1_calls = 0;
     uint64_t hit_ns = 0, miss_ns = 0;

@@ -475,16 +475,6 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_w8a8_dma_kernel(
     }
 }
 
-// The generation a split launch stamps its arrivals with: distinct for every
-// launch of the process (until it wraps after 2^32 - 1 of them), never 0,
-// which is what a zeroed or reset stamp holds.
-uint32_t next_split_generation() {
-    static std::atomic<uint32_t> gen{0};
-    uint32_t g = gen.fetch_add(1, std::memory_order_relaxed) + 1;
-    while (g == 0) g = gen.fetch_add(1, std::memory_order_relaxed) + 1;
-    return g;
-}
-
 // Splits that get K stages when `splits` are asked for over `ks` stages, and
 // the stages of each (the last may have fewer).
 struct SplitK {
@@ -525,6 +515,16 @@ int launch_dma(const int8_t* a8, int64_t lda, const int8_t* w8, int64_t ldw, con
 }
 
 }  // namespace
+
+// The generation a split launch stamps its arrivals with: distinct for every
+// launch of the process (until it wraps after 2^32 - 1 of them), never 0,
+// which is what a zeroed or reset stamp holds.
+uint32_t next_split_generation() {
+    static std::atomic<uint32_t> gen{0};
+    uint32_t g = gen.fetch_add(1, std::memory_order_relaxed) + 1;
+    while (g == 0) g = gen.fetch_add(1, std::memory_order_relaxed) + 1;
+    return g;
+}
 
 int launch_gemm_w8a8_skinny(const int8_t* a8, int64_t lda, const int8_t* w8, int64_t ldw, const float* as,
                             const float* ws, int m, int n, int k, float* out, int64_t ldo, int32_t* oi,

@@ -79,6 +79,12 @@ struct MfmaArgs {
     int nb;
     int tiles;
     int iters;  // blocks per wave and tile: ceil(nb / W)
+    // gemv_tiled_kernel with a K split (S = 2): blocks per range, the
+    // exchange slots, the error word and the launch's generation
+    int nbs;
+    unsigned long long* split_slot;
+    uint32_t* split_err;
+    uint32_t gen;
 };
 
 // The wave-owned activation blocks in LDS: block b, activation row mi.

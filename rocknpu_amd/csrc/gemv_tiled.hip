@@ -66,34 +66,52 @@ struct AllActs {
     }
 };
 
-template <int KIND, int MT, bool FUSED, int W, bool AREG, int NI, int D, int IT, bool LAZY = false>
-__global__ __launch_bounds__(W * 64) void gemv_tiled_kernel(const MfmaArgs p) {
+//
+// K split (S = 2): the grid holds one workgroup per (tile, block range) unit,
+// unit u = blockIdx.x being tile u / 2's blocks [nbs * (u % 2), ..): each
+// workgroup quantises only its range's activations and reads only its range's
+// weights, so a launch of few tiles fills twice the CUs. The two partial sums
+// of a tile's output meet in an exchange slot (gemv_tiled_split below).
+template <int KIND, int MT, bool FUSED, int W, bool AREG, int NI, int D, int IT, bool LAZY = false, int S = 1>
+__global__ __launch_bounds__(W * 64) void gemv_tiled_kernel(const MfmaArgs p0) {
     constexpr int BB = block_bytes(KIND);
     constexpr int NR = MT / 4;
     static_assert(D >= 1 && D <= NI, "one to NI items in flight");
+    static_assert(S == 1 || S == 2, "unsplit, or two block ranges");
     using Piece = typename PieceOf<KIND, true>::type;
     extern __shared__ __align__(16) uint8_t smem[];
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int grid = gridDim.x, bid = blockIdx.x;
+    // p: the range's view of the activations (its blocks from b0); the tile
+    // lookups read the members from p0 (a copy indexed at run time would live
+    // in scratch memory)
+    const int sp = S > 1 ? bid % S : 0, b0 = sp * p0.nbs;
+    MfmaArgs p = p0;
+    if constexpr (S > 1) {
+        p.nb = min(p0.nbs, p0.nb - b0);
+        if constexpr (FUSED) p.x = p0.x + static_cast<int64_t>(b0) * kQK;
+        else p.q8k = p0.q8k + static_cast<int64_t>(b0) * kQ8KBytes;
+    }
     const int nb = p.nb, m = p.m, iters = p.iters;
-    const ActLds<MT> act{smem, nb};
+    const int lnb = S > 1 ? p0.nbs : nb;  // blocks the LDS layout holds
+    const ActLds<MT> act{smem, lnb};
     // partial sums [2][W][64][NR], then the tile sums [NI][64][NR]
-    float* part = reinterpret_cast<float*>(smem + ((nb * MT * kPerRowBlock + 15) & ~15));
+    float* part = reinterpret_cast<float*>(smem + ((lnb * MT * kPerRowBlock + 15) & ~15));
     float* res = part + 2 * W * 64 * NR;
     const int n = lane & 15, q = lane >> 4;
-    const int grid = gridDim.x, bid = blockIdx.x;
-    const int ntile = (p.tiles - bid + grid - 1) / grid;  // tiles bid, bid + grid, ..
-    const int items = ntile * iters;                       // <= NI (the host's choice)
-    // item i: tile i / iters of the workgroup, block index i % iters; items
+    const int ntile = (p0.tiles * S - bid + grid - 1) / grid;  // units bid, bid + grid, ..
+    const int items = ntile * iters;                           // <= NI (the host's choice)
+    // item i: unit i / iters of the workgroup, block index i % iters; items
     // past the workgroup's last re-read its last one (in bounds) and are dropped
     auto load_item = [&](int i, Piece& k) {
         const int ic = min(i, items - 1);
         const int kt = ic / iters, it = ic - kt * iters;
-        const int t = bid + kt * grid;
-        const TileOut to = tile_out(p, t);
-        const int b = min(wave + W * it, nb - 1);
-        const gbytes w = reinterpret_cast<gbytes>(reinterpret_cast<uint64_t>(tile_weights(p, t)));
-        k.load_tiled(w + (static_cast<int64_t>(to.row0 / kTileRows) * nb + b) * (kTileRows * BB), lane);
+        const int t = (bid + kt * grid) / S;
+        const TileOut to = tile_out(p0, t);
+        const int b = b0 + min(wave + W * it, nb - 1);
+        const gbytes w = reinterpret_cast<gbytes>(reinterpret_cast<uint64_t>(tile_weights(p0, t)));
+        k.load_tiled(w + (static_cast<int64_t>(to.row0 / kTileRows) * p0.nb + b) * (kTileRows * BB), lane);
     };
 
     // The activations of the wave's IT = iters block indices: with one, as
@@ -171,14 +189,43 @@ __global__ __launch_bounds__(W * 64) void gemv_tiled_kernel(const MfmaArgs p) {
     }
     __syncthreads();
     for (int kt = wave; kt < ntile; kt += W) {
-        const TileOut to = tile_out(p, bid + kt * grid);
+        const int t = (bid + kt * grid) / S;
+        const TileOut to = tile_out(p0, t);
         const int row = to.row0 + n;
 #pragma unroll
         for (int lr = 0; lr < NR; ++lr) {
+            float r = res[(kt * 64 + lane) * NR + lr];
+            if constexpr (S > 1) {
+                // Each (tile, lane, register row) value meets its other range's
+                // in one slot, by one atomic swap that leaves this range's tag
+                // (gen * 2 + range) and value there. Finding the slot empty
+                // (0), the unit is first and stops. Finding the other range's
+                // tag of this launch, it is second: it adds the two values
+                // (two addends: the same sum in either order) and empties the
+                // slot, so every launch leaves the slots as it found them.
+                // Anything else (a slot not emptied by an earlier launch, or
+                // a launch sharing the workspace) gives NaN and sets the error
+                // word, never another value. Relaxed agent-scope atomics on
+                // one address are ordered for all workgroups of the device.
+                unsigned long long* slot = p0.split_slot + (static_cast<int64_t>(t) * 64 + lane) * NR + lr;
+                const uint32_t g = p0.gen % 0x7fffffffu + 1u;  // tags 2 .. 2^32 - 1, never 0
+                const uint32_t mine = 2 * g + sp, other = 2 * g + (1 - sp);
+                const unsigned long long old = __hip_atomic_exchange(
+                    slot, static_cast<unsigned long long>(mine) << 32 | __float_as_uint(r), __ATOMIC_RELAXED,
+                    __HIP_MEMORY_SCOPE_AGENT);
+                const uint32_t tag = static_cast<uint32_t>(old >> 32);
+                if (old == 0) continue;  // first of the two
+                if (tag == other) {
+                    r += __uint_as_float(static_cast<uint32_t>(old));
+                } else {
+                    r = __builtin_nanf("");
+                    __hip_atomic_store(p0.split_err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                }
+                __hip_atomic_store(slot, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
             const int mo = NR * q + lr;
             if (mo < m && row < to.rows)
-                reinterpret_cast<gfloats>(reinterpret_cast<uint64_t>(to.out))[mo * to.ldo + row] =
-                    res[(kt * 64 + lane) * NR + lr];
+                reinterpret_cast<gfloats>(reinterpret_cast<uint64_t>(to.out))[mo * to.ldo + row] = r;
         }
     }
 }
@@ -341,12 +388,61 @@ int tiled_waves(int nb, int64_t tiles, int cus) {
 // workgroup per CU at most, each walking its tiles; one block in flight per
 // wave in the item loop, or the pipelined kernel where a wave has at most four
 // items and the launch at most 8 rows.
+// The K split of a tiled launch: for 2 to 8 activation rows over rows of 17 to
+// 31 blocks (8 waves, three or four block indices a wave unsplit), two block
+// ranges of at most 16 blocks, one workgroup per (tile, range) unit, which
+// doubles the workgroups of a launch of few tiles. TinyLlama down (Q6_K 2048 x
+// 5632, 128 tiles) at 4 rows: 6.58 -> 5.65 us. Rows of at most 16 blocks
+// (one or two block indices a wave) measured slower split (TinyLlama o,
+// 2048 x 2048: 3.50 -> 4.0 us): there the exchange costs more than the
+// second range's workgroups save. The slots follow the error word:
+// [error word, padding to 256 bytes][tiles][64 lanes][MT / 4 rows] x 8 bytes.
+constexpr size_t kSplitSlotBase = 256;
+bool gemv_tiled_split(int kind, int m, int nb) {
+    return (kind == 4 || kind == 6) && m >= 2 && m <= 8 && nb >= 17 && nb <= 31;
+}
+size_t gemv_tiled_split_bytes(int kind, int m, int nb, int64_t tiles) {
+    if (!gemv_tiled_split(kind, m, nb)) return 0;
+    return kSplitSlotBase + static_cast<size_t>(tiles) * 64 * (m <= 4 ? 1 : 2) * 8;
+}
+
+namespace {
+template <int KIND, int MT, bool FUSED>
+void launch_split(const MfmaArgs& p, dim3 grid, size_t lds, hipStream_t stream) {
+    // two block indices a wave, the second quantised after the first item
+    gemv_tiled_kernel<KIND, MT, FUSED, 8, false, 2, 2, 2, true, 2><<<grid, dim3(8 * 64), lds, stream>>>(p);
+}
+}  // namespace
+
 int launch_gemv_tiled(int kind, bool fused, GemvParams& p, hipStream_t stream) {
     if ((kind != 4 && kind != 6) || p.m < 1 || p.m > gemv_mfma_rows(kind, p.nb)) return kStatusInvalid;
     const int mt = p.m <= 4 ? 4 : p.m <= 8 ? 8 : 16;
     const int cus = device_cu_count();
     int64_t tiles = 0;
     for (int i = 0; i < p.count; ++i) tiles += (p.rows[i] + kTileRows - 1) / kTileRows;
+    if (gemv_tiled_split(kind, p.m, p.nb)) {
+        if (!p.split_ws || p.split_ws_bytes < gemv_tiled_split_bytes(kind, p.m, p.nb, tiles) ||
+            reinterpret_cast<uintptr_t>(p.split_ws) % 256 != 0)
+            return kStatusInvalid;
+        MfmaArgs ka;
+        if (mfma_args(p, 8, ka) != kStatusOk) return kStatusInvalid;
+        ka.nbs = (p.nb + 1) / 2;
+        ka.iters = 2;  // ranges of 9 to 16 blocks on 8 waves
+        ka.split_err = static_cast<uint32_t*>(p.split_ws);
+        ka.split_slot = reinterpret_cast<unsigned long long*>(static_cast<uint8_t*>(p.split_ws) + kSplitSlotBase);
+        ka.gen = next_split_generation();
+        const dim3 grid(static_cast<unsigned>(2 * ka.tiles));
+        const size_t lds = gemv_mfma_lds(mt, ka.nbs, 8) + static_cast<size_t>(2) * 64 * (mt / 4) * 4;
+        if (lds > static_cast<size_t>(kLdsMax)) return kStatusInvalid;
+        if (kind == 4) {
+            if (mt == 4) fused ? launch_split<4, 4, true>(ka, grid, lds, stream) : launch_split<4, 4, false>(ka, grid, lds, stream);
+            else fused ? launch_split<4, 8, true>(ka, grid, lds, stream) : launch_split<4, 8, false>(ka, grid, lds, stream);
+        } else {
+            if (mt == 4) fused ? launch_split<6, 4, true>(ka, grid, lds, stream) : launch_split<6, 4, false>(ka, grid, lds, stream);
+            else fused ? launch_split<6, 8, true>(ka, grid, lds, stream) : launch_split<6, 8, false>(ka, grid, lds, stream);
+        }
+        return hipGetLastError() == hipSuccess ? kStatusOk : kStatusExec;
+    }
     const int w = tiled_waves(p.nb, tiles, cus);
     MfmaArgs ka;
     if (mfma_args(p, w, ka) != kStatusOk) return kStatusInvalid;

@@ -284,8 +284,40 @@ size_t tiled_rows_per_launch(uint32_t kind, size_t nb) {
 }
 }  // namespace
 
+extern "C" size_t rocknpu_hip_gemv_tiled_workspace_bytes(uint32_t kind, size_t m, size_t k, size_t rows) {
+    if ((kind != 4 && kind != 6) || m == 0 || k == 0 || k % rk::kQK != 0 || rows == 0 || rows > INT32_MAX / 2)
+        return 0;
+    const size_t nb = k / rk::kQK, chunk = tiled_rows_per_launch(kind, nb);
+    if (chunk == 0) return 0;
+    const int64_t tiles = static_cast<int64_t>((rows + 15) / 16);  // 16-row tiles
+    // the launches of m rows: full chunks, then the rest
+    const size_t full = std::min(chunk, m), rest = m % chunk;
+    return std::max(rk::gemv_tiled_split_bytes(static_cast<int>(kind), static_cast<int>(full), static_cast<int>(nb), tiles),
+                    rest ? rk::gemv_tiled_split_bytes(static_cast<int>(kind), static_cast<int>(rest),
+                                                      static_cast<int>(nb), tiles)
+                         : size_t{0});
+}
+
+extern "C" int rocknpu_hip_gemv_tiled_workspace_check(void* workspace, void* stream) {
+    // the error word is the workspace's first
+    if (!workspace) return rk::kStatusInvalid;
+    const hipStream_t s = static_cast<hipStream_t>(stream);
+    uint32_t* word = static_cast<uint32_t*>(workspace);
+    uint32_t flag = 0;
+    if (hipMemcpyAsync(&flag, word, sizeof flag, hipMemcpyDeviceToHost, s) != hipSuccess ||
+        hipStreamSynchronize(s) != hipSuccess)
+        return rk::kStatusExec;
+    if (flag == 0) return rk::kStatusOk;
+    static const uint32_t zero = 0;
+    if (hipMemcpyAsync(word, &zero, sizeof zero, hipMemcpyHostToDevice, s) != hipSuccess ||
+        hipStreamSynchronize(s) != hipSuccess)
+        return rk::kStatusExec;
+    return rk::kStatusExec;
+}
+
 extern "C" int rocknpu_hip_gemv_q8_k_tiled(uint32_t kind, const uint8_t* w, size_t w_bytes, size_t k, size_t n,
-                                           const uint8_t* q8k, size_t m, float* out, size_t ldo, void* stream) {
+                                           const uint8_t* q8k, size_t m, float* out, size_t ldo, void* workspace,
+                                           size_t workspace_bytes, void* stream) {
     if ((kind != 4 && kind != 6) || !w || !q8k || !out || k == 0 || k % rk::kQK != 0 || n == 0 || m == 0 ||
         ldo < n || n > INT32_MAX / 2)
         return rk::kStatusInvalid;
@@ -306,6 +338,8 @@ extern "C" int rocknpu_hip_gemv_q8_k_tiled(uint32_t kind, const uint8_t* w, size
         p.ldx = static_cast<int64_t>(per_row);
         p.m = static_cast<int>(std::min(chunk, m - m0));
         p.nb = static_cast<int>(nb);
+        p.split_ws = workspace;
+        p.split_ws_bytes = workspace ? workspace_bytes : 0;
         const int st = rk::launch_gemv_tiled(static_cast<int>(kind), false, p, s);
         if (st != rk::kStatusOk) return st;
     }
@@ -315,7 +349,7 @@ extern "C" int rocknpu_hip_gemv_q8_k_tiled(uint32_t kind, const uint8_t* w, size
 extern "C" int rocknpu_hip_gemv_q_f32_tiled(uint32_t kind, size_t count, const uint8_t* const* w,
                                             const size_t* w_bytes, const size_t* n, size_t k, const float* x,
                                             size_t ldx, size_t m, float* const* out, const size_t* ldo,
-                                            void* stream) {
+                                            void* workspace, size_t workspace_bytes, void* stream) {
     if ((kind != 4 && kind != 6) || count < 1 || count > static_cast<size_t>(rk::kGemvMaxMembers) || !w ||
         !w_bytes || !n || !x || !out || !ldo || k == 0 || k % rk::kQK != 0 || m == 0 || ldx < k)
         return rk::kStatusInvalid;
@@ -344,6 +378,8 @@ extern "C" int rocknpu_hip_gemv_q_f32_tiled(uint32_t kind, size_t count, const u
         p.ldx = static_cast<int64_t>(ldx);
         p.m = static_cast<int>(std::min(chunk, m - m0));
         p.nb = static_cast<int>(nb);
+        p.split_ws = workspace;
+        p.split_ws_bytes = workspace ? workspace_bytes : 0;
         const int st = rk::launch_gemv_tiled(static_cast<int>(kind), true, p, s);
         if (st != rk::kStatusOk) return st;
     }

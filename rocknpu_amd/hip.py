@@ -240,30 +240,86 @@ def gemv_tile_weights(kind: int, w: torch.Tensor, k: int, n: int, tiled: torch.T
     return tiled
 
 
-def gemv_q_f32_tiled(kind: int, weights, k: int, ns, x: torch.Tensor, outs=None):
-    """gemv_q_f32 on tiled copies (gemv_tile_weights) of 1..4 projections."""
+def gemv_tiled_workspace_bytes(kind: int, m: int, k: int, rows: int) -> int:
+    """Bytes of the K-split workspace a tiled GEMV call of m rows over K = k
+    and `rows` output rows in all needs (0: none of its launches splits)."""
+    return int(_lib.load().rocknpu_hip_gemv_tiled_workspace_bytes(kind, m, k, rows))
+
+
+# The tiled GEMV's K-split workspaces, one per (device, stream), each zeroed
+# when made; every completed call leaves its workspace zero. Under graph
+# capture none is made or grown (the zeroing would run only at replay): a
+# captured split call needs the stream to have one already, from an eager call
+# on it, and raises otherwise.
+_gemv_workspaces: dict[tuple[int, int], torch.Tensor] = {}
+
+
+def gemv_workspace_for(device: torch.device, nbytes: int) -> torch.Tensor:
+    dev = torch.device(device)
+    index = dev.index if dev.index is not None else torch.cuda.current_device()
+    stream = torch.cuda.current_stream(index)
+    key = (index, stream.cuda_stream)
+    ws = _gemv_workspaces.get(key)
+    if ws is not None and ws.numel() >= nbytes:
+        return ws
+    if torch.cuda.is_current_stream_capturing():
+        raise LaunchError("a split tiled GEMV under graph capture needs this stream's K-split workspace: "
+                          "make one eager call of the same shape on the capturing stream first")
+    new = torch.zeros(max(nbytes, 1 << 16), dtype=torch.uint8, device=torch.device("cuda", index))
+    if ws is not None:
+        ws.record_stream(stream)
+    _gemv_workspaces[key] = new
+    return new
+
+
+def gemv_workspace_check(workspace: torch.Tensor) -> bool:
+    """Waits for the current stream and reads and clears the tiled GEMV
+    workspace's error word: True when no split call on it found it not clear
+    since the last check. A False workspace must be zeroed before reuse."""
+    st = _lib.load().rocknpu_hip_gemv_tiled_workspace_check(_ptr(workspace), _stream())
+    if st not in (0, -3):
+        raise LaunchError(f"gemv_tiled_workspace_check returned status {st}")
+    return st == 0
+
+
+def _gemv_ws(kind: int, m: int, k: int, rows: int, device, workspace):
+    need = gemv_tiled_workspace_bytes(kind, m, k, rows)
+    if need == 0:
+        return None, 0
+    ws = gemv_workspace_for(device, need) if workspace is None else workspace
+    return ws, ws.numel()
+
+
+def gemv_q_f32_tiled(kind: int, weights, k: int, ns, x: torch.Tensor, outs=None,
+                     workspace: torch.Tensor | None = None):
+    """gemv_q_f32 on tiled copies (gemv_tile_weights) of 1..4 projections.
+    Split launches (rows of 17-31 blocks at 2-8 activation rows) use
+    `workspace`, or this stream's own (gemv_workspace_for)."""
     m = x.shape[0]
     count = len(weights)
     if outs is None:
         outs = [torch.empty((m, n), dtype=torch.float32, device=x.device) for n in ns]
+    ws, ws_bytes = _gemv_ws(kind, m, k, sum(ns), x.device, workspace)
     w_arr = (ctypes.c_void_p * count)(*[w.data_ptr() for w in weights])
     b_arr = (ctypes.c_size_t * count)(*[w.numel() for w in weights])
     n_arr = (ctypes.c_size_t * count)(*ns)
     o_arr = (ctypes.c_void_p * count)(*[o.data_ptr() for o in outs])
     l_arr = (ctypes.c_size_t * count)(*[_ld(o) for o in outs])
     _check(_lib.load().rocknpu_hip_gemv_q_f32_tiled(kind, count, w_arr, b_arr, n_arr, k, _ptr(x), _ld(x), m,
-                                                    o_arr, l_arr, _stream()), "gemv_q_f32_tiled")
+                                                    o_arr, l_arr, _ptr(ws), ws_bytes, _stream()), "gemv_q_f32_tiled")
     return outs
 
 
 def gemv_q8_k_tiled(kind: int, w: torch.Tensor, k: int, n: int, q8k: torch.Tensor,
-                    out: torch.Tensor | None = None) -> torch.Tensor:
-    """gemv_q8_k on a tiled copy (gemv_tile_weights)."""
+                    out: torch.Tensor | None = None, workspace: torch.Tensor | None = None) -> torch.Tensor:
+    """gemv_q8_k on a tiled copy (gemv_tile_weights); split launches as in
+    gemv_q_f32_tiled."""
     m = q8k.shape[0]
     if out is None:
         out = torch.empty((m, n), dtype=torch.float32, device=q8k.device)
+    ws, ws_bytes = _gemv_ws(kind, m, k, n, q8k.device, workspace)
     _check(_lib.load().rocknpu_hip_gemv_q8_k_tiled(kind, _ptr(w), w.numel(), k, n, _ptr(q8k), m, _ptr(out),
-                                                   _ld(out), _stream()), "gemv_q8_k_tiled")
+                                                   _ld(out), _ptr(ws), ws_bytes, _stream()), "gemv_q8_k_tiled")
     return out
 
 

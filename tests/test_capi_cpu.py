@@ -124,14 +124,36 @@ def test_tiled_decode_layout_host_side():
     assert lib.rocknpu_hip_gemv_tile_weights(4, p, raw, 256, 16, ctypes.c_void_p((1 << 20) + 8), tb, None) == -1
     assert lib.rocknpu_hip_gemv_tile_weights(4, None, raw, 256, 16, p, tb, None) == -1
     out = ctypes.c_void_p(1 << 21)
-    assert lib.rocknpu_hip_gemv_q8_k_tiled(4, p, 17 * 144, 256, 17, p, 1, out, 17, None) == -1  # raw size, not tiled
-    assert lib.rocknpu_hip_gemv_q8_k_tiled(4, p, tb, 256, 16, p, 1, out, 8, None) == -1     # ldo < n
+    assert lib.rocknpu_hip_gemv_q8_k_tiled(4, p, 17 * 144, 256, 17, p, 1, out, 17, None, 0, None) == -1  # raw size, not tiled
+    assert lib.rocknpu_hip_gemv_q8_k_tiled(4, p, tb, 256, 16, p, 1, out, 8, None, 0, None) == -1     # ldo < n
     w_arr = (ctypes.c_void_p * 1)(1 << 20)
     b_arr = (ctypes.c_size_t * 1)(tb)
     n_arr = (ctypes.c_size_t * 1)(16)
     o_arr = (ctypes.c_void_p * 1)(1 << 21)
     l_arr = (ctypes.c_size_t * 1)(16)
-    assert lib.rocknpu_hip_gemv_q_f32_tiled(4, 1, w_arr, b_arr, n_arr, 256, p, 255, 1, o_arr, l_arr, None) == -1
-    assert lib.rocknpu_hip_gemv_q_f32_tiled(4, 5, w_arr, b_arr, n_arr, 256, p, 256, 1, o_arr, l_arr, None) == -1
+    assert lib.rocknpu_hip_gemv_q_f32_tiled(4, 1, w_arr, b_arr, n_arr, 256, p, 255, 1, o_arr, l_arr, None, 0, None) == -1
+    assert lib.rocknpu_hip_gemv_q_f32_tiled(4, 5, w_arr, b_arr, n_arr, 256, p, 256, 1, o_arr, l_arr, None, 0, None) == -1
     b_arr[0], n_arr[0], l_arr[0] = 17 * 144, 17, 17  # raw size of 17 rows, not the tiled 32
-    assert lib.rocknpu_hip_gemv_q_f32_tiled(4, 1, w_arr, b_arr, n_arr, 256, p, 256, 1, o_arr, l_arr, None) == -1
+    assert lib.rocknpu_hip_gemv_q_f32_tiled(4, 1, w_arr, b_arr, n_arr, 256, p, 256, 1, o_arr, l_arr, None, 0, None) == -1
+
+
+def test_tiled_split_workspace_bytes_host_side():
+    """The tiled GEMV's K-split workspace (rows of 17-31 blocks at 2-8
+    activation rows): 256 bytes (the error word) and one 8-byte slot per
+    16-row tile, lane and register row (one for launches of up to 4 rows, two
+    for 5-8), sized by the call's largest launch; 0 where nothing splits."""
+    lib = _lib.load()
+    wsb = lib.rocknpu_hip_gemv_tiled_workspace_bytes
+    tiles = 2048 // 16
+    assert wsb(6, 4, 5632, 2048) == 256 + tiles * 64 * 8
+    assert wsb(6, 2, 5632, 2048) == 256 + tiles * 64 * 8
+    assert wsb(6, 8, 5632, 2048) == 256 + tiles * 64 * 2 * 8
+    assert wsb(4, 5, 4352, 1000) == 256 + 63 * 64 * 2 * 8          # 17 blocks, ragged rows
+    assert wsb(6, 20, 5632, 2048) == 256 + tiles * 64 * 2 * 8      # launches of 8, 8 and 4 rows
+    assert wsb(6, 9, 5632, 2048) == 256 + tiles * 64 * 2 * 8       # 8 rows, then 1 (unsplit)
+    assert wsb(6, 1, 5632, 2048) == 0                              # one row: unsplit
+    assert wsb(4, 4, 2048, 2048) == 0                              # 8 blocks
+    assert wsb(4, 4, 4096, 4096) == 0                              # 16 blocks
+    assert wsb(6, 4, 8192, 2048) == 0                              # 32 blocks
+    assert wsb(4, 12, 5632, 2048) == 0                             # 9-16 rows (Q4_K): unsplit
+    assert wsb(5, 4, 5632, 2048) == 0 and wsb(6, 4, 5000, 2048) == 0

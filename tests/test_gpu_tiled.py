@@ -40,11 +40,18 @@ def _check_vs_oracle(kind, w, k, n, x, got):
         assert err.max() <= 1e-5 * np.abs(ref[mi]).max(), (kind, k, n, mi)
 
 
-def _same_order_as_raw(nb):
+def _split(kind, m, nb):
+    """Whether a tiled launch of m rows splits each tile's blocks in two ranges
+    (rocknpu_hip_gemv_q_f32_tiled): rows of 17-31 blocks at 2-8 rows."""
+    return kind in (4, 6) and 2 <= m <= 8 and 17 <= nb <= 31
+
+
+def _same_order_as_raw(nb, m=16):
     """Whether the tiled kernels add a row's block terms in the order of the
     raw-row matrix-core kernel (8 waves): rows of at most 16 blocks whatever
-    the tiled launch's waves, and rows of 17-31 blocks (8 waves there)."""
-    return nb < 32
+    the tiled launch's waves, and rows of 17-31 blocks (8 waves there) where
+    the launch does not split."""
+    return nb < 32 and not _split(4, m, nb)
 
 
 @pytest.mark.parametrize("kind,k,n", [
@@ -78,6 +85,9 @@ CASES = [
     (4, 4096, [4096, 1024, 1024], (3, 6)),
     (6, 4096, [1000], (2, 7)),
     (6, 14336, [4096], (1, 4, 5, 8)),
+    (4, 5632, [2048, 300], (2, 3, 5, 8, 12)),  # 22 blocks: split at 2-8 rows, not at 12
+    (6, 4352, [40, 2048], (2, 7)),             # 17 blocks: ranges of 9 and 8
+    (4, 7936, [33], (4,)),                     # 31 blocks: ranges of 16 and 15
     (4, 512, [100], (1, 3)),
     (6, 256, [40], (1, 2)),
     (4, 2048, [1000, 17], (4, 13)),
@@ -101,7 +111,7 @@ def test_tiled_gemv(kind, k, ns, ms):
         torch.cuda.synchronize()
         # the raw rows take the matrix cores from 3 rows (Q4_K); with 8 or more
         # blocks per row both kernels run 8-wave orders
-        raw_mfma = kind == 4 and 3 <= m <= 16 and nb >= 8 and _same_order_as_raw(nb)
+        raw_mfma = kind == 4 and 3 <= m <= 16 and nb >= 8 and _same_order_as_raw(nb, m)
         for i, n in enumerate(ns):
             got = fused[i].cpu().numpy()
             assert np.array_equal(_bits(got), _bits(fromq[i].cpu().numpy())), "fused vs Q8_K input"
@@ -168,3 +178,111 @@ def test_capi_decode_rows_read_the_tiled_copy():
         _check_vs_oracle(4, w4, k, n, x4, outs[0])
         _check_vs_oracle(6, w6, k, n, x4, outs[1])
         assert np.array_equal(_bits(outs[0]), _bits(out4))
+
+
+def test_split_grouped_equals_separate_and_q8k_input():
+    """Split launches (22-block rows at 4 and 6 rows): a member's results are
+    the same bits alone, grouped with another member of either size, and from
+    Q8_K input; within the oracle bounds."""
+    k = 5632
+    ws = [synth.kquant(6, n, k, index=3500 + i) for i, n in enumerate((2048, 48))]
+    td = [hip.gemv_tile_weights(6, _dev(w), k, n) for w, n in zip(ws, (2048, 48))]
+    for m in (4, 6):
+        print(f"split grouping m={m}", flush=True)
+        x = synth.activations(m, k, index=3510 + m)
+        xd = _dev(x)
+        both = hip.gemv_q_f32_tiled(6, td, k, [2048, 48], xd)
+        alone = [hip.gemv_q_f32_tiled(6, [t], k, [n], xd)[0] for t, n in zip(td, (2048, 48))]
+        q8 = hip.quantize_q8_k(xd)
+        fromq = [hip.gemv_q8_k_tiled(6, t, k, n, q8) for t, n in zip(td, (2048, 48))]
+        torch.cuda.synchronize()
+        for i, n in enumerate((2048, 48)):
+            got = both[i].cpu().numpy()
+            assert np.array_equal(_bits(got), _bits(alone[i].cpu().numpy())), ("grouped vs alone", m, n)
+            assert np.array_equal(_bits(got), _bits(fromq[i].cpu().numpy())), ("fused vs Q8_K input", m, n)
+            _check_vs_oracle(6, ws[i], k, n, x, got)
+
+
+def test_split_workspace_left_clear_and_dirty_detected():
+    """Every completed split call leaves its workspace zero; a workspace with a
+    slot left set gives NaN (never other bits) where it is met, and the error
+    word, which the check clears; zeroed again, the call is exact."""
+    k, n, m = 5632, 2048, 4
+    w = synth.kquant(6, n, k, index=3600)
+    td = [hip.gemv_tile_weights(6, _dev(w), k, n)]
+    xd = _dev(synth.activations(m, k, index=3601))
+    nbytes = hip.gemv_tiled_workspace_bytes(6, m, k, n)
+    assert nbytes == 256 + (n // 16) * 64 * 8
+    ws = torch.zeros(nbytes, dtype=torch.uint8, device=DEV)
+    print("split clean calls", flush=True)
+    ref = hip.gemv_q_f32_tiled(6, td, k, [n], xd, workspace=ws)[0].cpu().numpy()
+    again = hip.gemv_q_f32_tiled(6, td, k, [n], xd, workspace=ws)[0].cpu().numpy()
+    assert np.array_equal(_bits(ref), _bits(again))
+    assert not ws.any().item()
+    assert hip.gemv_workspace_check(ws)
+    # a slot left holding a value (tile 3, lane 5, which holds row 53 of
+    # activation row 0): the first arrival there finds a tag of no launch;
+    # that output is NaN, the rest exact
+    slots = ws[256:].view(torch.int64)
+    slots[3 * 64 + 5] = (1 << 32) | 0x3F800000  # tag 1: no launch's (tags are 2 or more)
+    print("split dirty call", flush=True)
+    got = hip.gemv_q_f32_tiled(6, td, k, [n], xd, workspace=ws)[0].cpu().numpy()
+    bad = np.isnan(got)
+    assert bad.any() and not hip.gemv_workspace_check(ws)
+    assert np.array_equal(_bits(got[~bad]), _bits(ref[~bad]))
+    assert bad.sum() == 1  # lane 5 of tile 3: row 53 of activation row 0
+    ws.zero_()
+    fixed = hip.gemv_q_f32_tiled(6, td, k, [n], xd, workspace=ws)[0].cpu().numpy()
+    assert np.array_equal(_bits(fixed), _bits(ref)) and hip.gemv_workspace_check(ws)
+
+
+def test_split_needs_a_workspace():
+    import ctypes
+    from rocknpu_amd import _lib
+    k, n, m = 5632, 32, 4
+    t = hip.gemv_tile_weights(6, _dev(synth.kquant(6, n, k, index=3700)), k, n)
+    x = _dev(synth.activations(m, k, index=3701))
+    out = torch.empty((m, n), device=DEV)
+    arr = lambda ty, *v: (ty * len(v))(*v)  # noqa: E731
+    st = _lib.load().rocknpu_hip_gemv_q_f32_tiled(6, 1, arr(ctypes.c_void_p, t.data_ptr()), arr(ctypes.c_size_t, t.numel()),
+                                                  arr(ctypes.c_size_t, n), k, ctypes.c_void_p(x.data_ptr()), k, m,
+                                                  arr(ctypes.c_void_p, out.data_ptr()), arr(ctypes.c_size_t, n),
+                                                  None, 0, None)
+    assert st == -1
+    small = torch.zeros(256, dtype=torch.uint8, device=DEV)
+    with pytest.raises(hip.LaunchError):
+        hip.gemv_q_f32_tiled(6, [t], k, [n], x, workspace=small)
+
+
+@pytest.mark.filterwarnings("ignore:The CUDA Graph is empty")
+def test_split_graph_replays_match_eager():
+    """A split launch captured on a stream that already has its workspace (one
+    eager call first) replays the eager bits, every replay; capturing on a
+    stream without one raises instead of running unsplit."""
+    k, ns, m = 5632, [2048], 4
+    td = [hip.gemv_tile_weights(6, _dev(synth.kquant(6, ns[0], k, index=3800)), k, ns[0])]
+    x = _dev(synth.activations(m, k, index=3801))
+    eager = hip.gemv_q_f32_tiled(6, td, k, ns, x)[0].cpu().numpy()
+    outs = [torch.empty((m, ns[0]), device=DEV)]
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        hip.gemv_q_f32_tiled(6, td, k, ns, x, outs=outs)
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        hip.gemv_q_f32_tiled(6, td, k, ns, x, outs=outs)
+    for rep in range(3):
+        print(f"split graph replay {rep}", flush=True)
+        outs[0].fill_(float("nan"))
+        g.replay()
+        torch.cuda.synchronize()
+        assert np.array_equal(_bits(outs[0].cpu().numpy()), _bits(eager)), rep
+        hip.gemv_q_f32_tiled(6, td, k, ns, x)  # eager work between replays
+        torch.cuda.synchronize()
+    fresh = torch.cuda.Stream()
+    g2 = torch.cuda.CUDAGraph()
+    with pytest.raises(hip.LaunchError):
+        with torch.cuda.graph(g2, stream=fresh):
+            hip.gemv_q_f32_tiled(6, td, k, ns, x, outs=outs)
