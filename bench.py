@@ -803,8 +803,9 @@ def main():
                         "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": measured_traffic("gemv_q4k"),
                         "avg_launch_us": round(q4_us, 3), "bytes_per_launch": q4_bpl},
         "decode_q6k_down": {"kernel": "Q6_K x Q8_K decode GEMV with fused Q8_K quant (M=1: gemv_q6_stream_kernel "
-                                      "on raw rows; M=4: gemv_tiled_kernel<6,4,true,8,false,3,2,3> on the tiled "
-                                      "copies), the 22 down launches of a step at each M", "peak": HBM_PEAK_GBS,
+                                      "on raw rows; M=4: gemv_tiled_kernel<6,4,true,8,false,2,2,2,true,2> on the "
+                                      "tiled copies, each tile's 22 blocks as two ranges of 11 on two workgroups), "
+                                      "the 22 down launches of a step at each M", "peak": HBM_PEAK_GBS,
                             "unit": "GB/s",
                             **q6},
     }
