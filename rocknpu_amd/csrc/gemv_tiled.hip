@@ -67,17 +67,18 @@ struct AllActs {
 };
 
 //
-// K split (S = 2): the grid holds one workgroup per (tile, block range) unit,
-// unit u = blockIdx.x being tile u / 2's blocks [nbs * (u % 2), ..): each
-// workgroup quantises only its range's activations and reads only its range's
-// weights, so a launch of few tiles fills twice the CUs. The two partial sums
-// of a tile's output meet in an exchange slot (gemv_tiled_split below).
+// K split (S = 2, 4 or 8 ranges): unit u = (tile u / S, block range u % S),
+// range r being blocks [r nb / S, (r + 1) nb / S); the grid is a multiple of
+// S, so the units bid, bid + grid, .. of a workgroup share its range, whose
+// activations it quantises once and whose weights alone it reads. A launch of
+// few tiles so fills S times the workgroups. The ranges' partial sums meet in
+// exchange slots (below, and gemv_tiled_ranges).
 template <int KIND, int MT, bool FUSED, int W, bool AREG, int NI, int D, int IT, bool LAZY = false, int S = 1>
 __global__ __launch_bounds__(W * 64) void gemv_tiled_kernel(const MfmaArgs p0) {
     constexpr int BB = block_bytes(KIND);
     constexpr int NR = MT / 4;
     static_assert(D >= 1 && D <= NI, "one to NI items in flight");
-    static_assert(S == 1 || S == 2, "unsplit, or two block ranges");
+    static_assert(S == 1 || S == 2 || S == 4 || S == 8, "unsplit, or 2, 4 or 8 block ranges");
     using Piece = typename PieceOf<KIND, true>::type;
     extern __shared__ __align__(16) uint8_t smem[];
     const int lane = threadIdx.x & 63;
@@ -86,10 +87,11 @@ __global__ __launch_bounds__(W * 64) void gemv_tiled_kernel(const MfmaArgs p0) {
     // p: the range's view of the activations (its blocks from b0); the tile
     // lookups read the members from p0 (a copy indexed at run time would live
     // in scratch memory)
-    const int sp = S > 1 ? bid % S : 0, b0 = sp * p0.nbs;
+    // range sp: blocks [sp nb / S, (sp + 1) nb / S), at most nbs = ceil(nb / S)
+    const int sp = S > 1 ? bid % S : 0, b0 = sp * p0.nb / S;
     MfmaArgs p = p0;
     if constexpr (S > 1) {
-        p.nb = min(p0.nbs, p0.nb - b0);
+        p.nb = (sp + 1) * p0.nb / S - b0;
         if constexpr (FUSED) p.x = p0.x + static_cast<int64_t>(b0) * kQK;
         else p.q8k = p0.q8k + static_cast<int64_t>(b0) * kQ8KBytes;
     }
@@ -196,32 +198,46 @@ __global__ __launch_bounds__(W * 64) void gemv_tiled_kernel(const MfmaArgs p0) {
         for (int lr = 0; lr < NR; ++lr) {
             float r = res[(kt * 64 + lane) * NR + lr];
             if constexpr (S > 1) {
-                // Each (tile, lane, register row) value meets its other range's
-                // in one slot, by one atomic swap that leaves this range's tag
-                // (gen * 2 + range) and value there. Finding the slot empty
-                // (0), the unit is first and stops. Finding the other range's
-                // tag of this launch, it is second: it adds the two values
-                // (two addends: the same sum in either order) and empties the
-                // slot, so every launch leaves the slots as it found them.
-                // Anything else (a slot not emptied by an earlier launch, or
-                // a launch sharing the workspace) gives NaN and sets the error
-                // word, never another value. Relaxed agent-scope atomics on
-                // one address are ordered for all workgroups of the device.
-                unsigned long long* slot = p0.split_slot + (static_cast<int64_t>(t) * 64 + lane) * NR + lr;
+                // The S ranges' values of each (tile, lane, register row) are
+                // added as a binary tree: at level L, node j = range >> (L + 1)
+                // has one slot where its two children's sums meet, by one
+                // atomic swap that leaves the child's tag (2 g + side, for
+                // the launch's generation g) and value there. Finding the slot
+                // empty (0), the child is first and stops. Finding the other
+                // side's tag of this launch, it is second: it adds the two
+                // values (two addends: the same sum in either order, so the
+                // tree's result is fixed), empties the slot and climbs; the
+                // root's second child writes the output. Every launch so
+                // leaves the slots as it found them. Anything else in a slot (one
+                // not emptied by an earlier launch, or a launch sharing the
+                // workspace) gives NaN at the output and the error word, never
+                // other bits. Relaxed agent-scope atomics on one address are
+                // ordered for all workgroups of the device.
                 const uint32_t g = p0.gen % 0x7fffffffu + 1u;  // tags 2 .. 2^32 - 1, never 0
-                const uint32_t mine = 2 * g + sp, other = 2 * g + (1 - sp);
-                const unsigned long long old = __hip_atomic_exchange(
-                    slot, static_cast<unsigned long long>(mine) << 32 | __float_as_uint(r), __ATOMIC_RELAXED,
-                    __HIP_MEMORY_SCOPE_AGENT);
-                const uint32_t tag = static_cast<uint32_t>(old >> 32);
-                if (old == 0) continue;  // first of the two
-                if (tag == other) {
+                bool first = false;
+                int64_t base = 0;
+#pragma unroll
+                for (int lv = 0; (1 << lv) < S; ++lv) {
+                    const int per = S >> (lv + 1), j = sp >> (lv + 1), side = (sp >> lv) & 1;
+                    unsigned long long* slot =
+                        p0.split_slot + base + ((static_cast<int64_t>(t) * per + j) * 64 + lane) * NR + lr;
+                    base += static_cast<int64_t>(p0.tiles) * per * 64 * NR;
+                    const unsigned long long old = __hip_atomic_exchange(
+                        slot, static_cast<unsigned long long>(2 * g + side) << 32 | __float_as_uint(r),
+                        __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    if (old == 0) {
+                        first = true;
+                        break;
+                    }
+                    __hip_atomic_store(slot, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    if (static_cast<uint32_t>(old >> 32) != 2 * g + (1 - side)) {
+                        r = __builtin_nanf("");
+                        __hip_atomic_store(p0.split_err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                        break;  // written now, as NaN
+                    }
                     r += __uint_as_float(static_cast<uint32_t>(old));
-                } else {
-                    r = __builtin_nanf("");
-                    __hip_atomic_store(p0.split_err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                 }
-                __hip_atomic_store(slot, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                if (first) continue;
             }
             const int mo = NR * q + lr;
             if (mo < m && row < to.rows)
@@ -388,29 +404,70 @@ int tiled_waves(int nb, int64_t tiles, int cus) {
 // workgroup per CU at most, each walking its tiles; one block in flight per
 // wave in the item loop, or the pipelined kernel where a wave has at most four
 // items and the launch at most 8 rows.
-// The K split of a tiled launch: for 2 to 8 activation rows over rows of 17 to
-// 31 blocks (8 waves, three or four block indices a wave unsplit), two block
-// ranges of at most 16 blocks, one workgroup per (tile, range) unit, which
-// doubles the workgroups of a launch of few tiles. TinyLlama down (Q6_K 2048 x
-// 5632, 128 tiles) at 4 rows: 6.58 -> 5.65 us. Rows of at most 16 blocks
-// (one or two block indices a wave) measured slower split (TinyLlama o,
-// 2048 x 2048: 3.50 -> 4.0 us): there the exchange costs more than the
-// second range's workgroups save. The slots follow the error word:
-// [error word, padding to 256 bytes][tiles][64 lanes][MT / 4 rows] x 8 bytes.
+// The K split of a tiled launch, by kind, rows and row length alone (so a
+// row's f32 order does not depend on the projections sharing the launch):
+// - 2 to 8 activation rows over rows of 17 to 31 blocks (8 waves with three or
+//   four block indices each unsplit): two ranges of 9-16 blocks, two block
+//   indices a wave. TinyLlama down (Q6_K 2048 x 5632, 128 tiles) at 4 rows:
+//   6.58 -> 5.42-5.65 us.
+// - 1 to 8 rows over rows of 32 to 64 blocks: 4 ranges (32 blocks) or 8, of at
+//   most 8 blocks, one block index a wave. Llama-3-8B down (Q6_K 4096 x 14336)
+//   at 1 / 4 / 8 rows 12.9 (raw rows) / 14.4 / 22.0 -> 12.4 / 12.6 / 16.4 us;
+//   its Q4_K form at 1 / 4 rows 11.3 (raw) / 12.7 -> 10.0 / 10.2; Llama-3.2-1B
+//   down (Q6_K 2048 x 8192) 7.05 (raw) / 7.8 -> 6.2 / 6.2.
+// Not split: rows of at most 16 blocks (one or two block indices a wave), which
+// measured slower in two ranges on 4 or 8 waves (TinyLlama o at 4 rows 3.50 ->
+// 3.92 us, gate+up 5.33 -> 6.73): there the exchange costs more than the
+// ranges' workgroups save; one row over 17-31 blocks, where Q6_K's raw LDS
+// stream stays faster; and rows of more than 64 blocks.
+// Workspace: the error word, padding to 256 bytes, then the tree's slots, level
+// by level: [level][tile][node][64 lanes][MT / 4 rows] x 8 bytes, S - 1 per
+// tile, lane and row.
 constexpr size_t kSplitSlotBase = 256;
-bool gemv_tiled_split(int kind, int m, int nb) {
-    return (kind == 4 || kind == 6) && m >= 2 && m <= 8 && nb >= 17 && nb <= 31;
+int gemv_tiled_ranges(int kind, int m, int nb) {
+    if ((kind != 4 && kind != 6) || m < 1 || m > 8) return 1;
+    if (m >= 2 && nb >= 17 && nb <= 31) return 2;
+    if (nb >= 32 && nb <= 64) return nb <= 32 ? 4 : 8;
+    return 1;
 }
+bool gemv_tiled_split(int kind, int m, int nb) { return gemv_tiled_ranges(kind, m, nb) > 1; }
 size_t gemv_tiled_split_bytes(int kind, int m, int nb, int64_t tiles) {
-    if (!gemv_tiled_split(kind, m, nb)) return 0;
-    return kSplitSlotBase + static_cast<size_t>(tiles) * 64 * (m <= 4 ? 1 : 2) * 8;
+    const int s = gemv_tiled_ranges(kind, m, nb);
+    if (s == 1) return 0;
+    return kSplitSlotBase + static_cast<size_t>(tiles) * 64 * (m <= 4 ? 1 : 2) * (s - 1) * 8;
 }
 
 namespace {
+// Split launches: ranges of 9-16 blocks (two ranges) take two block indices a
+// wave, the second quantised after the first item; ranges of at most 8 one.
+template <int KIND, int MT, bool FUSED, int S>
+void launch_split_s(int ni, const MfmaArgs& p, dim3 grid, size_t lds, hipStream_t stream) {
+    const dim3 block(8 * 64);
+    if (p.iters == 2) {
+        if constexpr (S == 2) {
+            if (ni == 2) gemv_tiled_kernel<KIND, MT, FUSED, 8, false, 2, 2, 2, true, 2><<<grid, block, lds, stream>>>(p);
+            else gemv_tiled_kernel<KIND, MT, FUSED, 8, false, 4, 1, 2, true, 2><<<grid, block, lds, stream>>>(p);
+        }
+    } else if (ni == 1) {
+        gemv_tiled_kernel<KIND, MT, FUSED, 8, true, 1, 1, 1, false, S><<<grid, block, lds, stream>>>(p);
+    } else if (ni == 2) {
+        gemv_tiled_kernel<KIND, MT, FUSED, 8, true, 2, 2, 1, false, S><<<grid, block, lds, stream>>>(p);
+    } else if (ni == 3) {
+        gemv_tiled_kernel<KIND, MT, FUSED, 8, true, 3, 2, 1, false, S><<<grid, block, lds, stream>>>(p);
+    } else {
+        gemv_tiled_kernel<KIND, MT, FUSED, 8, true, 4, 1, 1, false, S><<<grid, block, lds, stream>>>(p);
+    }
+}
 template <int KIND, int MT, bool FUSED>
-void launch_split(const MfmaArgs& p, dim3 grid, size_t lds, hipStream_t stream) {
-    // two block indices a wave, the second quantised after the first item
-    gemv_tiled_kernel<KIND, MT, FUSED, 8, false, 2, 2, 2, true, 2><<<grid, dim3(8 * 64), lds, stream>>>(p);
+void launch_split(int s, int ni, const MfmaArgs& p, dim3 grid, size_t lds, hipStream_t stream) {
+    if (s == 2) launch_split_s<KIND, MT, FUSED, 2>(ni, p, grid, lds, stream);
+    else if (s == 4) launch_split_s<KIND, MT, FUSED, 4>(ni, p, grid, lds, stream);
+    else launch_split_s<KIND, MT, FUSED, 8>(ni, p, grid, lds, stream);
+}
+template <int KIND, bool FUSED>
+void launch_split_k(int mt, int s, int ni, const MfmaArgs& p, dim3 grid, size_t lds, hipStream_t stream) {
+    if (mt == 4) launch_split<KIND, 4, FUSED>(s, ni, p, grid, lds, stream);
+    else launch_split<KIND, 8, FUSED>(s, ni, p, grid, lds, stream);
 }
 }  // namespace
 
@@ -420,26 +477,34 @@ int launch_gemv_tiled(int kind, bool fused, GemvParams& p, hipStream_t stream) {
     const int cus = device_cu_count();
     int64_t tiles = 0;
     for (int i = 0; i < p.count; ++i) tiles += (p.rows[i] + kTileRows - 1) / kTileRows;
-    if (gemv_tiled_split(kind, p.m, p.nb)) {
+    if (const int sr = gemv_tiled_ranges(kind, p.m, p.nb); sr > 1) {
         if (!p.split_ws || p.split_ws_bytes < gemv_tiled_split_bytes(kind, p.m, p.nb, tiles) ||
             reinterpret_cast<uintptr_t>(p.split_ws) % 256 != 0)
             return kStatusInvalid;
         MfmaArgs ka;
         if (mfma_args(p, 8, ka) != kStatusOk) return kStatusInvalid;
-        ka.nbs = (p.nb + 1) / 2;
-        ka.iters = 2;  // ranges of 9 to 16 blocks on 8 waves
+        ka.nbs = (p.nb + sr - 1) / sr;
+        ka.iters = (ka.nbs + 7) / 8;  // 8 waves: ranges of at most 8 blocks one a wave, of 9-16 two
+        if (ka.iters > 2 || (ka.iters == 2 && sr != 2)) return kStatusInvalid;
         ka.split_err = static_cast<uint32_t*>(p.split_ws);
         ka.split_slot = reinterpret_cast<unsigned long long*>(static_cast<uint8_t*>(p.split_ws) + kSplitSlotBase);
         ka.gen = next_split_generation();
-        const dim3 grid(static_cast<unsigned>(2 * ka.tiles));
-        const size_t lds = gemv_mfma_lds(mt, ka.nbs, 8) + static_cast<size_t>(2) * 64 * (mt / 4) * 4;
-        if (lds > static_cast<size_t>(kLdsMax)) return kStatusInvalid;
+        // (tile, range) units on a grid of a multiple of sr workgroups (so a
+        // workgroup's units share its range): one round on the CUs, or as
+        // many workgroups as keep a workgroup's items within 4
+        const int64_t units = static_cast<int64_t>(ka.tiles) * sr, upw = 4 / ka.iters;
+        int64_t wgs = std::min<int64_t>(units, cus) / sr * sr;
+        if ((units + wgs - 1) / wgs > upw) wgs = ((units + upw - 1) / upw + sr - 1) / sr * sr;
+        const int ni = static_cast<int>((units + wgs - 1) / wgs) * ka.iters;
+        const dim3 grid(static_cast<unsigned>(wgs));
+        const size_t lds = gemv_mfma_lds(mt, ka.nbs, 8) + static_cast<size_t>(std::min(ni, 4)) * 64 * (mt / 4) * 4;
+        if (lds > static_cast<size_t>(kLdsMax) || ni > 4) return kStatusInvalid;
         if (kind == 4) {
-            if (mt == 4) fused ? launch_split<4, 4, true>(ka, grid, lds, stream) : launch_split<4, 4, false>(ka, grid, lds, stream);
-            else fused ? launch_split<4, 8, true>(ka, grid, lds, stream) : launch_split<4, 8, false>(ka, grid, lds, stream);
+            if (fused) launch_split_k<4, true>(mt, sr, ni, ka, grid, lds, stream);
+            else launch_split_k<4, false>(mt, sr, ni, ka, grid, lds, stream);
         } else {
-            if (mt == 4) fused ? launch_split<6, 4, true>(ka, grid, lds, stream) : launch_split<6, 4, false>(ka, grid, lds, stream);
-            else fused ? launch_split<6, 8, true>(ka, grid, lds, stream) : launch_split<6, 8, false>(ka, grid, lds, stream);
+            if (fused) launch_split_k<6, true>(mt, sr, ni, ka, grid, lds, stream);
+            else launch_split_k<6, false>(mt, sr, ni, ka, grid, lds, stream);
         }
         return hipGetLastError() == hipSuccess ? kStatusOk : kStatusExec;
     }

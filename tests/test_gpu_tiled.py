@@ -41,9 +41,10 @@ def _check_vs_oracle(kind, w, k, n, x, got):
 
 
 def _split(kind, m, nb):
-    """Whether a tiled launch of m rows splits each tile's blocks in two ranges
-    (rocknpu_hip_gemv_q_f32_tiled): rows of 17-31 blocks at 2-8 rows."""
-    return kind in (4, 6) and 2 <= m <= 8 and 17 <= nb <= 31
+    """Whether a tiled launch of m rows splits each tile's blocks in ranges
+    (rocknpu_hip_gemv_q_f32_tiled): rows of 17-31 blocks at 2-8 rows, of
+    32-64 blocks at 1-8 rows."""
+    return kind in (4, 6) and ((2 <= m <= 8 and 17 <= nb <= 31) or (1 <= m <= 8 and 32 <= nb <= 64))
 
 
 def _same_order_as_raw(nb, m=16):
@@ -87,7 +88,10 @@ CASES = [
     (6, 14336, [4096], (1, 4, 5, 8)),
     (4, 5632, [2048, 300], (2, 3, 5, 8, 12)),  # 22 blocks: split at 2-8 rows, not at 12
     (6, 4352, [40, 2048], (2, 7)),             # 17 blocks: ranges of 9 and 8
-    (4, 7936, [33], (4,)),                     # 31 blocks: ranges of 16 and 15
+    (4, 7936, [33], (4,)),                     # 31 blocks: ranges of 15 and 16
+    (6, 8192, [2048], (1, 4)),                 # 32 blocks: 4 ranges of 8
+    (6, 8448, [300, 17], (1, 3, 8)),           # 33 blocks: 8 ranges of 4-5
+    (4, 16384, [64], (2,)),                    # 64 blocks: 8 ranges of 8
     (4, 512, [100], (1, 3)),
     (6, 256, [40], (1, 2)),
     (4, 2048, [1000, 17], (4, 13)),
