@@ -206,16 +206,18 @@ int rocknpu_hip_gemv_tile_weights(uint32_t kind, const uint8_t * w, size_t w_byt
  * fused, grouped and Q8_K-input calls agree bit for bit.
  *
  * K split: launches of 2 to 8 rows over rows of 17 to 31 blocks (K 4352 to
- * 7936, e.g. a 5632-wide down projection), and of 1 to 8 rows over rows of 32
- * to 64 blocks (K 8192 to 16384), split each 16-row tile's blocks into 2, 4
- * or 8 ranges on as many workgroups, whose partial sums meet in the workspace
+ * 7936, e.g. a 5632-wide down projection; 2 ranges up to 4 rows, 4 from 5),
+ * and of 1 to 8 rows over rows of 32 to 64 blocks (K 8192 to 16384; 4 ranges
+ * at 32 blocks, else 8), split each 16-row tile's blocks into ranges on as
+ * many workgroups, whose partial sums meet in the workspace
  * (rocknpu_hip_gemv_tiled_workspace_bytes for the call's m, k and total rows;
  * 256-byte aligned; zeroed before its first use). Such a row's sum is the
  * ranges' sums added pairwise in a fixed tree, the same bits in grouped,
  * separate, fused and Q8_K-input calls, but not those of the unsplit kernels. Every completed call leaves the
  * workspace as it found it; calls that share one must not overlap (one per
- * stream). A call that finds it not clear writes NaN where it did and sets
- * its error word (rocknpu_hip_gemv_tiled_workspace_check). Calls that do not
+ * stream). A call that finds it not clear sets its error word
+ * (rocknpu_hip_gemv_tiled_workspace_check) and writes NaN, or the exact
+ * value, where it did; never other bits. Calls that do not
  * split ignore workspace (it may be null); a split call without one large
  * enough returns ROCKNPU_STATUS_INVALID_ARGUMENT. No counterpart in the
  * reference. */

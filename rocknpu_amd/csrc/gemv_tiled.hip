@@ -210,9 +210,11 @@ __global__ __launch_bounds__(W * 64) void gemv_tiled_kernel(const MfmaArgs p0) {
                 // root's second child writes the output. Every launch so
                 // leaves the slots as it found them. Anything else in a slot (one
                 // not emptied by an earlier launch, or a launch sharing the
-                // workspace) gives NaN at the output and the error word, never
-                // other bits. Relaxed agent-scope atomics on one address are
-                // ordered for all workgroups of the device.
+                // workspace) sets the error word, and its finder writes NaN;
+                // the other side, if it swaps before the finder empties the
+                // slot, adds and writes the exact sum instead. Never other
+                // bits. Relaxed agent-scope atomics on one address are ordered
+                // for all workgroups of the device.
                 const uint32_t g = p0.gen % 0x7fffffffu + 1u;  // tags 2 .. 2^32 - 1, never 0
                 bool first = false;
                 int64_t base = 0;
@@ -407,9 +409,11 @@ int tiled_waves(int nb, int64_t tiles, int cus) {
 // The K split of a tiled launch, by kind, rows and row length alone (so a
 // row's f32 order does not depend on the projections sharing the launch):
 // - 2 to 8 activation rows over rows of 17 to 31 blocks (8 waves with three or
-//   four block indices each unsplit): two ranges of 9-16 blocks, two block
-//   indices a wave. TinyLlama down (Q6_K 2048 x 5632, 128 tiles) at 4 rows:
-//   6.58 -> 5.42-5.65 us.
+//   four block indices each unsplit): at up to 4 rows two ranges of 9-16
+//   blocks, two block indices a wave (TinyLlama down, Q6_K 2048 x 5632, 128
+//   tiles, at 4 rows: 6.58 -> 5.42-5.65 us; four ranges measure the same
+//   there), at 5-8 rows four ranges of 5-8 (at 8 rows 8.1 -> 7.7 us against
+//   two ranges).
 // - 1 to 8 rows over rows of 32 to 64 blocks: 4 ranges (32 blocks) or 8, of at
 //   most 8 blocks, one block index a wave. Llama-3-8B down (Q6_K 4096 x 14336)
 //   at 1 / 4 / 8 rows 12.9 (raw rows) / 14.4 / 22.0 -> 12.4 / 12.6 / 16.4 us;
@@ -426,7 +430,7 @@ int tiled_waves(int nb, int64_t tiles, int cus) {
 constexpr size_t kSplitSlotBase = 256;
 int gemv_tiled_ranges(int kind, int m, int nb) {
     if ((kind != 4 && kind != 6) || m < 1 || m > 8) return 1;
-    if (m >= 2 && nb >= 17 && nb <= 31) return 2;
+    if (m >= 2 && nb >= 17 && nb <= 31) return m <= 4 ? 2 : 4;
     if (nb >= 32 && nb <= 64) return nb <= 32 ? 4 : 8;
     return 1;
 }

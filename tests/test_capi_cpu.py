@@ -138,19 +138,19 @@ def test_tiled_decode_layout_host_side():
 
 
 def test_tiled_split_workspace_bytes_host_side():
-    """The tiled GEMV's K-split workspace (rows of 17-31 blocks at 2-8
-    activation rows): 256 bytes (the error word) and one 8-byte slot per
-    16-row tile, lane and register row (one for launches of up to 4 rows, two
-    for 5-8), sized by the call's largest launch; 0 where nothing splits."""
+    """The tiled GEMV's K-split workspace: 256 bytes (the error word) and
+    S - 1 8-byte slots (S ranges) per 16-row tile, lane and register row (one
+    for launches of up to 4 rows, two for 5-8), sized by the call's largest
+    launch; 0 where nothing splits."""
     lib = _lib.load()
     wsb = lib.rocknpu_hip_gemv_tiled_workspace_bytes
     tiles = 2048 // 16
     assert wsb(6, 4, 5632, 2048) == 256 + tiles * 64 * 8
     assert wsb(6, 2, 5632, 2048) == 256 + tiles * 64 * 8
-    assert wsb(6, 8, 5632, 2048) == 256 + tiles * 64 * 2 * 8
-    assert wsb(4, 5, 4352, 1000) == 256 + 63 * 64 * 2 * 8          # 17 blocks, ragged rows
-    assert wsb(6, 20, 5632, 2048) == 256 + tiles * 64 * 2 * 8      # launches of 8, 8 and 4 rows
-    assert wsb(6, 9, 5632, 2048) == 256 + tiles * 64 * 2 * 8       # 8 rows, then 1 (unsplit)
+    assert wsb(6, 8, 5632, 2048) == 256 + tiles * 64 * 2 * 3 * 8   # 5-8 rows: 4 ranges
+    assert wsb(4, 5, 4352, 1000) == 256 + 63 * 64 * 2 * 3 * 8      # 17 blocks, ragged rows
+    assert wsb(6, 20, 5632, 2048) == 256 + tiles * 64 * 2 * 3 * 8  # launches of 8, 8 and 4 rows
+    assert wsb(6, 9, 5632, 2048) == 256 + tiles * 64 * 2 * 3 * 8   # 8 rows, then 1 (unsplit)
     assert wsb(6, 1, 5632, 2048) == 0                              # one row of 22 blocks: unsplit
     assert wsb(4, 4, 2048, 2048) == 0                              # 8 blocks
     assert wsb(4, 4, 4096, 4096) == 0                              # 16 blocks

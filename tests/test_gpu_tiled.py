@@ -209,8 +209,10 @@ def test_split_grouped_equals_separate_and_q8k_input():
 
 def test_split_workspace_left_clear_and_dirty_detected():
     """Every completed split call leaves its workspace zero; a workspace with a
-    slot left set gives NaN (never other bits) where it is met, and the error
-    word, which the check clears; zeroed again, the call is exact."""
+    slot left set always sets the error word (the check clears it), and the
+    output there is NaN or, when the other range swaps between the finder's
+    swap and its emptying the slot, the exact sum: never other bits. Zeroed
+    again, the call is exact."""
     k, n, m = 5632, 2048, 4
     w = synth.kquant(6, n, k, index=3600)
     td = [hip.gemv_tile_weights(6, _dev(w), k, n)]
@@ -225,16 +227,16 @@ def test_split_workspace_left_clear_and_dirty_detected():
     assert not ws.any().item()
     assert hip.gemv_workspace_check(ws)
     # a slot left holding a value (tile 3, lane 5, which holds row 53 of
-    # activation row 0): the first arrival there finds a tag of no launch;
-    # that output is NaN, the rest exact
+    # activation row 0): the first arrival there finds a tag of no launch
     slots = ws[256:].view(torch.int64)
     slots[3 * 64 + 5] = (1 << 32) | 0x3F800000  # tag 1: no launch's (tags are 2 or more)
     print("split dirty call", flush=True)
     got = hip.gemv_q_f32_tiled(6, td, k, [n], xd, workspace=ws)[0].cpu().numpy()
-    bad = np.isnan(got)
-    assert bad.any() and not hip.gemv_workspace_check(ws)
-    assert np.array_equal(_bits(got[~bad]), _bits(ref[~bad]))
-    assert bad.sum() == 1  # lane 5 of tile 3: row 53 of activation row 0
+    assert not hip.gemv_workspace_check(ws)
+    at = np.zeros(got.shape, bool)
+    at[0, 3 * 16 + 5] = True
+    assert np.array_equal(_bits(got[~at]), _bits(ref[~at]))
+    assert np.isnan(got[at][0]) or _bits(got[at])[0] == _bits(ref[at])[0]
     ws.zero_()
     fixed = hip.gemv_q_f32_tiled(6, td, k, [n], xd, workspace=ws)[0].cpu().numpy()
     assert np.array_equal(_bits(fixed), _bits(ref)) and hip.gemv_workspace_check(ws)
