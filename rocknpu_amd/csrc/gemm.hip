@@ -337,7 +337,6 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_w8a8_dma_kernel(
         constexpr int PART = FM * FN * 16 * 64;  // ints of one wave's partial
         __shared__ int verdict;                  // 0: not last, 1: last, 2: dirty counters
         int32_t* mine = partials + (static_cast<int64_t>(t) * splits + split) * (WM * WN * PART) + wave * PART;
-        uint32_t* tile_stamps = stamps + static_cast<int64_t>(t) * splits;
 #pragma unroll
         for (int i = 0; i < FM; ++i)
 #pragma unroll
@@ -346,27 +345,29 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_w8a8_dma_kernel(
                 for (int e = 0; e < 16; ++e)
                     __hip_atomic_store(mine + ((i * FN + j) * 16 + e) * 64 + lane, acc[i][j][e], __ATOMIC_RELAXED,
                                        __HIP_MEMORY_SCOPE_AGENT);
-        // the arrival stamp goes out with the partials, and one wait covers
-        // both: every wave's partial and the stamp reach the device-coherent
-        // level before the count
-        if (threadIdx.x == 0) __hip_atomic_store(tile_stamps + split, gen, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        // every wave's partial has reached the device-coherent level before the count
         wait_vm<0>();
         __syncthreads();
+        uint32_t* tile_stamps = stamps + static_cast<int64_t>(t) * splits;
         if (threadIdx.x == 0) {
+            __hip_atomic_store(tile_stamps + split, gen, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            wait_vm<0>();  // the stamp, like the partials, lands before the count
             const uint32_t old = __hip_atomic_fetch_add(counters + t, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            verdict = old == static_cast<uint32_t>(splits - 1) ? 1 : old >= static_cast<uint32_t>(splits) ? 2 : 0;
+            int v = old == static_cast<uint32_t>(splits - 1) ? 1 : old >= static_cast<uint32_t>(splits) ? 2 : 0;
+            if (v == 1)  // every split of this call has counted in, or the count started dirty
+                for (int s2 = 0; s2 < splits; ++s2)
+                    if (__hip_atomic_load(tile_stamps + s2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != gen) v = 2;
+            if (v == 2)
+                __hip_atomic_store(counters + kSplitErrorWord, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            verdict = v;
         }
         __syncthreads();
-        int v = verdict;
+        const int v = verdict;
         if (v == 0) return;
-        if (v == 1) {
-            // every split of this call has counted in, or the count started
-            // dirty: the other splits' partials (which completed before their
-            // counts) and every stamp are read together, at device scope (past
-            // this XCD's L2); the stamps decide afterwards
-            uint32_t stamp_ok = 1;
-            if (threadIdx.x < splits)
-                stamp_ok = __hip_atomic_load(tile_stamps + threadIdx.x, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == gen;
+        poison = v == 2;
+        if (!poison) {
+            // the other splits counted in after their partials completed; read
+            // them at device scope (past this XCD's L2)
             for (int s2 = 0; s2 < splits; ++s2) {
                 if (s2 == split) continue;
                 int32_t* other =
@@ -380,19 +381,12 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_w8a8_dma_kernel(
                             acc[i][j][e] += __hip_atomic_load(other + ((i * FN + j) * 16 + e) * 64 + lane,
                                                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             }
-            if (!__syncthreads_and(static_cast<int>(stamp_ok))) v = 2;
-        }
-        if (v == 2) {
-            if (threadIdx.x == 0)
-                __hip_atomic_store(counters + kSplitErrorWord, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        } else {
             // a dirty tile keeps its state, so every later call on the
             // workspace reports it until the caller zeroes the workspace
             if (threadIdx.x < splits)
                 __hip_atomic_store(tile_stamps + threadIdx.x, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             if (threadIdx.x == 0) __hip_atomic_store(counters + t, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
-        poison = v == 2;
     }
 
     // Epilogue. lane l holds column l%32 of each 32x32 fragment, rows
