@@ -207,9 +207,8 @@ int rocknpu_hip_gemv_tile_weights(uint32_t kind, const uint8_t * w, size_t w_byt
  *
  * K split: launches of 2 to 8 rows over rows of 17 to 31 blocks (K 4352 to
  * 7936, e.g. a 5632-wide down projection; 2 ranges up to 4 rows, 4 from 5),
- * and of 1 to 8 rows over rows of 32 to 64 blocks (K 8192 to 16384; 4 ranges
- * at 32 blocks, else 8), split each 16-row tile's blocks into ranges on as
- * many workgroups, whose partial sums meet in the workspace
+ * and of 1 to 8 rows over rows of 32 to 64 blocks (K 8192 to 16384; 4
+ * ranges), split each 16-row tile's blocks into ranges on as many workgroups, whose partial sums meet in the workspace
  * (rocknpu_hip_gemv_tiled_workspace_bytes for the call's m, k and total rows;
  * 256-byte aligned; zeroed before its first use). Such a row's sum is the
  * ranges' sums added pairwise in a fixed tree, the same bits in grouped,
@@ -243,7 +242,7 @@ int rocknpu_hip_gemv_tiled_workspace_check(void * workspace, void * stream);
 /* Whether a decode GEMV of m activation rows over Q4_K (kind 4) or Q6_K
  * (kind 6) rows of K = k runs faster on the tiled copy (1) or on the raw rows
  * (0): the tiled copy from two rows, and at one row for Q4_K rows of 16 or more
- * blocks and Q6_K rows of 32 to 64 blocks (split in 4 or 8 ranges); other
+ * blocks and Q6_K rows of 32 to 64 blocks (split in 4 ranges); other
  * one-row launches keep the lane-per-block and LDS-stream kernels on raw rows.
  * Host code only. No counterpart in the reference. */
 int rocknpu_hip_gemv_tiled_preferred(uint32_t kind, size_t m, size_t k);

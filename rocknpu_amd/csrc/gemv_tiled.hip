@@ -414,11 +414,13 @@ int tiled_waves(int nb, int64_t tiles, int cus) {
 //   tiles, at 4 rows: 6.58 -> 5.42-5.65 us; four ranges measure the same
 //   there), at 5-8 rows four ranges of 5-8 (at 8 rows 8.1 -> 7.7 us against
 //   two ranges).
-// - 1 to 8 rows over rows of 32 to 64 blocks: 4 ranges (32 blocks) or 8, of at
-//   most 8 blocks, one block index a wave. Llama-3-8B down (Q6_K 4096 x 14336)
-//   at 1 / 4 / 8 rows 12.9 (raw rows) / 14.4 / 22.0 -> 12.4 / 12.6 / 16.4 us;
-//   its Q4_K form at 1 / 4 rows 11.3 (raw) / 12.7 -> 10.0 / 10.2; Llama-3.2-1B
-//   down (Q6_K 2048 x 8192) 7.05 (raw) / 7.8 -> 6.2 / 6.2.
+// - 1 to 8 rows over rows of 32 to 64 blocks: 4 ranges, one block index a
+//   wave: of 8 blocks on 8 waves at 32 blocks, of 9-16 on 16 waves above.
+//   Llama-3-8B down (Q6_K 4096 x 14336) at 1 / 4 / 8 rows 12.9 (raw rows) /
+//   14.4 / 22.0 -> 11.8 / 11.9 / 14.7 us (8 ranges of 7 blocks on 8 waves:
+//   12.3 / 12.5 / 16.3, one tree level more); its Q4_K form at 1 / 4 rows 11.3
+//   (raw) / 12.7 -> 9.6 / 9.7; Llama-3.2-1B down (Q6_K 2048 x 8192) 7.05 (raw)
+//   / 7.8 -> 6.2 / 6.2 (two ranges of 16 on 16 waves: the same).
 // Not split: rows of at most 16 blocks (one or two block indices a wave), which
 // measured slower in two ranges on 4 or 8 waves (TinyLlama o at 4 rows 3.50 ->
 // 3.92 us, gate+up 5.33 -> 6.73): there the exchange costs more than the
@@ -431,7 +433,7 @@ constexpr size_t kSplitSlotBase = 256;
 int gemv_tiled_ranges(int kind, int m, int nb) {
     if ((kind != 4 && kind != 6) || m < 1 || m > 8) return 1;
     if (m >= 2 && nb >= 17 && nb <= 31) return m <= 4 ? 2 : 4;
-    if (nb >= 32 && nb <= 64) return nb <= 32 ? 4 : 8;
+    if (nb >= 32 && nb <= 64) return 4;
     return 1;
 }
 bool gemv_tiled_split(int kind, int m, int nb) { return gemv_tiled_ranges(kind, m, nb) > 1; }
@@ -462,16 +464,24 @@ void launch_split_s(int ni, const MfmaArgs& p, dim3 grid, size_t lds, hipStream_
         gemv_tiled_kernel<KIND, MT, FUSED, 8, true, 4, 1, 1, false, S><<<grid, block, lds, stream>>>(p);
     }
 }
+template <int KIND, int MT, bool FUSED, int S>
+void launch_split_w16(int ni, const MfmaArgs& p, dim3 grid, size_t lds, hipStream_t stream) {
+    const dim3 block(16 * 64);
+    if (ni == 1) gemv_tiled_kernel<KIND, MT, FUSED, 16, true, 1, 1, 1, false, S><<<grid, block, lds, stream>>>(p);
+    else if (ni == 2) gemv_tiled_kernel<KIND, MT, FUSED, 16, true, 2, 2, 1, false, S><<<grid, block, lds, stream>>>(p);
+    else if (ni == 3) gemv_tiled_kernel<KIND, MT, FUSED, 16, true, 3, 2, 1, false, S><<<grid, block, lds, stream>>>(p);
+    else gemv_tiled_kernel<KIND, MT, FUSED, 16, true, 4, 1, 1, false, S><<<grid, block, lds, stream>>>(p);
+}
 template <int KIND, int MT, bool FUSED>
-void launch_split(int s, int ni, const MfmaArgs& p, dim3 grid, size_t lds, hipStream_t stream) {
-    if (s == 2) launch_split_s<KIND, MT, FUSED, 2>(ni, p, grid, lds, stream);
-    else if (s == 4) launch_split_s<KIND, MT, FUSED, 4>(ni, p, grid, lds, stream);
-    else launch_split_s<KIND, MT, FUSED, 8>(ni, p, grid, lds, stream);
+void launch_split(int s, int w, int ni, const MfmaArgs& p, dim3 grid, size_t lds, hipStream_t stream) {
+    if (w == 16) launch_split_w16<KIND, MT, FUSED, 4>(ni, p, grid, lds, stream);
+    else if (s == 2) launch_split_s<KIND, MT, FUSED, 2>(ni, p, grid, lds, stream);
+    else launch_split_s<KIND, MT, FUSED, 4>(ni, p, grid, lds, stream);
 }
 template <int KIND, bool FUSED>
-void launch_split_k(int mt, int s, int ni, const MfmaArgs& p, dim3 grid, size_t lds, hipStream_t stream) {
-    if (mt == 4) launch_split<KIND, 4, FUSED>(s, ni, p, grid, lds, stream);
-    else launch_split<KIND, 8, FUSED>(s, ni, p, grid, lds, stream);
+void launch_split_k(int mt, int s, int w, int ni, const MfmaArgs& p, dim3 grid, size_t lds, hipStream_t stream) {
+    if (mt == 4) launch_split<KIND, 4, FUSED>(s, w, ni, p, grid, lds, stream);
+    else launch_split<KIND, 8, FUSED>(s, w, ni, p, grid, lds, stream);
 }
 }  // namespace
 
@@ -485,10 +495,14 @@ int launch_gemv_tiled(int kind, bool fused, GemvParams& p, hipStream_t stream) {
         if (!p.split_ws || p.split_ws_bytes < gemv_tiled_split_bytes(kind, p.m, p.nb, tiles) ||
             reinterpret_cast<uintptr_t>(p.split_ws) % 256 != 0)
             return kStatusInvalid;
+        // waves: 8, with one block index each for ranges of at most 8 blocks
+        // and two for the 9-16 of two ranges; 16 with one each for the 9-16 of
+        // four ranges
         MfmaArgs ka;
-        if (mfma_args(p, 8, ka) != kStatusOk) return kStatusInvalid;
-        ka.nbs = (p.nb + sr - 1) / sr;
-        ka.iters = (ka.nbs + 7) / 8;  // 8 waves: ranges of at most 8 blocks one a wave, of 9-16 two
+        const int nbs = (p.nb + sr - 1) / sr, sw = sr == 4 && nbs > 8 ? 16 : 8;
+        if (mfma_args(p, sw, ka) != kStatusOk) return kStatusInvalid;
+        ka.nbs = nbs;
+        ka.iters = (nbs + sw - 1) / sw;
         if (ka.iters > 2 || (ka.iters == 2 && sr != 2)) return kStatusInvalid;
         ka.split_err = static_cast<uint32_t*>(p.split_ws);
         ka.split_slot = reinterpret_cast<unsigned long long*>(static_cast<uint8_t*>(p.split_ws) + kSplitSlotBase);
@@ -501,14 +515,14 @@ int launch_gemv_tiled(int kind, bool fused, GemvParams& p, hipStream_t stream) {
         if ((units + wgs - 1) / wgs > upw) wgs = ((units + upw - 1) / upw + sr - 1) / sr * sr;
         const int ni = static_cast<int>((units + wgs - 1) / wgs) * ka.iters;
         const dim3 grid(static_cast<unsigned>(wgs));
-        const size_t lds = gemv_mfma_lds(mt, ka.nbs, 8) + static_cast<size_t>(std::min(ni, 4)) * 64 * (mt / 4) * 4;
+        const size_t lds = gemv_mfma_lds(mt, ka.nbs, sw) + static_cast<size_t>(std::min(ni, 4)) * 64 * (mt / 4) * 4;
         if (lds > static_cast<size_t>(kLdsMax) || ni > 4) return kStatusInvalid;
         if (kind == 4) {
-            if (fused) launch_split_k<4, true>(mt, sr, ni, ka, grid, lds, stream);
-            else launch_split_k<4, false>(mt, sr, ni, ka, grid, lds, stream);
+            if (fused) launch_split_k<4, true>(mt, sr, sw, ni, ka, grid, lds, stream);
+            else launch_split_k<4, false>(mt, sr, sw, ni, ka, grid, lds, stream);
         } else {
-            if (fused) launch_split_k<6, true>(mt, sr, ni, ka, grid, lds, stream);
-            else launch_split_k<6, false>(mt, sr, ni, ka, grid, lds, stream);
+            if (fused) launch_split_k<6, true>(mt, sr, sw, ni, ka, grid, lds, stream);
+            else launch_split_k<6, false>(mt, sr, sw, ni, ka, grid, lds, stream);
         }
         return hipGetLastError() == hipSuccess ? kStatusOk : kStatusExec;
     }

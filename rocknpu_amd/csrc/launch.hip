@@ -269,8 +269,8 @@ extern "C" int rocknpu_hip_gemv_tile_weights(uint32_t kind, const uint8_t* w, si
 // at one row the raw-row kernels win for TinyLlama o (3.47 against 3.60 us),
 // gate+up (5.15 against 5.30) and down (Q6_K LDS stream, 5.6 against 6.9);
 // the tiled copy wins for Llama-3-8B gate+up (16 blocks per row: 13.3 against
-// 14.4 us), for Q6_K rows of 32-64 blocks, split in 4 or 8 ranges (Llama-3-8B
-// down 12.4 against 12.9-13.1 us, Llama-3.2-1B down 6.2 against 7.05), and
+// 14.4 us), for Q6_K rows of 32-64 blocks, split in 4 ranges (Llama-3-8B down
+// 11.8 against 12.9-13.1 us, Llama-3.2-1B down 6.2 against 7.05), and
 // from two rows on every shape (TinyLlama o at 4 rows 3.63 against 4.19 us,
 // gate+up 5.32 against 7.48, down 5.42 against 7.90).
 extern "C" int rocknpu_hip_gemv_tiled_preferred(uint32_t kind, size_t m, size_t k) {

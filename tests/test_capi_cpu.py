@@ -154,11 +154,11 @@ def test_tiled_split_workspace_bytes_host_side():
     assert wsb(6, 1, 5632, 2048) == 0                              # one row of 22 blocks: unsplit
     assert wsb(4, 4, 2048, 2048) == 0                              # 8 blocks
     assert wsb(4, 4, 4096, 4096) == 0                              # 16 blocks
-    # 32-64 blocks from one row: 4 or 8 ranges, a tree of S - 1 slots
+    # 32-64 blocks from one row: 4 ranges, a tree of 3 slots
     assert wsb(6, 4, 8192, 2048) == 256 + tiles * 64 * 3 * 8       # 32 blocks: 4 ranges
-    assert wsb(6, 1, 14336, 4096) == 256 + 256 * 64 * 7 * 8        # 56 blocks: 8 ranges
-    assert wsb(6, 8, 14336, 4096) == 256 + 256 * 64 * 2 * 7 * 8    # 56 blocks, 8 rows
-    assert wsb(4, 8, 16384, 4096) == 256 + 256 * 64 * 7 * 8        # 64 blocks: launches of 4 rows
+    assert wsb(6, 1, 14336, 4096) == 256 + 256 * 64 * 3 * 8        # 56 blocks: 4 ranges
+    assert wsb(6, 8, 14336, 4096) == 256 + 256 * 64 * 2 * 3 * 8    # 56 blocks, 8 rows
+    assert wsb(4, 8, 16384, 4096) == 256 + 256 * 64 * 3 * 8        # 64 blocks: launches of 4 rows
     assert wsb(6, 4, 16640, 4096) == 0                             # 65 blocks: unsplit
     assert wsb(4, 12, 5632, 2048) == 0                             # 9-16 rows (Q4_K): unsplit
     assert wsb(5, 4, 5632, 2048) == 0 and wsb(6, 4, 5000, 2048) == 0

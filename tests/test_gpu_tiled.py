@@ -89,9 +89,9 @@ CASES = [
     (4, 5632, [2048, 300], (2, 3, 5, 8, 12)),  # 22 blocks: split at 2-8 rows, not at 12
     (6, 4352, [40, 2048], (2, 7)),             # 17 blocks: ranges of 9 and 8
     (4, 7936, [33], (4,)),                     # 31 blocks: ranges of 15 and 16
-    (6, 8192, [2048], (1, 4)),                 # 32 blocks: 4 ranges of 8
-    (6, 8448, [300, 17], (1, 3, 8)),           # 33 blocks: 8 ranges of 4-5
-    (4, 16384, [64], (2,)),                    # 64 blocks: 8 ranges of 8
+    (6, 8192, [2048], (1, 4)),                 # 32 blocks: 4 ranges of 8 on 8 waves
+    (6, 8448, [300, 17], (1, 3, 8)),           # 33 blocks: 4 ranges of 8-9 on 16 waves
+    (4, 16384, [64], (2,)),                    # 64 blocks: 4 ranges of 16 on 16 waves
     (4, 512, [100], (1, 3)),
     (6, 256, [40], (1, 2)),
     (4, 2048, [1000, 17], (4, 13)),
