@@ -385,20 +385,21 @@ void launch_tiled_kind(int mt, int w, int ni, const MfmaArgs& p, dim3 grid, size
 }
 }  // namespace
 
-// Waves per workgroup of a tiled launch. A row's f32 order must not depend on
-// how many projections share the launch (grouped and separate calls agree bit
-// for bit), so where the wave count changes the order it follows from the row
-// length alone: rows of more than 16 blocks take 16 waves from 32 blocks
-// (Llama-3-8B down, 4096 x 14336: 14.3 us against 16.4 with 8) and 8 below
-// (TinyLlama down, 2048 x 5632: 6.9 against 7.4 us with 16). Rows of at most
-// 16 blocks give the same bits with 8 or 16 waves (tile_row_sum), so there the
-// launch's tiles decide: 16 waves for 16-block rows making four or more tiles
-// per CU (Llama-3-8B gate+up, 2 x 14336 x 4096: 13.3 against 18.3 us), else 8.
-// Rows shorter than 8 blocks leave waves without a block; they compute block
-// nb - 1 and drop it, adding +0.0 to the row's sum.
-int tiled_waves(int nb, int64_t tiles, int cus) {
+// Waves per workgroup of a tiled launch, from the row length alone (a row's f32
+// order must not depend on how many projections share the launch, so grouped
+// and separate calls agree bit for bit): 8 up to 8 blocks a row, 16 from 9.
+// Rows of at most 16 blocks give the same bits with 8 or 16 waves (with 16,
+// tile_row_sum adds waves s and s + 8 first, which is the 8-wave order), and 16
+// measured faster for every such row (Llama-3-8B q/o, 4096 x 4096, at one row
+// 5.11 -> 4.67 us, q/k/v 6.75 -> 5.90, gate+up 18.3 -> 13.3; 3072-wide rows: q/o
+// at 4 rows 4.67 -> 4.31, gate+up 2 x 8192 11.1 -> 8.1). Longer rows take 16
+// from 32 blocks (Llama-3-8B down unsplit 16.4 -> 14.3 us) and 8 for 17-31
+// (TinyLlama down 6.9 against 7.4 us with 16), where the split launches take
+// over from two rows. Rows shorter than 8 blocks leave waves without a block;
+// they compute block nb - 1 and drop it, adding +0.0 to the row's sum.
+int tiled_waves(int nb) {
     if (nb > 16) return nb >= 32 ? 16 : 8;
-    return nb == 16 && tiles >= 4 * int64_t{cus} ? 16 : 8;
+    return nb >= 9 ? 16 : 8;
 }
 
 // The matrix-core GEMV on tiled weights (p.w[i] each a tiled copy of its
@@ -526,7 +527,7 @@ int launch_gemv_tiled(int kind, bool fused, GemvParams& p, hipStream_t stream) {
         }
         return hipGetLastError() == hipSuccess ? kStatusOk : kStatusExec;
     }
-    const int w = tiled_waves(p.nb, tiles, cus);
+    const int w = tiled_waves(p.nb);
     MfmaArgs ka;
     if (mfma_args(p, w, ka) != kStatusOk) return kStatusInvalid;
     const int wgs = std::min(ka.tiles, cus);

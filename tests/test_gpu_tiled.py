@@ -86,6 +86,8 @@ CASES = [
     (4, 4096, [4096, 1024, 1024], (3, 6)),
     (6, 4096, [1000], (2, 7)),
     (6, 14336, [4096], (1, 4, 5, 8)),
+    (4, 3072, [3072, 100], (3, 4, 9)),        # 12 blocks on 16 waves (4 without a block)
+    (6, 2560, [500], (2, 8)),                  # 10 blocks on 16 waves
     (4, 5632, [2048, 300], (2, 3, 5, 8, 12)),  # 22 blocks: split at 2-8 rows, not at 12
     (6, 4352, [40, 2048], (2, 7)),             # 17 blocks: ranges of 9 and 8
     (4, 7936, [33], (4,)),                     # 31 blocks: ranges of 15 and 16
