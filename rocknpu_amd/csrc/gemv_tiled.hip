@@ -530,7 +530,16 @@ int launch_gemv_tiled(int kind, bool fused, GemvParams& p, hipStream_t stream) {
     const int w = tiled_waves(p.nb);
     MfmaArgs ka;
     if (mfma_args(p, w, ka) != kStatusOk) return kStatusInvalid;
-    const int wgs = std::min(ka.tiles, cus);
+    // one round of workgroups on the CUs; but eight-wave launches of one block
+    // index a wave and more than four tiles a CU get a workgroup per four
+    // tiles (two on some CUs), so the pipelined kernel takes them instead of
+    // the item loop: the 32000 x 2048 Q6_K head at 1/4/8 rows 12.1/12.5/13.8
+    // -> 11.4/11.6/12.3 us, the 128256 x 2048 one 41.0/44.2/48.3 ->
+    // 38.8/41.6/46.4 us. Fewer tiles a workgroup than four measured slower
+    // there, and so did this for 16-wave launches (Llama-3-8B gate+up,
+    // 2 x 14336 x 4096, one row: 13.4 -> 15.5 us).
+    int wgs = std::min(ka.tiles, cus);
+    if (w == 8 && mt <= 8 && ka.iters == 1 && ka.tiles > 4 * wgs) wgs = (ka.tiles + 3) / 4;
     const dim3 grid(static_cast<unsigned>(wgs));
     const int ni = (ka.tiles + wgs - 1) / wgs * ka.iters;
     const size_t lds_loop = gemv_mfma_lds(mt, p.nb, w);

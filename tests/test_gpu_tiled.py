@@ -75,7 +75,7 @@ def test_tile_weights_equal_the_restatement(kind, k, n):
 # (16 waves, seven tiles per workgroup: the item loop) and down (16 waves, four
 # blocks per wave; at 5-8 rows the item loop), rows shorter than eight blocks,
 # a single block, ragged N; 9-16 activation rows run the item loop on 16-row
-# register tiles.
+# register tiles; launches of more than four tiles a CU on eight waves.
 CASES = [
     (4, 2048, [2048], (1, 2, 3, 4, 8, 16)),
     (4, 2048, [2048, 256, 256], (2, 4, 5, 9)),
@@ -97,6 +97,8 @@ CASES = [
     (4, 512, [100], (1, 3)),
     (6, 256, [40], (1, 2)),
     (4, 2048, [1000, 17], (4, 13)),
+    (6, 2048, [32000], (1, 4, 8)),             # 2000 tiles: a workgroup per four (pipelined)
+    (4, 2048, [8192, 8192, 2000], (3, 4)),     # 1149 tiles: the same, bits of the raw rows
 ]
 
 
