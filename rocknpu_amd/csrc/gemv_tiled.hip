@@ -330,7 +330,11 @@ namespace {
 // tiles per workgroup at 4 rows: 5.32 us against 5.51 with one and 5.42 with
 // three; TinyLlama down, 2048 x 5632 on 8 waves, three blocks per wave: 6.95
 // against 7.46 with one), one for four (Llama-3-8B down, 4096 x 14336 on 16
-// waves: 14.8 against 14.8-15.1 us with two or four).
+// waves: 14.8 against 14.8-15.1 us with two or four; the 32000 x 2048 Q6_K
+// head, two eight-wave workgroups on most CUs: 11.4 against 11.9 / 12.5 us),
+// but two for four on eight waves with one workgroup per CU (Llama-3.2-1B
+// gate+up, 2 x 8192 x 2048, four tiles per workgroup: 6.0 against 6.3 us at
+// one row, 6.9 against 7.3 at eight).
 template <int KIND, int MT, bool FUSED, int W>
 void launch_pipe(int ni, int iters, const MfmaArgs& p, dim3 grid, size_t lds, hipStream_t stream) {
     const dim3 block(W * 64);
@@ -338,6 +342,8 @@ void launch_pipe(int ni, int iters, const MfmaArgs& p, dim3 grid, size_t lds, hi
         if (ni == 1) gemv_tiled_kernel<KIND, MT, FUSED, W, true, 1, 1, 1><<<grid, block, lds, stream>>>(p);
         else if (ni == 2) gemv_tiled_kernel<KIND, MT, FUSED, W, true, 2, 2, 1><<<grid, block, lds, stream>>>(p);
         else if (ni == 3) gemv_tiled_kernel<KIND, MT, FUSED, W, true, 3, 2, 1><<<grid, block, lds, stream>>>(p);
+        else if (W == 8 && static_cast<int>(grid.x) <= device_cu_count())
+            gemv_tiled_kernel<KIND, MT, FUSED, W, true, 4, 2, 1><<<grid, block, lds, stream>>>(p);
         else gemv_tiled_kernel<KIND, MT, FUSED, W, true, 4, 1, 1><<<grid, block, lds, stream>>>(p);
     } else if (iters == 2) {
         // block index 1 quantised after item 0's terms (Llama-3-8B q/o, 4096 x
