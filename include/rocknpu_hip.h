@@ -139,6 +139,16 @@ int rocknpu_hip_matmul_w8a8_f32_noalloc(const float * a, size_t m, size_t k, siz
  * NPU tiles are fixed by the register-command programs. */
 int rocknpu_hip_gemm_route(size_t m, size_t n, size_t k_pad, int cus, int * bm, int * bn, int * stages);
 
+/* Whether rocknpu_hip_gemm_w8a8 runs an M x N x k_pad product (M > 256) as two
+ * launches on a GPU of `cus` compute units (cus <= 0: the current device's):
+ * *n0 > 0 when the 256 x 256 tiles make one or more whole rounds plus a last
+ * round at most half full; columns [0, *n0) then run on 256 x 256 tiles and
+ * [*n0, N) as a product of their own (rocknpu_hip_gemm_route of M x (N - *n0)
+ * x k_pad). *n0 = 0: one launch on rocknpu_hip_gemm_route's tile. Host code
+ * only; the results are the same bits either way. No counterpart in the
+ * reference. */
+int rocknpu_hip_gemm_column_split(size_t m, size_t n, size_t k_pad, int cus, size_t * n0);
+
 /* The launch shape rocknpu_hip_gemv_q_f32 (fused != 0) or rocknpu_hip_gemv_q8_k
  * (fused == 0) takes for `count` projections of n[i] rows, K = k and m
  * activation rows on `cus` compute units (cus <= 0: the current device's), for

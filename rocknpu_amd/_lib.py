@@ -64,6 +64,7 @@ SIGNATURES = {
     "rocknpu_hip_quantize_a8": (_i, [_vp, _sz, _sz, _sz, _sz, _vp, _vp, _vp]),
     "rocknpu_hip_gemm_w8a8": (_i, [_vp, _vp, _vp, _vp, _sz, _sz, _sz, _vp, _sz, _vp, _vp]),
     "rocknpu_hip_gemm_route": (_i, [_sz, _sz, _sz, _i, _vp, _vp, _vp]),
+    "rocknpu_hip_gemm_column_split": (_i, [_sz, _sz, _sz, _i, _vp]),
     "rocknpu_hip_gemm_w8a8_ws": (_i, [_vp, _vp, _vp, _vp, _sz, _sz, _sz, _vp, _sz, _vp, _vp, _sz, _vp]),
     "rocknpu_hip_gemm_workspace": (_i, [_sz, _sz, _sz, _i, _vp, _vp]),
     "rocknpu_hip_gemm_workspace_check": (_i, [_vp, _vp]),

@@ -42,6 +42,9 @@ struct GemmTile {
     int splits = 1;
 };
 GemmTile gemm_route(int m, int n, int k, int cus);  // gemm.hip
+// Columns of the first of two launches that launch_gemm_w8a8 splits an
+// M x N x K product into (0: one launch). gemm.hip.
+int gemm_column_split(int m, int n, int k, int cus);
 // A K-split workspace starts with a fixed 16 KiB block: kSplitCounters tile
 // counters (whatever the shape, so a workspace reused for other shapes never
 // finds another shape's partials in its counters) and, in its last word, a

@@ -162,6 +162,15 @@ extern "C" int rocknpu_hip_gemm_workspace_check(void* workspace, void* stream) {
     return rk::kStatusExec;
 }
 
+extern "C" int rocknpu_hip_gemm_column_split(size_t m, size_t n, size_t k_pad, int cus, size_t* n0) {
+    if (!n0 || m == 0 || n == 0 || k_pad == 0 || k_pad % 64 != 0 || m > INT_MAX || n > INT_MAX || k_pad > INT_MAX)
+        return rk::kStatusInvalid;
+    if (cus <= 0) cus = rk::device_cu_count();
+    *n0 = static_cast<size_t>(
+        rk::gemm_column_split(static_cast<int>(m), static_cast<int>(n), static_cast<int>(k_pad), cus));
+    return rk::kStatusOk;
+}
+
 extern "C" int rocknpu_hip_gemm_route(size_t m, size_t n, size_t k_pad, int cus, int* bm, int* bn, int* stages) {
     if (!bm || !bn || !stages || m == 0 || n == 0 || k_pad == 0 || k_pad % 64 != 0 || m > INT_MAX || n > INT_MAX ||
         k_pad > INT_MAX)

@@ -174,3 +174,48 @@ def test_workspace_and_tile_bad_arguments():
     assert lib.rocknpu_hip_gemm_w8a8_tile(64, 32, 4, 2, *args, p, small, None) == -1
     assert lib.rocknpu_hip_gemm_w8a8_ws(*args, ctypes.c_void_p((1 << 20) + 16), 4096, None) == -1  # unaligned
     assert lib.rocknpu_hip_gemm_w8a8_ws(*args, None, 4096, None) == -1
+
+
+def column_split(m, n, k, cus=CUS):
+    n0 = ctypes.c_size_t()
+    assert _lib.load().rocknpu_hip_gemm_column_split(m, n, k, cus, ctypes.byref(n0)) == 0
+    return n0.value
+
+
+@pytest.mark.parametrize("m,n,k,expect", [
+    # whole rounds of 256 x 256 tiles plus a last round at most half full: the
+    # whole rounds' columns as one launch, the rest as a second
+    (4096, 14336, 4096, 12288),   # 896 tiles: 3 rounds + 128 (Llama-3-8B gate/up at 4096 tokens)
+    (1536, 11264, 4096, 10752),   # 264 tiles: 1 round + 8
+    (1536, 14336, 2048, 10752),   # 336 tiles: 1 round + 80
+    (768, 28672, 2048, 21760),    # 336 tiles
+    (4096, 5632, 4096, 4096),     # 352 tiles: 1 round + 96
+    (2048, 28672, 4096, 24576),   # 896 tiles: 3 rounds + 128, exactly half full
+    # one launch: the last round more than half full, no whole round, whole
+    # rounds only, or M <= 256
+    (1024, 28672, 4096, 0),       # 448 tiles: 1 round + 192
+    (4096, 11264, 2048, 0),       # 704 tiles: 2 rounds + 192
+    (2048, 5632, 4096, 0),        # 176 tiles: less than a round
+    (4096, 28672, 4096, 0),       # 1792 tiles: 7 whole rounds
+    (256, 28672, 2048, 0),
+    (4096, 256, 4096, 0),
+])
+def test_column_split(m, n, k, expect):
+    assert column_split(m, n, k) == expect
+
+
+def test_column_split_invariants():
+    for m, n in itertools.product((257, 512, 1000, 1536, 2048, 3000, 4096, 8192), range(256, 40000, 768)):
+        n0 = column_split(m, n, 2048)
+        t = tiles(m, n, 256, 256)
+        if n0 == 0:
+            continue
+        assert n0 % 256 == 0 and 0 < n0 < n
+        main = tiles(m, n0, 256, 256)
+        assert main % CUS == 0 or main <= CUS * (t // CUS)    # whole rounds' worth at most
+        assert t // CUS >= 1 and 2 * (t - CUS * (t // CUS)) <= CUS
+    lib = _lib.load()
+    n0 = ctypes.c_size_t()
+    assert lib.rocknpu_hip_gemm_column_split(0, 64, 64, CUS, ctypes.byref(n0)) == -1
+    assert lib.rocknpu_hip_gemm_column_split(4, 64, 100, CUS, ctypes.byref(n0)) == -1
+    assert lib.rocknpu_hip_gemm_column_split(4096, 14336, 4096, CUS, None) == -1
