@@ -256,7 +256,8 @@ def w8a8_gemm(torch, hip, synth, m: int, n: int, k: int, reps: int, rotate_bytes
     byts = n * kp + m * kp + 4 * (m + n) + 4 * m * n
     tops = ops / (per * 1e-3) / 1e12
     bound_tops = min(INT8_PEAK_TOPS, HBM_PEAK_GBS * ops / byts / 1e3)
-    return {"m": m, "n": n, "k": k, "k_splits": hip.gemm_workspace(m, n, kp)[1], "us": round(per * 1e3, 3),
+    return {"m": m, "n": n, "k": k, "k_splits": hip.gemm_workspace(m, n, kp)[1],
+            "column_split": hip.gemm_column_split(m, n, kp), "us": round(per * 1e3, 3),
             "tops": round(tops, 2),
             "frac_int8_peak": round(tops / INT8_PEAK_TOPS, 4),
             "roofline_tops": round(bound_tops, 1), "frac_roofline": round(tops / bound_tops, 4),

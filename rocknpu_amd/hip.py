@@ -82,6 +82,14 @@ def gemm_workspace(m: int, n: int, k_pad: int, cus: int = 0) -> tuple[int, int]:
     return nb.value, sp.value
 
 
+def gemm_column_split(m: int, n: int, k_pad: int, cus: int = 0) -> int:
+    """Columns of the first of the two launches the GEMM runs an m x n x k_pad
+    product as (0: one launch); rocknpu_hip_gemm_column_split."""
+    n0 = ctypes.c_size_t()
+    _check(_lib.load().rocknpu_hip_gemm_column_split(m, n, k_pad, cus, ctypes.byref(n0)), "gemm_column_split")
+    return n0.value
+
+
 # Zeroed K-split workspaces, one per (device, stream): the GEMM leaves them
 # zeroed, so each is zeroed once, when it is made. Calls on one stream are
 # ordered with each other, so they can share its workspace; calls on other
