@@ -645,17 +645,19 @@ size_t gemm_workspace_bytes(const GemmTile& tile, int m, int n) {
 }
 
 bool gemm_split_supported() {
-    static int cached[64] = {};  // 0 unknown, 1 yes, 2 no
+    static std::atomic<int> cached[64] = {};  // 0 unknown, 1 yes, 2 no (host threads may ask at once)
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return false;
-    if (cached[dev] == 0) {
+    int v = cached[dev].load(std::memory_order_relaxed);
+    if (v == 0) {
         hipDeviceProp_t prop{};
         const bool ok = hipGetDeviceProperties(&prop, dev) == hipSuccess &&
                         std::strncmp(prop.gcnArchName, "gfx950", 6) == 0 &&
                         (prop.gcnArchName[6] == '\0' || prop.gcnArchName[6] == ':');
-        cached[dev] = ok ? 1 : 2;
+        v = ok ? 1 : 2;
+        cached[dev].store(v, std::memory_order_relaxed);
     }
-    return cached[dev] == 1;
+    return v == 1;
 }
 
 // The GEMM on a given tile, stage count and split (splits > 1 needs a

@@ -2,6 +2,7 @@
 // checks, then one enqueue per kernel. Every shape and alignment the kernels
 // assume is checked here, before anything reaches the GPU.
 #include <algorithm>
+#include <atomic>
 #include <climits>
 
 #include "common.h"
@@ -15,15 +16,16 @@ int launch_quantize_q8_k(const float* x, int64_t m, int64_t k, int64_t ldx, uint
 int launch_gemv(int kind, bool fused, GemvParams& p, hipStream_t stream);
 
 int device_cu_count() {
-    static int cached[64] = {};
+    // per device, filled on first use; atomic, as host threads may ask at once
+    static std::atomic<int> cached[64] = {};
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-    if (cached[dev] == 0) {
-        int n = 0;
+    int n = cached[dev].load(std::memory_order_relaxed);
+    if (n == 0) {
         if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
-        cached[dev] = n;
+        cached[dev].store(n, std::memory_order_relaxed);
     }
-    return cached[dev];
+    return n;
 }
 }  // namespace rk
 
