@@ -492,9 +492,13 @@ int launch_dma(const int8_t* a8, int64_t lda, const int8_t* w8, int64_t ldw, con
                int64_t ldoi, int splits, uint8_t* workspace, hipStream_t stream) {
     // 128-byte stages need K % 128 == 0 (a stage never reads past a row)
     if constexpr (KB != 64)
-        if (k % KB != 0)
-            return launch_dma<BM, BN, WM, WN, (ST < 4 ? 4 : ST), 64>(a8, lda, w8, ldw, as, ws, m, n, k, out, ldo, oi,
-                                                                     ldoi, splits, workspace, stream);
+        if (k % KB != 0) {
+            if constexpr (BM >= 64)
+                return launch_dma<BM, BN, WM, WN, (ST < 4 ? 4 : ST), 64>(a8, lda, w8, ldw, as, ws, m, n, k, out, ldo,
+                                                                         oi, ldoi, splits, workspace, stream);
+            else
+                return kStatusInvalid;
+        }
     const int64_t tiles = static_cast<int64_t>((m + BM - 1) / BM) * ((n + BN - 1) / BN);
     const SplitK sk =
         split_k(k / KB, workspace && tiles <= kSplitCounters && gemm_split_supported() ? splits : 1);
@@ -545,10 +549,16 @@ GemmTile gemm_tile(int m, int n, int k, int cus);
 //
 // By M (times on MI355X):
 // - <= 16: the weight-streaming kernel while its A8 rows fit its LDS.
-// - <= 64: 64 x 32 tiles (for M = 32, N = 5632, K = 2048 they take 7.6 us
-//   against 18.5 us for register-staged 32 x 64 tiles); 64 x 64 with four
-//   stages when 64 x 32 tiles do not fit but those do (32 x 11264 x 2048:
-//   13.8 -> 9.7 us).
+// - <= 64: 64 x 32 tiles with four stages when they fit (for M = 32, N =
+//   5632, K = 2048 they take 7.6 us against 18.5 us for register-staged 32 x
+//   64 tiles). Else, up to 32 rows (K % 128 == 0), 32 x 64 direct-load tiles
+//   with four stages: half the activation rows per tile (32 x 28672 x 4096:
+//   31.8 -> 28.4 us; 17 x 32000 x 2048 18.4 -> 15.7; 32 x 11264 x 2048 8.6
+//   -> 8.2; 17 x 32000 x 2048 against 64 x 64 tiles 16.1 against 16.9 us);
+//   from 33 rows 64 x 64 tiles, four stages while they are at most 1.75 per
+//   CU (64 x 28672 x 4096, 448 tiles: 34.5 -> 31.1 us), else two (64 x 32000
+//   x 2048, 500 tiles: 17.9 against 19.2 us with four; 64 x 128256 x 2048:
+//   77.3 -> 62.0 us).
 // - <= 128: 128 x 64 with four stages when 64 x 64 tiles do not fit but those
 //   do (128 x 11264 x 2048: 15.5 -> 11.8 us); 128 x 128 with three stages when
 //   64 x 64 tiles would be more than three per CU, 128 x 64 tiles do not fit
@@ -577,9 +587,12 @@ GemmTile gemm_tile(int m, int n, int k, int cus);
 //
 // K split (with a workspace): when the chosen tiles are at most 64 x 64 and
 // fill at most half the CUs, each tile's K range is split over
-// min(cus / tiles, stages / 8, 4) workgroups, so the units fill the CUs with
-// at least 8 stages each (128 x 2048 x 2048: 8.19 -> 7.56 us; 128 x 2048 x
-// 5632: 13.6 -> 10.7 us; 128 x 2048 x 8192: 18.1 -> 12.9 us). Larger tiles,
+// min(cus / tiles, stages / 10, 3) workgroups, so the units fill the CUs with
+// at least 10 stages each: K of 4096 and more (128 x 2048 x 4096: 10.9 ->
+// 10.2 us; 128 x 2048 x 5632: 13.6 -> 11.7; 128 x 2048 x 8192: 18.0 -> 13.8;
+// 32 x 2048 x 5632 in three: 13.2 -> 10.5), but not 2048 (128 x 2048 x 2048:
+// 6.6 unsplit against 8.0 in two; 32 x 2560 x 2048: 7.3 against 8.4), and
+// at most three (32 x 2560 x 4096: 9.8 against 10.6 in four). Larger tiles,
 // and tiles filling more than half the CUs, measured slower split (128 x 5632
 // x 2048 on 176 64 x 64 tiles: 8.4 -> 12.0 us at two splits; 1024 x 8192 x
 // 4096 on 128 256 x 256 tiles: 58.5 -> 63.9 us).
@@ -589,7 +602,7 @@ GemmTile gemm_route(int m, int n, int k, int cus) {
     const int64_t tiles = static_cast<int64_t>((m + r.bm - 1) / r.bm) * ((n + r.bn - 1) / r.bn);
     const int stages = k % 128 == 0 ? k / 128 : k / 64;
     if (2 * tiles > cus || tiles > kSplitCounters) return r;
-    const int s = static_cast<int>(std::min<int64_t>(std::min(cus / tiles, static_cast<int64_t>(stages / 8)), 4));
+    const int s = static_cast<int>(std::min<int64_t>(std::min(cus / tiles, static_cast<int64_t>(stages / 10)), 3));
     if (s >= 2) r.splits = s;
     return r;
 }
@@ -607,8 +620,10 @@ GemmTile gemm_tile(int m, int n, int k, int cus) {
     };
     if (m <= 16 && k % 64 == 0 && static_cast<int64_t>(m) * k <= kSkinnyMaxA8) return GemmTile{0, 0, 0};
     if (m <= 64) {
-        if (tiles(64, 32) > cus && tiles(64, 64) <= cus) return GemmTile{64, 64, 4};
-        return by_tiles(64, 32);
+        if (tiles(64, 32) <= cus) return GemmTile{64, 32, 4};
+        if (m <= 32 && k % 128 == 0) return GemmTile{32, 64, 4};
+        if (4 * tiles(64, 64) <= 7 * static_cast<int64_t>(cus)) return GemmTile{64, 64, 4};
+        return GemmTile{64, 64, 2};
     }
     if (m <= 128) {
         if (tiles(64, 64) > cus && tiles(128, 64) <= cus) return GemmTile{128, 64, 4};
@@ -670,6 +685,7 @@ int launch_gemm_w8a8_tile(const GemmTile& r, const int8_t* a8, int64_t lda, cons
 #define RK_GEMM(BM, BN, WM, WN, ST) \
     launch_dma<BM, BN, WM, WN, ST, 128>(a8, lda, w8, ldw, as, ws, m, n, k, out, ldo, oi, ldoi, sp, workspace, stream)
     if (r.bm == 0) return launch_gemm_w8a8_skinny(a8, lda, w8, ldw, as, ws, m, n, k, out, ldo, oi, ldoi, stream);
+    if (r.bm == 32 && r.bn == 64) return RK_GEMM(32, 64, 1, 2, 4);
     if (r.bm == 64 && r.bn == 32) return r.stages == 2 ? RK_GEMM(64, 32, 2, 1, 2) : RK_GEMM(64, 32, 2, 1, 4);
     if (r.bm == 64) return r.stages == 2 ? RK_GEMM(64, 64, 2, 2, 2) : RK_GEMM(64, 64, 2, 2, 4);
     if (r.bm == 128 && r.bn == 64) return r.stages == 2 ? RK_GEMM(128, 64, 4, 1, 2) : RK_GEMM(128, 64, 4, 1, 4);

@@ -30,8 +30,15 @@ def tiles(m, n, bm, bn):
     (16, 40, 7232, (64, 32, 4)),
     # up to 64 rows
     (24, 5632, 2048, (64, 32, 4)),
-    (32, 11264, 2048, (64, 64, 4)),      # 64x32 tiles do not fit, 64x64 do
-    (64, 16500, 128, (64, 32, 2)),       # neither fits
+    (40, 11264, 2048, (64, 64, 4)),      # 64x32 tiles do not fit, 64x64 do
+    (32, 11264, 2048, (32, 64, 4)),      # up to 32 rows: 32x64 tiles (8.6 -> 8.2 us)
+    (32, 28672, 4096, (32, 64, 4)),      # 31.8 -> 28.4 us
+    (17, 32000, 2048, (32, 64, 4)),      # 18.4 -> 15.7 us
+    (32, 28672, 4160, (64, 64, 4)),      # K % 128 != 0: no 32-row tiles
+    (64, 28672, 4096, (64, 64, 4)),      # 448 64x64 tiles, two per CU: 34.5 -> 31.1 us
+    (64, 32000, 2048, (64, 64, 2)),      # 500 tiles, more than 1.75 per CU: 17.9 against 19.2 us
+    (64, 128256, 2048, (64, 64, 2)),     # 77.3 -> 62.0 us
+    (64, 16500, 128, (64, 64, 4)),
     # up to 128 rows
     (128, 5632, 2048, (64, 64, 4)),      # the 5632 x 2048 Q4_K weight at 128 tokens
     (128, 2048, 2048, (64, 32, 4)),
@@ -74,12 +81,18 @@ def test_invariants_over_a_grid():
             assert m <= 16 and m * k <= 112 * 1024
             continue
         assert not (m <= 16 and m * k <= 112 * 1024)
-        assert (bm, bn) in {(64, 32), (64, 64), (128, 64), (128, 128), (256, 128), (256, 256)}
+        assert (bm, bn) in {(32, 64), (64, 32), (64, 64), (128, 64), (128, 128), (256, 128), (256, 256)}
         t = tiles(m, n, bm, bn)
-        # tile height follows M: 64 rows up to 64, at most 128 up to 256, more only above
-        assert bm == 64 or m > 64
+        # tile height follows M: 32 or 64 rows up to 64, at most 128 up to 256, more only above
+        assert bm in (32, 64) or m > 64
         assert bm <= 128 or m > 256
-        if bm <= 128 and (bm, bn) != (128, 128):
+        if (bm, bn) == (32, 64):
+            # up to 32 rows where 64x32 tiles do not fit, 128-byte stages only
+            assert m <= 32 and k % 128 == 0 and st == 4 and tiles(m, n, 64, 32) > CUS
+        elif m <= 64 and (bm, bn) == (64, 64):
+            # four stages while at most 1.75 per CU
+            assert (st == 4) == (4 * t <= 7 * CUS), (m, n, k, st)
+        elif bm <= 128 and (bm, bn) != (128, 128):
             # two stages exactly when the tiles outnumber the CUs (two per CU)
             assert (st == 2) == (t > CUS), (m, n, k, bm, bn, st)
             assert st in (2, 4)
@@ -111,11 +124,15 @@ def workspace(m, n, k, cus=CUS):
 
 @pytest.mark.parametrize("m,n,k,splits", [
     # 64 x 32 tiles on half the CUs, long K: split so the units fill the CUs
-    (128, 2048, 2048, 2),    # TinyLlama o at 128 tokens: 8.19 -> 7.56 us
-    (128, 2048, 5632, 2),    # TinyLlama down: 13.6 -> 10.7 us
-    (128, 2048, 8192, 2),    # Llama-3.2-1B down: 18.1 -> 12.9 us
+    (128, 2048, 4096, 2),    # 10.9 -> 10.2 us
+    (128, 2048, 5632, 2),    # TinyLlama down: 13.6 -> 11.7 us
+    (128, 2048, 8192, 2),    # Llama-3.2-1B down: 18.0 -> 13.8 us
     (64, 4096, 14336, 2),
-    (32, 2048, 8192, 4),     # 32 tiles: four splits of 16 stages
+    (32, 2048, 5632, 3),     # 32 tiles: at most three splits (13.2 -> 10.5 us)
+    (32, 2560, 4096, 3),     # 9.8 us against 10.6 in four
+    (32, 2048, 8192, 3),
+    (128, 2048, 2048, 1),    # 16 stages: 6.6 us unsplit against 8.0 in two (TinyLlama o at 128 tokens)
+    (32, 2560, 2048, 1),     # 7.3 against 8.4
     # measured slower split, or not under-filled: unsplit
     (128, 5632, 2048, 1),    # 176 64 x 64 tiles (8.4 against 12.0 us split)
     (128, 2560, 2048, 1),    # 160 tiles: more than half the CUs
