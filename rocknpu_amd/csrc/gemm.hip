@@ -563,10 +563,14 @@ GemmTile gemm_tile(int m, int n, int k, int cus);
 //   do (128 x 11264 x 2048: 15.5 -> 11.8 us); 128 x 128 with three stages when
 //   64 x 64 tiles would be more than three per CU, 128 x 64 tiles do not fit
 //   and those do (the TinyLlama head, 128 x 32000 x 2048: 28.4 -> 23.8 us with
-//   1000 64 x 64 tiles against 250);
-//   else the filling choice without 128-row tiles.
+//   1000 64 x 64 tiles against 250), two per CU when they do not fit either
+//   (the Llama-3.2-1B head, 128 x 128256 x 2048: 95.6 -> 71.3 us against 64 x
+//   64 tiles two per CU); else the filling choice without 128-row tiles.
 // - <= 256: 128 x 128 with three stages when 128 x 64 tiles do not fit but
-//   those do (256 x 11264 x 2048: 19.1 -> 15.5 us); else the filling choice.
+//   those do (256 x 11264 x 2048: 19.1 -> 15.5 us); the rules below when
+//   128 x 128 tiles do not fit (256 x 28672 x 2048 on 256 x 128 tiles: 40.8 ->
+//   22.6 us; 256 x 128256 x 2048 on 256 x 256: 138.7 -> 90.5); else the
+//   filling choice.
 // - above, with a 256 x 256 tile per CU: 256 x 256 tiles, or 256 x 128 tiles
 //   with eight waves and three stages when their rounds cost less (a round of
 //   them takes about 0.61 of a round of 256 x 256 tiles; 2048 x 11264 x 2048:
@@ -627,12 +631,14 @@ GemmTile gemm_tile(int m, int n, int k, int cus) {
     }
     if (m <= 128) {
         if (tiles(64, 64) > cus && tiles(128, 64) <= cus) return GemmTile{128, 64, 4};
-        if (tiles(64, 64) > 3 * cus && tiles(128, 64) > cus && tiles(128, 128) <= cus) return GemmTile{128, 128, 3};
+        if (tiles(64, 64) > 3 * cus && tiles(128, 64) > cus)
+            return GemmTile{128, 128, tiles(128, 128) <= cus ? 3 : 2};
         return filling(false);
     }
     if (m <= 256) {
         if (tiles(128, 64) > cus && tiles(128, 128) <= cus) return GemmTile{128, 128, 3};
-        return filling(true);
+        // 128 x 128 tiles that do not fit: the rules of longer products below
+        if (tiles(128, 128) <= cus) return filling(true);
     }
     if (tiles(256, 256) >= cus) {
         if (rounds(tiles(256, 128), 1) * 61 < rounds(tiles(256, 256), 1) * 100) return GemmTile{256, 128, 3};

@@ -49,7 +49,11 @@ def tiles(m, n, bm, bn):
     (256, 11264, 2048, (128, 128, 3)),
     (256, 14336, 4096, (128, 128, 3)),
     (200, 2048, 2048, (64, 32, 4)),
-    (250, 16500, 128, (128, 64, 2)),
+    (250, 16500, 128, (256, 128, 3)),    # 128x128 tiles do not fit: the longer products' rules
+    (256, 28672, 2048, (256, 128, 3)),   # 40.8 -> 22.6 us against 128x64 two per CU
+    (256, 32000, 2048, (256, 128, 3)),   # 42.9 -> 24.5 us
+    (256, 128256, 2048, (256, 256, 2)),  # 138.7 -> 90.5 us
+    (128, 128256, 2048, (128, 128, 2)),  # the Llama-3.2-1B head: 95.6 -> 71.3 us against 64x64
     # above: one 256 x 256 tile per CU or more
     (4096, 14336, 4096, (256, 256, 2)),  # 4 rounds against 7 x 0.61 of 256x128
     (8192, 8192, 8192, (256, 256, 2)),
@@ -83,9 +87,10 @@ def test_invariants_over_a_grid():
         assert not (m <= 16 and m * k <= 112 * 1024)
         assert (bm, bn) in {(32, 64), (64, 32), (64, 64), (128, 64), (128, 128), (256, 128), (256, 256)}
         t = tiles(m, n, bm, bn)
-        # tile height follows M: 32 or 64 rows up to 64, at most 128 up to 256, more only above
+        # tile height follows M: 32 or 64 rows up to 64, at most 128 up to 128, 256 from 129 rows
+        # only where 128x128 tiles do not fit
         assert bm in (32, 64) or m > 64
-        assert bm <= 128 or m > 256
+        assert bm <= 128 or m > 256 or (m > 128 and tiles(m, n, 128, 128) > CUS)
         if (bm, bn) == (32, 64):
             # up to 32 rows where 64x32 tiles do not fit, 128-byte stages only
             assert m <= 32 and k % 128 == 0 and st == 4 and tiles(m, n, 64, 32) > CUS
