@@ -251,9 +251,10 @@ int rocknpu_hip_gemv_tiled_workspace_check(void * workspace, void * stream);
 
 /* Whether a decode GEMV of m activation rows over Q4_K (kind 4) or Q6_K
  * (kind 6) rows of K = k runs faster on the tiled copy (1) or on the raw rows
- * (0): the tiled copy from two rows, and at one row for Q4_K rows of 16 or more
- * blocks and Q6_K rows of 32 to 64 blocks (split in 4 ranges); other
- * one-row launches keep the lane-per-block and LDS-stream kernels on raw rows.
+ * (0): the tiled copy from two rows; at one row for Q4_K rows of 9-16 blocks
+ * or 32 and more, and Q6_K rows of 8-16 blocks or 32-64; other one-row
+ * launches (rows of 17-31 blocks, shorter rows) keep the lane-per-block and
+ * LDS-stream kernels on raw rows.
  * Host code only. No counterpart in the reference. */
 int rocknpu_hip_gemv_tiled_preferred(uint32_t kind, size_t m, size_t k);
 

@@ -277,18 +277,29 @@ extern "C" int rocknpu_hip_gemv_tile_weights(uint32_t kind, const uint8_t* w, si
                                         tiled, static_cast<hipStream_t>(stream));
 }
 
-// Measured on the decode shapes (HIP graph, weights rotating through > 1 GB):
-// at one row the raw-row kernels win for TinyLlama o (3.47 against 3.60 us),
-// gate+up (5.15 against 5.30) and down (Q6_K LDS stream, 5.6 against 6.9);
-// the tiled copy wins for Llama-3-8B gate+up (16 blocks per row: 13.3 against
-// 14.4 us), for Q6_K rows of 32-64 blocks, split in 4 ranges (Llama-3-8B down
-// 11.8 against 12.9-13.1 us, Llama-3.2-1B down 6.2 against 7.05), and
-// from two rows on every shape (TinyLlama o at 4 rows 3.63 against 4.19 us,
-// gate+up 5.32 against 7.48, down 5.42 against 7.90).
+// Measured on the decode shapes of TinyLlama, Llama-3.2-1B and Llama-3-8B and
+// on rows of 2-20 blocks (HIP graph, weights rotating through > 1 GB): from
+// two rows the tiled copy wins on every shape (TinyLlama o at 4 rows 3.57
+// against 4.21 us, gate+up 6.0 against 8.5 at Llama-3.2-1B size, down 5.42
+// against 7.90). At one row:
+// - rows of 9-16 blocks (16 waves, one block index each) and of 32-64 (split
+//   in four ranges) run faster tiled, Q4_K and Q6_K alike (Q4_K 2560 x 2560
+//   4.16 against 7.33 us, 3072-wide gate+up 7.8 against 9.2; Q6_K 3072 x 3072
+//   4.63 against 5.66, 4096 x 4096 5.36 against 6.46; Llama-3-8B down 11.8
+//   against 12.4), and so do Q6_K rows of 8 blocks (2048 x 2048 3.74 against
+//   5.09 on the raw rows' LDS stream);
+// - rows of 17-31 blocks keep the raw rows (TinyLlama down, Q6_K on the LDS
+//   stream, 5.3 against 6.7 tiled; Q4_K 2048 x 5632 4.71 against 6.08), as
+//   do Q4_K rows of at most 8 blocks (TinyLlama o 3.47 against 3.56, gate+up
+//   5.15 against 5.30) and Q6_K rows of fewer than 8 (512-1024 wide: 3.49
+//   against 3.63-3.69).
 extern "C" int rocknpu_hip_gemv_tiled_preferred(uint32_t kind, size_t m, size_t k) {
     if ((kind != 4 && kind != 6) || m == 0 || k == 0 || k % rk::kQK != 0) return 0;
+    if (m >= 2) return 1;
     const size_t nb = k / rk::kQK;
-    return m >= 2 || (kind == 4 && nb >= 16) || (kind == 6 && nb >= 32 && nb <= 64) ? 1 : 0;
+    if (nb >= 17 && nb <= 31) return 0;
+    if (kind == 4) return nb >= 9 ? 1 : 0;
+    return nb >= 8 && nb <= 64 ? 1 : 0;
 }
 
 namespace {

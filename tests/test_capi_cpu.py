@@ -137,6 +137,20 @@ def test_tiled_decode_layout_host_side():
     assert lib.rocknpu_hip_gemv_q_f32_tiled(4, 1, w_arr, b_arr, n_arr, 256, p, 256, 1, o_arr, l_arr, None, 0, None) == -1
 
 
+@pytest.mark.parametrize("kind,m,k,tiled", [
+    (4, 2, 2048, 1), (6, 4, 5632, 1), (4, 8, 256, 1),       # from two rows: always the tiled copy
+    (4, 1, 2048, 0),                                         # TinyLlama o / gate+up: 8 blocks, raw
+    (4, 1, 2560, 1), (4, 1, 4096, 1),                        # 9-16 blocks: tiled
+    (4, 1, 5632, 0), (6, 1, 5632, 0), (6, 1, 7936, 0),       # 17-31 blocks: raw
+    (4, 1, 8192, 1), (6, 1, 14336, 1), (4, 1, 28672, 1),     # 32 and more (Q6_K up to 64): tiled
+    (6, 1, 16640, 0),                                        # Q6_K beyond 64 blocks: raw
+    (6, 1, 2048, 1), (6, 1, 4096, 1), (6, 1, 1024, 0),       # Q6_K: tiled from 8 blocks
+    (4, 1, 1024, 0), (5, 2, 2048, 0), (4, 1, 100, 0),        # short Q4_K rows raw; no Q5_K; K % 256
+])
+def test_tiled_rule_host_side(kind, m, k, tiled):
+    assert _lib.load().rocknpu_hip_gemv_tiled_preferred(kind, m, k) == tiled
+
+
 def test_tiled_split_workspace_bytes_host_side():
     """The tiled GEMV's K-split workspace: 256 bytes (the error word) and
     S - 1 8-byte slots (S ranges) per 16-row tile, lane and register row (one

@@ -6,7 +6,7 @@ import numpy as np
 import pytest
 
 from oracle import oracle as orc
-from rocknpu_amd import synth
+from rocknpu_amd import hip, synth
 from rocknpu_amd.capi import STATUS_INVALID_ARGUMENT, STATUS_OK, Context
 
 pytestmark = pytest.mark.gpu
@@ -285,7 +285,9 @@ def test_w8_sidecar_get_converts_writes_and_reloads(tmp_path):
 
 def test_decode_cache_stats_count_the_q8k_route():
     """The Q8_K decode route's resident raw blocks are decode-cache entries:
-    entries, resident bytes, hits and misses move with its calls."""
+    entries, resident bytes, hits and misses move with its calls (a weight the
+    one-row rule reads tiled, here the 8-block Q6_K one, also holds its tiled
+    copy)."""
     k, n = 2048, 96
     w4 = synth.q4_k(n, k, index=1720)
     w6 = synth.q6_k(n, k, index=1721)
@@ -303,7 +305,9 @@ def test_decode_cache_stats_count_the_q8k_route():
         outs = [np.empty((1, n), np.float32) for _ in range(2)]
         assert c.matmul_q_q8k_group([w4, w6], [4, 6], [n, n], x, outs, k) == STATUS_OK
         s3 = c.decode_cache_stats()
-        assert (s3.entries, s3.resident_bytes, s3.misses, s3.hits) == (2, w4.nbytes + w6.nbytes, 2, 1)
+        assert not hip.gemv_tiled_preferred(4, 1, k) and hip.gemv_tiled_preferred(6, 1, k)
+        tiled6 = hip.gemv_tiled_bytes(6, k, n)
+        assert (s3.entries, s3.resident_bytes, s3.misses, s3.hits) == (2, w4.nbytes + w6.nbytes + tiled6, 2, 1)
         assert s3.miss_ns > 0 and s3.hit_ns > 0 and s3.worker1_calls == 3
 
 
