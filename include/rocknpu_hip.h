@@ -88,9 +88,10 @@ int rocknpu_hip_gemm_workspace(size_t m, size_t n, size_t k_pad, int cus, size_t
  * NULL workspace. No counterpart in the reference. */
 int rocknpu_hip_gemm_workspace_check(void * workspace, void * stream);
 
-/* The W8A8 GEMM on a given tile (bm x bn: 64x32 and 64x64 with 2 or 4 stages,
- * 128x64 with 2 or 4, 128x128 with 2 or 3, 256x128 with 3, 256x256 with 2;
- * bm = 0: the weight-streaming kernel, m <= 16) and K split (1 to 16; above 1
+/* The W8A8 GEMM on a given tile (bm x bn: 32x64 with 4 stages, k_pad % 128
+ * == 0 only; 64x32 and 64x64 with 2 or 4 stages, 128x64 with 2 or 4, 128x128
+ * with 2 or 3, 256x128 with 3, 256x256 with 2; bm = 0: the weight-streaming
+ * kernel, m <= 16) and K split (1 to 16; above 1
  * the workspace must be a zeroed one of rocknpu_hip_gemm_w8a8_ws's layout: the
  * 16 KiB counter block, one counter per tile and at most 4095 tiles, then
  * splits x bm x bn int32 per tile, then splits x tiles stamps rounded up to

@@ -123,7 +123,7 @@ extern "C" int rocknpu_hip_gemm_w8a8_tile(int bm, int bn, int stages, int splits
                        (bm == 128 && bn == 64 && (stages == 2 || stages == 4)) ||
                        (bm == 128 && bn == 128 && (stages == 2 || stages == 3)) ||
                        (bm == 256 && bn == 128 && stages == 3) || (bm == 256 && bn == 256 && stages == 2) ||
-                       (bm == 32 && bn == 64 && stages == 4);
+                       (bm == 32 && bn == 64 && stages == 4 && k_pad % 128 == 0);
     if (!known || splits < 1 || splits > 16) return rk::kStatusInvalid;
     rk::GemmTile r{bm, bn, stages};
     r.splits = bm == 0 ? 1 : splits;
