@@ -113,11 +113,10 @@ __device__ __forceinline__ void unroll_seq(F&& f, std::integer_sequence<int, I..
 #endif
 template <int BM, int BN, int WM, int WN, int ST, int KB, bool SK>
 __global__ __launch_bounds__(WM* WN * 64) void gemm_w8a8_dma_kernel(
-    const int8_t* __restrict__ a8, int64_t lda, const int8_t* __restrict__ w8, int64_t ldw,
-    const float* __restrict__ a_scales, const float* __restrict__ w_scales, int m, int n, int k,
-    float* __restrict__ out, int64_t ldo, int32_t* __restrict__ out_i32, int64_t ldo_i32, int splits,
-    int k_split, int32_t* __restrict__ partials, uint32_t* __restrict__ counters, uint32_t* __restrict__ stamps,
-    uint32_t gen) {
+    const int8_t* __restrict__ a8, int64_t lda, const int8_t* __restrict__ w8, int64_t ldw, int m, int n, int k,
+    int splits, int k_split, const float* __restrict__ a_scales, const float* __restrict__ w_scales,
+    float* __restrict__ out, int64_t ldo, int32_t* __restrict__ out_i32, int64_t ldo_i32,
+    int32_t* __restrict__ partials, uint32_t* __restrict__ counters, uint32_t* __restrict__ stamps, uint32_t gen) {
     using Cfg = DmaTile<BM, BN, WM, WN, KB>;
     constexpr int TM = BM / WM, TN = BN / WN;
     constexpr int FM = TM / 32, FN = TN / 32;  // 32x32 fragments
@@ -508,12 +507,13 @@ int launch_dma(const int8_t* a8, int64_t lda, const int8_t* w8, int64_t ldw, con
         uint32_t* stamps = reinterpret_cast<uint32_t*>(partials + tiles * sk.splits * BM * BN);
         gemm_w8a8_dma_kernel<BM, BN, WM, WN, ST, KB, true>
             <<<dim3(static_cast<unsigned>(tiles * sk.splits)), dim3(WM * WN * 64), 0, stream>>>(
-                a8, lda, w8, ldw, as, ws, m, n, k, out, ldo, oi, ldoi, sk.splits, sk.stages_per * KB, partials,
+                a8, lda, w8, ldw, m, n, k, sk.splits, sk.stages_per * KB, as, ws, out, ldo, oi, ldoi, partials,
                 counters, stamps, next_split_generation());
     } else {
         gemm_w8a8_dma_kernel<BM, BN, WM, WN, ST, KB, false><<<dim3(static_cast<unsigned>(tiles)), dim3(WM * WN * 64), 0,
-                                                              stream>>>(a8, lda, w8, ldw, as, ws, m, n, k, out, ldo,
-                                                                        oi, ldoi, 1, k, nullptr, nullptr, nullptr, 0);
+                                                              stream>>>(a8, lda, w8, ldw, m, n, k, 1, k, as, ws,
+                                                                        out, ldo, oi, ldoi, nullptr, nullptr, nullptr,
+                                                                        0);
     }
     return hipGetLastError() == hipSuccess ? kStatusOk : kStatusExec;
 }

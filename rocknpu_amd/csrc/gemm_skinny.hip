@@ -31,9 +31,9 @@ constexpr int kSkinnyWaves = 8;
 
 template <int D>
 __global__ __launch_bounds__(kSkinnyWaves * 64) void gemm_w8a8_skinny_kernel(
-    const int8_t* __restrict__ a8, int64_t lda, const int8_t* __restrict__ w8, int64_t ldw,
-    const float* __restrict__ a_scales, const float* __restrict__ w_scales, int m, int n, int k,
-    float* __restrict__ out, int64_t ldo, int32_t* __restrict__ out_i32, int64_t ldo_i32) {
+    const int8_t* __restrict__ a8, int64_t lda, const int8_t* __restrict__ w8, int64_t ldw, int m, int n, int k,
+    const float* __restrict__ a_scales, const float* __restrict__ w_scales, float* __restrict__ out, int64_t ldo,
+    int32_t* __restrict__ out_i32, int64_t ldo_i32) {
     constexpr int W = kSkinnyWaves;
     extern __shared__ __align__(16) uint8_t smem[];
     const int lane = threadIdx.x & 63;
@@ -157,11 +157,11 @@ int launch_gemm_w8a8_skinny(const int8_t* a8, int64_t lda, const int8_t* w8, int
     const int per_wave = (tiles + wgs - 1) / wgs * iters;
     const dim3 grid(static_cast<unsigned>(wgs)), block(kSkinnyWaves * 64);
     if (per_wave >= 8)
-        gemm_w8a8_skinny_kernel<8><<<grid, block, lds, stream>>>(a8, lda, w8, ldw, as, ws, m, n, k, out, ldo, oi, ldoi);
+        gemm_w8a8_skinny_kernel<8><<<grid, block, lds, stream>>>(a8, lda, w8, ldw, m, n, k, as, ws, out, ldo, oi, ldoi);
     else if (per_wave >= 4)
-        gemm_w8a8_skinny_kernel<4><<<grid, block, lds, stream>>>(a8, lda, w8, ldw, as, ws, m, n, k, out, ldo, oi, ldoi);
+        gemm_w8a8_skinny_kernel<4><<<grid, block, lds, stream>>>(a8, lda, w8, ldw, m, n, k, as, ws, out, ldo, oi, ldoi);
     else
-        gemm_w8a8_skinny_kernel<2><<<grid, block, lds, stream>>>(a8, lda, w8, ldw, as, ws, m, n, k, out, ldo, oi, ldoi);
+        gemm_w8a8_skinny_kernel<2><<<grid, block, lds, stream>>>(a8, lda, w8, ldw, m, n, k, as, ws, out, ldo, oi, ldoi);
     return hipGetLastError() == hipSuccess ? kStatusOk : kStatusExec;
 }
 

@@ -337,6 +337,61 @@ struct GemvArgs {
     int wave_major;   // row groups dealt to waves across the workgroups first (else workgroup by workgroup)
 };
 
+// The fields of GemvArgs that a launch's first loads need, passed ahead of it
+// as scalar kernel arguments (14 dwords, preloaded in SGPRs; the struct itself
+// is read from the argument segment, a memory round trip at the start of
+// every wave): the activations (f32 or Q8_K), the first three members'
+// weights and rows, and the counts packed. A launch with a fourth member is
+// split on the host, so a workgroup's member is one of three.
+struct LaneHead {
+    const void* x;
+    const uint8_t* w0;
+    const uint8_t* w1;
+    const uint8_t* w2;
+    int rows0, rows1, rows2;
+    int wg_ends;  // the members' workgroup ends, 10 bits each: e0 | e1 << 10 | e2 << 20
+    int counts;   // nb | iters << 10 | m << 20 | log2g << 24 | wave_major << 27
+    int ldx;
+};
+#define RK_LANE_HEAD(h) h.x, h.w0, h.w1, h.w2, h.rows0, h.rows1, h.rows2, h.wg_ends, h.counts, h.ldx
+// The workgroup's member on the device: its weights, rows and workgroup
+// range [wg0, wg1), and (by the same selects) which member it is.
+struct LaneMember {
+    const uint8_t* w;
+    int rows, wg0, wg1;
+    bool c1, c2;
+};
+__device__ __forceinline__ LaneMember lane_member(int wg, const uint8_t* w0, const uint8_t* w1, const uint8_t* w2,
+                                                  int rows0, int rows1, int rows2, int wg_ends) {
+    const int e0 = wg_ends & 0x3ff, e1 = (wg_ends >> 10) & 0x3ff, e2 = (wg_ends >> 20) & 0x3ff;
+    const bool c1 = wg >= e0, c2 = wg >= e1;
+    return LaneMember{c2 ? w2 : c1 ? w1 : w0, c2 ? rows2 : c1 ? rows1 : rows0, c2 ? e1 : c1 ? e0 : 0,
+                      c2 ? e2 : c1 ? e1 : e0, c1, c2};
+}
+// The preloaded arguments of a launch (LaneHead), and whether its fields fit
+// their packed slots: at most three members (launch_gemv splits a fourth off,
+// so member 3 repeats member 2) and 1023 workgroups, rows of at most 1023
+// blocks (the LDS holds far fewer), up to 15 activation rows.
+LaneHead lane_head(const GemvArgs& p, bool fused) {
+    const auto u = [](int v) { return static_cast<uint32_t>(v); };
+    return LaneHead{fused ? static_cast<const void*>(p.x) : static_cast<const void*>(p.q8k),
+                    p.mb[0].w,
+                    p.mb[1].w,
+                    p.mb[2].w,
+                    p.mb[0].rows,
+                    p.mb[1].rows,
+                    p.mb[2].rows,
+                    static_cast<int>(u(p.mb[0].wg_end) | u(p.mb[1].wg_end) << 10 | u(p.mb[2].wg_end) << 20),
+                    static_cast<int>(u(p.nb) | u(p.iters) << 10 | u(p.m) << 20 | u(p.log2g) << 24 |
+                                     u(p.wave_major) << 27),
+                    p.ldx};
+}
+bool lane_head_fits(const GemvArgs& p) {
+    return p.mb[3].wg_end == p.mb[2].wg_end && p.mb[0].wg_end >= 0 && p.mb[2].wg_end <= 0x3ff && p.nb >= 0 &&
+           p.nb <= 0x3ff && p.iters >= 0 && p.iters <= 0x3ff && p.m >= 0 && p.m <= 0xf && p.log2g >= 0 &&
+           p.log2g <= 7 && (p.wave_major == 0 || p.wave_major == 1);
+}
+
 // The activations into LDS, after the first weight loads are issued. Fused
 // launches: the quantising waves (whose activation loads went out first)
 // quantise and count themselves in `ready`; every wave (owners too: each
@@ -376,7 +431,9 @@ __device__ __forceinline__ bool stage_activations(const GemvArgs& p, const XPre<
 // SUMS: also write every block's exact integer sums (p.isum / p.msum).
 // QP: activation quantisation passes whose loads are issued up front.
 template <int KIND, int L, int MT, bool FUSED, int D, bool SUMS, int W, int QP>
-__global__ __launch_bounds__(W * 64) void gemv_kernel(const GemvArgs p) {
+__global__ __launch_bounds__(W * 64) void gemv_kernel(const void* x, const uint8_t* w0, const uint8_t* w1,
+                                                        const uint8_t* w2, int rows0, int rows1, int rows2, int wg_ends,
+                                                        int counts, int ldx, const GemvArgs pa) {
     constexpr int BB = block_bytes(KIND);
     constexpr int SW = 64 / L;  // block slots per wave
     constexpr int LOG2L = L == 1 ? 0 : L == 2 ? 1 : L == 4 ? 2 : 3;
@@ -384,23 +441,32 @@ __global__ __launch_bounds__(W * 64) void gemv_kernel(const GemvArgs p) {
     __shared__ int q8_ready;  // waves done quantising the activations (fused launches)
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // uniform: keeps row math scalar
+    // p: the arguments, with the preloaded fields (LaneHead) in place of the
+    // struct's copies; only its scalar fields are read
+    GemvArgs p = pa;
+    p.x = static_cast<const float*>(x);
+    p.q8k = static_cast<const uint8_t*>(x);
+    p.ldx = ldx;
+    p.nb = counts & 0x3ff;
+    p.iters = (counts >> 10) & 0x3ff;
+    p.m = (counts >> 20) & 0xf;
+    p.log2g = (counts >> 24) & 0x7;
+    p.wave_major = (counts >> 27) & 1;
     const int nb = p.nb, m = p.m, iters = p.iters, log2g = p.log2g;
     const Q8Lds a = q8_lds(smem, MT, nb);
 
-    // The projection this workgroup serves (wave-uniform). Every member's
-    // fields are read unconditionally and selected, so the arguments arrive
-    // in one round of scalar loads; unused members repeat the last one.
+    // The projection this workgroup serves (wave-uniform), from the preloaded
+    // fields; its output from the struct's (read at the first store).
     const int wg = blockIdx.x;
-    const bool c1 = wg >= p.mb[0].wg_end, c2 = wg >= p.mb[1].wg_end, c3 = wg >= p.mb[2].wg_end;
-    auto pick = [&](auto v0, auto v1, auto v2, auto v3) { return c3 ? v3 : c2 ? v2 : c1 ? v1 : v0; };
-    const uint8_t* w = pick(p.mb[0].w, p.mb[1].w, p.mb[2].w, p.mb[3].w);
-    float* out = pick(p.mb[0].out, p.mb[1].out, p.mb[2].out, p.mb[3].out);
-    const int ldo = pick(p.mb[0].ldo, p.mb[1].ldo, p.mb[2].ldo, p.mb[3].ldo);
-    const int rows = pick(p.mb[0].rows, p.mb[1].rows, p.mb[2].rows, p.mb[3].rows);
-    const int groups = pick(p.mb[0].groups, p.mb[1].groups, p.mb[2].groups, p.mb[3].groups);
-    const int wg0 = pick(0, p.mb[0].wg_end, p.mb[1].wg_end, p.mb[2].wg_end);
-    const int wg1 = pick(p.mb[0].wg_end, p.mb[1].wg_end, p.mb[2].wg_end, p.mb[3].wg_end);
-    const gbytes wg_w = reinterpret_cast<gbytes>(reinterpret_cast<uint64_t>(w));
+    const LaneMember mem = lane_member(wg, w0, w1, w2, rows0, rows1, rows2, wg_ends);
+    const bool c1 = mem.c1, c2 = mem.c2;
+    float* out = c2 ? pa.mb[2].out : c1 ? pa.mb[1].out : pa.mb[0].out;
+    const int ldo = c2 ? pa.mb[2].ldo : c1 ? pa.mb[1].ldo : pa.mb[0].ldo;
+    const int rows = mem.rows;
+    // row groups: the host's ceil(rows / rows_per_group), a power of two
+    const int groups = (rows + (SW >> log2g) - 1) >> (6 - LOG2L - log2g);
+    const int wg0 = mem.wg0, wg1 = mem.wg1;
+    const gbytes wg_w = reinterpret_cast<gbytes>(reinterpret_cast<uint64_t>(mem.w));
     const gfloats wg_out = reinterpret_cast<gfloats>(reinterpret_cast<uint64_t>(out));
 
     const int sl = lane >> LOG2L, pc = lane & (L - 1);  // block slot, lane inside the block
@@ -558,13 +624,25 @@ __device__ __forceinline__ void dma16_untracked(const uint8_t* base, uint32_t of
 // LDS: the activations of m rows (m * nb * kGemvLdsPerBlock bytes, rounded up
 // to 16), then S ring slots of WS waves.
 template <int MT, int WS, int S, bool FUSED, int QP>
-__global__ __launch_bounds__(kQ6Waves * 64) void gemv_q6_stream_kernel(const GemvArgs p) {
+__global__ __launch_bounds__(kQ6Waves * 64) void gemv_q6_stream_kernel(const void* x, const uint8_t* w0,
+                                                                       const uint8_t* w1, const uint8_t* w2,
+                                                                       int rows0, int rows1, int rows2, int wg_ends,
+                                                                       int counts, int ldx, const GemvArgs pa) {
     static_assert(WS == 8 || WS == 16, "8 or 16 stream waves");
     static_assert(S == 2 || S == 4, "2 or 4 ring slots");
     extern __shared__ __align__(16) uint8_t smem[];
     __shared__ int ready;  // waves done staging their share of the activations
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    // p: the arguments, with the preloaded fields (LaneHead) in place of the
+    // struct's copies; only its scalar fields are read
+    GemvArgs p = pa;
+    p.x = static_cast<const float*>(x);
+    p.q8k = static_cast<const uint8_t*>(x);
+    p.ldx = ldx;
+    p.nb = counts & 0x3ff;
+    p.iters = (counts >> 10) & 0x3ff;
+    p.m = (counts >> 20) & 0xf;
     const int nb = p.nb, m = p.m, iters = p.iters;
     const Q8Lds a = q8_lds(smem, m, nb);
     uint8_t* const ring_base = smem + (m * nb * kGemvLdsPerBlock + 15) / 16 * 16;
@@ -575,15 +653,13 @@ __global__ __launch_bounds__(kQ6Waves * 64) void gemv_q6_stream_kernel(const Gem
     asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 
     const int wg = blockIdx.x;
-    const bool c1 = wg >= p.mb[0].wg_end, c2 = wg >= p.mb[1].wg_end, c3 = wg >= p.mb[2].wg_end;
-    auto pick = [&](auto v0, auto v1, auto v2, auto v3) { return c3 ? v3 : c2 ? v2 : c1 ? v1 : v0; };
-    const uint8_t* w = pick(p.mb[0].w, p.mb[1].w, p.mb[2].w, p.mb[3].w);
-    float* out = pick(p.mb[0].out, p.mb[1].out, p.mb[2].out, p.mb[3].out);
-    const int ldo = pick(p.mb[0].ldo, p.mb[1].ldo, p.mb[2].ldo, p.mb[3].ldo);
-    const int rows = pick(p.mb[0].rows, p.mb[1].rows, p.mb[2].rows, p.mb[3].rows);
-    const int wg0 = pick(0, p.mb[0].wg_end, p.mb[1].wg_end, p.mb[2].wg_end);
-    const int wg1 = pick(p.mb[0].wg_end, p.mb[1].wg_end, p.mb[2].wg_end, p.mb[3].wg_end);
-    const gbytes wg_w = reinterpret_cast<gbytes>(reinterpret_cast<uint64_t>(w));
+    const LaneMember mem = lane_member(wg, w0, w1, w2, rows0, rows1, rows2, wg_ends);
+    const bool c1 = mem.c1, c2 = mem.c2;
+    float* out = c2 ? pa.mb[2].out : c1 ? pa.mb[1].out : pa.mb[0].out;
+    const int ldo = c2 ? pa.mb[2].ldo : c1 ? pa.mb[1].ldo : pa.mb[0].ldo;
+    const int rows = mem.rows;
+    const int wg0 = mem.wg0, wg1 = mem.wg1;
+    const gbytes wg_w = reinterpret_cast<gbytes>(reinterpret_cast<uint64_t>(mem.w));
     const gfloats wg_out = reinterpret_cast<gfloats>(reinterpret_cast<uint64_t>(out));
 
     const int sl = lane >> 3, pc = lane & 7;  // block slot (block of the step), lane inside the block
@@ -759,8 +835,10 @@ void launch_d(const GemvArgs& p, int d, dim3 grid, size_t lds, hipStream_t strea
     constexpr int DM = SUMS ? 1 : (HALF ? (max_depth<KIND, L>() > 1 ? max_depth<KIND, L>() / 2 : 1)
                                         : max_depth<KIND, L>());
     const dim3 block(W * 64);
-    if (DM >= 2 && d >= 2) gemv_kernel<KIND, L, MT, FUSED, (DM >= 2 ? 2 : 1), SUMS, W, QP><<<grid, block, lds, stream>>>(p);
-    else gemv_kernel<KIND, L, MT, FUSED, 1, SUMS, W, QP><<<grid, block, lds, stream>>>(p);
+    const LaneHead h = lane_head(p, FUSED);
+    if (DM >= 2 && d >= 2)
+        gemv_kernel<KIND, L, MT, FUSED, (DM >= 2 ? 2 : 1), SUMS, W, QP><<<grid, block, lds, stream>>>(RK_LANE_HEAD(h), p);
+    else gemv_kernel<KIND, L, MT, FUSED, 1, SUMS, W, QP><<<grid, block, lds, stream>>>(RK_LANE_HEAD(h), p);
 }
 
 // Activation passes loaded up front: all of them (up to 4) in 8-wave
@@ -892,6 +970,7 @@ int plan_args(const GemvParams& p, int W, int64_t rows_per_group, int cus, GemvA
     ka.nb = p.nb;
     ka.log2g = p.log2g;
     ka.iters = p.iters;
+    if (!lane_head_fits(ka)) return kStatusInvalid;
     if constexpr (FUSED) return set_wait(ka);
     return kStatusOk;
 }
@@ -906,14 +985,15 @@ bool q6_stream_fits(int m, int nb, bool sums) {
 template <int MT, int WS, bool FUSED>
 void launch_q6_stream_ws(const GemvArgs& ka, int passes, int slots, size_t lds, dim3 grid, hipStream_t stream) {
     const dim3 block(kQ6Waves * 64);
+    const LaneHead h = lane_head(ka, FUSED);
     auto go = [&](auto s) {
         constexpr int S = decltype(s)::value;
         // activation passes, all loaded up front (q6_stream_fits keeps them <= 4)
         if constexpr (FUSED) {
-            if (passes > 2) return gemv_q6_stream_kernel<MT, WS, S, FUSED, 4><<<grid, block, lds, stream>>>(ka);
-            if (passes > 1) return gemv_q6_stream_kernel<MT, WS, S, FUSED, 2><<<grid, block, lds, stream>>>(ka);
+            if (passes > 2) return gemv_q6_stream_kernel<MT, WS, S, FUSED, 4><<<grid, block, lds, stream>>>(RK_LANE_HEAD(h), ka);
+            if (passes > 1) return gemv_q6_stream_kernel<MT, WS, S, FUSED, 2><<<grid, block, lds, stream>>>(RK_LANE_HEAD(h), ka);
         }
-        gemv_q6_stream_kernel<MT, WS, S, FUSED, 1><<<grid, block, lds, stream>>>(ka);
+        gemv_q6_stream_kernel<MT, WS, S, FUSED, 1><<<grid, block, lds, stream>>>(RK_LANE_HEAD(h), ka);
     };
     if (slots >= 4) go(std::integral_constant<int, 4>{});
     else go(std::integral_constant<int, 2>{});
@@ -1085,6 +1165,20 @@ bool gemv_uses_mfma(int kind, int m, int nb, int64_t rows, int cus) {
 }
 
 int launch_gemv(int kind, bool fused, GemvParams& p, hipStream_t stream) {
+    if (p.count == 4) {
+        // the lane and stream kernels take three members' fields as preloaded
+        // arguments (LaneHead): the fourth member is a launch of its own, with
+        // the same bits (a row's arithmetic does not depend on its launch)
+        GemvParams a = p, b = p;
+        a.count = 3;
+        b.count = 1;
+        b.w[0] = p.w[3];
+        b.out[0] = p.out[3];
+        b.ldo[0] = p.ldo[3];
+        b.rows[0] = p.rows[3];
+        const int st = launch_gemv(kind, fused, a, stream);
+        return st != kStatusOk ? st : launch_gemv(kind, fused, b, stream);
+    }
     int64_t rows = 0;
     for (int i = 0; i < p.count; ++i) rows += p.rows[i];
     if (gemv_stream_waves(kind, p.m, p.nb, rows, p.isum != nullptr, device_cu_count()) != 0)

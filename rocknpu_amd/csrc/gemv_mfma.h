@@ -437,6 +437,45 @@ struct OwnedActs {
     }
 };
 
+// The fields of MfmaArgs that a tiled launch's first loads need, passed ahead
+// of it as scalar kernel arguments (14 dwords, preloaded in SGPRs; the struct
+// itself is read from the argument segment, a memory round trip at the start
+// of every wave): the activations (f32 or Q8_K), the first three members'
+// weights and tile ends, the grid size and the counts, two 16-bit halves a
+// dword. A launch with a fourth member, or more than 0xffff tiles, is split
+// on the host, so member 3 repeats member 2.
+struct TiledHead {
+    const void* x;
+    const uint8_t* w0;
+    const uint8_t* w1;
+    const uint8_t* w2;
+    int te01;     // tile ends of members 0 and 1: te0 | te1 << 16
+    int tiles;    // at most 0xffff
+    int grid;     // workgroups (gridDim.x, a hidden argument after the struct)
+    int ldx;
+    int nb_nbs;   // nb | nbs << 16
+    int m_iters;  // m | iters << 16
+};
+// The tile lookups of tile_out / tile_weights on the preloaded fields (t below
+// the launch's tile count, so at most member 2). The selects are of values:
+// a conditional of two members (lvalues) selects their addresses, and the
+// struct would then live in scratch memory.
+struct TileMap {
+    const uint8_t* w0;
+    const uint8_t* w1;
+    const uint8_t* w2;
+    int te0, te1;
+    __device__ __forceinline__ const uint8_t* weights(int t) const {
+        const uint8_t *a = w0, *b = w1, *c = w2;
+        const int e0 = te0, e1 = te1;
+        return t >= e1 ? c : t >= e0 ? b : a;
+    }
+    __device__ __forceinline__ int row0(int t) const {
+        const int e0 = te0, e1 = te1;
+        return (t - (t >= e1 ? e1 : t >= e0 ? e0 : 0)) * kTileRows;
+    }
+};
+
 // The member (projection) of tile t and the tile's first row in it.
 struct TileOut {
     float* out;

@@ -74,7 +74,9 @@ struct AllActs {
 // few tiles so fills S times the workgroups. The ranges' partial sums meet in
 // exchange slots (below, and gemv_tiled_ranges).
 template <int KIND, int MT, bool FUSED, int W, bool AREG, int NI, int D, int IT, bool LAZY = false, int S = 1>
-__global__ __launch_bounds__(W * 64) void gemv_tiled_kernel(const MfmaArgs p0) {
+__global__ __launch_bounds__(W * 64) void gemv_tiled_kernel(const void* x, const uint8_t* w0, const uint8_t* w1,
+                                                              const uint8_t* w2, int te01, int tiles, int grid,
+                                                              int ldx, int nb_nbs, int m_iters, const MfmaArgs pa) {
     constexpr int BB = block_bytes(KIND);
     constexpr int NR = MT / 4;
     static_assert(D >= 1 && D <= NI, "one to NI items in flight");
@@ -83,26 +85,38 @@ __global__ __launch_bounds__(W * 64) void gemv_tiled_kernel(const MfmaArgs p0) {
     extern __shared__ __align__(16) uint8_t smem[];
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int grid = gridDim.x, bid = blockIdx.x;
-    // p: the range's view of the activations (its blocks from b0); the tile
-    // lookups read the members from p0 (a copy indexed at run time would live
-    // in scratch memory)
+    const int bid = blockIdx.x;
+    // The launch's arguments: pa, with the fields the first loads need
+    // preloaded ahead of it (TiledHead) and taken from there. Only scalar
+    // fields of the local copy p are read (an array member indexed at run time
+    // would put the copy in scratch memory).
+    const MfmaArgs& p0 = pa;
+    const int nb0 = nb_nbs & 0xffff, nbs0 = static_cast<int>(static_cast<uint32_t>(nb_nbs) >> 16);
+    const TileMap tmap{w0, w1, w2, te01 & 0xffff, static_cast<int>(static_cast<uint32_t>(te01) >> 16)};
+    // p: the range's view of the activations (its blocks from b0)
     // range sp: blocks [sp nb / S, (sp + 1) nb / S), at most nbs = ceil(nb / S)
-    const int sp = S > 1 ? bid % S : 0, b0 = sp * p0.nb / S;
-    MfmaArgs p = p0;
+    const int sp = S > 1 ? bid % S : 0, b0 = sp * nb0 / S;
+    MfmaArgs p = pa;
+    p.x = static_cast<const float*>(x);
+    p.q8k = static_cast<const uint8_t*>(x);
+    p.ldx = ldx;
+    p.nb = nb0;
+    p.m = m_iters & 0xffff;
+    p.iters = static_cast<int>(static_cast<uint32_t>(m_iters) >> 16);
+    p.tiles = tiles;
     if constexpr (S > 1) {
-        p.nb = (sp + 1) * p0.nb / S - b0;
-        if constexpr (FUSED) p.x = p0.x + static_cast<int64_t>(b0) * kQK;
-        else p.q8k = p0.q8k + static_cast<int64_t>(b0) * kQ8KBytes;
+        p.nb = (sp + 1) * nb0 / S - b0;
+        if constexpr (FUSED) p.x = static_cast<const float*>(x) + static_cast<int64_t>(b0) * kQK;
+        else p.q8k = static_cast<const uint8_t*>(x) + static_cast<int64_t>(b0) * kQ8KBytes;
     }
     const int nb = p.nb, m = p.m, iters = p.iters;
-    const int lnb = S > 1 ? p0.nbs : nb;  // blocks the LDS layout holds
+    const int lnb = S > 1 ? nbs0 : nb;  // blocks the LDS layout holds
     const ActLds<MT> act{smem, lnb};
     // partial sums [2][W][64][NR], then the tile sums [NI][64][NR]
     float* part = reinterpret_cast<float*>(smem + ((lnb * MT * kPerRowBlock + 15) & ~15));
     float* res = part + 2 * W * 64 * NR;
     const int n = lane & 15, q = lane >> 4;
-    const int ntile = (p0.tiles * S - bid + grid - 1) / grid;  // units bid, bid + grid, ..
+    const int ntile = (tiles * S - bid + grid - 1) / grid;  // units bid, bid + grid, ..
     const int items = ntile * iters;                           // <= NI (the host's choice)
     // item i: unit i / iters of the workgroup, block index i % iters; items
     // past the workgroup's last re-read its last one (in bounds) and are dropped
@@ -110,10 +124,9 @@ __global__ __launch_bounds__(W * 64) void gemv_tiled_kernel(const MfmaArgs p0) {
         const int ic = min(i, items - 1);
         const int kt = ic / iters, it = ic - kt * iters;
         const int t = (bid + kt * grid) / S;
-        const TileOut to = tile_out(p0, t);
         const int b = b0 + min(wave + W * it, nb - 1);
-        const gbytes w = reinterpret_cast<gbytes>(reinterpret_cast<uint64_t>(tile_weights(p0, t)));
-        k.load_tiled(w + (static_cast<int64_t>(to.row0 / kTileRows) * p0.nb + b) * (kTileRows * BB), lane);
+        const gbytes w = reinterpret_cast<gbytes>(reinterpret_cast<uint64_t>(tmap.weights(t)));
+        k.load_tiled(w + (static_cast<int64_t>(tmap.row0(t) / kTileRows) * nb0 + b) * (kTileRows * BB), lane);
     };
 
     // The activations of the wave's IT = iters block indices: with one, as
@@ -223,7 +236,7 @@ __global__ __launch_bounds__(W * 64) void gemv_tiled_kernel(const MfmaArgs p0) {
                     const int per = S >> (lv + 1), j = sp >> (lv + 1), side = (sp >> lv) & 1;
                     unsigned long long* slot =
                         p0.split_slot + base + ((static_cast<int64_t>(t) * per + j) * 64 + lane) * NR + lr;
-                    base += static_cast<int64_t>(p0.tiles) * per * 64 * NR;
+                    base += static_cast<int64_t>(tiles) * per * 64 * NR;
                     const unsigned long long old = __hip_atomic_exchange(
                         slot, static_cast<unsigned long long>(2 * g + side) << 32 | __float_as_uint(r),
                         __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -325,6 +338,23 @@ int launch_gemv_tile_weights(int kind, const uint8_t* src, int64_t n, int nb, ui
 }
 
 namespace {
+// The scalar arguments ahead of MfmaArgs (TiledHead); p has at most three
+// members (launch_gemv_tiled splits a fourth off) and 16-bit counts.
+TiledHead tiled_head(const MfmaArgs& p, bool fused, unsigned grid) {
+    return TiledHead{fused ? static_cast<const void*>(p.x) : static_cast<const void*>(p.q8k), p.mb[0].w, p.mb[1].w,
+                     p.mb[2].w,
+                     static_cast<int>(static_cast<uint32_t>(p.mb[0].tile_end) |
+                                      static_cast<uint32_t>(p.mb[1].tile_end) << 16),
+                     p.tiles, static_cast<int>(grid), p.ldx,
+                     static_cast<int>(static_cast<uint32_t>(p.nb) | static_cast<uint32_t>(p.nbs) << 16),
+                     static_cast<int>(static_cast<uint32_t>(p.m) | static_cast<uint32_t>(p.iters) << 16)};
+}
+bool head_fits(const MfmaArgs& p) {
+    return p.mb[2].tile_end == p.tiles && p.tiles <= 0xffff && p.nb >= 0 && p.nb <= 0xffff && p.nbs >= 0 && p.nbs <= 0xffff && p.m >= 0 &&
+           p.m <= 0xffff && p.iters >= 0 && p.iters <= 0xffff;
+}
+#define RK_HEAD(h) h.x, h.w0, h.w1, h.w2, h.te01, h.tiles, h.grid, h.ldx, h.nb_nbs, h.m_iters
+
 // Pipelined kernel, NI items per wave (ni tiles of iters block indices): two
 // in flight for two or three items (TinyLlama gate+up, 2 x 5632 x 2048, three
 // tiles per workgroup at 4 rows: 5.32 us against 5.51 with one and 5.42 with
@@ -338,22 +368,23 @@ namespace {
 template <int KIND, int MT, bool FUSED, int W>
 void launch_pipe(int ni, int iters, const MfmaArgs& p, dim3 grid, size_t lds, hipStream_t stream) {
     const dim3 block(W * 64);
+    const TiledHead h = tiled_head(p, FUSED, grid.x);
     if (iters == 1) {
-        if (ni == 1) gemv_tiled_kernel<KIND, MT, FUSED, W, true, 1, 1, 1><<<grid, block, lds, stream>>>(p);
-        else if (ni == 2) gemv_tiled_kernel<KIND, MT, FUSED, W, true, 2, 2, 1><<<grid, block, lds, stream>>>(p);
-        else if (ni == 3) gemv_tiled_kernel<KIND, MT, FUSED, W, true, 3, 2, 1><<<grid, block, lds, stream>>>(p);
+        if (ni == 1) gemv_tiled_kernel<KIND, MT, FUSED, W, true, 1, 1, 1><<<grid, block, lds, stream>>>(RK_HEAD(h), p);
+        else if (ni == 2) gemv_tiled_kernel<KIND, MT, FUSED, W, true, 2, 2, 1><<<grid, block, lds, stream>>>(RK_HEAD(h), p);
+        else if (ni == 3) gemv_tiled_kernel<KIND, MT, FUSED, W, true, 3, 2, 1><<<grid, block, lds, stream>>>(RK_HEAD(h), p);
         else if (W == 8 && static_cast<int>(grid.x) <= device_cu_count())
-            gemv_tiled_kernel<KIND, MT, FUSED, W, true, 4, 2, 1><<<grid, block, lds, stream>>>(p);
-        else gemv_tiled_kernel<KIND, MT, FUSED, W, true, 4, 1, 1><<<grid, block, lds, stream>>>(p);
+            gemv_tiled_kernel<KIND, MT, FUSED, W, true, 4, 2, 1><<<grid, block, lds, stream>>>(RK_HEAD(h), p);
+        else gemv_tiled_kernel<KIND, MT, FUSED, W, true, 4, 1, 1><<<grid, block, lds, stream>>>(RK_HEAD(h), p);
     } else if (iters == 2) {
         // block index 1 quantised after item 0's terms (Llama-3-8B q/o, 4096 x
         // 4096: 5.37 -> 5.19 us; q/k/v, 6144 x 4096: 7.17 -> 6.76 us)
-        if (ni == 2) gemv_tiled_kernel<KIND, MT, FUSED, W, false, 2, 2, 2, true><<<grid, block, lds, stream>>>(p);
-        else gemv_tiled_kernel<KIND, MT, FUSED, W, false, 4, 1, 2, true><<<grid, block, lds, stream>>>(p);
+        if (ni == 2) gemv_tiled_kernel<KIND, MT, FUSED, W, false, 2, 2, 2, true><<<grid, block, lds, stream>>>(RK_HEAD(h), p);
+        else gemv_tiled_kernel<KIND, MT, FUSED, W, false, 4, 1, 2, true><<<grid, block, lds, stream>>>(RK_HEAD(h), p);
     } else if (iters == 3) {
-        gemv_tiled_kernel<KIND, MT, FUSED, W, false, 3, 2, 3><<<grid, block, lds, stream>>>(p);
+        gemv_tiled_kernel<KIND, MT, FUSED, W, false, 3, 2, 3><<<grid, block, lds, stream>>>(RK_HEAD(h), p);
     } else {
-        gemv_tiled_kernel<KIND, MT, FUSED, W, false, 4, 1, 4><<<grid, block, lds, stream>>>(p);
+        gemv_tiled_kernel<KIND, MT, FUSED, W, false, 4, 1, 4><<<grid, block, lds, stream>>>(RK_HEAD(h), p);
     }
 }
 
@@ -456,28 +487,30 @@ namespace {
 template <int KIND, int MT, bool FUSED, int S>
 void launch_split_s(int ni, const MfmaArgs& p, dim3 grid, size_t lds, hipStream_t stream) {
     const dim3 block(8 * 64);
+    const TiledHead h = tiled_head(p, FUSED, grid.x);
     if (p.iters == 2) {
         if constexpr (S == 2) {
-            if (ni == 2) gemv_tiled_kernel<KIND, MT, FUSED, 8, false, 2, 2, 2, true, 2><<<grid, block, lds, stream>>>(p);
-            else gemv_tiled_kernel<KIND, MT, FUSED, 8, false, 4, 1, 2, true, 2><<<grid, block, lds, stream>>>(p);
+            if (ni == 2) gemv_tiled_kernel<KIND, MT, FUSED, 8, false, 2, 2, 2, true, 2><<<grid, block, lds, stream>>>(RK_HEAD(h), p);
+            else gemv_tiled_kernel<KIND, MT, FUSED, 8, false, 4, 1, 2, true, 2><<<grid, block, lds, stream>>>(RK_HEAD(h), p);
         }
     } else if (ni == 1) {
-        gemv_tiled_kernel<KIND, MT, FUSED, 8, true, 1, 1, 1, false, S><<<grid, block, lds, stream>>>(p);
+        gemv_tiled_kernel<KIND, MT, FUSED, 8, true, 1, 1, 1, false, S><<<grid, block, lds, stream>>>(RK_HEAD(h), p);
     } else if (ni == 2) {
-        gemv_tiled_kernel<KIND, MT, FUSED, 8, true, 2, 2, 1, false, S><<<grid, block, lds, stream>>>(p);
+        gemv_tiled_kernel<KIND, MT, FUSED, 8, true, 2, 2, 1, false, S><<<grid, block, lds, stream>>>(RK_HEAD(h), p);
     } else if (ni == 3) {
-        gemv_tiled_kernel<KIND, MT, FUSED, 8, true, 3, 2, 1, false, S><<<grid, block, lds, stream>>>(p);
+        gemv_tiled_kernel<KIND, MT, FUSED, 8, true, 3, 2, 1, false, S><<<grid, block, lds, stream>>>(RK_HEAD(h), p);
     } else {
-        gemv_tiled_kernel<KIND, MT, FUSED, 8, true, 4, 1, 1, false, S><<<grid, block, lds, stream>>>(p);
+        gemv_tiled_kernel<KIND, MT, FUSED, 8, true, 4, 1, 1, false, S><<<grid, block, lds, stream>>>(RK_HEAD(h), p);
     }
 }
 template <int KIND, int MT, bool FUSED, int S>
 void launch_split_w16(int ni, const MfmaArgs& p, dim3 grid, size_t lds, hipStream_t stream) {
     const dim3 block(16 * 64);
-    if (ni == 1) gemv_tiled_kernel<KIND, MT, FUSED, 16, true, 1, 1, 1, false, S><<<grid, block, lds, stream>>>(p);
-    else if (ni == 2) gemv_tiled_kernel<KIND, MT, FUSED, 16, true, 2, 2, 1, false, S><<<grid, block, lds, stream>>>(p);
-    else if (ni == 3) gemv_tiled_kernel<KIND, MT, FUSED, 16, true, 3, 2, 1, false, S><<<grid, block, lds, stream>>>(p);
-    else gemv_tiled_kernel<KIND, MT, FUSED, 16, true, 4, 1, 1, false, S><<<grid, block, lds, stream>>>(p);
+    const TiledHead h = tiled_head(p, FUSED, grid.x);
+    if (ni == 1) gemv_tiled_kernel<KIND, MT, FUSED, 16, true, 1, 1, 1, false, S><<<grid, block, lds, stream>>>(RK_HEAD(h), p);
+    else if (ni == 2) gemv_tiled_kernel<KIND, MT, FUSED, 16, true, 2, 2, 1, false, S><<<grid, block, lds, stream>>>(RK_HEAD(h), p);
+    else if (ni == 3) gemv_tiled_kernel<KIND, MT, FUSED, 16, true, 3, 2, 1, false, S><<<grid, block, lds, stream>>>(RK_HEAD(h), p);
+    else gemv_tiled_kernel<KIND, MT, FUSED, 16, true, 4, 1, 1, false, S><<<grid, block, lds, stream>>>(RK_HEAD(h), p);
 }
 template <int KIND, int MT, bool FUSED>
 void launch_split(int s, int w, int ni, const MfmaArgs& p, dim3 grid, size_t lds, hipStream_t stream) {
@@ -494,6 +527,40 @@ void launch_split_k(int mt, int s, int w, int ni, const MfmaArgs& p, dim3 grid, 
 
 int launch_gemv_tiled(int kind, bool fused, GemvParams& p, hipStream_t stream) {
     if ((kind != 4 && kind != 6) || p.m < 1 || p.m > gemv_mfma_rows(kind, p.nb)) return kStatusInvalid;
+    if (p.count == 4) {
+        // the kernels take three members' fields as preloaded arguments
+        // (TiledHead): the fourth member is a launch of its own, with the
+        // same bits (a row's arithmetic does not depend on its launch)
+        GemvParams a = p, b = p;
+        a.count = 3;
+        b.count = 1;
+        b.w[0] = p.w[3];
+        b.out[0] = p.out[3];
+        b.ldo[0] = p.ldo[3];
+        b.rows[0] = p.rows[3];
+        const int st = launch_gemv_tiled(kind, fused, a, stream);
+        return st != kStatusOk ? st : launch_gemv_tiled(kind, fused, b, stream);
+    }
+    // and at most 0xffff tiles (1,048,560 rows): larger launches go member by
+    // member, and a larger member in runs of 0xffff tiles
+    int64_t all_tiles = 0;
+    for (int i = 0; i < p.count; ++i) all_tiles += (p.rows[i] + kTileRows - 1) / kTileRows;
+    if (all_tiles > 0xffff) {
+        for (int i = 0; i < p.count; ++i) {
+            constexpr int64_t kRun = int64_t{0xffff} * kTileRows;
+            for (int64_t r0 = 0; r0 < p.rows[i]; r0 += kRun) {
+                GemvParams a = p;
+                a.count = 1;
+                a.w[0] = p.w[i] + (r0 / kTileRows) * p.nb * kTileRows * block_bytes(kind);
+                a.out[0] = p.out[i] + r0;
+                a.ldo[0] = p.ldo[i];
+                a.rows[0] = std::min(kRun, p.rows[i] - r0);
+                const int st = launch_gemv_tiled(kind, fused, a, stream);
+                if (st != kStatusOk) return st;
+            }
+        }
+        return kStatusOk;
+    }
     const int mt = p.m <= 4 ? 4 : p.m <= 8 ? 8 : 16;
     const int cus = device_cu_count();
     int64_t tiles = 0;
@@ -510,7 +577,7 @@ int launch_gemv_tiled(int kind, bool fused, GemvParams& p, hipStream_t stream) {
         if (mfma_args(p, sw, ka) != kStatusOk) return kStatusInvalid;
         ka.nbs = nbs;
         ka.iters = (nbs + sw - 1) / sw;
-        if (ka.iters > 2 || (ka.iters == 2 && sr != 2)) return kStatusInvalid;
+        if (ka.iters > 2 || (ka.iters == 2 && sr != 2) || !head_fits(ka)) return kStatusInvalid;
         ka.split_err = static_cast<uint32_t*>(p.split_ws);
         ka.split_slot = reinterpret_cast<unsigned long long*>(static_cast<uint8_t*>(p.split_ws) + kSplitSlotBase);
         ka.gen = next_split_generation();
@@ -535,7 +602,7 @@ int launch_gemv_tiled(int kind, bool fused, GemvParams& p, hipStream_t stream) {
     }
     const int w = tiled_waves(p.nb);
     MfmaArgs ka;
-    if (mfma_args(p, w, ka) != kStatusOk) return kStatusInvalid;
+    if (mfma_args(p, w, ka) != kStatusOk || !head_fits(ka)) return kStatusInvalid;
     // one round of workgroups on the CUs; but eight-wave launches of one block
     // index a wave and more than four tiles a CU get a workgroup per four
     // tiles (two on some CUs), so the pipelined kernel takes them instead of

@@ -51,7 +51,8 @@ __global__ __launch_bounds__(kA8Threads) void quantize_a8_kernel(const float* __
                                                                  int64_t k, int64_t lda,
                                                                  int64_t k_pad,
                                                                  int8_t* __restrict__ a8,
-                                                                 float* __restrict__ scales, uint32_t* __restrict__ zero_words, int nzero) {
+                                                                 uint32_t* __restrict__ zero_words, int nzero,
+                                                                 float* __restrict__ scales) {
     __shared__ float red[kA8Threads / 64];
     zero_counters(zero_words, nzero);
     const int64_t row = blockIdx.x;
@@ -117,7 +118,8 @@ template <int R>
 __global__ __launch_bounds__(1024) void quantize_a8_regs_kernel(const float* __restrict__ a, int64_t k,
                                                                 int64_t lda, int64_t k_pad,
                                                                 int8_t* __restrict__ a8,
-                                                                float* __restrict__ scales, uint32_t* __restrict__ zero_words, int nzero) {
+                                                                uint32_t* __restrict__ zero_words, int nzero,
+                                                                float* __restrict__ scales) {
     __shared__ uint32_t red[16];
     zero_counters(zero_words, nzero);
     const int64_t row = blockIdx.x;
@@ -230,12 +232,12 @@ int launch_quantize_a8(const float* a, int64_t m, int64_t k, int64_t lda, int64_
     const int64_t r = (k4 + nt - 1) / nt;
     if (vec && r <= 4) {
         const dim3 rb(static_cast<unsigned>(nt));
-        if (r <= 1) quantize_a8_regs_kernel<1><<<grid, rb, 0, stream>>>(a, k, lda, k_pad, a8, scales, zero_words, nzero);
-        else if (r <= 2) quantize_a8_regs_kernel<2><<<grid, rb, 0, stream>>>(a, k, lda, k_pad, a8, scales, zero_words, nzero);
-        else if (r <= 3) quantize_a8_regs_kernel<3><<<grid, rb, 0, stream>>>(a, k, lda, k_pad, a8, scales, zero_words, nzero);
-        else quantize_a8_regs_kernel<4><<<grid, rb, 0, stream>>>(a, k, lda, k_pad, a8, scales, zero_words, nzero);
-    } else if (vec) quantize_a8_kernel<true><<<grid, block, 0, stream>>>(a, k, lda, k_pad, a8, scales, zero_words, nzero);
-    else quantize_a8_kernel<false><<<grid, block, 0, stream>>>(a, k, lda, k_pad, a8, scales, zero_words, nzero);
+        if (r <= 1) quantize_a8_regs_kernel<1><<<grid, rb, 0, stream>>>(a, k, lda, k_pad, a8, zero_words, nzero, scales);
+        else if (r <= 2) quantize_a8_regs_kernel<2><<<grid, rb, 0, stream>>>(a, k, lda, k_pad, a8, zero_words, nzero, scales);
+        else if (r <= 3) quantize_a8_regs_kernel<3><<<grid, rb, 0, stream>>>(a, k, lda, k_pad, a8, zero_words, nzero, scales);
+        else quantize_a8_regs_kernel<4><<<grid, rb, 0, stream>>>(a, k, lda, k_pad, a8, zero_words, nzero, scales);
+    } else if (vec) quantize_a8_kernel<true><<<grid, block, 0, stream>>>(a, k, lda, k_pad, a8, zero_words, nzero, scales);
+    else quantize_a8_kernel<false><<<grid, block, 0, stream>>>(a, k, lda, k_pad, a8, zero_words, nzero, scales);
     return hipGetLastError() == hipSuccess ? kStatusOk : kStatusExec;
 }
 

@@ -362,6 +362,10 @@ def test_gemv_m_chunking():
     # at 2 rows with a ragged last workgroup, and 4 rows of 64 blocks on a wide
     # weight (a two-slot ring beside the activations)
     (6, (333,), 14592, 1), (6, (4101,), 14592, 2), (6, (4096,), 16384, 4),
+    # four members on the lane kernel and the Q6_K stream (the fourth runs as a
+    # launch of its own: the kernels take three members' fields as preloaded
+    # arguments)
+    (4, (2048, 256, 256, 512), 2048, 1), (6, (2048, 100, 300, 48), 5632, 1),
 ])
 def test_gemv_fused_grouped(kind, ns, k, m):
     """Fused Q8_K quant + grouped GEMV == separate quant + per-member GEMV, bit for bit,

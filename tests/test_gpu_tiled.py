@@ -99,6 +99,9 @@ CASES = [
     (4, 2048, [1000, 17], (4, 13)),
     (6, 2048, [32000], (1, 4, 8)),             # 2000 tiles: a workgroup per four (pipelined)
     (4, 2048, [8192, 8192, 2000], (3, 4)),     # 1149 tiles: the same, bits of the raw rows
+    (4, 2048, [2048, 256, 256, 512], (1, 4)),  # four members: the fourth a launch of its own
+    (6, 5632, [2048, 48, 100, 16], (4,)),      # the same for split launches
+    (4, 256, [65537 * 16 + 5], (1,)),          # more than 0xffff tiles: runs of 0xffff tiles
 ]
 
 
