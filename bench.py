@@ -798,8 +798,8 @@ def main():
         "data": "synthetic (seeded Q4_K/Q6_K weights, N(0,1) activations)",
         "config": {"workload": "decode GEMV set: TinyLlama-1.1B projections x 22 layers, M=1 and M=4, "
                                "Q8_K activation quant fused into the Q4_K/Q6_K x Q8_K GEMV, one launch per "
-                               "shared input (qkv, o, gate+up, down), raw rows at M=1 and the decode cache's "
-                               "tiled copies at M=4, HIP graph",
+                               "shared input (qkv, o, gate+up, down), the decode cache's tiled copies (the Q6_K "
+                               "down at M=1: raw rows), HIP graph",
                    "layers": synth.TINYLLAMA_LAYERS, "m": [1, 4], "launches_per_step": n_gemv,
                    "bytes_per_step": step_bytes},
         "roofline": {"bound": "hbm", "kernel": "Q4_K x Q8_K decode GEMV at M=4 on the matrix cores over the "
@@ -810,7 +810,8 @@ def main():
                      "frac": round(m4_achieved / HBM_PEAK_GBS, 4), "traffic": measured_traffic("gemv_q4k_m4"),
                      "avg_launch_us": round(m4_us, 3), "bytes_per_launch": m4_bpl},
         "roofline_m1": {"bound": "hbm", "kernel": "Q4_K x Q8_K decode GEMV with fused Q8_K quant at M=1 "
-                                                  "(gemv_kernel<4,...>), the 66 Q4_K launches of a step",
+                                                  "on the tiled copies (gemv_tiled_kernel<4,4,true,8,...>), the 66 "
+                                                  "Q4_K launches of a step",
                         "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                         "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": measured_traffic("gemv_q4k"),
                         "avg_launch_us": round(q4_us, 3), "bytes_per_launch": q4_bpl},

@@ -252,10 +252,11 @@ int rocknpu_hip_gemv_tiled_workspace_check(void * workspace, void * stream);
 
 /* Whether a decode GEMV of m activation rows over Q4_K (kind 4) or Q6_K
  * (kind 6) rows of K = k runs faster on the tiled copy (1) or on the raw rows
- * (0): the tiled copy from two rows; at one row for Q4_K rows of 9-16 blocks
- * or 32 and more, and Q6_K rows of 8-16 blocks or 32-64; other one-row
- * launches (rows of 17-31 blocks, shorter rows) keep the lane-per-block and
- * LDS-stream kernels on raw rows.
+ * (0): the tiled copy from two rows; at one row for rows of 5-16 blocks, of
+ * 17-31 blocks that do not fill 8 block slots a row in whole passes (17-20 and
+ * 25-27), and of 32 or more (Q6_K: up to 64); other one-row launches (rows of
+ * at most 4 blocks, of 21-24 or 28-31, Q6_K rows beyond 64) keep the
+ * lane-per-block and LDS-stream kernels on raw rows.
  * Host code only. No counterpart in the reference. */
 int rocknpu_hip_gemv_tiled_preferred(uint32_t kind, size_t m, size_t k);
 

@@ -85,6 +85,9 @@ bool gemv_uses_mfma(int kind, int m, int nb, int64_t rows, int cus);            
 // Stream waves per workgroup of the Q6_K LDS-stream kernel for such a launch,
 // or 0 when another kernel runs it. Defined in gemv.hip.
 int gemv_stream_waves(int kind, int m, int nb, int64_t rows, bool sums, int cus);
+// Block slots per row of the lane-per-block GEMV (log2): the largest power of
+// two <= min(slots, nb) whose last pass over a row keeps >= 85% of them busy.
+int slots_per_row_log2(int nb, int slots);
 // Activation rows per launch the matrix-core GEMV holds for rows of nb blocks
 // (0: none). Defined in gemv_mfma.hip.
 int gemv_mfma_rows(int kind, int nb);

@@ -874,6 +874,8 @@ void launch_l(const GemvArgs& p, int w, int mt, int d, int passes, dim3 grid, si
     launch_w<KIND, L, FUSED, SUMS, 16>(p, mt, d, passes, grid, lds, stream);
 }
 
+}  // namespace
+
 // Slots per row: the largest power of two <= min(slots, nb) whose last pass
 // over the row's blocks keeps at least 85% of the slots busy.
 int slots_per_row_log2(int nb, int slots) {
@@ -886,6 +888,8 @@ int slots_per_row_log2(int nb, int slots) {
     }
     return lg;
 }
+
+namespace {
 
 // The stall flag of fused launches: one int of pinned host memory, allocated
 // by the first fused launch and kept until the process ends.

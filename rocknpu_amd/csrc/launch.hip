@@ -278,28 +278,33 @@ extern "C" int rocknpu_hip_gemv_tile_weights(uint32_t kind, const uint8_t* w, si
 }
 
 // Measured on the decode shapes of TinyLlama, Llama-3.2-1B and Llama-3-8B and
-// on rows of 2-20 blocks (HIP graph, weights rotating through > 1 GB): from
-// two rows the tiled copy wins on every shape (TinyLlama o at 4 rows 3.57
-// against 4.21 us, gate+up 6.0 against 8.5 at Llama-3.2-1B size, down 5.42
-// against 7.90). At one row:
-// - rows of 9-16 blocks (16 waves, one block index each) and of 32-64 (split
-//   in four ranges) run faster tiled, Q4_K and Q6_K alike (Q4_K 2560 x 2560
-//   4.16 against 7.33 us, 3072-wide gate+up 7.8 against 9.2; Q6_K 3072 x 3072
-//   4.63 against 5.66, 4096 x 4096 5.36 against 6.46; Llama-3-8B down 11.8
-//   against 12.4), and so do Q6_K rows of 8 blocks (2048 x 2048 3.74 against
-//   5.09 on the raw rows' LDS stream);
-// - rows of 17-31 blocks keep the raw rows (TinyLlama down, Q6_K on the LDS
-//   stream, 5.3 against 6.7 tiled; Q4_K 2048 x 5632 4.71 against 6.08), as
-//   do Q4_K rows of at most 8 blocks (TinyLlama o 3.47 against 3.56, gate+up
-//   5.15 against 5.30) and Q6_K rows of fewer than 8 (512-1024 wide: 3.49
-//   against 3.63-3.69).
+// on rows of 2-31 blocks, 2048 and 4096 rows (HIP graph, weights rotating
+// through > 1 GB): from two rows the tiled copy wins on every shape (TinyLlama
+// o at 4 rows 3.41 against 4.21 us, gate+up 4.85 against 7.43, down 5.41
+// against 7.24). At one row the lane-per-block kernel on raw rows runs well
+// where a row's blocks fill its 8 block slots in whole passes, and the Q6_K
+// LDS stream likewise; elsewhere it takes one to four slots a row and runs
+// 1.3-2.6x longer. So at one row:
+// - rows of at most 4 blocks keep the raw rows (level: 3.12-3.45 us either
+//   way, and no tiled copy is needed);
+// - rows of 5-16 blocks and of 32-64 run tiled (Q4_K 2048 wide: 5 blocks 3.35
+//   against 6.85 us, 7 blocks 3.37 against 3.77, TinyLlama qkv 3.38 against
+//   3.48 and gate+up 4.87 against 5.17, o 3.32 against 3.30; 10 blocks 4.13
+//   against 6.95; Q6_K 6 blocks 3.47 against 5.32; Llama-3-8B down 11.5
+//   against 11.8), and Q4_K rows of more than 64;
+// - rows of 17-31 blocks keep the raw rows where those fill 8 slots (21-24
+//   and 28-31 blocks: TinyLlama down, Q6_K 2048 x 5632, 4.85 against 6.22 on
+//   the LDS stream; Q4_K 2048 x 5632 4.73 against 5.80) and run tiled where
+//   not (17-20 and 25-27: Q4_K 17 blocks 5.43 against 7.22, Q6_K 26 blocks
+//   7.41 against 11.5).
 extern "C" int rocknpu_hip_gemv_tiled_preferred(uint32_t kind, size_t m, size_t k) {
     if ((kind != 4 && kind != 6) || m == 0 || k == 0 || k % rk::kQK != 0) return 0;
     if (m >= 2) return 1;
     const size_t nb = k / rk::kQK;
-    if (nb >= 17 && nb <= 31) return 0;
-    if (kind == 4) return nb >= 9 ? 1 : 0;
-    return nb >= 8 && nb <= 64 ? 1 : 0;
+    if (nb <= 4) return 0;
+    if (nb >= 17 && nb <= 31) return rk::slots_per_row_log2(static_cast<int>(nb), 8) < 3 ? 1 : 0;
+    if (kind == 4) return 1;
+    return nb <= 64 ? 1 : 0;
 }
 
 namespace {

@@ -139,13 +139,15 @@ def test_tiled_decode_layout_host_side():
 
 @pytest.mark.parametrize("kind,m,k,tiled", [
     (4, 2, 2048, 1), (6, 4, 5632, 1), (4, 8, 256, 1),       # from two rows: always the tiled copy
-    (4, 1, 2048, 0),                                         # TinyLlama o / gate+up: 8 blocks, raw
-    (4, 1, 2560, 1), (4, 1, 4096, 1),                        # 9-16 blocks: tiled
-    (4, 1, 5632, 0), (6, 1, 5632, 0), (6, 1, 7936, 0),       # 17-31 blocks: raw
+    (4, 1, 2048, 1), (6, 1, 2048, 1),                        # TinyLlama o / qkv / gate+up: 8 blocks, tiled
+    (4, 1, 1280, 1), (6, 1, 1792, 1),                        # 5-7 blocks: tiled
+    (4, 1, 2560, 1), (4, 1, 4096, 1), (6, 1, 4096, 1),       # 9-16 blocks: tiled
+    (4, 1, 5632, 0), (6, 1, 5632, 0), (6, 1, 7936, 0),       # 17-31 blocks filling 8 slots (21-24, 28-31): raw
+    (4, 1, 4352, 1), (6, 1, 5120, 1), (6, 1, 6656, 1),       # 17, 20 and 26 blocks (fewer slots): tiled
     (4, 1, 8192, 1), (6, 1, 14336, 1), (4, 1, 28672, 1),     # 32 and more (Q6_K up to 64): tiled
     (6, 1, 16640, 0),                                        # Q6_K beyond 64 blocks: raw
-    (6, 1, 2048, 1), (6, 1, 4096, 1), (6, 1, 1024, 0),       # Q6_K: tiled from 8 blocks
-    (4, 1, 1024, 0), (5, 2, 2048, 0), (4, 1, 100, 0),        # short Q4_K rows raw; no Q5_K; K % 256
+    (4, 1, 1024, 0), (6, 1, 1024, 0), (4, 1, 256, 0),        # at most 4 blocks: raw
+    (5, 2, 2048, 0), (4, 1, 100, 0),                         # no Q5_K; K % 256
 ])
 def test_tiled_rule_host_side(kind, m, k, tiled):
     assert _lib.load().rocknpu_hip_gemv_tiled_preferred(kind, m, k) == tiled

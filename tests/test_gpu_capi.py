@@ -283,12 +283,17 @@ def test_w8_sidecar_get_converts_writes_and_reloads(tmp_path):
         c.close()
 
 
-def test_decode_cache_stats_count_the_q8k_route():
+@pytest.mark.parametrize("k", [1024, 2048])
+def test_decode_cache_stats_count_the_q8k_route(k):
     """The Q8_K decode route's resident raw blocks are decode-cache entries:
-    entries, resident bytes, hits and misses move with its calls (a weight the
-    one-row rule reads tiled, here the 8-block Q6_K one, also holds its tiled
-    copy)."""
-    k, n = 2048, 96
+    entries, resident bytes, hits and misses move with its calls. A weight the
+    one-row rule reads tiled (8-block rows here; 4-block rows stay raw) also
+    holds its tiled copy."""
+    n = 96
+    tiled = k == 2048
+    assert all(hip.gemv_tiled_preferred(kind, 1, k) == tiled for kind in (4, 6))
+    t4 = hip.gemv_tiled_bytes(4, k, n) if tiled else 0
+    t6 = hip.gemv_tiled_bytes(6, k, n) if tiled else 0
     w4 = synth.q4_k(n, k, index=1720)
     w6 = synth.q6_k(n, k, index=1721)
     x = synth.activations(1, k, index=1722)
@@ -298,16 +303,14 @@ def test_decode_cache_stats_count_the_q8k_route():
         assert (s0.entries, s0.resident_bytes, s0.hits, s0.misses) == (0, 0, 0, 0)
         assert c.matmul_q_q8k(4, w4, x, out, k, n) == STATUS_OK
         s1 = c.decode_cache_stats()
-        assert (s1.entries, s1.resident_bytes, s1.misses, s1.hits) == (1, w4.nbytes, 1, 0)
+        assert (s1.entries, s1.resident_bytes, s1.misses, s1.hits) == (1, w4.nbytes + t4, 1, 0)
         assert c.matmul_q_q8k(4, w4, x, out, k, n) == STATUS_OK
         s2 = c.decode_cache_stats()
-        assert (s2.entries, s2.resident_bytes, s2.misses, s2.hits) == (1, w4.nbytes, 1, 1)
+        assert (s2.entries, s2.resident_bytes, s2.misses, s2.hits) == (1, w4.nbytes + t4, 1, 1)
         outs = [np.empty((1, n), np.float32) for _ in range(2)]
         assert c.matmul_q_q8k_group([w4, w6], [4, 6], [n, n], x, outs, k) == STATUS_OK
         s3 = c.decode_cache_stats()
-        assert not hip.gemv_tiled_preferred(4, 1, k) and hip.gemv_tiled_preferred(6, 1, k)
-        tiled6 = hip.gemv_tiled_bytes(6, k, n)
-        assert (s3.entries, s3.resident_bytes, s3.misses, s3.hits) == (2, w4.nbytes + w6.nbytes + tiled6, 2, 1)
+        assert (s3.entries, s3.resident_bytes, s3.misses, s3.hits) == (2, w4.nbytes + t4 + w6.nbytes + t6, 2, 1)
         assert s3.miss_ns > 0 and s3.hit_ns > 0 and s3.worker1_calls == 3
 
 
@@ -341,7 +344,8 @@ def test_gemv_stall_gives_nan_and_execution_error():
     from rocknpu_amd import _lib, hip
     from rocknpu_amd.capi import STATUS_EXECUTION_ERROR
 
-    kind, ns, k, m = 4, (256, 512), 2048, 1
+    kind, ns, k, m = 4, (256, 512), 1024, 1
+    assert not hip.gemv_tiled_preferred(kind, m, k)  # the C ABI reads the raw rows
     mf, lanes, waves = ctypes.c_int(), ctypes.c_int(), ctypes.c_int()
     arr = (ctypes.c_size_t * 2)(*ns)
     assert _lib.load().rocknpu_hip_gemv_shape(kind, m, k, arr, 2, 1, 0, ctypes.byref(mf), ctypes.byref(lanes),

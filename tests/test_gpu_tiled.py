@@ -162,8 +162,10 @@ def test_capi_decode_rows_read_the_tiled_copy():
     """The C ABI's decode entries from two rows read the tiled copy it builds
     once per weight: results within the oracle bound, equal to the launch
     layer's tiled call, the copy's bytes counted as resident and its build as a
-    miss; one-row calls keep the raw rows."""
-    k, n = 2048, 2048
+    miss; one-row calls over rows the one-row rule keeps raw (4 blocks) read
+    the raw rows."""
+    k, n = 1024, 2048
+    assert not hip.gemv_tiled_preferred(4, 1, k) and hip.gemv_tiled_preferred(4, 4, k)
     w4 = synth.q4_k(n, k, index=3400)
     w6 = synth.q6_k(n, k, index=3401)
     x1 = synth.activations(1, k, index=3402)
