@@ -476,6 +476,24 @@ struct TileMap {
     }
 };
 
+// The scalar arguments ahead of MfmaArgs (TiledHead); p has at most three
+// members (launch_gemv splits a fourth off, and launch_gemv_tiled /
+// launch_gemv_mfma larger launches) and 16-bit counts.
+TiledHead tiled_head(const MfmaArgs& p, bool fused, unsigned grid) {
+    return TiledHead{fused ? static_cast<const void*>(p.x) : static_cast<const void*>(p.q8k), p.mb[0].w, p.mb[1].w,
+                     p.mb[2].w,
+                     static_cast<int>(static_cast<uint32_t>(p.mb[0].tile_end) |
+                                      static_cast<uint32_t>(p.mb[1].tile_end) << 16),
+                     p.tiles, static_cast<int>(grid), p.ldx,
+                     static_cast<int>(static_cast<uint32_t>(p.nb) | static_cast<uint32_t>(p.nbs) << 16),
+                     static_cast<int>(static_cast<uint32_t>(p.m) | static_cast<uint32_t>(p.iters) << 16)};
+}
+bool head_fits(const MfmaArgs& p) {
+    return p.mb[2].tile_end == p.tiles && p.tiles <= 0xffff && p.nb >= 0 && p.nb <= 0xffff && p.nbs >= 0 && p.nbs <= 0xffff && p.m >= 0 &&
+           p.m <= 0xffff && p.iters >= 0 && p.iters <= 0xffff;
+}
+#define RK_HEAD(h) h.x, h.w0, h.w1, h.w2, h.te01, h.tiles, h.grid, h.ldx, h.nb_nbs, h.m_iters
+
 // The member (projection) of tile t and the tile's first row in it.
 struct TileOut {
     float* out;
@@ -515,13 +533,26 @@ __device__ __forceinline__ const uint8_t* tile_weights(const MfmaArgs& p, int t)
 }
 
 template <int KIND, int MT, bool FUSED, int W, bool AREG, int D, bool TILED>
-__global__ __launch_bounds__(W * 64) void gemv_mfma_kernel(const MfmaArgs p) {
+__global__ __launch_bounds__(W * 64) void gemv_mfma_kernel(const void* x, const uint8_t* w0, const uint8_t* w1,
+                                                             const uint8_t* w2, int te01, int tiles, int grid,
+                                                             int ldx, int nb_nbs, int m_iters, const MfmaArgs pa) {
     constexpr int BB = block_bytes(KIND);
     using Piece = typename PieceOf<KIND, TILED>::type;
     constexpr int NR = MT / 4;
     extern __shared__ __align__(16) uint8_t smem[];
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    // p: the arguments, with the preloaded fields (TiledHead) in place of the
+    // struct's copies; only its scalar fields are read
+    MfmaArgs p = pa;
+    p.x = static_cast<const float*>(x);
+    p.q8k = static_cast<const uint8_t*>(x);
+    p.ldx = ldx;
+    p.nb = nb_nbs & 0xffff;
+    p.m = m_iters & 0xffff;
+    p.iters = static_cast<int>(static_cast<uint32_t>(m_iters) >> 16);
+    p.tiles = tiles;
+    const TileMap tmap{w0, w1, w2, te01 & 0xffff, static_cast<int>(static_cast<uint32_t>(te01) >> 16)};
     const int nb = p.nb, m = p.m, iters = p.iters;
     const ActLds<MT> act{smem, nb};
     // f32 partial sums of a tile: [buffer][wave][lane][NR], after the activations
@@ -536,21 +567,21 @@ __global__ __launch_bounds__(W * 64) void gemv_mfma_kernel(const MfmaArgs p) {
         int it;
     };
     auto advance = [&](Pos& c) {
-        if (++c.it == iters) { c.it = 0; c.t += gridDim.x; }
+        if (++c.it == iters) { c.it = 0; c.t += grid; }
     };
-    const int last_t = p.tiles - 1 - (p.tiles - 1 - static_cast<int>(blockIdx.x)) % static_cast<int>(gridDim.x);
+    const int last_t = tiles - 1 - (tiles - 1 - static_cast<int>(blockIdx.x)) % grid;
     auto load = [&](const Pos& c, Piece& k) {
-        const bool live = c.t < p.tiles;
+        const bool live = c.t < tiles;
         const int t = live ? c.t : last_t;
-        const TileOut to = tile_out(p, t);
         const int b = min(live ? wave + W * c.it : 0, nb - 1);
-        const gbytes w = reinterpret_cast<gbytes>(reinterpret_cast<uint64_t>(tile_weights(p, t)));
+        const gbytes w = reinterpret_cast<gbytes>(reinterpret_cast<uint64_t>(tmap.weights(t)));
         if constexpr (TILED) {
             // tile block (tile of the member, b): the member's rows are padded to
             // whole tiles, so every lane's bytes exist
-            k.load_tiled(w + (static_cast<int64_t>(to.row0 / kTileRows) * nb + b) * (kTileRows * BB), lane);
+            k.load_tiled(w + (static_cast<int64_t>(tmap.row0(t) / kTileRows) * nb + b) * (kTileRows * BB), lane);
         } else {
-            const int row = min(to.row0 + n, to.rows - 1);
+            // the member's rows from the struct (raw rows are not padded)
+            const int row = min(tmap.row0(t) + n, tile_out(pa, t).rows - 1);
             k.load(w + static_cast<int64_t>(row) * (nb * BB) + b * BB, q);
         }
     };
@@ -591,10 +622,10 @@ __global__ __launch_bounds__(W * 64) void gemv_mfma_kernel(const MfmaArgs p) {
     for (int lr = 0; lr < NR; ++lr) acc[lr] = 0.0f;
     int tile_iter = 0;
     Pos cq{static_cast<int>(blockIdx.x), 0};  // item being computed
-    while (cq.t < p.tiles) {
+    while (cq.t < tiles) {
 #pragma unroll
         for (int j = 0; j < D; ++j) {
-            if (cq.t < p.tiles) {  // uniform
+            if (cq.t < tiles) {  // uniform
                 const int it = cq.it;
                 const int b = wave + W * it;
                 const bool have = b < nb;  // uniform; a missing block is computed on block nb-1 and dropped
@@ -612,7 +643,7 @@ __global__ __launch_bounds__(W * 64) void gemv_mfma_kernel(const MfmaArgs p) {
                 // 4.45 -> 3.9 us). With more in flight the loads stay
                 // unconditional, so the wait counts cover exactly the block each
                 // value needs.
-                if (D > 1 || lq.t < p.tiles) load(lq, buf[j]);
+                if (D > 1 || lq.t < tiles) load(lq, buf[j]);
                 advance(lq);
                 if (it == iters - 1) {
                     // tile done: partial sums to LDS, then one wave adds them in wave order
@@ -626,7 +657,7 @@ __global__ __launch_bounds__(W * 64) void gemv_mfma_kernel(const MfmaArgs p) {
                     // barrier too, and no wait for the weight loads in flight
                     asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
                     if (wave == (tile_iter & (W - 1))) {
-                        const TileOut to = tile_out(p, cq.t);
+                        const TileOut to = tile_out(pa, cq.t);
                         const int row = to.row0 + n;
 #pragma unroll
                         for (int lr = 0; lr < NR; ++lr) {

@@ -219,9 +219,10 @@ __global__ __launch_bounds__(kStageBlocks * 64) void gemv_q4_staged_kernel(const
 
 template <int KIND, int MT, bool FUSED, int W, bool AREG>
 void launch_d(const MfmaArgs& p, int depth, dim3 grid, size_t lds, hipStream_t stream) {
-    if (depth >= 4) gemv_mfma_kernel<KIND, MT, FUSED, W, AREG, 4, false><<<grid, dim3(W * 64), lds, stream>>>(p);
-    else if (depth >= 2) gemv_mfma_kernel<KIND, MT, FUSED, W, AREG, 2, false><<<grid, dim3(W * 64), lds, stream>>>(p);
-    else gemv_mfma_kernel<KIND, MT, FUSED, W, AREG, 1, false><<<grid, dim3(W * 64), lds, stream>>>(p);
+    const TiledHead h = tiled_head(p, FUSED, grid.x);
+    if (depth >= 4) gemv_mfma_kernel<KIND, MT, FUSED, W, AREG, 4, false><<<grid, dim3(W * 64), lds, stream>>>(RK_HEAD(h), p);
+    else if (depth >= 2) gemv_mfma_kernel<KIND, MT, FUSED, W, AREG, 2, false><<<grid, dim3(W * 64), lds, stream>>>(RK_HEAD(h), p);
+    else gemv_mfma_kernel<KIND, MT, FUSED, W, AREG, 1, false><<<grid, dim3(W * 64), lds, stream>>>(RK_HEAD(h), p);
 }
 
 template <int KIND, int MT, bool FUSED, int W>
@@ -294,8 +295,29 @@ int launch_gemv_mfma(int kind, bool fused, GemvParams& p, hipStream_t stream) {
     const int mt = p.m <= 4 ? 4 : p.m <= 8 ? 8 : 16;
     // eight waves (eight block slots per tile) unless the rows are shorter
     const int w = p.nb < 8 ? 4 : 8;
+    int64_t all_tiles = 0;
+    for (int i = 0; i < p.count; ++i) all_tiles += (p.rows[i] + kTileRows - 1) / kTileRows;
+    if (all_tiles > 0xffff) {
+        // the preloaded arguments (TiledHead) hold at most 0xffff tiles: larger
+        // launches go member by member, and a larger member in runs of rows
+        // (the same bits: a row's arithmetic does not depend on its launch)
+        for (int i = 0; i < p.count; ++i) {
+            constexpr int64_t kRun = int64_t{0xffff} * kTileRows;
+            for (int64_t r0 = 0; r0 < p.rows[i]; r0 += kRun) {
+                GemvParams a = p;
+                a.count = 1;
+                a.w[0] = p.w[i] + r0 * p.nb * block_bytes(kind);
+                a.out[0] = p.out[i] + r0;
+                a.ldo[0] = p.ldo[i];
+                a.rows[0] = std::min(kRun, p.rows[i] - r0);
+                const int st = launch_gemv_mfma(kind, fused, a, stream);
+                if (st != kStatusOk) return st;
+            }
+        }
+        return kStatusOk;
+    }
     MfmaArgs ka;
-    if (mfma_args(p, w, ka) != kStatusOk) return kStatusInvalid;
+    if (mfma_args(p, w, ka) != kStatusOk || !head_fits(ka)) return kStatusInvalid;
     const int tiles = ka.tiles;
     // one workgroup per CU at most; each walks its tiles
     const int cus = device_cu_count();

@@ -338,23 +338,6 @@ int launch_gemv_tile_weights(int kind, const uint8_t* src, int64_t n, int nb, ui
 }
 
 namespace {
-// The scalar arguments ahead of MfmaArgs (TiledHead); p has at most three
-// members (launch_gemv_tiled splits a fourth off) and 16-bit counts.
-TiledHead tiled_head(const MfmaArgs& p, bool fused, unsigned grid) {
-    return TiledHead{fused ? static_cast<const void*>(p.x) : static_cast<const void*>(p.q8k), p.mb[0].w, p.mb[1].w,
-                     p.mb[2].w,
-                     static_cast<int>(static_cast<uint32_t>(p.mb[0].tile_end) |
-                                      static_cast<uint32_t>(p.mb[1].tile_end) << 16),
-                     p.tiles, static_cast<int>(grid), p.ldx,
-                     static_cast<int>(static_cast<uint32_t>(p.nb) | static_cast<uint32_t>(p.nbs) << 16),
-                     static_cast<int>(static_cast<uint32_t>(p.m) | static_cast<uint32_t>(p.iters) << 16)};
-}
-bool head_fits(const MfmaArgs& p) {
-    return p.mb[2].tile_end == p.tiles && p.tiles <= 0xffff && p.nb >= 0 && p.nb <= 0xffff && p.nbs >= 0 && p.nbs <= 0xffff && p.m >= 0 &&
-           p.m <= 0xffff && p.iters >= 0 && p.iters <= 0xffff;
-}
-#define RK_HEAD(h) h.x, h.w0, h.w1, h.w2, h.te01, h.tiles, h.grid, h.ldx, h.nb_nbs, h.m_iters
-
 // Pipelined kernel, NI items per wave (ni tiles of iters block indices): two
 // in flight for two or three items (TinyLlama gate+up, 2 x 5632 x 2048, three
 // tiles per workgroup at 4 rows: 5.32 us against 5.51 with one and 5.42 with
@@ -404,8 +387,10 @@ void launch_tiled_w(int ni, const MfmaArgs& p, dim3 grid, size_t lds_loop, size_
     {
         // more items per wave than the pipelined kernel unrolls: the item loop
         // with one block in flight (two or four measured slower there)
-        if (p.iters == 1) gemv_mfma_kernel<KIND, MT, FUSED, W, true, 1, true><<<grid, dim3(W * 64), lds_loop, stream>>>(p);
-        else gemv_mfma_kernel<KIND, MT, FUSED, W, false, 1, true><<<grid, dim3(W * 64), lds_loop, stream>>>(p);
+        const TiledHead h = tiled_head(p, FUSED, grid.x);
+        if (p.iters == 1)
+            gemv_mfma_kernel<KIND, MT, FUSED, W, true, 1, true><<<grid, dim3(W * 64), lds_loop, stream>>>(RK_HEAD(h), p);
+        else gemv_mfma_kernel<KIND, MT, FUSED, W, false, 1, true><<<grid, dim3(W * 64), lds_loop, stream>>>(RK_HEAD(h), p);
     }
 }
 
