@@ -460,14 +460,11 @@ __global__ __launch_bounds__(W * 64) void gemv_kernel(const void* x, const uint8
     const int wg = blockIdx.x;
     const LaneMember mem = lane_member(wg, w0, w1, w2, rows0, rows1, rows2, wg_ends);
     const bool c1 = mem.c1, c2 = mem.c2;
-    float* out = c2 ? pa.mb[2].out : c1 ? pa.mb[1].out : pa.mb[0].out;
-    const int ldo = c2 ? pa.mb[2].ldo : c1 ? pa.mb[1].ldo : pa.mb[0].ldo;
     const int rows = mem.rows;
     // row groups: the host's ceil(rows / rows_per_group), a power of two
     const int groups = (rows + (SW >> log2g) - 1) >> (6 - LOG2L - log2g);
     const int wg0 = mem.wg0, wg1 = mem.wg1;
     const gbytes wg_w = reinterpret_cast<gbytes>(reinterpret_cast<uint64_t>(mem.w));
-    const gfloats wg_out = reinterpret_cast<gfloats>(reinterpret_cast<uint64_t>(out));
 
     const int sl = lane >> LOG2L, pc = lane & (L - 1);  // block slot, lane inside the block
     const int G = 1 << log2g;
@@ -524,6 +521,16 @@ __global__ __launch_bounds__(W * 64) void gemv_kernel(const void* x, const uint8
         load_block(lq, buf[j]);
         advance(lq);
     }
+    // the member's output, read from the argument segment now, behind the
+    // first loads, rather than at the first store
+    MemberOuts mo;
+    mo.fetch(pa);
+    const float* out = c2 ? mo.o2 : c1 ? mo.o1 : mo.o0;
+    const int ldo = c2 ? mo.l2 : c1 ? mo.l1 : mo.l0;
+    // (held here: the compiler would otherwise sink the loads past the wait
+    // below to the first store; here the wait below covers them)
+    asm volatile("" ::"s"(out), "s"(ldo));
+    const gfloats wg_out = reinterpret_cast<gfloats>(reinterpret_cast<uint64_t>(out));
     stalled = stage_activations<FUSED>(p, xpre, quant_wave, quant_waves, a, q8_ready);
 
     float acc[MT];

@@ -241,6 +241,28 @@ struct XPre {
     }
 };
 
+// The first three members' output fields (out, ldo, rows), read from the
+// argument segment where fetch() is called (behind a launch's first loads)
+// rather than at the first store, where the compiler puts them otherwise.
+struct MemberOuts {
+    const float* o0;
+    const float* o1;
+    const float* o2;
+    int l0, l1, l2, r0, r1, r2;
+    template <class Args>
+    __device__ __forceinline__ void fetch(const Args& p) {
+        o0 = p.mb[0].out;
+        o1 = p.mb[1].out;
+        o2 = p.mb[2].out;
+        l0 = p.mb[0].ldo;
+        l1 = p.mb[1].ldo;
+        l2 = p.mb[2].ldo;
+        r0 = p.mb[0].rows;
+        r1 = p.mb[1].rows;
+        r2 = p.mb[2].rows;
+    }
+};
+
 // Copy Q8_K rows (292-byte blocks: f32 d, 256 quants, 16 int16 bsums) into
 // the LDS layout, one 32-bit word per thread and step.
 // t: this thread's index among the THREADS that copy.

@@ -506,6 +506,16 @@ __device__ __forceinline__ TileOut tile_out(const MfmaArgs& p, int t) {
                    c3 ? p.mb[3].ldo : c2 ? p.mb[2].ldo : c1 ? p.mb[1].ldo : p.mb[0].ldo,
                    c3 ? p.mb[3].rows : c2 ? p.mb[2].rows : c1 ? p.mb[1].rows : p.mb[0].rows, (t - t0) * kTileRows};
 }
+// tile_out on the preloaded tile ends and the fetched output fields (values
+// selected, so nothing lives in scratch memory).
+__device__ __forceinline__ TileOut tile_out(const TileMap& tm, const MemberOuts& mo, int t) {
+    const int e0 = tm.te0, e1 = tm.te1;
+    const bool c1 = t >= e0, c2 = t >= e1;
+    const float *a = mo.o0, *b = mo.o1, *c = mo.o2;
+    const int la = mo.l0, lb = mo.l1, lc = mo.l2, ra = mo.r0, rb = mo.r1, rc = mo.r2;
+    return TileOut{const_cast<float*>(c2 ? c : c1 ? b : a), c2 ? lc : c1 ? lb : la, c2 ? rc : c1 ? rb : ra,
+                   (t - (c2 ? e1 : c1 ? e0 : 0)) * kTileRows};
+}
 // A row's f32 sum from the W waves' partial sums pb[wave][lane][NR] of a tile,
 // in the order of the 8-wave kernel: the partials in wave order. With 16 waves
 // and one block per wave (rows of at most 16 blocks), wave s + 8 holds the
@@ -570,6 +580,11 @@ __global__ __launch_bounds__(W * 64) void gemv_mfma_kernel(const void* x, const 
         if (++c.it == iters) { c.it = 0; c.t += grid; }
     };
     const int last_t = tiles - 1 - (tiles - 1 - static_cast<int>(blockIdx.x)) % grid;
+    // the members' output fields (MemberOuts): on raw rows first thing (the
+    // first load needs the member's row count), on tiled copies behind the
+    // first weight load (as gemv_tiled_kernel)
+    MemberOuts mo{};
+    if constexpr (!TILED) mo.fetch(pa);
     auto load = [&](const Pos& c, Piece& k) {
         const bool live = c.t < tiles;
         const int t = live ? c.t : last_t;
@@ -580,8 +595,8 @@ __global__ __launch_bounds__(W * 64) void gemv_mfma_kernel(const void* x, const 
             // whole tiles, so every lane's bytes exist
             k.load_tiled(w + (static_cast<int64_t>(tmap.row0(t) / kTileRows) * nb + b) * (kTileRows * BB), lane);
         } else {
-            // the member's rows from the struct (raw rows are not padded)
-            const int row = min(tmap.row0(t) + n, tile_out(pa, t).rows - 1);
+            // the member's row count (raw rows are not padded to whole tiles)
+            const int row = min(tmap.row0(t) + n, tile_out(tmap, mo, t).rows - 1);
             k.load(w + static_cast<int64_t>(row) * (nb * BB) + b * BB, q);
         }
     };
@@ -598,6 +613,7 @@ __global__ __launch_bounds__(W * 64) void gemv_mfma_kernel(const void* x, const 
     Pos lq{static_cast<int>(blockIdx.x), 0};  // next item to load
     load(lq, buf[0]);
     advance(lq);
+    if constexpr (TILED) mo.fetch(pa);
     owned.template stage<AREG>(p, wave, act);
 #pragma unroll
     for (int j = 1; j < D; ++j) {
@@ -657,7 +673,7 @@ __global__ __launch_bounds__(W * 64) void gemv_mfma_kernel(const void* x, const 
                     // barrier too, and no wait for the weight loads in flight
                     asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
                     if (wave == (tile_iter & (W - 1))) {
-                        const TileOut to = tile_out(pa, cq.t);
+                        const TileOut to = tile_out(tmap, mo, cq.t);
                         const int row = to.row0 + n;
 #pragma unroll
                         for (int lr = 0; lr < NR; ++lr) {

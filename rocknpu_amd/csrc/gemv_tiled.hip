@@ -87,10 +87,10 @@ __global__ __launch_bounds__(W * 64) void gemv_tiled_kernel(const void* x, const
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int bid = blockIdx.x;
     // The launch's arguments: pa, with the fields the first loads need
-    // preloaded ahead of it (TiledHead) and taken from there. Only scalar
-    // fields of the local copy p are read (an array member indexed at run time
-    // would put the copy in scratch memory).
-    const MfmaArgs& p0 = pa;
+    // preloaded ahead of it (TiledHead) and taken from there; the rest of pa
+    // is read behind the first weight load (MemberOuts, below). Only
+    // scalar fields of the local copy p are read (an array member indexed at
+    // run time would put the copy in scratch memory).
     const int nb0 = nb_nbs & 0xffff, nbs0 = static_cast<int>(static_cast<uint32_t>(nb_nbs) >> 16);
     const TileMap tmap{w0, w1, w2, te01 & 0xffff, static_cast<int>(static_cast<uint32_t>(te01) >> 16)};
     // p: the range's view of the activations (its blocks from b0)
@@ -143,6 +143,19 @@ __global__ __launch_bounds__(W * 64) void gemv_tiled_kernel(const void* x, const
     __builtin_amdgcn_s_barrier();
     Piece buf[D];
     load_item(0, buf[0]);
+    // Unsplit launches read the members' outputs here, behind the first
+    // weight load: read where the stores use them, they are scalar loads that
+    // the compiler issues at the stores, and their round trips (the member's
+    // selection first, then its fields) sit at the end of every launch
+    // (TinyLlama o at one row 3.32 -> 3.05 us; the decode set's 66 Q4_K
+    // launches at one row 3.90 -> 3.67 us on average, at four rows 3.91 ->
+    // 3.68). Holding them in registers right here (an empty asm) waits for
+    // them at once: 0.4 us slower than that. Split launches keep them at
+    // the stores: read here, the compiler places the exchange's loads just
+    // before the quantisation's LDS wait, which then waits for them
+    // (TinyLlama down at four rows 5.22 -> 5.38 us).
+    MemberOuts mo{};
+    if constexpr (S == 1) mo.fetch(pa);
     // LAZY: only block index 0 quantised here, block index i (< IT) just
     // before item i, the first that reads it, so item 0's terms wait for one
     // quantisation instead of IT (each wave quantises and reads only its own
@@ -205,7 +218,7 @@ __global__ __launch_bounds__(W * 64) void gemv_tiled_kernel(const void* x, const
     __syncthreads();
     for (int kt = wave; kt < ntile; kt += W) {
         const int t = (bid + kt * grid) / S;
-        const TileOut to = tile_out(p0, t);
+        const TileOut to = S == 1 ? tile_out(tmap, mo, t) : tile_out(pa, t);
         const int row = to.row0 + n;
 #pragma unroll
         for (int lr = 0; lr < NR; ++lr) {
@@ -228,14 +241,14 @@ __global__ __launch_bounds__(W * 64) void gemv_tiled_kernel(const void* x, const
                 // slot, adds and writes the exact sum instead. Never other
                 // bits. Relaxed agent-scope atomics on one address are ordered
                 // for all workgroups of the device.
-                const uint32_t g = p0.gen % 0x7fffffffu + 1u;  // tags 2 .. 2^32 - 1, never 0
+                const uint32_t g = pa.gen % 0x7fffffffu + 1u;  // tags 2 .. 2^32 - 1, never 0
                 bool first = false;
                 int64_t base = 0;
 #pragma unroll
                 for (int lv = 0; (1 << lv) < S; ++lv) {
                     const int per = S >> (lv + 1), j = sp >> (lv + 1), side = (sp >> lv) & 1;
                     unsigned long long* slot =
-                        p0.split_slot + base + ((static_cast<int64_t>(t) * per + j) * 64 + lane) * NR + lr;
+                        pa.split_slot + base + ((static_cast<int64_t>(t) * per + j) * 64 + lane) * NR + lr;
                     base += static_cast<int64_t>(tiles) * per * 64 * NR;
                     const unsigned long long old = __hip_atomic_exchange(
                         slot, static_cast<unsigned long long>(2 * g + side) << 32 | __float_as_uint(r),
@@ -247,7 +260,7 @@ __global__ __launch_bounds__(W * 64) void gemv_tiled_kernel(const void* x, const
                     __hip_atomic_store(slot, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                     if (static_cast<uint32_t>(old >> 32) != 2 * g + (1 - side)) {
                         r = __builtin_nanf("");
-                        __hip_atomic_store(p0.split_err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                        __hip_atomic_store(pa.split_err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                         break;  // written now, as NaN
                     }
                     r += __uint_as_float(static_cast<uint32_t>(old));
