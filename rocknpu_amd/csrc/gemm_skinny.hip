@@ -32,8 +32,8 @@ constexpr int kSkinnyWaves = 8;
 template <int D>
 __global__ __launch_bounds__(kSkinnyWaves * 64) void gemm_w8a8_skinny_kernel(
     const int8_t* __restrict__ a8, int64_t lda, const int8_t* __restrict__ w8, int64_t ldw, int m, int n, int k,
-    const float* __restrict__ a_scales, const float* __restrict__ w_scales, float* __restrict__ out, int64_t ldo,
-    int32_t* __restrict__ out_i32, int64_t ldo_i32) {
+    int grid, const float* __restrict__ a_scales, const float* __restrict__ w_scales, float* __restrict__ out,
+    int64_t ldo, int32_t* __restrict__ out_i32, int64_t ldo_i32) {
     constexpr int W = kSkinnyWaves;
     extern __shared__ __align__(16) uint8_t smem[];
     const int lane = threadIdx.x & 63;
@@ -50,7 +50,7 @@ __global__ __launch_bounds__(kSkinnyWaves * 64) void gemm_w8a8_skinny_kernel(
         int it;
     };
     auto advance = [&](Pos& c) {
-        if (++c.it == iters) { c.it = 0; c.t += gridDim.x; }
+        if (++c.it == iters) { c.it = 0; c.t += grid; }  // grid = gridDim.x, preloaded
     };
     // Weight loads: 16 bytes of row col of tile t, K chunk wave + 8 it, and the
     // row's scale (rows and chunks past the ends re-read row n-1 / chunk 0;
@@ -157,11 +157,11 @@ int launch_gemm_w8a8_skinny(const int8_t* a8, int64_t lda, const int8_t* w8, int
     const int per_wave = (tiles + wgs - 1) / wgs * iters;
     const dim3 grid(static_cast<unsigned>(wgs)), block(kSkinnyWaves * 64);
     if (per_wave >= 8)
-        gemm_w8a8_skinny_kernel<8><<<grid, block, lds, stream>>>(a8, lda, w8, ldw, m, n, k, as, ws, out, ldo, oi, ldoi);
+        gemm_w8a8_skinny_kernel<8><<<grid, block, lds, stream>>>(a8, lda, w8, ldw, m, n, k, static_cast<int>(grid.x), as, ws, out, ldo, oi, ldoi);
     else if (per_wave >= 4)
-        gemm_w8a8_skinny_kernel<4><<<grid, block, lds, stream>>>(a8, lda, w8, ldw, m, n, k, as, ws, out, ldo, oi, ldoi);
+        gemm_w8a8_skinny_kernel<4><<<grid, block, lds, stream>>>(a8, lda, w8, ldw, m, n, k, static_cast<int>(grid.x), as, ws, out, ldo, oi, ldoi);
     else
-        gemm_w8a8_skinny_kernel<2><<<grid, block, lds, stream>>>(a8, lda, w8, ldw, m, n, k, as, ws, out, ldo, oi, ldoi);
+        gemm_w8a8_skinny_kernel<2><<<grid, block, lds, stream>>>(a8, lda, w8, ldw, m, n, k, static_cast<int>(grid.x), as, ws, out, ldo, oi, ldoi);
     return hipGetLastError() == hipSuccess ? kStatusOk : kStatusExec;
 }
 

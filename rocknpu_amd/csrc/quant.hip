@@ -37,11 +37,12 @@ __device__ __forceinline__ uint32_t pack4(int a, int b, int c, int d) {
     return (a & 0xFF) | (b & 0xFF) << 8 | (c & 0xFF) << 16 | static_cast<uint32_t>(d & 0xFF) << 24;
 }
 
-// Workgroup 0 clears `nzero` words (the split-K counters of the GEMM that
-// follows on the stream), so the prompt route needs no separate fill launch.
-__device__ __forceinline__ void zero_counters(uint32_t* words, int nzero) {
+// Workgroup 0 (of nt threads) clears `nzero` words (the split-K counters of
+// the GEMM that follows on the stream), so the prompt route needs no separate
+// fill launch.
+__device__ __forceinline__ void zero_counters(uint32_t* words, int nzero, int nt) {
     if (blockIdx.x == 0)
-        for (int i = threadIdx.x; i < nzero; i += blockDim.x) words[i] = 0;
+        for (int i = threadIdx.x; i < nzero; i += nt) words[i] = 0;
 }
 
 // One workgroup per activation row. VEC: k, lda and k_pad are multiples of 4
@@ -54,7 +55,7 @@ __global__ __launch_bounds__(kA8Threads) void quantize_a8_kernel(const float* __
                                                                  uint32_t* __restrict__ zero_words, int nzero,
                                                                  float* __restrict__ scales) {
     __shared__ float red[kA8Threads / 64];
-    zero_counters(zero_words, nzero);
+    zero_counters(zero_words, nzero, kA8Threads);
     const int64_t row = blockIdx.x;
     const float* x = a + row * lda;
     int8_t* q = a8 + row * k_pad;
@@ -119,13 +120,14 @@ __global__ __launch_bounds__(1024) void quantize_a8_regs_kernel(const float* __r
                                                                 int64_t lda, int64_t k_pad,
                                                                 int8_t* __restrict__ a8,
                                                                 uint32_t* __restrict__ zero_words, int nzero,
-                                                                float* __restrict__ scales) {
+                                                                int nthreads, float* __restrict__ scales) {
     __shared__ uint32_t red[16];
-    zero_counters(zero_words, nzero);
+    // nthreads = blockDim.x, passed as a preloaded argument: blockDim is a
+    // hidden argument, read from memory before the row's loads could go out
     const int64_t row = blockIdx.x;
     const float4* x = reinterpret_cast<const float4*>(a + row * lda);
     uint32_t* q = reinterpret_cast<uint32_t*>(a8 + row * k_pad);
-    const int t = threadIdx.x, nt = blockDim.x;
+    const int t = threadIdx.x, nt = nthreads;
     const int k4 = static_cast<int>(k / 4);
     float vals[4 * R];
 #pragma unroll
@@ -137,6 +139,7 @@ __global__ __launch_bounds__(1024) void quantize_a8_regs_kernel(const float* __r
         vals[4 * j + 2] = v.z;
         vals[4 * j + 3] = v.w;
     }
+    zero_counters(zero_words, nzero, nthreads);  // behind the row's loads
     uint32_t um = 0;
 #pragma unroll
     for (int i = 0; i < 4 * R; ++i) um = max(um, __float_as_uint(vals[i]) & 0x7fffffffu);
@@ -232,10 +235,11 @@ int launch_quantize_a8(const float* a, int64_t m, int64_t k, int64_t lda, int64_
     const int64_t r = (k4 + nt - 1) / nt;
     if (vec && r <= 4) {
         const dim3 rb(static_cast<unsigned>(nt));
-        if (r <= 1) quantize_a8_regs_kernel<1><<<grid, rb, 0, stream>>>(a, k, lda, k_pad, a8, zero_words, nzero, scales);
-        else if (r <= 2) quantize_a8_regs_kernel<2><<<grid, rb, 0, stream>>>(a, k, lda, k_pad, a8, zero_words, nzero, scales);
-        else if (r <= 3) quantize_a8_regs_kernel<3><<<grid, rb, 0, stream>>>(a, k, lda, k_pad, a8, zero_words, nzero, scales);
-        else quantize_a8_regs_kernel<4><<<grid, rb, 0, stream>>>(a, k, lda, k_pad, a8, zero_words, nzero, scales);
+        const int tn = static_cast<int>(nt);
+        if (r <= 1) quantize_a8_regs_kernel<1><<<grid, rb, 0, stream>>>(a, k, lda, k_pad, a8, zero_words, nzero, tn, scales);
+        else if (r <= 2) quantize_a8_regs_kernel<2><<<grid, rb, 0, stream>>>(a, k, lda, k_pad, a8, zero_words, nzero, tn, scales);
+        else if (r <= 3) quantize_a8_regs_kernel<3><<<grid, rb, 0, stream>>>(a, k, lda, k_pad, a8, zero_words, nzero, tn, scales);
+        else quantize_a8_regs_kernel<4><<<grid, rb, 0, stream>>>(a, k, lda, k_pad, a8, zero_words, nzero, tn, scales);
     } else if (vec) quantize_a8_kernel<true><<<grid, block, 0, stream>>>(a, k, lda, k_pad, a8, zero_words, nzero, scales);
     else quantize_a8_kernel<false><<<grid, block, 0, stream>>>(a, k, lda, k_pad, a8, zero_words, nzero, scales);
     return hipGetLastError() == hipSuccess ? kStatusOk : kStatusExec;

@@ -265,13 +265,13 @@ template <int KIND>
 __global__ __launch_bounds__(kWaves * 64) void repack_w8_stream_kernel(const uint8_t* __restrict__ blocks,
                                                                        int64_t n, int nb, int64_t k_pad,
                                                                        int8_t* __restrict__ w8,
-                                                                       float* __restrict__ scales) {
+                                                                       float* __restrict__ scales, int grid) {
     constexpr int BB = block_bytes(KIND);
     static_assert(kChunkBlocks * BB <= 128 * 16, "a row's pieces fit two per lane");
     __shared__ float lds[kWaves][kChunkBlocks * 16];
     __shared__ __align__(16) uint8_t raw[kWaves][kChunkBlocks * BB];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int64_t stride = static_cast<int64_t>(gridDim.x) * kWaves;
+    const int64_t stride = static_cast<int64_t>(grid) * kWaves;  // grid = gridDim.x, preloaded
     int64_t row = static_cast<int64_t>(blockIdx.x) * kWaves + wave;
     const int pieces = nb * BB / 16;
     const int64_t row_bytes = static_cast<int64_t>(nb) * BB;
@@ -331,7 +331,8 @@ void launch_kind(int64_t n, int nb, int64_t k_pad, const uint8_t* blocks, int8_t
         // twelve workgroups per CU at most; each wave walks rows from there
         const int64_t wgs = std::min<int64_t>((n + kWaves - 1) / kWaves, static_cast<int64_t>(device_cu_count()) * 12);
         repack_w8_stream_kernel<KIND><<<dim3(static_cast<unsigned>(wgs)), block, 0, stream>>>(blocks, n, nb, k_pad,
-                                                                                            w8, scales);
+                                                                                            w8, scales,
+                                                                                            static_cast<int>(wgs));
     } else if (nchunks == 1) repack_w8_kernel<KIND, 1><<<grid, block, 0, stream>>>(blocks, n, nb, k_pad, w8, scales);
     else if (nchunks == 2) repack_w8_kernel<KIND, 2><<<grid, block, 0, stream>>>(blocks, n, nb, k_pad, w8, scales);
     else repack_w8_kernel<KIND, 0><<<grid, block, 0, stream>>>(blocks, n, nb, k_pad, w8, scales);
