@@ -302,10 +302,33 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_w8a8_dma_kernel(
 #pragma unroll
         for (int j = 0; j < FN; ++j) ws_pre[j] = load_ws(j);
     }
+    // Larger tiles have no registers to spare: each thread loads one or two
+    // of the tile's BM + BN scales here (rows and columns past the matrix
+    // re-read its last one; they are never stored), and writes them to LDS
+    // once the first stage has landed (the loads are older, so they have
+    // too); the K loop's barriers publish them, and the epilogue reads them
+    // from LDS.
+    constexpr int NSC = BM + BN, THREADS = WM * WN * 64, SCP = PRE ? 1 : (NSC + THREADS - 1) / THREADS;
+    __shared__ float lsc[PRE ? 1 : NSC];
+    float scv[SCP];
+    if constexpr (!PRE) {
+#pragma unroll
+        for (int u = 0; u < SCP; ++u) {
+            const int idx = threadIdx.x + u * THREADS;
+            scv[u] = idx < BM ? a_scales[min(m0 + idx, m - 1)] : w_scales[min(n0 + min(idx, NSC - 1) - BM, n - 1)];
+        }
+    }
     // prologue: stages 0 .. ST-2 in flight, wait for stage 0, then stage ST-1
     unroll_seq([&](auto i) { issue(i, min(static_cast<int>(decltype(i)::value), KS - 1)); },
                std::make_integer_sequence<int, ST - 1>{});
     wait_vm<(ST - 2) * PER_STAGE>();
+    if constexpr (!PRE) {
+#pragma unroll
+        for (int u = 0; u < SCP; ++u) {
+            const int idx = threadIdx.x + u * THREADS;
+            if (idx < NSC) lsc[idx] = scv[u];
+        }
+    }
     __builtin_amdgcn_s_barrier();
     issue(std::integral_constant<int, ST - 1>{}, min(ST - 1, KS - 1));
     read_frags(S0{}, R0{}, S0{});
@@ -451,7 +474,9 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_w8a8_dma_kernel(
 #pragma unroll
             for (int e = 0; e < 16; ++e) rs[e] = rs_pre[i][e];
         } else {
-            load_rs(i, rs);
+            // row rbase + (e & 3) + 8 (e >> 2) of the tile's scales in LDS
+#pragma unroll
+            for (int e = 0; e < 16; ++e) rs[e] = lsc[rbase - m0 + (e & 3) + 8 * (e >> 2)];
         }
         if constexpr (SK)
             if (poison)
@@ -460,7 +485,7 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_w8a8_dma_kernel(
 #pragma unroll
         for (int j = 0; j < FN; ++j) {
             const int c0 = n0 + wn * TN + j * 32;
-            const float ws = PRE ? ws_pre[PRE ? j : 0] : load_ws(j);
+            const float ws = PRE ? ws_pre[PRE ? j : 0] : lsc[PRE ? 0 : BM + wn * TN + j * 32 + (lane & 31)];
 #pragma unroll
             for (int h = 0; h < 32 / HR; ++h) {
                 // elements e of rows [h*HR, (h+1)*HR) are e in [h*HR/2, (h+1)*HR/2)
