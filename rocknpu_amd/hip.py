@@ -333,7 +333,8 @@ def gemv_q8_k_tiled(kind: int, w: torch.Tensor, k: int, n: int, q8k: torch.Tenso
 
 def gemv_tiled_preferred(kind: int, m: int, k: int) -> bool:
     """Whether an m-row decode GEMV over K = k runs faster on the tiled copy
-    (from two rows; Q4_K rows of 16 or more blocks at one row) than on raw rows."""
+    than on raw rows: from two rows, and at one row for rows of 5-20, 25-27
+    and 32 or more blocks (Q6_K: up to 64)."""
     return bool(_lib.load().rocknpu_hip_gemv_tiled_preferred(kind, m, k))
 
 
