@@ -356,10 +356,11 @@ namespace {
 // Pipelined kernel, NI items per wave (ni tiles of iters block indices): two
 // in flight for two or three items (TinyLlama gate+up, 2 x 5632 x 2048, three
 // tiles per workgroup at 4 rows: 5.32 us against 5.51 with one and 5.42 with
-// three; TinyLlama down, 2048 x 5632 on 8 waves, three blocks per wave: 6.95
-// against 7.46 with one), one for four (Llama-3-8B down, 4096 x 14336 on 16
-// waves: 14.8 against 14.8-15.1 us with two or four; the 32000 x 2048 Q6_K
-// head, two eight-wave workgroups on most CUs: 11.4 against 11.9 / 12.5 us),
+// three, and with the arguments preloaded 4.77 against 4.93 with three;
+// TinyLlama down, 2048 x 5632 on 8 waves, three blocks per wave: 6.95 against
+// 7.46 with one), one for four (Llama-3-8B down, 4096 x 14336 on 16 waves:
+// 14.8 against 14.8-15.1 us with two or four; the 32000 x 2048 Q6_K head, two
+// eight-wave workgroups on most CUs: 11.4 against 11.9 / 12.5 us),
 // but two for four on eight waves with one workgroup per CU (Llama-3.2-1B
 // gate+up, 2 x 8192 x 2048, four tiles per workgroup: 6.0 against 6.3 us at
 // one row, 6.9 against 7.3 at eight).
@@ -503,6 +504,8 @@ void launch_split_s(int ni, const MfmaArgs& p, dim3 grid, size_t lds, hipStream_
         gemv_tiled_kernel<KIND, MT, FUSED, 8, true, 4, 1, 1, false, S><<<grid, block, lds, stream>>>(RK_HEAD(h), p);
     }
 }
+// Four items a wave keep one in flight (Llama-3-8B down in four ranges at one
+// row, arguments preloaded: 11.6 against 12.8 us with two).
 template <int KIND, int MT, bool FUSED, int S>
 void launch_split_w16(int ni, const MfmaArgs& p, dim3 grid, size_t lds, hipStream_t stream) {
     const dim3 block(16 * 64);
