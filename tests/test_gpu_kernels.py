@@ -366,6 +366,8 @@ def test_gemv_m_chunking():
     # launch of its own: the kernels take three members' fields as preloaded
     # arguments)
     (4, (2048, 256, 256, 512), 2048, 1), (6, (2048, 100, 300, 48), 5632, 1),
+    # raw rows on the matrix cores beyond 0xffff tiles (runs of 0xffff tiles)
+    (4, (65537 * 16 + 5,), 256, 4),
 ])
 def test_gemv_fused_grouped(kind, ns, k, m):
     """Fused Q8_K quant + grouped GEMV == separate quant + per-member GEMV, bit for bit,
